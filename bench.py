@@ -1,0 +1,191 @@
+#!/usr/bin/env python3
+"""Headline benchmark: Llama-2-7B-shape int8 batch-1 greedy decode on one MI355X.
+
+Workload: dim 4096, 32 layers, 32 heads, FFN 11008,
+vocab 32000, RoPE theta 1e4, untied lm_head, random-init N(0, 0.02) weights
+(fastrand seed 0) quantized per tensor to int8, batch 1, a 512-token seeded
+prompt (seed 1) fed through the cache path, then greedy decode steps.
+
+A "step" is one decode token (all 32 layers + lm_head + device argmax), one
+replay of the captured decode-step graph.  W untimed warm-up steps run after the
+prompt; the position is then rewound to the first decode position and exactly K
+steps are timed with HIP events on the launch stream (device synchronised
+before and after).  value = K / elapsed = decode tok/s on the one GPU.
+
+Also reported:
+  roofline      the dominant projection kernel (largest device time per token),
+                timed with HIP events over launches that rotate through all 32
+                layers' weights (so they stream from HBM, not the 256 MB MALL);
+                achieved = algorithmic bytes per launch / average launch time
+  cpu_baseline  the oracle (C restatement of the reference CPU path) on the same
+                int8 weights, reference-faithful single-threaded
+                matmul_i8_f32_tiled, timed over a few decode steps on the host
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def weight_bytes(cfg) -> int:
+    """int8 weight bytes + per-tensor scales read per decode token."""
+    h, ffn, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.n_layers
+    hd = h // cfg.n_heads
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    per_layer = h * (qd + 2 * kvd) + qd * h + 2 * h * ffn + ffn * h
+    return L * per_layer + V * h + 4 * (5 * L + 1)
+
+
+def cpu_baseline(model, cfg, prompt, n_tok: int) -> dict:
+    """Oracle decode on the GPU model's own int8 weights, single-threaded."""
+    from oracle import oracle as O
+    import esolearn_amd.llama as EL
+
+    oc = O.LlamaConfig(cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size, cfg.n_layers,
+                       cfg.n_heads, cfg.n_kv_heads, cfg.max_seq_len, cfg.rms_norm_eps,
+                       cfg.rope_theta, cfg.tie_word_embeddings, cfg.rope_scaling)
+    om = O.Llama(oc, None)
+    for layer in range(cfg.n_layers):
+        for tid in (EL.T_QKV, EL.T_O, EL.T_GATE, EL.T_UP, EL.T_DOWN):
+            q, s = model.qtensor(tid, layer)
+            om.set_qtensor(tid, layer, q, s)
+    q, s = model.qtensor(EL.T_LM_HEAD)
+    om.set_qtensor(EL.T_LM_HEAD, 0, q, s)
+    del q
+    om.set_embed(model.embed())
+    O.set_threads(0)  # matmul_i8_f32_tiled exactly as written: one thread
+    cache = om.new_cache(n_tok + 1)
+    t0 = time.perf_counter()
+    for i in range(n_tok):
+        om.forward_with_cache(cache, int(prompt[i]), i, mode=1)
+    dt = time.perf_counter() - t0
+    om.close()
+    return {
+        "value": round(n_tok / dt, 5),
+        "unit": "tok/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{n_tok} decode steps (positions 0..{n_tok - 1}) of the same "
+                   "Llama-2-7B-shape int8 model on the host, oracle in reference-faithful "
+                   "mode (single-threaded matmul_i8_f32_tiled, f64 products); "
+                   f"{dt:.1f} s; host {platform.processor() or platform.machine()}, "
+                   f"nproc {os.cpu_count()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode steps (K)")
+    ap.add_argument("--warmup", type=int, default=16, help="untimed decode steps (W)")
+    ap.add_argument("--prompt-len", type=int, default=512)
+    ap.add_argument("--proj-iters", type=int, default=96)
+    ap.add_argument("--cpu-tokens", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--host-init", action="store_true",
+                    help="draw the random weights on the host (slow) instead of the GPU")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build runs on exactly one GPU (the int8 decode path has no "
+              "multi-GPU mode; see DESIGN.md for how it would shard). Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import esolearn_amd as E
+    import esolearn_amd.llama as EL
+
+    E.init(0)
+    info = E.HipBackend.device_info()
+    cfg = E.LlamaConfig.llama2_7b()
+    t0 = time.perf_counter()
+    model = E.LlamaModel.new_random(cfg, seed=0, init_on_device=not args.host_init)
+    t_init = time.perf_counter() - t0
+    prompt = E.synth.prompt_ids(1, args.prompt_len, cfg.vocab_size)
+    print(f"[bench] {info['name']} {info['arch']} CUs={info['cu_count']}; model init "
+          f"{t_init:.1f} s", file=sys.stderr, flush=True)
+
+    E.HipBackend.synchronize()
+    t0 = time.perf_counter()
+    ms, toks = model.bench_decode(prompt, args.warmup, args.steps)
+    wall = time.perf_counter() - t0
+    E.HipBackend.synchronize()
+    tok_s = args.steps / (ms / 1000.0)
+    print(f"[bench] decode {args.steps} steps in {ms:.2f} ms -> {tok_s:.1f} tok/s "
+          f"(call wall {wall:.2f} s incl. prompt + warm-up)", file=sys.stderr, flush=True)
+
+    # per-projection kernel timing (HIP events, rotating over layers)
+    proj = {}
+    per_token = {"qkv": cfg.n_layers, "o": cfg.n_layers, "gate_up": cfg.n_layers,
+                 "down": cfg.n_layers, "lm_head": 1}
+    for name, tid in (("qkv", EL.T_QKV), ("o", EL.T_O), ("gate_up", EL.T_GATE),
+                      ("down", EL.T_DOWN), ("lm_head", EL.T_LM_HEAD)):
+        us, b = model.time_projection(tid, args.proj_iters)
+        proj[name] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1),
+                      "us_per_token": round(us * per_token[name], 1)}
+        print(f"[bench] {name:8s} {us:8.2f} us  {b / 1e6:8.2f} MB  {b / us / 1e3:7.1f} GB/s",
+              file=sys.stderr, flush=True)
+    dom = max(proj, key=lambda k: proj[k]["us_per_token"])
+    wb = weight_bytes(cfg)
+    roofline = {
+        "bound": "hbm",
+        "achieved": proj[dom]["gbs"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(proj[dom]["gbs"] / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "kernel": f"k_qgemv ({dom} projection, decode epilogue)",
+        "bytes_per_launch": proj[dom]["bytes"],
+        "avg_launch_us": proj[dom]["avg_us"],
+    }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print(f"[bench] cpu baseline: {args.cpu_tokens} tokens", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(model, cfg, prompt, args.cpu_tokens)
+
+    line = {
+        "metric": "decode tok/s, Llama-7B-shape int8 batch 1; quant-GEMV achieved HBM GB/s",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "llama2-7b-shape int8 batch-1 greedy decode (BASELINE config 4)",
+            "dim": cfg.hidden_size, "layers": cfg.n_layers, "heads": cfg.n_heads,
+            "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size, "batch": 1,
+            "prompt_tokens": args.prompt_len, "decode_tokens": args.steps,
+            "context_end": args.prompt_len + args.steps, "weights": "int8 per-tensor (W8A32)",
+            "parallelism": "single GPU",
+        },
+        "weight_bytes_per_token": wb,
+        "decode_roofline_frac": round(tok_s * wb / (HBM_PEAK_GBS * 1e9), 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "projections": proj,
+        "greedy_tokens_head": [int(t) for t in toks[:8]],
+    }
+    print(json.dumps(line), flush=True)
+    model.free()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

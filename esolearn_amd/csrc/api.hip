@@ -1,0 +1,608 @@
+// Runtime (device, stream, errors) and the op-level C ABI: DeviceBackend
+// storage and the MathBackend methods on the int8 Llama path.  The reference
+// trait methods are static and panic on failure (backend/mod.rs:12-622); here
+// every entry point returns a status code instead.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "internal.h"
+
+namespace scry {
+
+Ctx &ctx() {
+    static Ctx c;
+    return c;
+}
+
+std::recursive_mutex &api_mutex() {
+    static std::recursive_mutex m;
+    return m;
+}
+
+static thread_local std::string g_err;
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *expr, const char *file, int line) {
+    const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? SCRY_ERR_OOM
+                                                                                  : SCRY_ERR_HIP;
+    (void)hipGetLastError();
+    return set_error(code, "%s failed: %s (%s:%d)", expr, hipGetErrorString(e), file, line);
+}
+
+int dev_alloc(void **p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return set_error(SCRY_ERR_OOM, "hipMalloc(%zu bytes) failed: %s", bytes, hipGetErrorString(e));
+    }
+    return SCRY_OK;
+}
+
+void dev_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+void packed_free(Packed &p) {
+    dev_free(p.d);
+    dev_free(p.s32);
+    p = Packed{};
+}
+
+}  // namespace scry
+
+using namespace scry;
+
+#define API_LOCK std::lock_guard<std::recursive_mutex> _api_lock(scry::api_mutex())
+
+namespace {
+
+int new_buf(size_t n, scry_buf *out) {
+    if (!out) return set_error(SCRY_ERR_INVALID, "null output handle");
+    auto *b = new (std::nothrow) scry_buf_s;
+    if (!b) return set_error(SCRY_ERR_OOM, "host allocation failed");
+    int rc = dev_alloc((void **)&b->d, n * sizeof(float));
+    if (rc) {
+        delete b;
+        return rc;
+    }
+    b->n = n;
+    *out = b;
+    return SCRY_OK;
+}
+
+void del_buf(scry_buf b) {
+    if (!b) return;
+    dev_free(b->d);
+    delete b;
+}
+
+int sync() {
+    SCRY_HIP(hipStreamSynchronize(ctx().stream));
+    return SCRY_OK;
+}
+
+#define CHECK_BUF(b, what)                                                      \
+    do {                                                                        \
+        if (!(b) || !(b)->d) return set_error(SCRY_ERR_INVALID, "%s: null storage", what); \
+    } while (0)
+
+// Ensure the GEMV layout of an I8Storage for logical [k, n].
+int ensure_packed(scry_i8buf q, int k, int n) {
+    Packed &p = q->packed;
+    if (p.d && p.k == k && p.n == n) return SCRY_OK;
+    packed_free(p);
+    p.k = k;
+    p.n = n;
+    p.kp = round_up(k, 16);
+    p.rows = n;
+    SCRY_TRY(dev_alloc((void **)&p.d, p.bytes()));
+    return launch_i8_pack(q->d, k, n, 0, p.d, p.kp, 1, 1, 0, ctx().stream);
+}
+
+int check_mkn(size_t a_len, size_t b_len, int m, int k, int n) {
+    if (m <= 0 || k <= 0 || n <= 0) return set_error(SCRY_ERR_INVALID, "matmul: m, k, n must be > 0");
+    if (a_len != (size_t)m * k) return set_error(SCRY_ERR_INVALID, "matmul: A has %zu elements, m*k = %zu", a_len, (size_t)m * k);
+    if (b_len != (size_t)k * n) return set_error(SCRY_ERR_INVALID, "matmul: B has %zu elements, k*n = %zu", b_len, (size_t)k * n);
+    return SCRY_OK;
+}
+
+int qmatmul(scry_buf a, scry_i8buf bq, float scale, const float *scales32, const float *bias, int m,
+            int k, int n, scry_buf *out) {
+    CHECK_BUF(a, "matmul_i8_f32");
+    if (!bq || !bq->d) return set_error(SCRY_ERR_INVALID, "matmul_i8_f32: null int8 storage");
+    SCRY_TRY(check_mkn(a->n, bq->n, m, k, n));
+    SCRY_TRY(ensure_packed(bq, k, n));
+    scry_buf o = nullptr;
+    SCRY_TRY(new_buf((size_t)m * n, &o));
+    Packed w = bq->packed;
+    w.scale = scale;
+    w.s32 = const_cast<float *>(scales32);
+    w.nb = (k + 31) / 32;
+    GemvArgs g;
+    g.w = &w;
+    g.x = a->d;
+    g.ldx = k;
+    g.m = m;
+    g.y = o->d;
+    g.ldy = n;
+    g.bias = bias;
+    int rc = launch_qgemv(EPI_STORE, g, ctx().stream);
+    if (rc) {
+        del_buf(o);
+        return rc;
+    }
+    *out = o;
+    return SCRY_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ------------------------------------------------------------------ runtime
+int scry_hip_init(int device) {
+    API_LOCK;
+    Ctx &c = ctx();
+    if (c.init) {
+        if (c.device == device) return SCRY_OK;
+        return set_error(SCRY_ERR_INVALID, "already initialised on device %d", c.device);
+    }
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+        (void)hipGetLastError();
+        return set_error(SCRY_ERR_NOT_INIT, "no HIP device available (%s)",
+                         e == hipSuccess ? "count 0" : hipGetErrorString(e));
+    }
+    if (device < 0 || device >= n) return set_error(SCRY_ERR_INVALID, "device %d of %d", device, n);
+    SCRY_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    SCRY_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(SCRY_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only",
+                         device, prop.gcnArchName);
+    SCRY_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    c.device = device;
+    c.cu_count = prop.multiProcessorCount;
+    c.name = prop.name;
+    c.arch = prop.gcnArchName;
+    c.init = true;
+    return SCRY_OK;
+}
+
+int scry_hip_shutdown(void) {
+    API_LOCK;
+    Ctx &c = ctx();
+    if (!c.init) return SCRY_OK;
+    (void)hipStreamSynchronize(c.stream);
+    (void)hipStreamDestroy(c.stream);
+    c = Ctx{};
+    return SCRY_OK;
+}
+
+const char *scry_hip_last_error(void) { return g_err.c_str(); }
+
+int scry_hip_synchronize(void) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    return sync();
+}
+
+int scry_hip_device_count(int *count) {
+    if (!count) return set_error(SCRY_ERR_INVALID, "null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        n = 0;
+    }
+    *count = n;
+    return SCRY_OK;
+}
+
+int scry_hip_device_info(char *name, size_t name_len, int *cu_count, char *arch, size_t arch_len) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    Ctx &c = ctx();
+    if (name && name_len) std::snprintf(name, name_len, "%s", c.name.c_str());
+    if (arch && arch_len) std::snprintf(arch, arch_len, "%s", c.arch.c_str());
+    if (cu_count) *cu_count = c.cu_count;
+    return SCRY_OK;
+}
+
+// ------------------------------------------------------------ f32 storage
+int scry_hip_zeros(size_t n, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    SCRY_TRY(new_buf(n, out));
+    return launch_fill_f32((*out)->d, n, 0.f, ctx().stream);
+}
+
+int scry_hip_from_vec(const float *host, size_t n, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!host && n) return set_error(SCRY_ERR_INVALID, "from_vec: null host pointer");
+    SCRY_TRY(new_buf(n, out));
+    if (n) {
+        SCRY_HIP(hipMemcpyAsync((*out)->d, host, n * sizeof(float), hipMemcpyHostToDevice, ctx().stream));
+        SCRY_TRY(sync());
+    }
+    return SCRY_OK;
+}
+
+int scry_hip_to_vec(scry_buf b, float *host, size_t n) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(b, "to_vec");
+    if (n != b->n) return set_error(SCRY_ERR_INVALID, "to_vec: storage has %zu elements, asked %zu", b->n, n);
+    if (n) SCRY_HIP(hipMemcpyAsync(host, b->d, n * sizeof(float), hipMemcpyDeviceToHost, ctx().stream));
+    return sync();
+}
+
+int scry_hip_clone_storage(scry_buf src, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(src, "clone_storage");
+    SCRY_TRY(new_buf(src->n, out));
+    if (src->n)
+        SCRY_HIP(hipMemcpyAsync((*out)->d, src->d, src->n * sizeof(float), hipMemcpyDeviceToDevice,
+                                ctx().stream));
+    return SCRY_OK;
+}
+
+int scry_hip_buf_len(scry_buf b, size_t *n) {
+    if (!b || !n) return set_error(SCRY_ERR_INVALID, "buf_len: null argument");
+    *n = b->n;
+    return SCRY_OK;
+}
+
+int scry_hip_free(scry_buf b) {
+    API_LOCK;
+    if (b && ctx().init) (void)hipStreamSynchronize(ctx().stream);
+    del_buf(b);
+    return SCRY_OK;
+}
+
+// ----------------------------------------------------------- int8 storage
+int scry_hip_i8_from_vec(const int8_t *host, size_t n, scry_i8buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!out || (!host && n)) return set_error(SCRY_ERR_INVALID, "i8_from_vec: null argument");
+    auto *q = new (std::nothrow) scry_i8buf_s;
+    if (!q) return set_error(SCRY_ERR_OOM, "host allocation failed");
+    int rc = dev_alloc((void **)&q->d, n);
+    if (rc) {
+        delete q;
+        return rc;
+    }
+    q->n = n;
+    if (n) {
+        hipError_t e = hipMemcpyAsync(q->d, host, n, hipMemcpyHostToDevice, ctx().stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx().stream);
+        if (e != hipSuccess) {
+            dev_free(q->d);
+            delete q;
+            return hip_fail(e, "i8_from_vec copy", __FILE__, __LINE__);
+        }
+    }
+    *out = q;
+    return SCRY_OK;
+}
+
+int scry_hip_i8_to_vec(scry_i8buf b, int8_t *host, size_t n) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!b || !b->d) return set_error(SCRY_ERR_INVALID, "i8_to_vec: null storage");
+    if (n != b->n) return set_error(SCRY_ERR_INVALID, "i8_to_vec: storage has %zu elements, asked %zu", b->n, n);
+    if (n) SCRY_HIP(hipMemcpyAsync(host, b->d, n, hipMemcpyDeviceToHost, ctx().stream));
+    return sync();
+}
+
+int scry_hip_i8_len(scry_i8buf b, size_t *n) {
+    if (!b || !n) return set_error(SCRY_ERR_INVALID, "i8_len: null argument");
+    *n = b->n;
+    return SCRY_OK;
+}
+
+int scry_hip_i8_free(scry_i8buf b) {
+    API_LOCK;
+    if (!b) return SCRY_OK;
+    if (ctx().init) (void)hipStreamSynchronize(ctx().stream);
+    packed_free(b->packed);
+    dev_free(b->d);
+    delete b;
+    return SCRY_OK;
+}
+
+// --------------------------------------------------------------- quantize
+int scry_hip_quantize_symmetric(scry_buf w, scry_i8buf *q_out, float *scale_out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(w, "quantize_symmetric");
+    if (!q_out || !scale_out) return set_error(SCRY_ERR_INVALID, "quantize_symmetric: null output");
+    auto *q = new (std::nothrow) scry_i8buf_s;
+    if (!q) return set_error(SCRY_ERR_OOM, "host allocation failed");
+    unsigned int *bits = nullptr;
+    float *dscale = nullptr;
+    int rc = dev_alloc((void **)&q->d, w->n);
+    if (!rc) rc = dev_alloc((void **)&bits, 16);
+    if (!rc) rc = dev_alloc((void **)&dscale, 16);
+    if (!rc) rc = launch_absmax(w->d, w->n, bits, ctx().stream);
+    if (!rc) rc = launch_quantize_plain(w->d, w->n, bits, q->d, dscale, ctx().stream);
+    float s = 0.f;
+    if (!rc && w->n) {
+        hipError_t e = hipMemcpyAsync(&s, dscale, sizeof(float), hipMemcpyDeviceToHost, ctx().stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx().stream);
+        if (e != hipSuccess) rc = hip_fail(e, "quantize scale readback", __FILE__, __LINE__);
+    }
+    dev_free(bits);
+    dev_free(dscale);
+    if (rc) {
+        dev_free(q->d);
+        delete q;
+        return rc;
+    }
+    q->n = w->n;
+    *q_out = q;
+    *scale_out = s;
+    return SCRY_OK;
+}
+
+int scry_hip_dequantize(scry_i8buf q, float scale, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!q || !q->d) return set_error(SCRY_ERR_INVALID, "dequantize: null storage");
+    SCRY_TRY(new_buf(q->n, out));
+    return launch_dequantize(q->d, q->n, scale, (*out)->d, ctx().stream);
+}
+
+int scry_hip_quantize_block32(scry_buf w, int k, int n, scry_i8buf *q_out, scry_buf *scales_out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(w, "quantize_block32");
+    if (k <= 0 || n <= 0 || w->n != (size_t)k * n)
+        return set_error(SCRY_ERR_INVALID, "quantize_block32: storage has %zu elements, k*n = %zu", w->n,
+                         (size_t)k * n);
+    auto *q = new (std::nothrow) scry_i8buf_s;
+    if (!q) return set_error(SCRY_ERR_OOM, "host allocation failed");
+    scry_buf sc = nullptr;
+    int rc = dev_alloc((void **)&q->d, w->n);
+    if (!rc) rc = new_buf((size_t)n * ((k + 31) / 32), &sc);
+    if (!rc) rc = launch_quant_block32(w->d, k, n, 0, q->d, sc->d, ctx().stream);
+    if (rc) {
+        dev_free(q->d);
+        delete q;
+        del_buf(sc);
+        return rc;
+    }
+    q->n = w->n;
+    *q_out = q;
+    *scales_out = sc;
+    return SCRY_OK;
+}
+
+// ------------------------------------------------------------- int8 matmul
+int scry_hip_matmul_i8_f32(scry_buf a, scry_i8buf b_q, float scale, int m, int k, int n,
+                           scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    return qmatmul(a, b_q, scale, nullptr, nullptr, m, k, n, out);
+}
+
+int scry_hip_matmul_i8_f32_bias(scry_buf a, scry_i8buf b_q, float scale, scry_buf bias, int m,
+                                int k, int n, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(bias, "matmul_i8_f32_bias");
+    if (bias->n < (size_t)n) return set_error(SCRY_ERR_INVALID, "matmul_i8_f32_bias: bias shorter than n");
+    return qmatmul(a, b_q, scale, nullptr, bias->d, m, k, n, out);
+}
+
+int scry_hip_matmul_i8_f32_block32(scry_buf a, scry_i8buf b_q, scry_buf scales, int m, int k,
+                                   int n, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(scales, "matmul_i8_f32_block32");
+    if (scales->n != (size_t)n * ((k + 31) / 32))
+        return set_error(SCRY_ERR_INVALID, "matmul_i8_f32_block32: need n*ceil(k/32) scales");
+    return qmatmul(a, b_q, 0.f, scales->d, nullptr, m, k, n, out);
+}
+
+// --------------------------------------------------------------- f32 glue
+int scry_hip_matmul(scry_buf a, scry_buf b, int m, int k, int n, int trans_a, int trans_b,
+                    scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(a, "matmul");
+    CHECK_BUF(b, "matmul");
+    SCRY_TRY(check_mkn(a->n, b->n, m, k, n));
+    SCRY_TRY(new_buf((size_t)m * n, out));
+    return launch_matmul_f32(a->d, b->d, 1, m, k, n, trans_a, trans_b, (*out)->d, ctx().stream);
+}
+
+int scry_hip_matmul_strided_batched(scry_buf a, scry_buf b, int batch, int m, int k, int n,
+                                    int trans_a, int trans_b, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(a, "matmul_strided_batched");
+    CHECK_BUF(b, "matmul_strided_batched");
+    if (batch <= 0 || m <= 0 || k <= 0 || n <= 0)
+        return set_error(SCRY_ERR_INVALID, "matmul_strided_batched: sizes must be > 0");
+    if (a->n < (size_t)batch * m * k || b->n < (size_t)batch * k * n)
+        return set_error(SCRY_ERR_INVALID, "matmul_strided_batched: operand too short");
+    SCRY_TRY(new_buf((size_t)batch * m * n, out));
+    return launch_matmul_f32(a->d, b->d, batch, m, k, n, trans_a, trans_b, (*out)->d, ctx().stream);
+}
+
+int scry_hip_rmsnorm(scry_buf x, scry_buf w, int rows, int d, float eps, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "rmsnorm");
+    CHECK_BUF(w, "rmsnorm");
+    if (rows <= 0 || d <= 0 || x->n != (size_t)rows * d || w->n < (size_t)d)
+        return set_error(SCRY_ERR_INVALID, "rmsnorm: shape mismatch");
+    SCRY_TRY(new_buf(x->n, out));
+    return launch_rmsnorm(x->d, w->d, rows, d, eps, (*out)->d, ctx().stream);
+}
+
+static int rope_common(scry_buf x, int seq, int n_heads, int head_dim, int start_pos, scry_buf freqs,
+                       int scaled, float scale, scry_buf *out) {
+    CHECK_BUF(x, "rope");
+    CHECK_BUF(freqs, "rope");
+    if (seq <= 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2 ||
+        x->n != (size_t)seq * n_heads * head_dim || freqs->n != (size_t)head_dim / 2)
+        return set_error(SCRY_ERR_INVALID, "rope: shape mismatch");
+    SCRY_TRY(new_buf(x->n, out));
+    return launch_rope(x->d, seq, n_heads, head_dim, start_pos, freqs->d, scaled, scale, (*out)->d,
+                       ctx().stream);
+}
+
+int scry_hip_rope_with_freqs_preloaded(scry_buf x, int seq, int n_heads, int head_dim,
+                                       int start_pos, scry_buf freqs, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    return rope_common(x, seq, n_heads, head_dim, start_pos, freqs, 0, 1.f, out);
+}
+
+int scry_hip_rope_with_freqs_scaled_preloaded(scry_buf x, int seq, int n_heads, int head_dim,
+                                              int start_pos, scry_buf freqs, float scale,
+                                              scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    return rope_common(x, seq, n_heads, head_dim, start_pos, freqs, 1, scale, out);
+}
+
+int scry_hip_scale(scry_buf x, float s, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "scale");
+    SCRY_TRY(new_buf(x->n, out));
+    return launch_scale(x->d, x->n, s, (*out)->d, ctx().stream);
+}
+
+int scry_hip_softmax(scry_buf x, int rows, int cols, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "softmax");
+    if (rows <= 0 || cols <= 0 || x->n != (size_t)rows * cols)
+        return set_error(SCRY_ERR_INVALID, "softmax: shape mismatch");
+    SCRY_TRY(new_buf(x->n, out));
+    return launch_softmax(x->d, rows, cols, (*out)->d, ctx().stream);
+}
+
+int scry_hip_swiglu(scry_buf gate, scry_buf up, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(gate, "swiglu");
+    CHECK_BUF(up, "swiglu");
+    if (gate->n != up->n) return set_error(SCRY_ERR_INVALID, "swiglu: length mismatch");
+    SCRY_TRY(new_buf(gate->n, out));
+    return launch_swiglu(gate->d, up->d, gate->n, (*out)->d, ctx().stream);
+}
+
+int scry_hip_add(scry_buf a, scry_buf b, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(a, "add");
+    CHECK_BUF(b, "add");
+    if (a->n != b->n) return set_error(SCRY_ERR_INVALID, "add: length mismatch (same-shape add only)");
+    SCRY_TRY(new_buf(a->n, out));
+    return launch_add(a->d, b->d, a->n, (*out)->d, ctx().stream);
+}
+
+int scry_hip_embedding(scry_buf weight, const int64_t *ids, int n_ids, int vocab, int dim,
+                       scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(weight, "embedding");
+    if (n_ids < 0 || vocab <= 0 || dim <= 0 || weight->n != (size_t)vocab * dim || (n_ids && !ids))
+        return set_error(SCRY_ERR_INVALID, "embedding: shape mismatch");
+    for (int i = 0; i < n_ids; i++)
+        if (ids[i] < 0 || ids[i] >= vocab)
+            return set_error(SCRY_ERR_RANGE, "embedding index out of range: %lld >= vocab %d",
+                             (long long)ids[i], vocab);
+    int64_t *d_ids = nullptr;
+    SCRY_TRY(dev_alloc((void **)&d_ids, sizeof(int64_t) * (size_t)(n_ids ? n_ids : 1)));
+    int rc = new_buf((size_t)n_ids * dim, out);
+    if (!rc && n_ids) {
+        hipError_t e = hipMemcpyAsync(d_ids, ids, sizeof(int64_t) * n_ids, hipMemcpyHostToDevice,
+                                      ctx().stream);
+        if (e != hipSuccess) rc = hip_fail(e, "embedding ids upload", __FILE__, __LINE__);
+        if (!rc) rc = launch_embedding(weight->d, d_ids, n_ids, dim, (*out)->d, ctx().stream);
+        if (!rc) rc = sync();
+    }
+    dev_free(d_ids);
+    return rc;
+}
+
+int scry_hip_gather_reshape_repeat_kv(scry_buf cache, int max_seq, int cached_len, int n_kv,
+                                      int n_q, int head_dim, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(cache, "gather_reshape_repeat_kv");
+    if (n_kv <= 0 || n_q % n_kv || cached_len < 0 || cached_len > max_seq ||
+        cache->n < (size_t)max_seq * n_kv * head_dim)
+        return set_error(SCRY_ERR_INVALID, "gather_reshape_repeat_kv: shape mismatch");
+    SCRY_TRY(new_buf((size_t)n_q * cached_len * head_dim, out));
+    return launch_gather_repeat_kv(cache->d, cached_len, n_kv, n_q, head_dim, (*out)->d, ctx().stream);
+}
+
+int scry_hip_repeat_kv(scry_buf x, int n_kv, int n_q, int seq, int d_head, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "repeat_kv");
+    if (n_kv <= 0 || n_q % n_kv || x->n != (size_t)n_kv * seq * d_head)
+        return set_error(SCRY_ERR_INVALID, "repeat_kv: shape mismatch");
+    SCRY_TRY(new_buf((size_t)n_q * seq * d_head, out));
+    return launch_repeat_kv(x->d, n_kv, n_q, seq, d_head, (*out)->d, ctx().stream);
+}
+
+int scry_hip_scatter_rows(scry_buf dst, scry_buf src, int total_rows, int cols, int row_start,
+                          int row_count) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(dst, "scatter_rows");
+    CHECK_BUF(src, "scatter_rows");
+    if (row_start < 0 || row_count < 0 || row_start + row_count > total_rows ||
+        dst->n < (size_t)total_rows * cols || src->n < (size_t)row_count * cols)
+        return set_error(SCRY_ERR_RANGE, "scatter_rows: rows [%d, %d) outside %d", row_start,
+                         row_start + row_count, total_rows);
+    if (row_count && cols)
+        SCRY_HIP(hipMemcpyAsync(dst->d + (size_t)row_start * cols, src->d,
+                                sizeof(float) * (size_t)row_count * cols, hipMemcpyDeviceToDevice,
+                                ctx().stream));
+    return SCRY_OK;
+}
+
+int scry_hip_argmax(scry_buf logits, int64_t *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(logits, "argmax");
+    if (!out) return set_error(SCRY_ERR_INVALID, "argmax: null output");
+    int64_t *d = nullptr;
+    SCRY_TRY(dev_alloc((void **)&d, sizeof(int64_t)));
+    int rc = launch_argmax(logits->d, (int64_t)logits->n, d, ctx().stream);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(out, d, sizeof(int64_t), hipMemcpyDeviceToHost, ctx().stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx().stream);
+        if (e != hipSuccess) rc = hip_fail(e, "argmax readback", __FILE__, __LINE__);
+    }
+    dev_free(d);
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,189 @@
+// Internal declarations shared by the scry_hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+#include "../../include/scry_hip.h"
+
+namespace scry {
+
+struct Ctx {
+    bool init = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    int cu_count = 0;
+    std::string name, arch;
+};
+
+Ctx &ctx();
+std::recursive_mutex &api_mutex();
+
+int set_error(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *expr, const char *file, int line);
+int dev_alloc(void **p, size_t bytes);
+void dev_free(void *p);
+
+#define SCRY_HIP(expr)                                                          \
+    do {                                                                        \
+        hipError_t _e = (expr);                                                 \
+        if (_e != hipSuccess) return ::scry::hip_fail(_e, #expr, __FILE__, __LINE__); \
+    } while (0)
+
+#define SCRY_TRY(expr)                 \
+    do {                               \
+        int _rc = (expr);              \
+        if (_rc != SCRY_OK) return _rc; \
+    } while (0)
+
+#define SCRY_REQUIRE_INIT()                                                          \
+    do {                                                                             \
+        if (!::scry::ctx().init) return ::scry::set_error(SCRY_ERR_NOT_INIT, "scry_hip_init not called"); \
+    } while (0)
+
+// ---------------------------------------------------------------- weights
+// GEMV stream layout of an int8 weight W[k,n] (k = in, n = out):
+// one row per output index, each row `kp` bytes (k rounded up to 16), byte =
+// q XOR 0x80 (= q + 128 as an unsigned byte), padding bytes 0x80 (q = 0).
+// A fused gate/up pair interleaves rows in groups of four:
+// gate[2t], gate[2t+1], up[2t], up[2t+1].
+struct Packed {
+    uint8_t *d = nullptr;
+    int k = 0;         // logical in-dimension
+    int n = 0;         // logical out-dimension (per tensor)
+    int kp = 0;        // row stride in bytes
+    int rows = 0;      // packed rows (n, or 2n when fused)
+    int fused = 0;     // 1 = gate/up interleave
+    float scale = 0.f; // per-tensor scale (gate scale when fused)
+    float scale2 = 0.f;// up scale when fused
+    float *s32 = nullptr; // block-32 scales [rows][nb] (packed-row order) or nullptr
+    int nb = 0;
+    size_t bytes() const { return (size_t)rows * kp; }
+};
+
+inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+void packed_free(Packed &p);
+
+// ---------------------------------------------------------------- kernels
+// quant.hip
+int launch_absmax(const float *w, size_t n, unsigned int *d_absmax_bits, hipStream_t s);
+int launch_quantize_plain(const float *w, size_t n, const unsigned int *d_absmax_bits, int8_t *q,
+                          float *d_scale, hipStream_t s);
+// Quantize (per tensor, from the absmax bits) and pack a f32 tensor in one pass.
+// src_nk = 1 when the source is stored [n,k] (embedding / lm_head).
+// Row mapping for output j: row = (j / grp) * stride + off + (j % grp).
+int launch_quant_pack(const float *w, int k, int n, int src_nk, const unsigned int *d_absmax_bits,
+                      uint8_t *dst, int kp, int grp, int stride, int off, hipStream_t s);
+int launch_i8_pack(const int8_t *q, int k, int n, int src_nk, uint8_t *dst, int kp, int grp,
+                   int stride, int off, hipStream_t s);
+int launch_unpack(const uint8_t *src, int kp, int k, int n, int dst_nk, int grp, int stride, int off,
+                  int8_t *q, hipStream_t s);
+int launch_quant_block32(const float *w, int k, int n, int src_nk, int8_t *q, float *scales,
+                         hipStream_t s);
+// scales [n][nb] (logical) -> packed-row order
+int launch_scales_pack(const float *scales, int n, int nb, float *dst, int grp, int stride, int off,
+                       hipStream_t s);
+int launch_dequantize(const int8_t *q, size_t n, float scale, float *out, hipStream_t s);
+int launch_normal_init(float *out, size_t n, uint64_t seed, uint64_t start_call, float mean,
+                       float stdv, int cols, int ld, int col0, hipStream_t s);
+
+// qgemv.hip
+enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3, EPI_LOGITS = 4 };
+
+struct DevState {  // per decode session, device resident
+    int pos;        // RoPE position of the token being processed
+    int cache_len;  // rows already in the KV cache (the new row is written here)
+    int n_prompt;   // prompt length (tokens beyond it are generated)
+    int max_tokens; // capacity of the token array minus one
+};
+
+struct GemvArgs {
+    const Packed *w = nullptr;
+    // activation rows: x (m rows, stride ldx); x == nullptr reads the embedding
+    // row of tokens[state->pos] instead (embedding fused into the prologue)
+    const float *x = nullptr;
+    int ldx = 0;
+    int m = 1;
+    const float *embed = nullptr;
+    const int64_t *tokens = nullptr;
+    DevState *state = nullptr;
+    const float *norm_w = nullptr;  // RMSNorm weight -> fused RMSNorm prologue
+    float eps = 1e-5f;
+    // outputs
+    float *y = nullptr;
+    int ldy = 0;
+    const float *resid = nullptr;   // EPI_RESID source (may alias y); nullptr -> embed row
+    const float *bias = nullptr;    // EPI_STORE optional bias
+    // EPI_QKV
+    float *q_out = nullptr, *k_cache = nullptr, *v_cache = nullptr;
+    const float2 *rope_cs = nullptr;  // [max_pos][head_dim/2] (cos, sin)
+    int q_dim = 0, kv_dim = 0, head_dim = 0;
+    float q_scale = 1.f;
+    // EPI_LOGITS (device argmax + step advance)
+    float *part_val = nullptr;
+    int *part_idx = nullptr, *part_nan = nullptr;
+    unsigned int *counter = nullptr;
+    int64_t *tokens_rw = nullptr;
+    int64_t *argmax_out = nullptr;
+    int advance = 0;
+};
+
+int launch_qgemv(int epi, const GemvArgs &a, hipStream_t s);
+
+// attn.hip
+struct AttnArgs {
+    const float *q = nullptr;     // [n_heads*hd] pre-scaled
+    const float *k_cache = nullptr, *v_cache = nullptr;  // [max_seq, n_kv*hd]
+    float *out = nullptr;         // [n_heads*hd]
+    float *part_o = nullptr, *part_ml = nullptr;  // scratch
+    unsigned int *counter = nullptr;  // [n_kv], zero between launches
+    const DevState *state = nullptr;
+    int n_heads = 0, n_kv = 0, head_dim = 0, n_splits = 1, max_chunk = 0;
+    int fixed_len = -1;  // >= 0: use this length instead of state->cache_len + 1
+};
+int launch_attn_decode(const AttnArgs &a, hipStream_t s);
+int attn_pick_splits(int n_kv, int max_seq, int *n_splits, int *max_chunk);
+
+// glue.hip
+int launch_rmsnorm(const float *x, const float *w, int rows, int d, float eps, float *out,
+                   hipStream_t s);
+int launch_rope(const float *x, int seq, int n_heads, int hd, int start_pos, const float *freqs,
+                int scaled, float scale, float *out, hipStream_t s);
+int launch_scale(const float *x, size_t n, float s_, float *out, hipStream_t s);
+int launch_softmax(const float *x, int rows, int cols, float *out, hipStream_t s);
+int launch_swiglu(const float *g, const float *u, size_t n, float *out, hipStream_t s);
+int launch_add(const float *a, const float *b, size_t n, float *out, hipStream_t s);
+int launch_embedding(const float *w, const int64_t *ids, int n_ids, int dim, float *out,
+                     hipStream_t s);
+int launch_gather_repeat_kv(const float *cache, int cached_len, int n_kv, int n_q, int hd,
+                            float *out, hipStream_t s);
+int launch_repeat_kv(const float *x, int n_kv, int n_q, int seq, int d_head, float *out,
+                     hipStream_t s);
+int launch_matmul_f32(const float *a, const float *b, int batch, int m, int k, int n, int ta,
+                      int tb, float *c, hipStream_t s);
+int launch_argmax(const float *x, int64_t n, int64_t *out, hipStream_t s);
+int launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
+int launch_fill_u32(unsigned int *p, size_t n, unsigned int v, hipStream_t s);
+
+// init.cpp -- host restatement of LlamaModel::new's random init (threaded)
+void host_normal_vec(uint64_t seed, uint64_t start_call, size_t n, float mean, float stdv,
+                     float *out, int threads);
+int host_threads();
+
+}  // namespace scry
+
+struct scry_buf_s {
+    float *d = nullptr;
+    size_t n = 0;
+};
+
+struct scry_i8buf_s {
+    int8_t *d = nullptr;   // reference layout bytes
+    size_t n = 0;
+    scry::Packed packed;   // GEMV layout, built on first matmul for (k, n)
+};

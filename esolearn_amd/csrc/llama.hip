@@ -1,0 +1,963 @@
+// Llama model with int8 projections on the device (llama.rs), the
+// device-resident KV cache (kv_cache.rs:70-145), the decode step
+// (llama.rs:744-763) as one captured HIP graph, and greedy generation
+// (generate.rs:51-98) as graph replays with the token loop on the device.
+//
+// Build-defined int8 composition (the reference LlamaModel has no int8 path):
+// every projection matmul -- fused qkv, o, gate, up, down, lm_head -- becomes
+// matmul_i8_f32 on quantize_symmetric weights (one scale per tensor; a tied
+// lm_head gets its own int8 copy of embed_tokens; the f32 table stays for the
+// embedding gather).
+//
+// Decode step, per layer (5 kernels):
+//   qkv   : RMSNorm(x) -> int8 GEMV -> RoPE(Q)*1/sqrt(hd), RoPE(K), K/V row append
+//           (layer 0 reads the embedding row of the current token directly)
+//   attn  : split-L attention over the cache in place, last-block merge
+//   o     : int8 GEMV + residual add into x
+//   gateup: RMSNorm(x) -> fused gate/up int8 GEMV -> silu(g)*u
+//   down  : int8 GEMV + residual add into x
+// then lm_head: RMSNorm(x) -> int8 GEMV -> logits -> device argmax -> next token
+// and position advance.  The current position and token live in device
+// memory, so the same captured graph replays for every token.
+#include <climits>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "internal.h"
+
+using namespace scry;
+
+struct scry_llama_s {
+    scry_llama_config cfg{};
+    int h = 0, V = 0, ffn = 0, nh = 0, nkv = 0, hd = 0, q_dim = 0, kv_dim = 0, qkv_dim = 0, L = 0;
+    int quant_mode = 0;
+    float *embed = nullptr;  // [V, h] f32
+    float *norms = nullptr;  // [2L+1][h] RMSNorm weights (RMSNorm::new: ones)
+    std::vector<float> freqs;  // [hd/2] f32 (llama.rs:618-622)
+    struct Layer {
+        Packed qkv, o, gu, down;
+    };
+    std::vector<Layer> layers;
+    Packed lm;
+    unsigned int *bits = nullptr;
+    float *stage = nullptr;  // device f32 staging for one tensor
+    size_t stage_n = 0;
+    int live_caches = 0;
+    const float *norm_in(int l) const { return norms + (size_t)(2 * l) * h; }
+    const float *norm_post(int l) const { return norms + (size_t)(2 * l + 1) * h; }
+    const float *norm_final() const { return norms + (size_t)(2 * L) * h; }
+};
+
+struct HostStage {
+    DevState st;
+    int64_t tok;
+    int64_t amax;
+};
+
+struct scry_kv_cache_s {
+    scry_llama m = nullptr;
+    int max_seq = 0;
+    int seq_len = 0;  // host mirror of LlamaLayerKvCache::seq_len
+    float *kv = nullptr;  // [L][2][max_seq][kv_dim]
+    float2 *rope_cs = nullptr;  // [max_seq][hd/2] (cos, sin), glibc values as cpu.rs:650-652
+    DevState *state = nullptr;
+    int64_t *tokens = nullptr;
+    int tokens_len = 0;
+    float *x = nullptr, *xq = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    float *ap_o = nullptr, *ap_ml = nullptr;
+    unsigned int *a_cnt = nullptr;
+    float *lp_val = nullptr;
+    int *lp_idx = nullptr, *lp_nan = nullptr;
+    unsigned int *l_cnt = nullptr;
+    int64_t *amax = nullptr;
+    int n_splits = 1, max_chunk = 16;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    HostStage *hs = nullptr;  // pinned
+    float *K(int l) const { return kv + (size_t)(2 * l) * max_seq * m->kv_dim; }
+    float *Vc(int l) const { return kv + (size_t)(2 * l + 1) * max_seq * m->kv_dim; }
+};
+
+#define API_LOCK std::lock_guard<std::recursive_mutex> _api_lock(scry::api_mutex())
+
+namespace {
+
+int sync_stream() {
+    SCRY_HIP(hipStreamSynchronize(ctx().stream));
+    return SCRY_OK;
+}
+
+// Quantize a device f32 tensor into (a slice of) a Packed weight.
+// src_nk: source stored [n,k]; (grp, stride, off): row interleave; second:
+// the tensor is the up half of a fused gate/up pair.
+int quant_into(scry_llama m, const float *dw, int k, int n, int src_nk, Packed &P, int grp,
+               int stride, int off, bool second) {
+    hipStream_t s = ctx().stream;
+    if (m->quant_mode == SCRY_QUANT_PER_TENSOR) {
+        SCRY_TRY(launch_absmax(dw, (size_t)k * n, m->bits, s));
+        unsigned int bits = 0;
+        SCRY_HIP(hipMemcpyAsync(&bits, m->bits, sizeof bits, hipMemcpyDeviceToHost, s));
+        SCRY_TRY(sync_stream());
+        float absmax;
+        std::memcpy(&absmax, &bits, sizeof absmax);
+        const float scale = absmax == 0.0f ? 0.0f : absmax / 127.0f;  // quantize.rs:23
+        if (second)
+            P.scale2 = scale;
+        else
+            P.scale = scale;
+        return launch_quant_pack(dw, k, n, src_nk, m->bits, P.d, P.kp, grp, stride, off, s);
+    }
+    // block-32: quantize per (output, 32-block), then pack bytes and scales
+    const int nb = (k + 31) / 32;
+    int8_t *q = nullptr;
+    float *sc = nullptr;
+    SCRY_TRY(dev_alloc((void **)&q, (size_t)k * n));
+    int rc = dev_alloc((void **)&sc, sizeof(float) * (size_t)n * nb);
+    if (!rc) rc = launch_quant_block32(dw, k, n, src_nk, q, sc, s);
+    if (!rc) rc = launch_i8_pack(q, k, n, src_nk, P.d, P.kp, grp, stride, off, s);
+    if (!rc) rc = launch_scales_pack(sc, n, nb, P.s32, grp, stride, off, s);
+    if (!rc) rc = sync_stream();
+    dev_free(q);
+    dev_free(sc);
+    return rc;
+}
+
+int alloc_packed(scry_llama m, Packed &P, int k, int n, int rows, int fused) {
+    P.k = k;
+    P.n = n;
+    P.kp = round_up(k, 16);
+    P.rows = rows;
+    P.fused = fused;
+    SCRY_TRY(dev_alloc((void **)&P.d, P.bytes()));
+    if (m->quant_mode == SCRY_QUANT_BLOCK32) {
+        P.nb = (k + 31) / 32;
+        SCRY_TRY(dev_alloc((void **)&P.s32, sizeof(float) * (size_t)rows * P.nb));
+    }
+    return SCRY_OK;
+}
+
+int upload_stage(scry_llama m, const float *host, size_t n) {
+    if (n > m->stage_n) return set_error(SCRY_ERR_INVALID, "tensor larger than the staging buffer");
+    SCRY_HIP(hipMemcpyAsync(m->stage, host, n * sizeof(float), hipMemcpyHostToDevice, ctx().stream));
+    return sync_stream();
+}
+
+// Load one tensor (reference layout) into the model.
+int load_tensor(scry_llama m, int id, int layer, const float *host) {
+    const int h = m->h, V = m->V, ffn = m->ffn;
+    if (id == SCRY_T_EMBED) {
+        SCRY_HIP(hipMemcpyAsync(m->embed, host, sizeof(float) * (size_t)V * h, hipMemcpyHostToDevice,
+                                ctx().stream));
+        SCRY_TRY(sync_stream());
+        if (m->cfg.tie_word_embeddings) return quant_into(m, m->embed, h, V, 1, m->lm, 1, 1, 0, false);
+        return SCRY_OK;
+    }
+    if (id == SCRY_T_LM_HEAD) {
+        if (m->cfg.tie_word_embeddings)
+            return set_error(SCRY_ERR_INVALID, "lm_head is tied to embed_tokens");
+        SCRY_TRY(upload_stage(m, host, (size_t)V * h));
+        return quant_into(m, m->stage, h, V, 1, m->lm, 1, 1, 0, false);
+    }
+    if (layer < 0 || layer >= m->L) return set_error(SCRY_ERR_INVALID, "layer %d out of range", layer);
+    auto &Ly = m->layers[layer];
+    switch (id) {
+        case SCRY_T_QKV:
+            SCRY_TRY(upload_stage(m, host, (size_t)h * m->qkv_dim));
+            return quant_into(m, m->stage, h, m->qkv_dim, 0, Ly.qkv, 1, 1, 0, false);
+        case SCRY_T_O:
+            SCRY_TRY(upload_stage(m, host, (size_t)m->q_dim * h));
+            return quant_into(m, m->stage, m->q_dim, h, 0, Ly.o, 1, 1, 0, false);
+        case SCRY_T_GATE:
+            SCRY_TRY(upload_stage(m, host, (size_t)h * ffn));
+            return quant_into(m, m->stage, h, ffn, 0, Ly.gu, 2, 4, 0, false);
+        case SCRY_T_UP:
+            SCRY_TRY(upload_stage(m, host, (size_t)h * ffn));
+            return quant_into(m, m->stage, h, ffn, 0, Ly.gu, 2, 4, 2, true);
+        case SCRY_T_DOWN:
+            SCRY_TRY(upload_stage(m, host, (size_t)ffn * h));
+            return quant_into(m, m->stage, ffn, h, 0, Ly.down, 1, 1, 0, false);
+    }
+    return set_error(SCRY_ERR_INVALID, "unknown tensor id %d", id);
+}
+
+void model_free(scry_llama m) {
+    if (!m) return;
+    for (auto &Ly : m->layers) {
+        packed_free(Ly.qkv);
+        packed_free(Ly.o);
+        packed_free(Ly.gu);
+        packed_free(Ly.down);
+    }
+    packed_free(m->lm);
+    dev_free(m->embed);
+    dev_free(m->norms);
+    dev_free(m->bits);
+    dev_free(m->stage);
+    delete m;
+}
+
+int model_alloc(const scry_llama_config *cfg, int quant_mode, scry_llama *out) {
+    if (!cfg || !out) return set_error(SCRY_ERR_INVALID, "null argument");
+    if (quant_mode != SCRY_QUANT_PER_TENSOR && quant_mode != SCRY_QUANT_BLOCK32)
+        return set_error(SCRY_ERR_INVALID, "unknown quant mode %d", quant_mode);
+    const int h = cfg->hidden_size, nh = cfg->n_heads, nkv = cfg->n_kv_heads;
+    if (h <= 0 || nh <= 0 || nkv <= 0 || h % nh || nh % nkv || cfg->vocab_size <= 0 ||
+        cfg->intermediate_size <= 0 || cfg->n_layers <= 0)
+        return set_error(SCRY_ERR_INVALID, "invalid Llama config");
+    const int hd = h / nh;
+    if (hd % 4 || cfg->intermediate_size % 2)
+        return set_error(SCRY_ERR_UNSUPPORTED, "head_dim must be a multiple of 4 and ffn even");
+    if (h > 16384 || cfg->intermediate_size > 16384 || nh * hd > 16384)
+        return set_error(SCRY_ERR_UNSUPPORTED, "GEMV k > 16384 not supported");
+    auto *m = new (std::nothrow) scry_llama_s;
+    if (!m) return set_error(SCRY_ERR_OOM, "host allocation failed");
+    m->cfg = *cfg;
+    m->quant_mode = quant_mode;
+    m->h = h;
+    m->V = cfg->vocab_size;
+    m->ffn = cfg->intermediate_size;
+    m->nh = nh;
+    m->nkv = nkv;
+    m->hd = hd;
+    m->q_dim = nh * hd;
+    m->kv_dim = nkv * hd;
+    m->qkv_dim = m->q_dim + 2 * m->kv_dim;
+    m->L = cfg->n_layers;
+    // llama.rs:1035-1067 compute_rope_freqs (f64), stored as f32 (llama.rs:621)
+    m->freqs.resize(hd / 2);
+    const double th = (double)cfg->rope_theta;
+    for (int i = 0; i < hd / 2; i++) {
+        double f = 1.0 / std::pow(th, 2.0 * (double)i / (double)hd);
+        if (cfg->has_rope_scaling) {
+            const double old_ctx = (double)cfg->rs_original_max_pos;
+            const double low_wl = old_ctx / cfg->rs_low_freq_factor;
+            const double high_wl = old_ctx / cfg->rs_high_freq_factor;
+            const double wl = 2.0 * M_PI / f;
+            double sf;
+            if (wl < high_wl)
+                sf = 1.0;
+            else if (wl > low_wl)
+                sf = cfg->rs_factor;
+            else {
+                const double smooth = (old_ctx / wl - cfg->rs_low_freq_factor) /
+                                      (cfg->rs_high_freq_factor - cfg->rs_low_freq_factor);
+                sf = 1.0 / ((1.0 - smooth) / cfg->rs_factor + smooth);
+            }
+            f /= sf;
+        }
+        m->freqs[i] = (float)f;
+    }
+    int rc = dev_alloc((void **)&m->embed, sizeof(float) * (size_t)m->V * h);
+    if (!rc) rc = dev_alloc((void **)&m->norms, sizeof(float) * (size_t)(2 * m->L + 1) * h);
+    if (!rc) rc = launch_fill_f32(m->norms, (size_t)(2 * m->L + 1) * h, 1.0f, ctx().stream);
+    if (!rc) rc = dev_alloc((void **)&m->bits, 16);
+    const size_t sizes[] = {(size_t)m->V * h, (size_t)h * m->qkv_dim, (size_t)h * m->ffn,
+                            (size_t)m->q_dim * h};
+    for (size_t s : sizes) m->stage_n = std::max(m->stage_n, s);
+    if (!rc) rc = dev_alloc((void **)&m->stage, sizeof(float) * m->stage_n);
+    m->layers.resize(m->L);
+    for (int l = 0; l < m->L && !rc; l++) {
+        auto &Ly = m->layers[l];
+        rc = alloc_packed(m, Ly.qkv, h, m->qkv_dim, m->qkv_dim, 0);
+        if (!rc) rc = alloc_packed(m, Ly.o, m->q_dim, h, h, 0);
+        if (!rc) rc = alloc_packed(m, Ly.gu, h, m->ffn, 2 * m->ffn, 1);
+        if (!rc) rc = alloc_packed(m, Ly.down, m->ffn, h, h, 0);
+    }
+    if (!rc) rc = alloc_packed(m, m->lm, h, m->V, m->V, 0);
+    if (rc) {
+        model_free(m);
+        return rc;
+    }
+    *out = m;
+    return SCRY_OK;
+}
+
+// ---------------------------------------------------------------- sessions
+void cache_free(scry_kv_cache c) {
+    if (!c) return;
+    if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    dev_free(c->kv);
+    dev_free(c->rope_cs);
+    dev_free(c->state);
+    dev_free(c->tokens);
+    dev_free(c->x);
+    dev_free(c->xq);
+    dev_free(c->attn);
+    dev_free(c->act);
+    dev_free(c->logits);
+    dev_free(c->ap_o);
+    dev_free(c->ap_ml);
+    dev_free(c->a_cnt);
+    dev_free(c->lp_val);
+    dev_free(c->lp_idx);
+    dev_free(c->lp_nan);
+    dev_free(c->l_cnt);
+    dev_free(c->amax);
+    if (c->hs) (void)hipHostFree(c->hs);
+    if (c->m) c->m->live_caches--;
+    delete c;
+}
+
+int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
+    if (max_seq <= 0) return set_error(SCRY_ERR_INVALID, "max_seq must be > 0");
+    auto *c = new (std::nothrow) scry_kv_cache_s;
+    if (!c) return set_error(SCRY_ERR_OOM, "host allocation failed");
+    c->m = m;
+    m->live_caches++;
+    c->max_seq = max_seq;
+    c->tokens_len = max_seq + 1;
+    attn_pick_splits(m->nkv, max_seq, &c->n_splits, &c->max_chunk);
+    hipStream_t s = ctx().stream;
+    const size_t kvn = (size_t)m->L * 2 * max_seq * m->kv_dim;
+    const int nparts = (m->V + 15) / 16;
+    int rc = dev_alloc((void **)&c->kv, sizeof(float) * kvn);
+    if (!rc) rc = launch_fill_f32(c->kv, kvn, 0.f, s);  // LlamaLayerKvCache::new zeros
+    if (!rc) rc = dev_alloc((void **)&c->rope_cs, sizeof(float2) * (size_t)max_seq * (m->hd / 2));
+    if (!rc) rc = dev_alloc((void **)&c->state, sizeof(DevState));
+    if (!rc) rc = dev_alloc((void **)&c->tokens, sizeof(int64_t) * c->tokens_len);
+    if (!rc) rc = dev_alloc((void **)&c->x, sizeof(float) * m->h);
+    if (!rc) rc = dev_alloc((void **)&c->xq, sizeof(float) * m->q_dim);
+    if (!rc) rc = dev_alloc((void **)&c->attn, sizeof(float) * m->q_dim);
+    if (!rc) rc = dev_alloc((void **)&c->act, sizeof(float) * m->ffn);
+    if (!rc) rc = dev_alloc((void **)&c->logits, sizeof(float) * m->V);
+    if (!rc) rc = dev_alloc((void **)&c->ap_o, sizeof(float) * (size_t)m->nh * c->n_splits * m->hd);
+    if (!rc) rc = dev_alloc((void **)&c->ap_ml, sizeof(float) * (size_t)m->nh * c->n_splits * 2);
+    if (!rc) rc = dev_alloc((void **)&c->a_cnt, sizeof(unsigned) * m->nkv);
+    if (!rc) rc = launch_fill_u32(c->a_cnt, m->nkv, 0u, s);
+    if (!rc) rc = dev_alloc((void **)&c->lp_val, sizeof(float) * nparts);
+    if (!rc) rc = dev_alloc((void **)&c->lp_idx, sizeof(int) * nparts);
+    if (!rc) rc = dev_alloc((void **)&c->lp_nan, sizeof(int) * nparts);
+    if (!rc) rc = dev_alloc((void **)&c->l_cnt, sizeof(unsigned));
+    if (!rc) rc = launch_fill_u32(c->l_cnt, 1, 0u, s);
+    if (!rc) rc = dev_alloc((void **)&c->amax, sizeof(int64_t));
+    if (!rc) {
+        hipError_t e = hipHostMalloc((void **)&c->hs, sizeof(HostStage), hipHostMallocDefault);
+        if (e != hipSuccess) rc = hip_fail(e, "hipHostMalloc", __FILE__, __LINE__);
+    }
+    if (!rc) {
+        // RoPE table: cos/sin of f64(pos) * f64(freq_f32) rounded to f32, with
+        // the host libm the reference uses (cpu.rs:648-652)
+        const int hh = m->hd / 2;
+        std::vector<float2> cs((size_t)max_seq * hh);
+        for (int p = 0; p < max_seq; p++)
+            for (int i = 0; i < hh; i++) {
+                const double ang = (double)p * (double)m->freqs[i];
+                cs[(size_t)p * hh + i] = make_float2((float)std::cos(ang), (float)std::sin(ang));
+            }
+        hipError_t e = hipMemcpyAsync(c->rope_cs, cs.data(), sizeof(float2) * cs.size(),
+                                      hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(e, "rope table upload", __FILE__, __LINE__);
+    }
+    if (rc) {
+        cache_free(c);
+        return rc;
+    }
+    *out = c;
+    return SCRY_OK;
+}
+
+GemvArgs qkv_args(scry_kv_cache c, int l) {
+    scry_llama m = c->m;
+    GemvArgs g;
+    g.w = &m->layers[l].qkv;
+    g.x = l == 0 ? nullptr : c->x;  // layer 0: embedding row fused into the prologue
+    g.ldx = m->h;
+    g.embed = m->embed;
+    g.tokens = c->tokens;
+    g.state = c->state;
+    g.norm_w = m->norm_in(l);
+    g.eps = 1e-5f;  // RMSNorm::new (rmsnorm.rs:17-22)
+    g.q_out = c->xq;
+    g.k_cache = c->K(l);
+    g.v_cache = c->Vc(l);
+    g.rope_cs = c->rope_cs;
+    g.q_dim = m->q_dim;
+    g.kv_dim = m->kv_dim;
+    g.head_dim = m->hd;
+    g.q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
+    return g;
+}
+
+AttnArgs attn_args(scry_kv_cache c, int l) {
+    scry_llama m = c->m;
+    AttnArgs a;
+    a.q = c->xq;
+    a.k_cache = c->K(l);
+    a.v_cache = c->Vc(l);
+    a.out = c->attn;
+    a.part_o = c->ap_o;
+    a.part_ml = c->ap_ml;
+    a.counter = c->a_cnt;
+    a.state = c->state;
+    a.n_heads = m->nh;
+    a.n_kv = m->nkv;
+    a.head_dim = m->hd;
+    a.n_splits = c->n_splits;
+    a.max_chunk = c->max_chunk;
+    return a;
+}
+
+GemvArgs o_args(scry_kv_cache c, int l) {
+    scry_llama m = c->m;
+    GemvArgs g;
+    g.w = &m->layers[l].o;
+    g.x = c->attn;
+    g.ldx = m->q_dim;
+    g.y = c->x;
+    g.ldy = m->h;
+    g.resid = l == 0 ? nullptr : c->x;  // layer 0: residual is the embedding row
+    g.embed = m->embed;
+    g.tokens = c->tokens;
+    g.state = c->state;
+    return g;
+}
+
+GemvArgs gu_args(scry_kv_cache c, int l) {
+    scry_llama m = c->m;
+    GemvArgs g;
+    g.w = &m->layers[l].gu;
+    g.x = c->x;
+    g.ldx = m->h;
+    g.norm_w = m->norm_post(l);
+    g.eps = 1e-5f;
+    g.y = c->act;
+    g.ldy = m->ffn;
+    return g;
+}
+
+GemvArgs down_args(scry_kv_cache c, int l) {
+    scry_llama m = c->m;
+    GemvArgs g;
+    g.w = &m->layers[l].down;
+    g.x = c->act;
+    g.ldx = m->ffn;
+    g.y = c->x;
+    g.ldy = m->h;
+    g.resid = c->x;
+    return g;
+}
+
+GemvArgs lm_args(scry_kv_cache c, int advance) {
+    scry_llama m = c->m;
+    GemvArgs g;
+    g.w = &m->lm;
+    g.x = c->x;
+    g.ldx = m->h;
+    g.norm_w = m->norm_final();
+    g.eps = 1e-5f;
+    g.y = c->logits;
+    g.ldy = m->V;
+    g.state = c->state;
+    g.part_val = c->lp_val;
+    g.part_idx = c->lp_idx;
+    g.part_nan = c->lp_nan;
+    g.counter = c->l_cnt;
+    g.tokens_rw = c->tokens;
+    g.argmax_out = c->amax;
+    g.advance = advance;
+    return g;
+}
+
+int record_step(scry_kv_cache c, hipStream_t s) {
+    scry_llama m = c->m;
+    for (int l = 0; l < m->L; l++) {
+        SCRY_TRY(launch_qgemv(EPI_QKV, qkv_args(c, l), s));
+        SCRY_TRY(launch_attn_decode(attn_args(c, l), s));
+        SCRY_TRY(launch_qgemv(EPI_RESID, o_args(c, l), s));
+        SCRY_TRY(launch_qgemv(EPI_SWIGLU, gu_args(c, l), s));
+        SCRY_TRY(launch_qgemv(EPI_RESID, down_args(c, l), s));
+    }
+    return launch_qgemv(EPI_LOGITS, lm_args(c, 1), s);
+}
+
+// One decode step: the captured graph when available, else direct launches.
+int run_step(scry_kv_cache c) {
+    hipStream_t s = ctx().stream;
+    if (!c->gexec) {
+        hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            int rc = record_step(c, s);
+            hipGraph_t g = nullptr;
+            e = hipStreamEndCapture(s, &g);
+            if (rc) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            if (e == hipSuccess && g) {
+                e = hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0);
+                if (e == hipSuccess) {
+                    c->graph = g;
+                } else {
+                    (void)hipGetLastError();
+                    (void)hipGraphDestroy(g);
+                    c->gexec = nullptr;
+                }
+            } else {
+                (void)hipGetLastError();
+            }
+        } else {
+            (void)hipGetLastError();
+        }
+    }
+    if (c->gexec) {
+        SCRY_HIP(hipGraphLaunch(c->gexec, s));
+        return SCRY_OK;
+    }
+    return record_step(c, s);
+}
+
+int set_state(scry_kv_cache c, int pos, int cache_len, int n_prompt) {
+    c->hs->st.pos = pos;
+    c->hs->st.cache_len = cache_len;
+    c->hs->st.n_prompt = n_prompt;
+    c->hs->st.max_tokens = c->tokens_len - 1;
+    SCRY_HIP(hipMemcpyAsync(c->state, &c->hs->st, sizeof(DevState), hipMemcpyHostToDevice, ctx().stream));
+    return sync_stream();
+}
+
+int check_ids(scry_llama m, const int64_t *ids, int n) {
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= m->V)
+            return set_error(SCRY_ERR_RANGE, "token id %lld out of range (vocab %d)", (long long)ids[i], m->V);
+    return SCRY_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int scry_hip_llama_new_random(const scry_llama_config *cfg, uint64_t seed, int quant_mode,
+                              int init_on_device, scry_llama *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    scry_llama m = nullptr;
+    SCRY_TRY(model_alloc(cfg, quant_mode, &m));
+    const int h = m->h, V = m->V, ffn = m->ffn, qd = m->q_dim, kvd = m->kv_dim, qkvd = m->qkv_dim;
+    const int T = host_threads();
+    const float stdv = 0.02f;  // llama.rs:598 (an f32, promoted in init.rs:8)
+    hipStream_t s = ctx().stream;
+    uint64_t calls = 0;
+    int rc = SCRY_OK;
+    std::vector<float> buf, fused;
+    if (!init_on_device) buf.resize(m->stage_n);
+    // Draw n samples of the next tensor into dst (device) as rows of `cols`
+    // values at stride ld starting at column col0; host draws go through buf.
+    auto draw = [&](float *dst, size_t n, int cols, int ld, int col0) -> int {
+        int r = SCRY_OK;
+        if (init_on_device) {
+            r = launch_normal_init(dst, n, seed, calls, 0.0f, stdv, cols, ld, col0, s);
+        } else {
+            host_normal_vec(seed, calls, n, 0.0f, stdv, buf.data(), T);
+            if (cols == ld) {
+                hipError_t e = hipMemcpyAsync(dst, buf.data(), n * sizeof(float), hipMemcpyHostToDevice, s);
+                if (e == hipSuccess) e = hipStreamSynchronize(s);
+                if (e != hipSuccess) r = hip_fail(e, "weight upload", __FILE__, __LINE__);
+            } else {
+                const size_t rows = n / cols;
+                hipError_t e = hipMemcpy2DAsync(dst + col0, sizeof(float) * ld, buf.data(),
+                                                sizeof(float) * cols, sizeof(float) * cols, rows,
+                                                hipMemcpyHostToDevice, s);
+                if (e == hipSuccess) e = hipStreamSynchronize(s);
+                if (e != hipSuccess) r = hip_fail(e, "weight upload", __FILE__, __LINE__);
+            }
+        }
+        calls += 2 * (uint64_t)n;
+        return r;
+    };
+    // llama.rs:602-605 embed_tokens first (a tied lm_head is quantized from it)
+    rc = draw(m->embed, (size_t)V * h, h, h, 0);
+    if (!rc && m->cfg.tie_word_embeddings) rc = quant_into(m, m->embed, h, V, 1, m->lm, 1, 1, 0, false);
+    for (int l = 0; l < m->L && !rc; l++) {
+        auto &Ly = m->layers[l];
+        // llama.rs:613-616 q, k, v, fused column-wise (fuse_qkv_weights, llama.rs:1009-1029)
+        rc = draw(m->stage, (size_t)h * qd, qd, qkvd, 0);
+        if (!rc) rc = draw(m->stage, (size_t)h * kvd, kvd, qkvd, qd);
+        if (!rc) rc = draw(m->stage, (size_t)h * kvd, kvd, qkvd, qd + kvd);
+        if (!rc) rc = quant_into(m, m->stage, h, qkvd, 0, Ly.qkv, 1, 1, 0, false);
+        // llama.rs:627-630 o_proj; 645-656 gate, up, down
+        if (!rc) rc = draw(m->stage, (size_t)qd * h, h, h, 0);
+        if (!rc) rc = quant_into(m, m->stage, qd, h, 0, Ly.o, 1, 1, 0, false);
+        if (!rc) rc = draw(m->stage, (size_t)h * ffn, ffn, ffn, 0);
+        if (!rc) rc = quant_into(m, m->stage, h, ffn, 0, Ly.gu, 2, 4, 0, false);
+        if (!rc) rc = draw(m->stage, (size_t)h * ffn, ffn, ffn, 0);
+        if (!rc) rc = quant_into(m, m->stage, h, ffn, 0, Ly.gu, 2, 4, 2, true);
+        if (!rc) rc = draw(m->stage, (size_t)ffn * h, h, h, 0);
+        if (!rc) rc = quant_into(m, m->stage, ffn, h, 0, Ly.down, 1, 1, 0, false);
+    }
+    // llama.rs:664-671 untied lm_head last
+    if (!rc && !m->cfg.tie_word_embeddings) {
+        rc = draw(m->stage, (size_t)V * h, h, h, 0);
+        if (!rc) rc = quant_into(m, m->stage, h, V, 1, m->lm, 1, 1, 0, false);
+    }
+    if (!rc) rc = sync_stream();
+    if (rc) {
+        model_free(m);
+        return rc;
+    }
+    *out = m;
+    return SCRY_OK;
+}
+
+int scry_hip_llama_free(scry_llama m) {
+    API_LOCK;
+    if (!m) return SCRY_OK;
+    if (m->live_caches > 0)
+        return set_error(SCRY_ERR_INVALID, "free the model's %d KV cache(s) first", m->live_caches);
+    if (ctx().init) (void)hipStreamSynchronize(ctx().stream);
+    model_free(m);
+    return SCRY_OK;
+}
+
+int scry_hip_llama_set_tensor(scry_llama m, int tensor_id, int layer, const float *host, size_t n) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || !host) return set_error(SCRY_ERR_INVALID, "null argument");
+    size_t need = 0;
+    switch (tensor_id) {
+        case SCRY_T_EMBED:
+        case SCRY_T_LM_HEAD: need = (size_t)m->V * m->h; break;
+        case SCRY_T_QKV: need = (size_t)m->h * m->qkv_dim; break;
+        case SCRY_T_O: need = (size_t)m->q_dim * m->h; break;
+        case SCRY_T_GATE:
+        case SCRY_T_UP: need = (size_t)m->h * m->ffn; break;
+        case SCRY_T_DOWN: need = (size_t)m->ffn * m->h; break;
+        default: return set_error(SCRY_ERR_INVALID, "unknown tensor id %d", tensor_id);
+    }
+    if (n != need) return set_error(SCRY_ERR_INVALID, "tensor %d: %zu elements, expected %zu", tensor_id, n, need);
+    SCRY_TRY(load_tensor(m, tensor_id, layer, host));
+    return sync_stream();
+}
+
+int scry_hip_llama_get_qtensor(scry_llama m, int tensor_id, int layer, int8_t *host, size_t n,
+                               float *scale) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || !host) return set_error(SCRY_ERR_INVALID, "null argument");
+    const Packed *P = nullptr;
+    int grp = 1, stride = 1, off = 0, nk = 0;
+    float sc = 0.f;
+    if (tensor_id == SCRY_T_LM_HEAD) {
+        P = &m->lm;
+        nk = 1;
+        sc = P->scale;
+    } else {
+        if (layer < 0 || layer >= m->L) return set_error(SCRY_ERR_INVALID, "layer out of range");
+        auto &Ly = m->layers[layer];
+        switch (tensor_id) {
+            case SCRY_T_QKV: P = &Ly.qkv; sc = P->scale; break;
+            case SCRY_T_O: P = &Ly.o; sc = P->scale; break;
+            case SCRY_T_GATE: P = &Ly.gu; grp = 2; stride = 4; off = 0; sc = P->scale; break;
+            case SCRY_T_UP: P = &Ly.gu; grp = 2; stride = 4; off = 2; sc = P->scale2; break;
+            case SCRY_T_DOWN: P = &Ly.down; sc = P->scale; break;
+            default: return set_error(SCRY_ERR_INVALID, "tensor id %d has no int8 weights", tensor_id);
+        }
+    }
+    if (n != (size_t)P->k * P->n) return set_error(SCRY_ERR_INVALID, "get_qtensor: expected %zu elements", (size_t)P->k * P->n);
+    int8_t *d = nullptr;
+    SCRY_TRY(dev_alloc((void **)&d, n));
+    int rc = launch_unpack(P->d, P->kp, P->k, P->n, nk, grp, stride, off, d, ctx().stream);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(host, d, n, hipMemcpyDeviceToHost, ctx().stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx().stream);
+        if (e != hipSuccess) rc = hip_fail(e, "get_qtensor readback", __FILE__, __LINE__);
+    }
+    dev_free(d);
+    if (scale) *scale = m->quant_mode == SCRY_QUANT_PER_TENSOR ? sc : 0.f;
+    return rc;
+}
+
+int scry_hip_llama_get_embed(scry_llama m, float *host, size_t n) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || !host || n != (size_t)m->V * m->h) return set_error(SCRY_ERR_INVALID, "get_embed: bad size");
+    SCRY_HIP(hipMemcpyAsync(host, m->embed, n * sizeof(float), hipMemcpyDeviceToHost, ctx().stream));
+    return sync_stream();
+}
+
+int scry_hip_llama_kv_cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || !out) return set_error(SCRY_ERR_INVALID, "null argument");
+    SCRY_TRY(cache_new(m, max_seq, out));
+    return sync_stream();
+}
+
+int scry_hip_kv_cache_free(scry_kv_cache c) {
+    API_LOCK;
+    if (!c) return SCRY_OK;
+    if (ctx().init) (void)hipStreamSynchronize(ctx().stream);
+    cache_free(c);
+    return SCRY_OK;
+}
+
+int scry_hip_kv_cache_seq_len(scry_kv_cache c, int *seq_len) {
+    if (!c || !seq_len) return set_error(SCRY_ERR_INVALID, "null argument");
+    *seq_len = c->seq_len;
+    return SCRY_OK;
+}
+
+int scry_hip_kv_cache_layer_to_vec(scry_kv_cache c, int layer, float *k_host, float *v_host,
+                                   size_t n) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!c || layer < 0 || layer >= c->m->L) return set_error(SCRY_ERR_INVALID, "bad layer");
+    const size_t need = (size_t)c->max_seq * c->m->kv_dim;
+    if (n != need) return set_error(SCRY_ERR_INVALID, "kv layer has %zu elements", need);
+    if (k_host) SCRY_HIP(hipMemcpyAsync(k_host, c->K(layer), need * 4, hipMemcpyDeviceToHost, ctx().stream));
+    if (v_host) SCRY_HIP(hipMemcpyAsync(v_host, c->Vc(layer), need * 4, hipMemcpyDeviceToHost, ctx().stream));
+    return sync_stream();
+}
+
+int scry_hip_llama_forward_with_cache(scry_llama m, scry_kv_cache c, int64_t token, int pos,
+                                      float *logits, int64_t *argmax_out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || !c || c->m != m) return set_error(SCRY_ERR_INVALID, "cache does not belong to the model");
+    SCRY_TRY(check_ids(m, &token, 1));
+    if (c->seq_len >= c->max_seq)
+        return set_error(SCRY_ERR_RANGE, "KV cache full (%d rows)", c->max_seq);
+    if (pos < 0 || pos >= c->max_seq)
+        return set_error(SCRY_ERR_RANGE, "position %d outside the cache's RoPE table (%d)", pos, c->max_seq);
+    hipStream_t s = ctx().stream;
+    c->hs->tok = token;
+    SCRY_HIP(hipMemcpyAsync(c->tokens + pos, &c->hs->tok, sizeof(int64_t), hipMemcpyHostToDevice, s));
+    SCRY_TRY(set_state(c, pos, c->seq_len, INT_MAX));
+    SCRY_TRY(run_step(c));
+    if (logits)
+        SCRY_HIP(hipMemcpyAsync(logits, c->logits, sizeof(float) * m->V, hipMemcpyDeviceToHost, s));
+    if (argmax_out) SCRY_HIP(hipMemcpyAsync(&c->hs->amax, c->amax, sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    SCRY_TRY(sync_stream());
+    if (argmax_out) *argmax_out = c->hs->amax;
+    c->seq_len++;
+    return SCRY_OK;
+}
+
+int scry_hip_llama_generate_greedy(scry_llama m, const int64_t *prompt, int n_prompt,
+                                   int max_tokens, int64_t *out_tokens, int *n_out,
+                                   float *step_logits) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || !prompt || !out_tokens || !n_out) return set_error(SCRY_ERR_INVALID, "null argument");
+    if (n_prompt <= 0) return set_error(SCRY_ERR_INVALID, "generate: prompt_tokens must not be empty");
+    if (max_tokens < 0) return set_error(SCRY_ERR_INVALID, "generate: max_tokens < 0");
+    SCRY_TRY(check_ids(m, prompt, n_prompt));
+    const int nout = max_tokens > 0 ? max_tokens : 1;
+    const int steps = n_prompt + nout - 1;
+    scry_kv_cache c = nullptr;
+    SCRY_TRY(cache_new(m, n_prompt + max_tokens, &c));  // generate.rs:62-63
+    hipStream_t s = ctx().stream;
+    int rc = SCRY_OK;
+    hipError_t e = hipMemcpyAsync(c->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) rc = hip_fail(e, "prompt upload", __FILE__, __LINE__);
+    if (!rc) rc = set_state(c, 0, 0, n_prompt);
+    for (int t = 0; t < steps && !rc; t++) {
+        rc = run_step(c);
+        if (!rc && step_logits && t >= n_prompt - 1) {
+            e = hipMemcpyAsync(step_logits + (size_t)(t - (n_prompt - 1)) * m->V, c->logits,
+                               sizeof(float) * m->V, hipMemcpyDeviceToHost, s);
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            if (e != hipSuccess) rc = hip_fail(e, "logits readback", __FILE__, __LINE__);
+        }
+    }
+    if (!rc) {
+        e = hipMemcpyAsync(out_tokens, c->tokens + n_prompt, sizeof(int64_t) * nout, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(e, "token readback", __FILE__, __LINE__);
+    }
+    cache_free(c);
+    if (rc) return rc;
+    *n_out = nout;
+    return SCRY_OK;
+}
+
+// ------------------------------------------------------------ measurement
+int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_prompt, int warmup,
+                                int steps, int64_t *out_tokens, double *ms) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || !prompt || n_prompt <= 0 || steps <= 0 || warmup < 0 || !ms)
+        return set_error(SCRY_ERR_INVALID, "bench_decode: bad arguments");
+    SCRY_TRY(check_ids(m, prompt, n_prompt));
+    scry_kv_cache c = nullptr;
+    SCRY_TRY(cache_new(m, n_prompt + std::max(warmup, steps) + 1, &c));
+    hipStream_t s = ctx().stream;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = SCRY_OK;
+    hipError_t e = hipMemcpyAsync(c->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) rc = hip_fail(e, "prompt upload", __FILE__, __LINE__);
+    if (!rc) rc = set_state(c, 0, 0, n_prompt);
+    // the prompt through the cache path, as generate() does
+    for (int t = 0; t < n_prompt && !rc; t++) rc = run_step(c);
+    for (int t = 0; t < warmup && !rc; t++) rc = run_step(c);
+    if (!rc) rc = sync_stream();
+    // rewind to the first decode position; the cache rows and token written
+    // there are the same ones the warm-up produced
+    if (!rc) rc = set_state(c, n_prompt, n_prompt, n_prompt);
+    if (!rc) {
+        e = hipEventCreate(&e0);
+        if (e == hipSuccess) e = hipEventCreate(&e1);
+        if (e == hipSuccess) e = hipEventRecord(e0, s);
+        if (e != hipSuccess) rc = hip_fail(e, "event setup", __FILE__, __LINE__);
+    }
+    for (int t = 0; t < steps && !rc; t++) rc = run_step(c);
+    if (!rc) {
+        e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float f = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&f, e0, e1);
+        if (e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
+        *ms = f;
+    }
+    if (!rc && out_tokens) {
+        e = hipMemcpyAsync(out_tokens, c->tokens + n_prompt + 1, sizeof(int64_t) * steps,
+                           hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(e, "token readback", __FILE__, __LINE__);
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    cache_free(c);
+    return rc;
+}
+
+int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int iters,
+                                   double *avg_us, double *bytes_per_launch) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    (void)layer;  // launches rotate over all layers so the weights stream from HBM
+    if (!m || iters <= 0 || !avg_us) return set_error(SCRY_ERR_INVALID, "time_projection: bad arguments");
+    scry_kv_cache c = nullptr;
+    SCRY_TRY(cache_new(m, 16, &c));
+    hipStream_t s = ctx().stream;
+    int rc = launch_fill_f32(c->x, m->h, 1.0f, s);
+    if (!rc) rc = launch_fill_f32(c->attn, m->q_dim, 0.5f, s);
+    if (!rc) rc = launch_fill_f32(c->act, m->ffn, 0.25f, s);
+    if (!rc) {
+        c->hs->tok = 0;
+        hipError_t e = hipMemcpyAsync(c->tokens, &c->hs->tok, sizeof(int64_t), hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) rc = hip_fail(e, "token upload", __FILE__, __LINE__);
+    }
+    if (!rc) rc = set_state(c, 0, 0, INT_MAX);
+    double bytes = 0;
+    auto launch = [&](int l) -> int {
+        switch (tensor_id) {
+            case SCRY_T_QKV: return launch_qgemv(EPI_QKV, qkv_args(c, l), s);
+            case SCRY_T_O: return launch_qgemv(EPI_RESID, o_args(c, l), s);
+            case SCRY_T_GATE: return launch_qgemv(EPI_SWIGLU, gu_args(c, l), s);
+            case SCRY_T_DOWN: return launch_qgemv(EPI_RESID, down_args(c, l), s);
+            case SCRY_T_LM_HEAD: return launch_qgemv(EPI_LOGITS, lm_args(c, 0), s);
+        }
+        return set_error(SCRY_ERR_INVALID, "time_projection: tensor id %d", tensor_id);
+    };
+    const Packed *P = nullptr;
+    switch (tensor_id) {
+        case SCRY_T_QKV: P = &m->layers[0].qkv; break;
+        case SCRY_T_O: P = &m->layers[0].o; break;
+        case SCRY_T_GATE: P = &m->layers[0].gu; break;
+        case SCRY_T_DOWN: P = &m->layers[0].down; break;
+        case SCRY_T_LM_HEAD: P = &m->lm; break;
+        default: rc = set_error(SCRY_ERR_INVALID, "time_projection: tensor id %d", tensor_id);
+    }
+    if (P) {
+        // algorithmic bytes: int8 weights + scales + activation in + result out
+        const double out_n = tensor_id == SCRY_T_GATE ? P->rows / 2.0 : (double)P->rows;
+        const double scales = P->s32 ? 4.0 * P->rows * P->nb : (P->fused ? 8.0 : 4.0);
+        bytes = (double)P->rows * P->k + scales + 4.0 * P->k + 4.0 * out_n;
+    }
+    const int nl = tensor_id == SCRY_T_LM_HEAD ? 1 : m->L;
+    for (int i = 0; i < std::min(iters, 8) && !rc; i++) rc = launch(i % nl);  // warm-up
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc) {
+        hipError_t e = hipEventCreate(&e0);
+        if (e == hipSuccess) e = hipEventCreate(&e1);
+        if (e == hipSuccess) e = hipEventRecord(e0, s);
+        if (e != hipSuccess) rc = hip_fail(e, "event setup", __FILE__, __LINE__);
+    }
+    for (int i = 0; i < iters && !rc; i++) rc = launch(i % nl);
+    if (!rc) {
+        hipError_t e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float f = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&f, e0, e1);
+        if (e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
+        *avg_us = 1000.0 * f / iters;
+    }
+    if (bytes_per_launch) *bytes_per_launch = bytes;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(s);
+    cache_free(c);
+    return rc;
+}
+
+int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, int warmup,
+                         int iters, double *avg_us, double *bytes_per_launch) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (m_rows <= 0 || k <= 0 || n <= 0 || n_bufs <= 0 || iters <= 0 || !avg_us)
+        return set_error(SCRY_ERR_INVALID, "bench_qgemv: bad arguments");
+    hipStream_t s = ctx().stream;
+    std::vector<Packed> W(n_bufs);
+    float *x = nullptr, *y = nullptr;
+    int rc = dev_alloc((void **)&x, sizeof(float) * (size_t)m_rows * k);
+    if (!rc) rc = dev_alloc((void **)&y, sizeof(float) * (size_t)m_rows * n);
+    if (!rc) rc = launch_fill_f32(x, (size_t)m_rows * k, 0.5f, s);
+    for (int b = 0; b < n_bufs && !rc; b++) {
+        Packed &P = W[b];
+        P.k = k;
+        P.n = n;
+        P.kp = round_up(k, 16);
+        P.rows = n;
+        P.scale = 1.0f / 127.0f;
+        rc = dev_alloc((void **)&P.d, P.bytes());
+        if (!rc) rc = launch_fill_u32((unsigned *)P.d, P.bytes() / 4, 0x8a7f9180u + b, s);
+        if (!rc && quant_mode == SCRY_QUANT_BLOCK32) {
+            P.nb = (k + 31) / 32;
+            rc = dev_alloc((void **)&P.s32, sizeof(float) * (size_t)n * P.nb);
+            if (!rc) rc = launch_fill_f32(P.s32, (size_t)n * P.nb, 1.0f / 127.0f, s);
+        }
+    }
+    auto launch = [&](int i) {
+        GemvArgs g;
+        g.w = &W[i % n_bufs];
+        g.x = x;
+        g.ldx = k;
+        g.m = m_rows;
+        g.y = y;
+        g.ldy = n;
+        return launch_qgemv(EPI_STORE, g, s);
+    };
+    for (int i = 0; i < warmup && !rc; i++) rc = launch(i);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc) {
+        hipError_t e = hipEventCreate(&e0);
+        if (e == hipSuccess) e = hipEventCreate(&e1);
+        if (e == hipSuccess) e = hipEventRecord(e0, s);
+        if (e != hipSuccess) rc = hip_fail(e, "event setup", __FILE__, __LINE__);
+    }
+    for (int i = 0; i < iters && !rc; i++) rc = launch(i);
+    if (!rc) {
+        hipError_t e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float f = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&f, e0, e1);
+        if (e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
+        *avg_us = 1000.0 * f / iters;
+    }
+    if (bytes_per_launch) {
+        const double scales = quant_mode == SCRY_QUANT_BLOCK32 ? 4.0 * n * ((k + 31) / 32) : 4.0;
+        *bytes_per_launch = (double)k * n + scales + 4.0 * m_rows * k + 4.0 * m_rows * n;
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(s);
+    for (auto &P : W) packed_free(P);
+    dev_free(x);
+    dev_free(y);
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,231 @@
+/*
+ * scry_hip -- C ABI of the MI355X (gfx950) backend for scry-llm's int8 Llama
+ * forward path.
+ *
+ * The reference boundary is Rust: `trait DeviceBackend` + `trait MathBackend`
+ * (crates/scry-llm/src/backend/mod.rs:12-45, 48-622) behind the `quantize`
+ * Cargo feature, with the Llama model in crates/scry-llm/src/nn/llama.rs and
+ * the sampling loop in crates/scry-llm/src/generate.rs.  Each entry point
+ * below names the reference item it replaces.  A Rust `HipBackend` maps
+ * `Storage` to `scry_buf`, `I8Storage` to `scry_i8buf`, and panics on a
+ * non-zero status, which is the reference's error behaviour (ops panic).
+ *
+ * Conventions
+ *  - Every call returns 0 on success or a SCRY_ERR_* code; it never aborts.
+ *    scry_hip_last_error() gives the message of the last failure on the
+ *    calling thread.
+ *  - Storage handles own device memory; the caller frees them.  Ops return
+ *    newly allocated storage (the reference's functional style), except
+ *    scatter_rows which writes in place like its `&mut` counterpart.
+ *  - All work is queued on one HIP stream per process; to_vec calls
+ *    synchronise, as the reference's to_vec does.  Calls from several host
+ *    threads are serialised internally.
+ *  - Only float32 storage and int8 weight storage exist, as in the
+ *    reference's `quantize` feature (W8A32).
+ */
+#ifndef SCRY_HIP_H
+#define SCRY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SCRY_OK = 0,
+    SCRY_ERR_INVALID = 1,     /* bad argument or shape (the reference panics) */
+    SCRY_ERR_HIP = 2,         /* HIP runtime error */
+    SCRY_ERR_OOM = 3,         /* device allocation failed */
+    SCRY_ERR_NOT_INIT = 4,    /* scry_hip_init not called / no device */
+    SCRY_ERR_RANGE = 5,       /* index out of range (embedding id, cache full) */
+    SCRY_ERR_UNSUPPORTED = 6  /* shape outside what the kernels implement */
+};
+
+typedef struct scry_buf_s *scry_buf;     /* f32 device storage (Storage)       */
+typedef struct scry_i8buf_s *scry_i8buf; /* int8 weight storage (I8Storage)    */
+typedef struct scry_llama_s *scry_llama; /* LlamaModel with int8 projections   */
+typedef struct scry_kv_cache_s *scry_kv_cache; /* LlamaKvCache (device)        */
+
+/* ---------------------------------------------------------------- runtime */
+/* replaces cuda.rs:39-52 init_gpu (context, stream, kernel set) */
+int scry_hip_init(int device);
+int scry_hip_shutdown(void);
+const char *scry_hip_last_error(void);
+/* replaces cuda.rs:1193-1197 CudaBackend::synchronize */
+int scry_hip_synchronize(void);
+int scry_hip_device_count(int *count);
+/* device name / CU count / gcnArch of the initialised device */
+int scry_hip_device_info(char *name, size_t name_len, int *cu_count, char *arch,
+                         size_t arch_len);
+
+/* -------------------------------------------- DeviceBackend (mod.rs:12-45) */
+/* DeviceBackend::zeros (mod.rs:23) */
+int scry_hip_zeros(size_t n, scry_buf *out);
+/* DeviceBackend::from_vec (mod.rs:25) */
+int scry_hip_from_vec(const float *host, size_t n, scry_buf *out);
+/* DeviceBackend::to_vec (mod.rs:33); n must equal the storage length */
+int scry_hip_to_vec(scry_buf b, float *host, size_t n);
+/* DeviceBackend::clone_storage (mod.rs:44) */
+int scry_hip_clone_storage(scry_buf src, scry_buf *out);
+int scry_hip_buf_len(scry_buf b, size_t *n);
+int scry_hip_free(scry_buf b);
+
+/* DeviceBackend::i8_from_vec (mod.rs:17-18, `quantize` feature) */
+int scry_hip_i8_from_vec(const int8_t *host, size_t n, scry_i8buf *out);
+/* DeviceBackend::i8_to_vec (mod.rs:19-20); takes the storage handle, which is
+ * what the trait needs (the reference signature takes &[i8]) */
+int scry_hip_i8_to_vec(scry_i8buf b, int8_t *host, size_t n);
+int scry_hip_i8_len(scry_i8buf b, size_t *n);
+int scry_hip_i8_free(scry_i8buf b);
+
+/* --------------------------------------------------- quantize.rs on device */
+/* quantize_symmetric (quantize.rs:16-32): per-tensor, bit-exact */
+int scry_hip_quantize_symmetric(scry_buf w, scry_i8buf *q_out, float *scale_out);
+/* dequantize (quantize.rs:35-40) */
+int scry_hip_dequantize(scry_i8buf q, float scale, scry_buf *out);
+/* Block-32 variant (no reference counterpart; builder-defined): quantize_symmetric
+ * on each 32-long k-block of each output column of W[k,n]; scales [n][ceil(k/32)] */
+int scry_hip_quantize_block32(scry_buf w, int k, int n, scry_i8buf *q_out, scry_buf *scales_out);
+
+/* ------------------------------------ MathBackend int8 (mod.rs:512-557) */
+/* MathBackend::matmul_i8_f32 (mod.rs:520-533; CPU cpu.rs:541-551 ->
+ * matmul_i8_f32_tiled cpu.rs:1128-1160): C[m,n] = A[m,k] . (f32(Bq[k,n]) * scale) */
+int scry_hip_matmul_i8_f32(scry_buf a, scry_i8buf b_q, float scale, int m, int k, int n,
+                           scry_buf *out);
+/* MathBackend::matmul_i8_f32_bias (mod.rs:536-557; cpu.rs:553-570) */
+int scry_hip_matmul_i8_f32_bias(scry_buf a, scry_i8buf b_q, float scale, scry_buf bias, int m,
+                                int k, int n, scry_buf *out);
+/* block-32 counterpart of matmul_i8_f32 (builder-defined) */
+int scry_hip_matmul_i8_f32_block32(scry_buf a, scry_i8buf b_q, scry_buf scales, int m, int k,
+                                   int n, scry_buf *out);
+
+/* --------------------------------------- MathBackend glue on the path */
+/* MathBackend::matmul (mod.rs:54-63; cpu.rs:924-961): f32 GEMM/GEMV */
+int scry_hip_matmul(scry_buf a, scry_buf b, int m, int k, int n, int trans_a, int trans_b,
+                    scry_buf *out);
+/* MathBackend::matmul_strided_batched (mod.rs:561-591; cpu.rs:1321-1350) */
+int scry_hip_matmul_strided_batched(scry_buf a, scry_buf b, int batch, int m, int k, int n,
+                                    int trans_a, int trans_b, scry_buf *out);
+/* MathBackend::rmsnorm (cpu.rs:574-599): rows x d */
+int scry_hip_rmsnorm(scry_buf x, scry_buf w, int rows, int d, float eps, scry_buf *out);
+/* MathBackend::rope_with_freqs_preloaded (mod.rs:203-211; cpu.rs:635-664) */
+int scry_hip_rope_with_freqs_preloaded(scry_buf x, int seq, int n_heads, int head_dim,
+                                       int start_pos, scry_buf freqs, scry_buf *out);
+/* MathBackend::rope_with_freqs_scaled_preloaded (mod.rs:219-230) */
+int scry_hip_rope_with_freqs_scaled_preloaded(scry_buf x, int seq, int n_heads, int head_dim,
+                                              int start_pos, scry_buf freqs, float scale,
+                                              scry_buf *out);
+/* MathBackend::scale (cpu.rs:509-511) */
+int scry_hip_scale(scry_buf x, float s, scry_buf *out);
+/* MathBackend::softmax over the last axis (cpu.rs:336-366): rows x cols */
+int scry_hip_softmax(scry_buf x, int rows, int cols, scry_buf *out);
+/* MathBackend::swiglu (cpu.rs:666-678) */
+int scry_hip_swiglu(scry_buf gate, scry_buf up, scry_buf *out);
+/* MathBackend::add, same-shape path (cpu.rs:104-113) */
+int scry_hip_add(scry_buf a, scry_buf b, scry_buf *out);
+/* MathBackend::embedding (cpu.rs:485-498); SCRY_ERR_RANGE for id >= vocab */
+int scry_hip_embedding(scry_buf weight, const int64_t *ids, int n_ids, int vocab, int dim,
+                       scry_buf *out);
+/* MathBackend::gather_reshape_repeat_kv (mod.rs:297-311; cpu.rs:707-730) */
+int scry_hip_gather_reshape_repeat_kv(scry_buf cache, int max_seq, int cached_len, int n_kv,
+                                      int n_q, int head_dim, scry_buf *out);
+/* MathBackend::repeat_kv (cpu.rs:680-705) */
+int scry_hip_repeat_kv(scry_buf x, int n_kv, int n_q, int seq, int d_head, scry_buf *out);
+/* MathBackend::scatter_rows (mod.rs:368-381): in place */
+int scry_hip_scatter_rows(scry_buf dst, scry_buf src, int total_rows, int cols, int row_start,
+                          int row_count);
+/* generate.rs:167-173 argmax (Iterator::max_by semantics), on device */
+int scry_hip_argmax(scry_buf logits, int64_t *out);
+
+/* ------------------------------------------------------ Llama (llama.rs) */
+typedef struct {
+    int32_t vocab_size, hidden_size, intermediate_size, n_layers, n_heads, n_kv_heads,
+        max_seq_len;
+    float rms_norm_eps, rope_theta;
+    int32_t tie_word_embeddings;
+    int32_t has_rope_scaling;
+    double rs_factor, rs_low_freq_factor, rs_high_freq_factor;
+    int64_t rs_original_max_pos;
+} scry_llama_config; /* LlamaConfig (llama.rs:20-34) */
+
+enum { SCRY_QUANT_PER_TENSOR = 0, SCRY_QUANT_BLOCK32 = 1 };
+
+enum {
+    SCRY_T_EMBED = 0,
+    SCRY_T_QKV = 1,
+    SCRY_T_O = 2,
+    SCRY_T_GATE = 3,
+    SCRY_T_UP = 4,
+    SCRY_T_DOWN = 5,
+    SCRY_T_LM_HEAD = 6
+};
+
+/* LlamaModel::new (llama.rs:593-680) with fastrand::Rng::with_seed(seed),
+ * followed by the int8 layout step: every projection (fused qkv, o, gate, up,
+ * down, lm_head; a tied lm_head gets its own int8 copy of embed_tokens) is
+ * quantized per tensor (quantize.rs:16-32) on the device and repacked into the
+ * GEMV stream layout.  quant_mode: SCRY_QUANT_PER_TENSOR or SCRY_QUANT_BLOCK32.
+ * init_on_device = 0 draws the N(0, 0.02) samples on the host with glibc libm
+ * (the reference's arithmetic); 1 draws the same stream on the GPU with the
+ * device libm (identical except where the two libms differ in the last bit). */
+int scry_hip_llama_new_random(const scry_llama_config *cfg, uint64_t seed, int quant_mode,
+                              int init_on_device, scry_llama *out);
+int scry_hip_llama_free(scry_llama m);
+/* Replace one tensor from host f32 data in the reference layout ([in,out]
+ * row-major; embed/lm_head [V,h]); it is quantized and repacked on device.
+ * This is the hook a safetensors loader (llama.rs:768-958) feeds. */
+int scry_hip_llama_set_tensor(scry_llama m, int tensor_id, int layer, const float *host,
+                              size_t n);
+/* Read back a projection's int8 weights in the reference layout (inverse of
+ * the repack) plus its per-tensor scale -- the i8_to_vec of a model tensor. */
+int scry_hip_llama_get_qtensor(scry_llama m, int tensor_id, int layer, int8_t *host, size_t n,
+                               float *scale);
+/* f32 embedding table back to host (V*h floats) */
+int scry_hip_llama_get_embed(scry_llama m, float *host, size_t n);
+
+/* LlamaModel::new_llama_kv_cache (llama.rs:712-719; kv_cache.rs:134-145) */
+int scry_hip_llama_kv_cache_new(scry_llama m, int max_seq, scry_kv_cache *out);
+int scry_hip_kv_cache_free(scry_kv_cache c);
+int scry_hip_kv_cache_seq_len(scry_kv_cache c, int *seq_len);
+/* K and V rows [max_seq, n_kv*hd] of one layer back to host */
+int scry_hip_kv_cache_layer_to_vec(scry_kv_cache c, int layer, float *k_host, float *v_host,
+                                   size_t n);
+
+/* LlamaModel::forward_with_llama_cache (llama.rs:744-763): one token through
+ * all layers, appending K/V at the cache's current length; logits [V] to host
+ * (logits may be NULL).  The device greedy token (argmax) is returned in
+ * *argmax_out when non-NULL. */
+int scry_hip_llama_forward_with_cache(scry_llama m, scry_kv_cache c, int64_t token, int pos,
+                                      float *logits, int64_t *argmax_out);
+
+/* generate() with temperature 0 (generate.rs:51-89, 92-98): the prompt is fed
+ * token by token through the cache path, then greedy tokens follow.  The whole
+ * loop runs on the device as replays of one captured decode-step graph; only
+ * the token ids come back.  Writes max(1, max_tokens) ids to out_tokens and
+ * the count to *n_out.  step_logits (optional) receives [n_out, V] logits. */
+int scry_hip_llama_generate_greedy(scry_llama m, const int64_t *prompt, int n_prompt,
+                                   int max_tokens, int64_t *out_tokens, int *n_out,
+                                   float *step_logits);
+
+/* ------------------------------------------------ measurement helpers */
+/* Decode-step session for benchmarks: binds a model and cache, feeds the
+ * prompt, then runs `steps` greedy decode steps as graph replays.  The time of
+ * the decode steps (HIP events on the launch stream) is returned in *ms. */
+int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_prompt, int warmup,
+                                int steps, int64_t *out_tokens, double *ms);
+/* Average device time (HIP events on the launch stream) of `iters` launches
+ * of one projection kernel of the model, with the same arguments the decode
+ * step uses.  tensor_id: SCRY_T_QKV / O / GATE (fused gate+up) / DOWN / LM_HEAD. */
+int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int iters,
+                                   double *avg_us, double *bytes_per_launch);
+/* Average device time of matmul_i8_f32 at m,k,n rotating over `n_bufs`
+ * distinct weight copies (defeats the 256 MB Infinity Cache). */
+int scry_hip_bench_qgemv(int m, int k, int n, int quant_mode, int n_bufs, int warmup, int iters,
+                         double *avg_us, double *bytes_per_launch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SCRY_HIP_H */
