@@ -98,7 +98,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build runs on exactly one GPU (the int8 decode path has no "
-              "multi-GPU mode; see DESIGN.md for how it would shard). Use --gpus 1.",
+              "multi-GPU mode: sequences would be sharded data-parallel). Use --gpus 1.",
               file=sys.stderr)
         return 2
 

@@ -8,11 +8,11 @@
 // The cache is read in place ([max_seq, n_kv*hd] rows, no repeat_kv copy):
 // workgroup (g, s) handles KV head g and position split s for all n_rep query
 // heads of the group, so each K/V row is read once per group.  Splits write
-// (max, sum, unnormalised output); the last workgroup to finish for a group
-// (atomic counter, reset by that workgroup) merges them with the usual
-// log-sum-exp rescaling.  The split count is fixed per cache, so the launch
-// shape does not depend on the current length and the kernel can live in a
-// replayed graph; the length comes from the device state.
+// (max, sum, unnormalised output) with plain stores -- no fences or atomics;
+// the consumer (the o_proj GEMV prologue, next kernel on the stream) merges
+// them with the usual log-sum-exp rescaling.  The split count is fixed per
+// cache, so the launch shape does not depend on the current length and the
+// kernel can live in a replayed graph; the length comes from the device state.
 #include "internal.h"
 
 namespace scry {
@@ -37,142 +37,124 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // G = lanes per cached position (each lane holds 4 of the hd values);
 // NR = max query heads per KV head handled by one workgroup.
+//
+// Each wave walks its positions U*P at a time: the K and V rows of a step are
+// requested together (one memory round trip per step), the scores are reduced
+// over the G lanes of a position, and an online softmax keeps (max, sum, out)
+// per lane group.  The 4*P lane groups of the workgroup are merged through LDS
+// into one partial per (query head, split).
 template <int G, int NR>
 __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
-    constexpr int P = 64 / G;  // positions per wave step
+    constexpr int P = 64 / G;  // positions per load instruction
+    constexpr int U = 4;       // load instructions per step
+    constexpr int PI = P * U;  // positions per wave step
+    constexpr int SLOTS = 4 * P;
     extern __shared__ float sm[];
+    float *s_o = sm;                    // [SLOTS][NR][hd]
+    __shared__ float s_m[SLOTS][NR], s_l[SLOTS][NR];
     const int g = blockIdx.x, split = blockIdx.y;
     const int nrep = a.n_heads / a.n_kv, hd = a.head_dim, kv_dim = a.n_kv * hd;
     const int L = a.fixed_len >= 0 ? a.fixed_len : a.state->cache_len + 1;
     const int chunk = (L + a.n_splits - 1) / a.n_splits;
     const int t0 = min(L, split * chunk), t1 = min(L, t0 + chunk);
-    const int n = t1 - t0;
-    const int mc = a.max_chunk;
-    float *sc = sm;                  // [NR][mc] scores, then probabilities
-    float *red = sm + NR * mc;       // [4*P][NR][hd] partial outputs
-    __shared__ float s_m[NR], s_l[NR];
-    __shared__ int s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = lane / G, gl = lane % G;
     const bool dact = gl * 4 < hd;
-    const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.k_cache, (size_t)(t1) * kv_dim * 4);
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v_cache, (size_t)(t1) * kv_dim * 4);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.k_cache, (size_t)t1 * kv_dim * 4);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v_cache, (size_t)t1 * kv_dim * 4);
     const unsigned col = (unsigned)(g * hd + gl * 4) * 4;
 
-    // ---- scores s[r][t] = q_r . K[t]
     float4 qf[NR];
+    float m[NR], l[NR];
+    float4 o[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         qf[r] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (r < nrep && dact) qf[r] = *(const float4 *)(a.q + (size_t)(g * nrep + r) * hd + gl * 4);
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+        o[r] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (int tb = t0 + wave * P; tb < t1; tb += 4 * P) {
-        const int t = tb + sub;
-        const bool ok = t < t1 && dact;
-        const float4 kv = bload16f(kr, ok ? (unsigned)t * kv_dim * 4 + col : 0x80000000u);
+    for (int tb = t0 + wave * PI; tb < t1; tb += 4 * PI) {
+        float4 kv[U], vv[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int t = tb + u * P + sub;
+            const unsigned off = (t < t1 && dact) ? (unsigned)t * kv_dim * 4 + col : 0x80000000u;
+            kv[u] = bload16f(kr, off);
+            vv[u] = bload16f(vr, off);
+        }
 #pragma unroll
         for (int r = 0; r < NR; r++) {
-            float s = qf[r].x * kv.x + qf[r].y * kv.y + qf[r].z * kv.z + qf[r].w * kv.w;
-            s = group_sum<G>(s);
-            if (gl == 0 && t < t1 && r < nrep) sc[r * mc + (t - t0)] = s;
+            if (r >= nrep) break;
+            float sc[U];
+            float mx = m[r];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                float d = qf[r].x * kv[u].x + qf[r].y * kv[u].y + qf[r].z * kv[u].z + qf[r].w * kv[u].w;
+                d = group_sum<G>(d);
+                sc[u] = (tb + u * P + sub < t1) ? d : -INFINITY;
+                mx = fmaxf(mx, sc[u]);
+            }
+            if (mx == -INFINITY) continue;  // this lane group has no position yet
+            const float f = expf(m[r] - mx);
+            l[r] *= f;
+            o[r].x *= f;
+            o[r].y *= f;
+            o[r].z *= f;
+            o[r].w *= f;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const float p = expf(sc[u] - mx);
+                l[r] += p;
+                o[r].x += p * vv[u].x;
+                o[r].y += p * vv[u].y;
+                o[r].z += p * vv[u].z;
+                o[r].w += p * vv[u].w;
+            }
+            m[r] = mx;
         }
     }
-    __syncthreads();
-
-    // ---- per-head max and sum of exp over this split
-    for (int r = wave; r < nrep; r += 4) {
-        float mx = -INFINITY;
-        for (int i = lane; i < n; i += 64) mx = fmaxf(mx, sc[r * mc + i]);
+    const int slot = wave * P + sub;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        float l = 0.f;
-        for (int i = lane; i < n; i += 64) {
-            const float p = expf(sc[r * mc + i] - mx);
-            sc[r * mc + i] = p;
-            l += p;
+    for (int r = 0; r < NR; r++) {
+        if (r >= nrep) break;
+        if (gl == 0) {
+            s_m[slot][r] = m[r];
+            s_l[slot][r] = l[r];
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
-        if (lane == 0) {
-            s_m[r] = mx;
-            s_l[r] = l;
-        }
+        if (dact) *(float4 *)(s_o + ((size_t)slot * NR + r) * hd + gl * 4) = o[r];
     }
     __syncthreads();
-
-    // ---- o[r] = sum_t p[r][t] V[t]
-    float4 o[NR];
+    for (int idx = tid; idx < nrep * hd; idx += TPB) {
+        const int r = idx / hd, d = idx % hd;
+        float M = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < NR; r++) o[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int tb = t0 + wave * P; tb < t1; tb += 4 * P) {
-        const int t = tb + sub;
-        const bool ok = t < t1 && dact;
-        const float4 v = bload16f(vr, ok ? (unsigned)t * kv_dim * 4 + col : 0x80000000u);
-        if (t < t1) {
+        for (int q = 0; q < SLOTS; q++) M = fmaxf(M, s_m[q][r]);
+        float lsum = 0.f, osum = 0.f;
+        if (M != -INFINITY) {
 #pragma unroll
-            for (int r = 0; r < NR; r++) {
-                if (r < nrep) {
-                    const float p = sc[r * mc + (t - t0)];
-                    o[r].x += p * v.x;
-                    o[r].y += p * v.y;
-                    o[r].z += p * v.z;
-                    o[r].w += p * v.w;
-                }
+            for (int q = 0; q < SLOTS; q++) {
+                if (s_m[q][r] == -INFINITY) continue;
+                const float f = expf(s_m[q][r] - M);
+                lsum += s_l[q][r] * f;
+                osum += s_o[((size_t)q * NR + r) * hd + d] * f;
             }
         }
-    }
-    if (dact) {
-        const int slot = wave * P + sub;
-#pragma unroll
-        for (int r = 0; r < NR; r++)
-            if (r < nrep) *(float4 *)(red + ((size_t)slot * NR + r) * hd + gl * 4) = o[r];
-    }
-    __syncthreads();
-    for (int idx = tid; idx < nrep * hd; idx += TPB) {
-        const int r = idx / hd, d = idx % hd;
-        float s = 0.f;
-        for (int slot = 0; slot < 4 * P; slot++) s += red[((size_t)slot * NR + r) * hd + d];
         const size_t ph = (size_t)(g * nrep + r) * a.n_splits + split;
-        a.part_o[ph * hd + d] = s;
+        a.part_o[ph * hd + d] = osum;
         if (d == 0) {
-            a.part_ml[ph * 2 + 0] = s_m[r];
-            a.part_ml[ph * 2 + 1] = s_l[r];
+            a.part_ml[ph * 2 + 0] = M;
+            a.part_ml[ph * 2 + 1] = lsum;
         }
     }
-
-    // ---- last workgroup of group g merges the splits
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        const unsigned prev = atomicAdd(a.counter + g, 1u);
-        s_last = (prev == (unsigned)a.n_splits - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int idx = tid; idx < nrep * hd; idx += TPB) {
-        const int r = idx / hd, d = idx % hd;
-        const size_t h0 = (size_t)(g * nrep + r) * a.n_splits;
-        float M = -INFINITY;
-        for (int s = 0; s < a.n_splits; s++) M = fmaxf(M, a.part_ml[(h0 + s) * 2]);
-        float lsum = 0.f, osum = 0.f;
-        for (int s = 0; s < a.n_splits; s++) {
-            const float ms = a.part_ml[(h0 + s) * 2];
-            if (ms == -INFINITY) continue;  // empty split
-            const float f = expf(ms - M);
-            lsum += a.part_ml[(h0 + s) * 2 + 1] * f;
-            osum += a.part_o[(h0 + s) * hd + d] * f;
-        }
-        a.out[(size_t)(g * nrep + r) * hd + d] = osum / lsum;
-    }
-    if (tid == 0) a.counter[g] = 0u;
 }
 
 template <int G>
 int launch_g(const AttnArgs &a, int nrep, hipStream_t s) {
     const int P = 64 / G;
-    auto lds = [&](int nr) { return (size_t)nr * a.max_chunk * 4 + (size_t)4 * P * nr * a.head_dim * 4; };
+    auto lds = [&](int nr) { return (size_t)4 * P * nr * a.head_dim * 4; };
     dim3 grid(a.n_kv, a.n_splits);
     if (nrep <= 1) {
         hipLaunchKernelGGL((k_attn_decode<G, 1>), grid, dim3(TPB), lds(1), s, a);
@@ -192,13 +174,15 @@ int launch_g(const AttnArgs &a, int nrep, hipStream_t s) {
 }  // namespace
 
 int attn_pick_splits(int n_kv, int max_seq, int *n_splits, int *max_chunk) {
-    // ~512 workgroups per launch, at least 16 positions per split
-    int ns = (512 + n_kv - 1) / n_kv;
+    // ~256 workgroups per launch, at most 16 splits (the consumer merges
+    // n_heads * n_splits partials per workgroup), >= 16 positions per split
+    int ns = (256 + n_kv - 1) / n_kv;
+    if (ns > 16) ns = 16;
     const int cap = (max_seq + 15) / 16;
     if (ns > cap) ns = cap;
     if (ns < 1) ns = 1;
     *n_splits = ns;
-    *max_chunk = ((max_seq + ns - 1) / ns + 3) & ~3;  // keeps the LDS reduction area 16-byte aligned
+    *max_chunk = (max_seq + ns - 1) / ns;
     return SCRY_OK;
 }
 

@@ -124,24 +124,26 @@ struct GemvArgs {
     const float2 *rope_cs = nullptr;  // [max_pos][head_dim/2] (cos, sin)
     int q_dim = 0, kv_dim = 0, head_dim = 0;
     float q_scale = 1.f;
-    // EPI_LOGITS (device argmax + step advance)
+    // EPI_LOGITS: per-workgroup argmax partials (reduced by launch_logits_finish,
+    // which also records the token and advances the step state)
     float *part_val = nullptr;
     int *part_idx = nullptr, *part_nan = nullptr;
-    unsigned int *counter = nullptr;
     int64_t *tokens_rw = nullptr;
     int64_t *argmax_out = nullptr;
     int advance = 0;
+    // attention-merge prologue (o_proj): split partials of the decode attention
+    const float *attn_part_o = nullptr, *attn_part_ml = nullptr;
+    int attn_nh = 0, attn_ns = 0, attn_hd = 0;
 };
 
 int launch_qgemv(int epi, const GemvArgs &a, hipStream_t s);
+int launch_logits_finish(const GemvArgs &a, hipStream_t s);
 
 // attn.hip
 struct AttnArgs {
     const float *q = nullptr;     // [n_heads*hd] pre-scaled
     const float *k_cache = nullptr, *v_cache = nullptr;  // [max_seq, n_kv*hd]
-    float *out = nullptr;         // [n_heads*hd]
-    float *part_o = nullptr, *part_ml = nullptr;  // scratch
-    unsigned int *counter = nullptr;  // [n_kv], zero between launches
+    float *part_o = nullptr, *part_ml = nullptr;  // per (head, split) partials
     const DevState *state = nullptr;
     int n_heads = 0, n_kv = 0, head_dim = 0, n_splits = 1, max_chunk = 0;
     int fixed_len = -1;  // >= 0: use this length instead of state->cache_len + 1

@@ -12,14 +12,15 @@
 // Decode step, per layer (5 kernels):
 //   qkv   : RMSNorm(x) -> int8 GEMV -> RoPE(Q)*1/sqrt(hd), RoPE(K), K/V row append
 //           (layer 0 reads the embedding row of the current token directly)
-//   attn  : split-L attention over the cache in place, last-block merge
-//   o     : int8 GEMV + residual add into x
+//   attn  : split-L attention over the cache in place -> per-split partials
+//   o     : merge of the attention partials (prologue) -> int8 GEMV + residual add into x
 //   gateup: RMSNorm(x) -> fused gate/up int8 GEMV -> silu(g)*u
 //   down  : int8 GEMV + residual add into x
-// then lm_head: RMSNorm(x) -> int8 GEMV -> logits -> device argmax -> next token
-// and position advance.  The current position and token live in device
+// then lm_head: RMSNorm(x) -> int8 GEMV -> logits + per-workgroup argmax, and a
+// one-workgroup finish kernel: ordered argmax -> next token, position advance.  The current position and token live in device
 // memory, so the same captured graph replays for every token.
 #include <climits>
+#include <cstdlib>
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -64,12 +65,10 @@ struct scry_kv_cache_s {
     DevState *state = nullptr;
     int64_t *tokens = nullptr;
     int tokens_len = 0;
-    float *x = nullptr, *xq = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    float *x = nullptr, *xq = nullptr, *act = nullptr, *logits = nullptr;
     float *ap_o = nullptr, *ap_ml = nullptr;
-    unsigned int *a_cnt = nullptr;
     float *lp_val = nullptr;
     int *lp_idx = nullptr, *lp_nan = nullptr;
-    unsigned int *l_cnt = nullptr;
     int64_t *amax = nullptr;
     int n_splits = 1, max_chunk = 16;
     hipGraph_t graph = nullptr;
@@ -284,16 +283,13 @@ void cache_free(scry_kv_cache c) {
     dev_free(c->tokens);
     dev_free(c->x);
     dev_free(c->xq);
-    dev_free(c->attn);
     dev_free(c->act);
     dev_free(c->logits);
     dev_free(c->ap_o);
     dev_free(c->ap_ml);
-    dev_free(c->a_cnt);
     dev_free(c->lp_val);
     dev_free(c->lp_idx);
     dev_free(c->lp_nan);
-    dev_free(c->l_cnt);
     dev_free(c->amax);
     if (c->hs) (void)hipHostFree(c->hs);
     if (c->m) c->m->live_caches--;
@@ -319,18 +315,13 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
     if (!rc) rc = dev_alloc((void **)&c->tokens, sizeof(int64_t) * c->tokens_len);
     if (!rc) rc = dev_alloc((void **)&c->x, sizeof(float) * m->h);
     if (!rc) rc = dev_alloc((void **)&c->xq, sizeof(float) * m->q_dim);
-    if (!rc) rc = dev_alloc((void **)&c->attn, sizeof(float) * m->q_dim);
     if (!rc) rc = dev_alloc((void **)&c->act, sizeof(float) * m->ffn);
     if (!rc) rc = dev_alloc((void **)&c->logits, sizeof(float) * m->V);
     if (!rc) rc = dev_alloc((void **)&c->ap_o, sizeof(float) * (size_t)m->nh * c->n_splits * m->hd);
     if (!rc) rc = dev_alloc((void **)&c->ap_ml, sizeof(float) * (size_t)m->nh * c->n_splits * 2);
-    if (!rc) rc = dev_alloc((void **)&c->a_cnt, sizeof(unsigned) * m->nkv);
-    if (!rc) rc = launch_fill_u32(c->a_cnt, m->nkv, 0u, s);
     if (!rc) rc = dev_alloc((void **)&c->lp_val, sizeof(float) * nparts);
     if (!rc) rc = dev_alloc((void **)&c->lp_idx, sizeof(int) * nparts);
     if (!rc) rc = dev_alloc((void **)&c->lp_nan, sizeof(int) * nparts);
-    if (!rc) rc = dev_alloc((void **)&c->l_cnt, sizeof(unsigned));
-    if (!rc) rc = launch_fill_u32(c->l_cnt, 1, 0u, s);
     if (!rc) rc = dev_alloc((void **)&c->amax, sizeof(int64_t));
     if (!rc) {
         hipError_t e = hipHostMalloc((void **)&c->hs, sizeof(HostStage), hipHostMallocDefault);
@@ -387,10 +378,8 @@ AttnArgs attn_args(scry_kv_cache c, int l) {
     a.q = c->xq;
     a.k_cache = c->K(l);
     a.v_cache = c->Vc(l);
-    a.out = c->attn;
     a.part_o = c->ap_o;
     a.part_ml = c->ap_ml;
-    a.counter = c->a_cnt;
     a.state = c->state;
     a.n_heads = m->nh;
     a.n_kv = m->nkv;
@@ -404,8 +393,12 @@ GemvArgs o_args(scry_kv_cache c, int l) {
     scry_llama m = c->m;
     GemvArgs g;
     g.w = &m->layers[l].o;
-    g.x = c->attn;
     g.ldx = m->q_dim;
+    g.attn_part_o = c->ap_o;
+    g.attn_part_ml = c->ap_ml;
+    g.attn_nh = m->nh;
+    g.attn_ns = c->n_splits;
+    g.attn_hd = m->hd;
     g.y = c->x;
     g.ldy = m->h;
     g.resid = l == 0 ? nullptr : c->x;  // layer 0: residual is the embedding row
@@ -454,7 +447,6 @@ GemvArgs lm_args(scry_kv_cache c, int advance) {
     g.part_val = c->lp_val;
     g.part_idx = c->lp_idx;
     g.part_nan = c->lp_nan;
-    g.counter = c->l_cnt;
     g.tokens_rw = c->tokens;
     g.argmax_out = c->amax;
     g.advance = advance;
@@ -470,12 +462,18 @@ int record_step(scry_kv_cache c, hipStream_t s) {
         SCRY_TRY(launch_qgemv(EPI_SWIGLU, gu_args(c, l), s));
         SCRY_TRY(launch_qgemv(EPI_RESID, down_args(c, l), s));
     }
-    return launch_qgemv(EPI_LOGITS, lm_args(c, 1), s);
+    const GemvArgs lg = lm_args(c, 1);
+    SCRY_TRY(launch_qgemv(EPI_LOGITS, lg, s));
+    return launch_logits_finish(lg, s);
 }
 
 // One decode step: the captured graph when available, else direct launches.
+// SCRY_HIP_NO_GRAPH=1 forces direct launches (same kernels), for tools that
+// do not follow graph launches.
 int run_step(scry_kv_cache c) {
     hipStream_t s = ctx().stream;
+    static const bool no_graph = std::getenv("SCRY_HIP_NO_GRAPH") != nullptr;
+    if (no_graph) return record_step(c, s);
     if (!c->gexec) {
         hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
         if (e == hipSuccess) {
@@ -833,7 +831,8 @@ int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int i
     SCRY_TRY(cache_new(m, 16, &c));
     hipStream_t s = ctx().stream;
     int rc = launch_fill_f32(c->x, m->h, 1.0f, s);
-    if (!rc) rc = launch_fill_f32(c->attn, m->q_dim, 0.5f, s);
+    if (!rc) rc = launch_fill_f32(c->ap_ml, (size_t)m->nh * c->n_splits * 2, 1.0f, s);
+    if (!rc) rc = launch_fill_f32(c->ap_o, (size_t)m->nh * c->n_splits * m->hd, 0.5f, s);
     if (!rc) rc = launch_fill_f32(c->act, m->ffn, 0.25f, s);
     if (!rc) {
         c->hs->tok = 0;

@@ -56,11 +56,12 @@ struct KArgs {
     float q_scale;
     float *part_val;
     int *part_idx, *part_nan;
-    unsigned int *counter;
-    int64_t *tokens_rw;
-    int64_t *argmax_out;
-    int advance;
+    const float *at_o, *at_ml;  // PRO_ATTN: attention split partials
+    int at_nh, at_ns, at_hd;
 };
+
+// activation prologues
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ATTN = 2 };
 
 __device__ __forceinline__ float dot16(u32x4 w, float4 x0, float4 x1, float4 x2, float4 x3,
                                        float acc) {
@@ -238,8 +239,9 @@ __device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RW], int c, const flo
     }
 }
 
-template <int EPI, bool NORM, bool B32, int MT, int NCH>
+template <int EPI, int PRO, bool B32, int MT, int NCH>
 __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
+    constexpr bool NORM = PRO == PRO_NORM;
     constexpr int XP = NCH > 0 ? NCH : 16;
     extern __shared__ float4 dyn4[];
     float *xs = reinterpret_cast<float *>(dyn4);
@@ -255,7 +257,7 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
     // ---- 1. activation loads first, then the first PF weight chunks: waiting
     // for the activations then leaves the weight stream in flight.
     float4 xr[XP];
-    load_x<XP>(act_row(a, m0), a.k, xr);
+    if (PRO != PRO_ATTN) load_x<XP>(act_row(a, m0), a.k, xr);
     float4 nw[NORM ? XP : 1];
     if (NORM) load_x<XP>(a.norm_w, a.k, reinterpret_cast<float4(&)[XP]>(nw));
 
@@ -271,6 +273,41 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
         for (int r = 0; r < RW; r++) wb[d][r] = bload16(wr, woff[r] + (d << 10));
 
     // ---- 2. stage the activation rows (optionally RMSNorm'd) into LDS
+    if (PRO == PRO_ATTN) {
+        // Merge the attention splits (log-sum-exp rescaling) into the input
+        // row: x[h*hd + d] = sum_s O_s[d] e^(M_s - M) / sum_s L_s e^(M_s - M).
+        float *wm = xs + MT * kc + (B32 ? MT * (kc >> 4) : 0);  // [nh][ns]
+        const int nh = a.at_nh, ns = a.at_ns, hd = a.at_hd;
+        for (int h = tid; h < nh; h += TPB) {
+            const float *ml = a.at_ml + (size_t)h * ns * 2;
+            float M = -INFINITY;
+            for (int q = 0; q < ns; q++) M = fmaxf(M, ml[2 * q]);
+            float Ls = 0.f;
+            for (int q = 0; q < ns; q++)
+                if (ml[2 * q] != -INFINITY) Ls += ml[2 * q + 1] * expf(ml[2 * q] - M);
+            for (int q = 0; q < ns; q++)
+                wm[h * ns + q] = ml[2 * q] == -INFINITY ? 0.f : expf(ml[2 * q] - M) / Ls;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < XP; p++) {
+            const int idx = (p << 10) + (tid << 2);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (idx < a.k) {
+                const int h = idx / hd, d = idx - h * hd;
+                const float *po = a.at_o + (size_t)h * ns * hd + d;
+                for (int q = 0; q < ns; q++) {
+                    const float w = wm[h * ns + q];
+                    const float4 o4 = *(const float4 *)(po + (size_t)q * hd);
+                    v.x += w * o4.x;
+                    v.y += w * o4.y;
+                    v.z += w * o4.z;
+                    v.w += w * o4.w;
+                }
+            }
+            xr[p] = v;
+        }
+    }
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         if (mi > 0) load_x<XP>(act_row(a, m0 + mi), a.k, xr);
@@ -443,9 +480,9 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
             }
         }
     } else if (EPI == EPI_LOGITS) {
+        // logits + this workgroup's ordered argmax partial (no fences: the
+        // finish kernel that reduces the partials is the next launch)
         __shared__ float s_v[RPB];
-        __shared__ ArgAcc s_arg[TPB];
-        __shared__ int s_last;
         if (lane < RW) {
             const int row = row0 + lane;
             float v = val[0][0];
@@ -474,80 +511,64 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
             a.part_val[blockIdx.x] = p.v;
             a.part_idx[blockIdx.x] = p.i;
             a.part_nan[blockIdx.x] = p.nan;
-            __threadfence();
-            const unsigned prev = atomicAdd(a.counter, 1u);
-            s_last = (prev == gridDim.x - 1);
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        // last workgroup: ordered reduction of the per-workgroup partials
-        const int np = gridDim.x;
-        const int per = (np + TPB - 1) / TPB;
-        ArgAcc acc1{0.f, -1, -1};
-        for (int t = tid * per; t < min(np, tid * per + per); t++) {
-            ArgAcc p{a.part_val[t], a.part_idx[t], a.part_nan[t]};
-            acc1 = arg_combine(acc1, p);
-        }
-        const ArgAcc r = block_argmax(acc1, s_arg);
-        const int tok = argmax_finish(r, a.y, a.rows, s_arg);
-        if (tid == 0) {
-            *a.counter = 0u;
-            DevState *st = a.state;
-            const int p = st->pos;
-            if (a.argmax_out) a.argmax_out[0] = tok;
-            if (a.advance) {
-                if (p + 1 <= st->max_tokens && p + 1 >= st->n_prompt) a.tokens_rw[p + 1] = tok;
-                st->pos = p + 1;
-                st->cache_len = st->cache_len + 1;
-            }
         }
     }
 }
 
-template <int EPI, bool NORM, bool B32, int MT, int NCH>
+template <int EPI, int PRO, bool B32, int MT, int NCH>
 int launch_t(const KArgs &ka, hipStream_t s) {
     const int kc = ka.nch << 10;
     size_t lds = (size_t)MT * kc * sizeof(float) + (B32 ? (size_t)MT * (kc >> 4) * sizeof(float) : 0);
+    if (PRO == PRO_ATTN) lds += (size_t)ka.at_nh * ka.at_ns * sizeof(float);
     dim3 grid((ka.rows + RPB - 1) / RPB, (ka.m + MT - 1) / MT);
-    hipLaunchKernelGGL((k_qgemv<EPI, NORM, B32, MT, NCH>), grid, dim3(TPB), lds, s, ka);
+    hipLaunchKernelGGL((k_qgemv<EPI, PRO, B32, MT, NCH>), grid, dim3(TPB), lds, s, ka);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }
 
 // NCH = compile-time chunk count (straight-line stream) for the k on the
 // Llama path; 0 = runtime loop for any other k <= 16384.
-template <int EPI, bool NORM, bool B32, int MT>
+template <int EPI, int PRO, bool B32, int MT>
 int launch_nch(const KArgs &ka, hipStream_t s) {
     switch (ka.nch) {
-        case 1: return launch_t<EPI, NORM, B32, MT, 1>(ka, s);
-        case 4: return launch_t<EPI, NORM, B32, MT, 4>(ka, s);
-        case 11: if (MT == 1) return launch_t<EPI, NORM, B32, MT, 11>(ka, s); break;
-        case 14: if (MT == 1) return launch_t<EPI, NORM, B32, MT, 14>(ka, s); break;
+        case 1: return launch_t<EPI, PRO, B32, MT, 1>(ka, s);
+        case 4: return launch_t<EPI, PRO, B32, MT, 4>(ka, s);
+        case 11: if (MT == 1) return launch_t<EPI, PRO, B32, MT, 11>(ka, s); break;
+        case 14: if (MT == 1) return launch_t<EPI, PRO, B32, MT, 14>(ka, s); break;
         default: break;
     }
-    return launch_t<EPI, NORM, B32, MT, 0>(ka, s);
+    return launch_t<EPI, PRO, B32, MT, 0>(ka, s);
 }
 
-template <int EPI, bool NORM, bool B32>
+template <int EPI, int PRO, bool B32>
 int launch_mt(const KArgs &ka, hipStream_t s) {
     // skinny GEMM: MT activation rows share one weight pass (k <= 4096 keeps
     // MT * k floats within the 64 KiB LDS stage)
     if constexpr (EPI == EPI_STORE) {
-        if (ka.m >= 4 && ka.nch <= 4) return launch_nch<EPI, NORM, B32, 4>(ka, s);
-        if (ka.m >= 2 && ka.nch <= 4) return launch_nch<EPI, NORM, B32, 2>(ka, s);
+        if (ka.m >= 4 && ka.nch <= 4) return launch_nch<EPI, PRO, B32, 4>(ka, s);
+        if (ka.m >= 2 && ka.nch <= 4) return launch_nch<EPI, PRO, B32, 2>(ka, s);
     }
-    return launch_nch<EPI, NORM, B32, 1>(ka, s);
+    return launch_nch<EPI, PRO, B32, 1>(ka, s);
 }
 
 template <int EPI>
-int launch_e(const KArgs &ka, bool norm, bool b32, hipStream_t s) {
-    // the decode epilogues always take a fused RMSNorm; STORE/RESID never do
+int launch_e(const KArgs &ka, bool norm, bool attn, bool b32, hipStream_t s) {
+    // decode epilogues QKV/SWIGLU/LOGITS always take the fused RMSNorm; the
+    // attention-merge prologue feeds only the residual epilogue (o_proj)
     constexpr bool kNorm = (EPI == EPI_QKV || EPI == EPI_SWIGLU || EPI == EPI_LOGITS);
     if (norm != kNorm)
         return set_error(SCRY_ERR_INVALID, "qgemv: epilogue %d %s a fused RMSNorm", EPI,
                          kNorm ? "requires" : "does not take");
-    return b32 ? launch_mt<EPI, kNorm, true>(ka, s) : launch_mt<EPI, kNorm, false>(ka, s);
+    if constexpr (kNorm) {
+        return b32 ? launch_mt<EPI, PRO_NORM, true>(ka, s) : launch_mt<EPI, PRO_NORM, false>(ka, s);
+    } else if constexpr (EPI == EPI_RESID) {
+        if (attn)
+            return b32 ? launch_mt<EPI, PRO_ATTN, true>(ka, s) : launch_mt<EPI, PRO_ATTN, false>(ka, s);
+        return b32 ? launch_mt<EPI, PRO_PLAIN, true>(ka, s) : launch_mt<EPI, PRO_PLAIN, false>(ka, s);
+    } else {
+        if (attn) return set_error(SCRY_ERR_INVALID, "qgemv: attention merge needs the residual epilogue");
+        return b32 ? launch_mt<EPI, PRO_PLAIN, true>(ka, s) : launch_mt<EPI, PRO_PLAIN, false>(ka, s);
+    }
 }
 
 }  // namespace
@@ -596,18 +617,22 @@ int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     ka.part_val = g.part_val;
     ka.part_idx = g.part_idx;
     ka.part_nan = g.part_nan;
-    ka.counter = g.counter;
-    ka.tokens_rw = g.tokens_rw;
-    ka.argmax_out = g.argmax_out;
-    ka.advance = g.advance;
+    ka.at_o = g.attn_part_o;
+    ka.at_ml = g.attn_part_ml;
+    ka.at_nh = g.attn_nh;
+    ka.at_ns = g.attn_ns;
+    ka.at_hd = g.attn_hd;
     const bool norm = g.norm_w != nullptr;
+    const bool attn = g.attn_part_o != nullptr;
     const bool b32 = w.s32 != nullptr;
+    if (attn && (g.attn_nh * g.attn_hd != w.k || g.attn_hd % 4 || g.m != 1))
+        return set_error(SCRY_ERR_INVALID, "qgemv: attention merge shape mismatch");
     switch (epi) {
-        case EPI_STORE: return launch_e<EPI_STORE>(ka, norm, b32, s);
-        case EPI_RESID: return launch_e<EPI_RESID>(ka, norm, b32, s);
-        case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(ka, norm, b32, s);
-        case EPI_QKV: return launch_e<EPI_QKV>(ka, norm, b32, s);
-        case EPI_LOGITS: return launch_e<EPI_LOGITS>(ka, norm, b32, s);
+        case EPI_STORE: return launch_e<EPI_STORE>(ka, norm, attn, b32, s);
+        case EPI_RESID: return launch_e<EPI_RESID>(ka, norm, attn, b32, s);
+        case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(ka, norm, attn, b32, s);
+        case EPI_QKV: return launch_e<EPI_QKV>(ka, norm, attn, b32, s);
+        case EPI_LOGITS: return launch_e<EPI_LOGITS>(ka, norm, attn, b32, s);
     }
     return set_error(SCRY_ERR_INVALID, "qgemv: unknown epilogue %d", epi);
 }
@@ -621,6 +646,42 @@ __global__ __launch_bounds__(TPB) void k_argmax(const float *__restrict__ x, int
     if (threadIdx.x == 0) *out = (n <= 0) ? 0 : tok;
 }
 }  // namespace
+
+// End of a decode step: reduce the LM head's per-workgroup argmax partials in
+// index order (one workgroup), then record the token and advance the state.
+namespace {
+__global__ __launch_bounds__(TPB) void k_logits_finish(const float *__restrict__ logits, int V,
+                                                       const float *__restrict__ pv,
+                                                       const int *__restrict__ pi,
+                                                       const int *__restrict__ pn, int np,
+                                                       DevState *st, int64_t *tokens,
+                                                       int64_t *argmax_out, int advance) {
+    __shared__ ArgAcc sh[TPB];
+    const int tid = threadIdx.x;
+    const int per = (np + TPB - 1) / TPB;
+    ArgAcc acc{0.f, -1, -1};
+    for (int t = tid * per; t < min(np, tid * per + per); t++) acc = arg_combine(acc, ArgAcc{pv[t], pi[t], pn[t]});
+    const ArgAcc r = block_argmax(acc, sh);
+    const int tok = argmax_finish(r, logits, V, sh);
+    if (tid == 0) {
+        const int p = st->pos;
+        if (argmax_out) argmax_out[0] = tok;
+        if (advance) {
+            if (p + 1 <= st->max_tokens && p + 1 >= st->n_prompt) tokens[p + 1] = tok;
+            st->pos = p + 1;
+            st->cache_len = st->cache_len + 1;
+        }
+    }
+}
+}  // namespace
+
+int launch_logits_finish(const GemvArgs &g, hipStream_t s) {
+    const int np = (g.w->rows + RPB - 1) / RPB;
+    hipLaunchKernelGGL(k_logits_finish, dim3(1), dim3(TPB), 0, s, g.y, g.w->rows, g.part_val,
+                       g.part_idx, g.part_nan, np, g.state, g.tokens_rw, g.argmax_out, g.advance);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
 
 int launch_argmax(const float *x, int64_t n, int64_t *out, hipStream_t s) {
     if (n > 0x7fffffff) return set_error(SCRY_ERR_UNSUPPORTED, "argmax: n too large");
