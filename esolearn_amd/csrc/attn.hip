@@ -14,19 +14,12 @@
 // cache, so the launch shape does not depend on the current length and the
 // kernel can live in a replayed graph; the length comes from the device state.
 #include "internal.h"
+#include "kdev.h"
 
 namespace scry {
 namespace {
 
-constexpr int TPB = 256;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, size_t bytes) {
-    const int n = bytes > 0x7fffffffu ? 0x7fffffff : (int)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
-}
-__device__ __forceinline__ float4 bload16f(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
+using namespace dev;
 
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {

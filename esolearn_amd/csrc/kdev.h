@@ -1,0 +1,149 @@
+// Device-side helpers shared by the GEMV, attention and decode kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace scry {
+namespace dev {
+
+constexpr int TPB = 256;  // threads per workgroup (4 waves of 64)
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float dot16(u32x4 w, float4 x0, float4 x1, float4 x2, float4 x3,
+                                       float acc) {
+    acc = fmaf(x0.x, (float)(w.x & 0xffu), acc);
+    acc = fmaf(x0.y, (float)((w.x >> 8) & 0xffu), acc);
+    acc = fmaf(x0.z, (float)((w.x >> 16) & 0xffu), acc);
+    acc = fmaf(x0.w, (float)(w.x >> 24), acc);
+    acc = fmaf(x1.x, (float)(w.y & 0xffu), acc);
+    acc = fmaf(x1.y, (float)((w.y >> 8) & 0xffu), acc);
+    acc = fmaf(x1.z, (float)((w.y >> 16) & 0xffu), acc);
+    acc = fmaf(x1.w, (float)(w.y >> 24), acc);
+    acc = fmaf(x2.x, (float)(w.z & 0xffu), acc);
+    acc = fmaf(x2.y, (float)((w.z >> 8) & 0xffu), acc);
+    acc = fmaf(x2.z, (float)((w.z >> 16) & 0xffu), acc);
+    acc = fmaf(x2.w, (float)(w.z >> 24), acc);
+    acc = fmaf(x3.x, (float)(w.w & 0xffu), acc);
+    acc = fmaf(x3.y, (float)((w.w >> 8) & 0xffu), acc);
+    acc = fmaf(x3.z, (float)((w.w >> 16) & 0xffu), acc);
+    acc = fmaf(x3.w, (float)(w.w >> 24), acc);
+    return acc;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// block-wide f64 sum (all 256 threads call it; result valid in every thread)
+__device__ __forceinline__ double block_sum_d(double v, double *red) {
+    v = wave_sum_d(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+__device__ __forceinline__ float silu_f(float g) {
+    double x = (double)g;  // cpu.rs:1119-1122: computed in f64, rounded once
+    return (float)(x / (1.0 + exp(-x)));
+}
+
+// ---- ordered argmax (generate.rs:167-173: the last index among equal maxima)
+struct ArgAcc {
+    float v;
+    int i;    // -1: empty
+    int nan;  // largest NaN index seen, -1 if none
+};
+
+__device__ __forceinline__ ArgAcc arg_combine(ArgAcc l, ArgAcc r) {  // l precedes r
+    ArgAcc o;
+    if (l.i < 0)
+        o = r;
+    else if (r.i < 0)
+        o = l;
+    else
+        o = (l.v > r.v) ? l : r;
+    o.nan = max(l.nan, r.nan);
+    return o;
+}
+
+// All 256 threads: ordered reduction of per-thread accumulators (thread t
+// covers an index range preceding thread t+1's).  Result in every thread.
+__device__ inline ArgAcc block_argmax(ArgAcc a, ArgAcc *sh) {
+    const int tid = threadIdx.x;
+    sh[tid] = a;
+    __syncthreads();
+    for (int off = 1; off < TPB; off <<= 1) {
+        ArgAcc mine = sh[tid];
+        ArgAcc other = (tid + off < TPB) ? sh[tid + off] : ArgAcc{0.f, -1, -1};
+        __syncthreads();
+        if ((tid & (2 * off - 1)) == 0) sh[tid] = arg_combine(mine, other);
+        __syncthreads();
+    }
+    ArgAcc r = sh[0];
+    __syncthreads();
+    return r;
+}
+
+// sequential-semantics argmax over x[lo, hi) by the whole block
+__device__ inline ArgAcc block_argmax_range(const float *x, int lo, int hi, ArgAcc *sh) {
+    const int n = hi - lo;
+    const int per = (n + TPB - 1) / TPB;
+    const int b = lo + threadIdx.x * per, e = min(hi, b + per);
+    ArgAcc a{0.f, -1, -1};
+    for (int i = b; i < e; i++) {
+        float v = x[i];
+        if (isnan(v)) {
+            a.nan = i;
+            continue;
+        }
+        if (a.i < 0 || !(a.v > v)) {
+            a.v = v;
+            a.i = i;
+        }
+    }
+    return block_argmax(a, sh);
+}
+
+// Full generate.rs argmax semantics from a reduced accumulator over [0, n):
+// with no NaN it is the last index of the maximum; with NaNs, max_by hands the
+// running best to the element after the last NaN, so the answer is the argmax
+// of the suffix after the last NaN (or that NaN if it is the last element).
+__device__ inline int argmax_finish(ArgAcc r, const float *x, int n, ArgAcc *sh) {
+    if (r.nan < 0) return r.i < 0 ? 0 : r.i;
+    if (r.nan == n - 1) return r.nan;
+    ArgAcc s = block_argmax_range(x, r.nan + 1, n, sh);
+    return s.i;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, size_t bytes) {
+    const int n = bytes > 0x7fffffffu ? 0x7fffffff : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+
+// 16-byte buffer load; offsets at or past the resource size read as zero.
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2));
+}
+__device__ __forceinline__ float4 bload16f(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+
+// LDS float offset of the float4 holding x[p*1024 + 4t .. +3] in the permuted layout
+__device__ __forceinline__ int xslot(int p, int t) { return (p << 10) | ((t & 3) << 8) | ((t >> 2) << 2); }
+
+}  // namespace dev
+}  // namespace scry
