@@ -172,6 +172,50 @@ int launch_argmax(const float *x, int64_t n, int64_t *out, hipStream_t s);
 int launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
 int launch_fill_u32(unsigned int *p, size_t n, unsigned int v, hipStream_t s);
 
+// decode.hip -- persistent decode step (one launch per token, every layer)
+struct DecLayer {
+    const uint8_t *w[4];        // packed qkv, o, fused gate/up, down
+    float scale[5];             // qkv, o, gate, up, down
+    const float *norm_in, *norm_post;
+    float *k_cache, *v_cache;   // [max_seq][kv_dim]
+};
+
+struct DecArgs {
+    const DecLayer *layers;
+    int L, h, qd, kvd, qkv_rows, ffn, V;
+    int n_heads, n_kv, hd, ns;  // ns: attention splits per query head
+    int kp_h, kp_q, kp_f;       // packed row strides for k = h, q_dim, ffn
+    int nch_max, part_cap;      // LDS activation chunks / partial slots per workgroup
+    const uint8_t *w_lm;
+    float s_lm;
+    const float *norm_final;
+    const float *embed;
+    int64_t *tokens;
+    DevState *state;
+    int64_t *argmax_out;
+    int advance;
+    const float2 *rope_cs;
+    float q_scale, eps;
+    float *ws;                  // per-layer activations, ws_stride floats per layer
+    size_t ws_stride;
+    int o_xq, o_xa, o_xo, o_xg, o_xd, o_apo, o_apm;
+    float *logits;
+    float *lm_pv;
+    int *lm_pi, *lm_pn;
+    unsigned *ctr;              // [5L+1][16] stage counters, then [L][n_heads] head counters
+    int *abort_flag;
+    unsigned epoch;             // launches completed on this counter set
+    unsigned spin_limit;
+};
+
+constexpr int DEC_THREADS = 512;
+// Dynamic LDS bytes for a configuration (before the one-workgroup-per-CU floor).
+size_t decode_lds_bytes(int nch_max, int part_cap);
+// Checks that the kernel for this head_dim can run n_wg co-resident workgroups
+// with `lds` bytes each; sets the LDS attribute.
+int decode_prepare(int hd, size_t lds, int n_wg);
+int launch_decode(const DecArgs &a, int n_wg, size_t lds, hipStream_t s);
+
 // init.cpp -- host restatement of LlamaModel::new's random init (threaded)
 void host_normal_vec(uint64_t seed, uint64_t start_call, size_t n, float mean, float stdv,
                      float *out, int threads);

@@ -45,6 +45,7 @@ struct scry_llama_s {
     float *stage = nullptr;  // device f32 staging for one tensor
     size_t stage_n = 0;
     int live_caches = 0;
+    unsigned version = 0;  // bumped whenever a tensor is replaced
     const float *norm_in(int l) const { return norms + (size_t)(2 * l) * h; }
     const float *norm_post(int l) const { return norms + (size_t)(2 * l + 1) * h; }
     const float *norm_final() const { return norms + (size_t)(2 * L) * h; }
@@ -54,6 +55,24 @@ struct HostStage {
     DevState st;
     int64_t tok;
     int64_t amax;
+    int abort;
+};
+
+// Resources of the persistent decode kernel (decode.hip) for one session.
+struct DecodeRes {
+    bool ok = false;        // the configuration runs on the persistent kernel
+    int n_wg = 0;
+    size_t lds = 0;
+    DecArgs args{};
+    DecLayer *layers = nullptr;  // device table
+    unsigned version = ~0u;      // model version the table was built for
+    float *ws = nullptr;
+    unsigned *ctr = nullptr;
+    size_t ctr_n = 0;
+    int *abort_flag = nullptr;
+    float *pv = nullptr;
+    int *pi = nullptr, *pn = nullptr;
+    unsigned epoch = 0;
 };
 
 struct scry_kv_cache_s {
@@ -74,6 +93,7 @@ struct scry_kv_cache_s {
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     HostStage *hs = nullptr;  // pinned
+    DecodeRes dr;
     float *K(int l) const { return kv + (size_t)(2 * l) * max_seq * m->kv_dim; }
     float *Vc(int l) const { return kv + (size_t)(2 * l + 1) * max_seq * m->kv_dim; }
 };
@@ -145,6 +165,7 @@ int upload_stage(scry_llama m, const float *host, size_t n) {
 // Load one tensor (reference layout) into the model.
 int load_tensor(scry_llama m, int id, int layer, const float *host) {
     const int h = m->h, V = m->V, ffn = m->ffn;
+    m->version++;  // scales change: persistent-decode tables are rebuilt
     if (id == SCRY_T_EMBED) {
         SCRY_HIP(hipMemcpyAsync(m->embed, host, sizeof(float) * (size_t)V * h, hipMemcpyHostToDevice,
                                 ctx().stream));
@@ -291,10 +312,19 @@ void cache_free(scry_kv_cache c) {
     dev_free(c->lp_idx);
     dev_free(c->lp_nan);
     dev_free(c->amax);
+    dev_free(c->dr.layers);
+    dev_free(c->dr.ws);
+    dev_free(c->dr.ctr);
+    dev_free(c->dr.abort_flag);
+    dev_free(c->dr.pv);
+    dev_free(c->dr.pi);
+    dev_free(c->dr.pn);
     if (c->hs) (void)hipHostFree(c->hs);
     if (c->m) c->m->live_caches--;
     delete c;
 }
+
+int decode_setup(scry_kv_cache c);
 
 int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
     if (max_seq <= 0) return set_error(SCRY_ERR_INVALID, "max_seq must be > 0");
@@ -342,12 +372,186 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e != hipSuccess) rc = hip_fail(e, "rope table upload", __FILE__, __LINE__);
     }
+    if (!rc) rc = decode_setup(c);
     if (rc) {
         cache_free(c);
         return rc;
     }
     *out = c;
     return SCRY_OK;
+}
+
+// ------------------------------------------------------ persistent decode
+// 0: persistent kernel where the configuration allows it; 1: per-kernel graph
+int g_decode_mode = -1;
+
+int decode_mode() {
+    if (g_decode_mode < 0) {
+        const char *e = std::getenv("SCRY_HIP_DECODE");
+        g_decode_mode = (e && std::strcmp(e, "kernels") == 0) ? 1 : 0;
+    }
+    return g_decode_mode;
+}
+
+int align64(int n) { return (n + 63) / 64 * 64; }
+
+// Device table of per-layer weight pointers and scales (rebuilt when a tensor
+// is replaced, since the per-tensor scales change).
+int decode_tables(scry_kv_cache c) {
+    scry_llama m = c->m;
+    DecodeRes &d = c->dr;
+    std::vector<DecLayer> t(m->L);
+    for (int l = 0; l < m->L; l++) {
+        const auto &Ly = m->layers[l];
+        DecLayer &x = t[l];
+        x.w[0] = Ly.qkv.d;
+        x.w[1] = Ly.o.d;
+        x.w[2] = Ly.gu.d;
+        x.w[3] = Ly.down.d;
+        x.scale[0] = Ly.qkv.scale;
+        x.scale[1] = Ly.o.scale;
+        x.scale[2] = Ly.gu.scale;
+        x.scale[3] = Ly.gu.scale2;
+        x.scale[4] = Ly.down.scale;
+        x.norm_in = m->norm_in(l);
+        x.norm_post = m->norm_post(l);
+        x.k_cache = c->K(l);
+        x.v_cache = c->Vc(l);
+    }
+    SCRY_HIP(hipMemcpyAsync(d.layers, t.data(), sizeof(DecLayer) * t.size(), hipMemcpyHostToDevice,
+                            ctx().stream));
+    SCRY_TRY(sync_stream());
+    d.args.s_lm = m->lm.scale;
+    d.version = m->version;
+    return SCRY_OK;
+}
+
+// Resources for the persistent decode kernel.  Configurations it does not
+// cover (block-32 scales, more heads than CUs, head_dim > 256, an LDS stage
+// that does not fit) keep the per-kernel path: dr.ok stays false.
+int decode_setup(scry_kv_cache c) {
+    scry_llama m = c->m;
+    DecodeRes &d = c->dr;
+    d.ok = false;
+    const int nwg = ctx().cu_count;
+    if (m->quant_mode != SCRY_QUANT_PER_TENSOR || nwg <= 0 || m->nh > nwg || m->hd > 256 ||
+        m->h % 4 || m->ffn % 4 || m->q_dim % 4)
+        return SCRY_OK;
+    const int ns = std::max(1, std::min(16, nwg / m->nh));
+    auto nch = [](int k) { return (k + 1023) / 1024; };
+    auto items = [&](int rows, int k) {
+        const int n_rg = (rows + 3) / 4;
+        return (n_rg + nwg - 1) / nwg * nch(k);
+    };
+    const int part_cap = std::max({items(m->qkv_dim, m->h), items(m->h, m->q_dim), items(2 * m->ffn, m->h),
+                                   items(m->h, m->ffn), items(m->V, m->h), 1});
+    const int nch_max = std::max({nch(m->h), nch(m->q_dim), nch(m->ffn)});
+    const Packed *ps[] = {&m->layers[0].qkv, &m->layers[0].o, &m->layers[0].gu, &m->layers[0].down, &m->lm};
+    for (const Packed *P : ps)
+        if (P->bytes() >= 0x7fffffffull) return SCRY_OK;
+    int max_lds = 0;
+    SCRY_HIP(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, ctx().device));
+    size_t lds = decode_lds_bytes(nch_max, part_cap);
+    if (lds > (size_t)max_lds) return SCRY_OK;
+    // ask for more than half the CU's LDS so no two workgroups share a CU
+    lds = std::max(lds, std::min<size_t>((size_t)max_lds, 96 * 1024));
+    if (decode_prepare(m->hd, lds, nwg) != SCRY_OK) return SCRY_OK;
+    DecArgs &a = d.args;
+    a = DecArgs{};
+    a.L = m->L;
+    a.h = m->h;
+    a.qd = m->q_dim;
+    a.kvd = m->kv_dim;
+    a.qkv_rows = m->qkv_dim;
+    a.ffn = m->ffn;
+    a.V = m->V;
+    a.n_heads = m->nh;
+    a.n_kv = m->nkv;
+    a.hd = m->hd;
+    a.ns = ns;
+    a.kp_h = m->layers[0].qkv.kp;
+    a.kp_q = m->layers[0].o.kp;
+    a.kp_f = m->layers[0].down.kp;
+    a.nch_max = nch_max;
+    a.part_cap = part_cap;
+    a.w_lm = m->lm.d;
+    a.norm_final = m->norm_final();
+    a.embed = m->embed;
+    a.tokens = c->tokens;
+    a.state = c->state;
+    a.argmax_out = c->amax;
+    a.advance = 1;
+    a.rope_cs = c->rope_cs;
+    a.q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
+    a.eps = 1e-5f;  // RMSNorm::new (rmsnorm.rs:17-22)
+    int o = 0;
+    a.o_xq = o; o += align64(m->q_dim);
+    a.o_xa = o; o += align64(m->q_dim);
+    a.o_xo = o; o += align64(m->h);
+    a.o_xg = o; o += align64(m->ffn);
+    a.o_xd = o; o += align64(m->h);
+    a.o_apo = o; o += align64(m->nh * ns * m->hd);
+    a.o_apm = o; o += align64(m->nh * ns * 2);
+    a.ws_stride = (size_t)o;
+    a.logits = c->logits;
+    a.spin_limit = 1u << 21;
+    d.ctr_n = (size_t)(5 * m->L + 1) * 16 + (size_t)m->L * m->nh;
+    hipStream_t s = ctx().stream;
+    SCRY_TRY(dev_alloc((void **)&d.ws, sizeof(float) * a.ws_stride * m->L));
+    SCRY_TRY(launch_fill_f32(d.ws, a.ws_stride * m->L, 0.f, s));
+    SCRY_TRY(dev_alloc((void **)&d.ctr, sizeof(unsigned) * d.ctr_n));
+    SCRY_TRY(launch_fill_u32(d.ctr, d.ctr_n, 0u, s));
+    SCRY_TRY(dev_alloc((void **)&d.abort_flag, sizeof(int)));
+    SCRY_TRY(launch_fill_u32((unsigned *)d.abort_flag, 1, 0u, s));
+    SCRY_TRY(dev_alloc((void **)&d.pv, sizeof(float) * nwg));
+    SCRY_TRY(dev_alloc((void **)&d.pi, sizeof(int) * nwg));
+    SCRY_TRY(dev_alloc((void **)&d.pn, sizeof(int) * nwg));
+    SCRY_TRY(dev_alloc((void **)&d.layers, sizeof(DecLayer) * m->L));
+    a.layers = d.layers;
+    a.ws = d.ws;
+    a.ctr = d.ctr;
+    a.abort_flag = d.abort_flag;
+    a.lm_pv = d.pv;
+    a.lm_pi = d.pi;
+    a.lm_pn = d.pn;
+    d.n_wg = nwg;
+    d.lds = lds;
+    d.epoch = 0;
+    SCRY_TRY(decode_tables(c));
+    d.ok = true;
+    return SCRY_OK;
+}
+
+int decode_launch(scry_kv_cache c) {
+    DecodeRes &d = c->dr;
+    hipStream_t s = ctx().stream;
+    if (d.version != c->m->version) SCRY_TRY(decode_tables(c));
+    if (d.epoch >= (1u << 26)) {  // keep (epoch + 1) * 16 far from wrapping
+        SCRY_TRY(sync_stream());
+        SCRY_TRY(launch_fill_u32(d.ctr, d.ctr_n, 0u, s));
+        d.epoch = 0;
+    }
+    d.args.epoch = d.epoch;
+    SCRY_TRY(launch_decode(d.args, d.n_wg, d.lds, s));
+    d.epoch++;
+    return SCRY_OK;
+}
+
+// After a synchronisation: report (and clear) an aborted persistent launch.
+int decode_check(scry_kv_cache c) {
+    DecodeRes &d = c->dr;
+    if (!d.ok || d.epoch == 0) return SCRY_OK;
+    hipStream_t s = ctx().stream;
+    SCRY_HIP(hipMemcpyAsync(&c->hs->abort, d.abort_flag, sizeof(int), hipMemcpyDeviceToHost, s));
+    SCRY_TRY(sync_stream());
+    if (!c->hs->abort) return SCRY_OK;
+    SCRY_TRY(launch_fill_u32(d.ctr, d.ctr_n, 0u, s));
+    SCRY_TRY(launch_fill_u32((unsigned *)d.abort_flag, 1, 0u, s));
+    SCRY_TRY(sync_stream());
+    d.epoch = 0;
+    return set_error(SCRY_ERR_HIP,
+                     "decode: the persistent kernel timed out waiting for other workgroups "
+                     "(not all co-resident?); results of this call are invalid");
 }
 
 GemvArgs qkv_args(scry_kv_cache c, int l) {
@@ -471,6 +675,7 @@ int record_step(scry_kv_cache c, hipStream_t s) {
 // SCRY_HIP_NO_GRAPH=1 forces direct launches (same kernels), for tools that
 // do not follow graph launches.
 int run_step(scry_kv_cache c) {
+    if (c->dr.ok && decode_mode() == 0) return decode_launch(c);
     hipStream_t s = ctx().stream;
     static const bool no_graph = std::getenv("SCRY_HIP_NO_GRAPH") != nullptr;
     if (no_graph) return record_step(c, s);
@@ -728,6 +933,7 @@ int scry_hip_llama_forward_with_cache(scry_llama m, scry_kv_cache c, int64_t tok
         SCRY_HIP(hipMemcpyAsync(logits, c->logits, sizeof(float) * m->V, hipMemcpyDeviceToHost, s));
     if (argmax_out) SCRY_HIP(hipMemcpyAsync(&c->hs->amax, c->amax, sizeof(int64_t), hipMemcpyDeviceToHost, s));
     SCRY_TRY(sync_stream());
+    SCRY_TRY(decode_check(c));
     if (argmax_out) *argmax_out = c->hs->amax;
     c->seq_len++;
     return SCRY_OK;
@@ -765,9 +971,29 @@ int scry_hip_llama_generate_greedy(scry_llama m, const int64_t *prompt, int n_pr
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e != hipSuccess) rc = hip_fail(e, "token readback", __FILE__, __LINE__);
     }
+    if (!rc) rc = decode_check(c);
     cache_free(c);
     if (rc) return rc;
     *n_out = nout;
+    return SCRY_OK;
+}
+
+int scry_hip_set_decode_mode(int mode) {
+    API_LOCK;
+    if (mode != SCRY_DECODE_AUTO && mode != SCRY_DECODE_KERNELS)
+        return set_error(SCRY_ERR_INVALID, "unknown decode mode %d", mode);
+    g_decode_mode = mode == SCRY_DECODE_AUTO ? 0 : 1;
+    return SCRY_OK;
+}
+
+int scry_hip_decode_mode_active(scry_llama m, int *persistent) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || !persistent) return set_error(SCRY_ERR_INVALID, "null argument");
+    scry_kv_cache c = nullptr;
+    SCRY_TRY(cache_new(m, 16, &c));
+    *persistent = (c->dr.ok && decode_mode() == 0) ? 1 : 0;
+    cache_free(c);
     return SCRY_OK;
 }
 
@@ -791,6 +1017,7 @@ int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_promp
     for (int t = 0; t < n_prompt && !rc; t++) rc = run_step(c);
     for (int t = 0; t < warmup && !rc; t++) rc = run_step(c);
     if (!rc) rc = sync_stream();
+    if (!rc) rc = decode_check(c);
     // rewind to the first decode position; the cache rows and token written
     // there are the same ones the warm-up produced
     if (!rc) rc = set_state(c, n_prompt, n_prompt, n_prompt);
@@ -809,6 +1036,7 @@ int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_promp
         if (e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
         *ms = f;
     }
+    if (!rc) rc = decode_check(c);
     if (!rc && out_tokens) {
         e = hipMemcpyAsync(out_tokens, c->tokens + n_prompt + 1, sizeof(int64_t) * steps,
                            hipMemcpyDeviceToHost, s);

@@ -18,6 +18,14 @@ from ._lib import LlamaConfigC, call, load
 QUANT_PER_TENSOR = 0
 QUANT_BLOCK32 = 1
 T_EMBED, T_QKV, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(7)
+DECODE_AUTO = 0      # persistent decode kernel where the configuration allows it
+DECODE_KERNELS = 1   # captured per-kernel graph
+
+
+def set_decode_mode(mode: int) -> None:
+    """Process-wide choice of the decode-step implementation (both give the
+    same tokens; a backend choice with no counterpart in the reference)."""
+    call("scry_hip_set_decode_mode", mode)
 
 
 @dataclass
@@ -169,6 +177,12 @@ class LlamaModel:
         if want_logits:
             return toks[: n.value], lg.reshape(nout, -1)[: n.value]
         return toks[: n.value]
+
+    def decode_persistent(self) -> bool:
+        """True when this model's decode steps run on the persistent kernel."""
+        v = C.c_int()
+        call("scry_hip_decode_mode_active", self.h, C.byref(v))
+        return bool(v.value)
 
     def bench_decode(self, prompt, warmup: int, steps: int):
         p = np.ascontiguousarray(prompt, dtype=np.int64)

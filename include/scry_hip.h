@@ -202,12 +202,25 @@ int scry_hip_llama_forward_with_cache(scry_llama m, scry_kv_cache c, int64_t tok
 
 /* generate() with temperature 0 (generate.rs:51-89, 92-98): the prompt is fed
  * token by token through the cache path, then greedy tokens follow.  The whole
- * loop runs on the device as replays of one captured decode-step graph; only
- * the token ids come back.  Writes max(1, max_tokens) ids to out_tokens and
+ * loop runs on the device (one persistent-kernel launch, or one replay of the
+ * captured per-kernel graph, per token); only the token ids come back.  Writes max(1, max_tokens) ids to out_tokens and
  * the count to *n_out.  step_logits (optional) receives [n_out, V] logits. */
 int scry_hip_llama_generate_greedy(scry_llama m, const int64_t *prompt, int n_prompt,
                                    int max_tokens, int64_t *out_tokens, int *n_out,
                                    float *step_logits);
+
+/* Decode-step implementation (no counterpart in the reference: a backend
+ * choice).  SCRY_DECODE_AUTO runs each token as one launch of the persistent
+ * decode kernel when the configuration allows it (per-tensor int8 scales,
+ * head_dim <= 256, n_heads <= CU count) and as the captured per-kernel graph
+ * otherwise; SCRY_DECODE_KERNELS always uses the per-kernel graph.  Both give
+ * the same tokens; logits agree to float rounding.  Process-wide; the
+ * environment variable SCRY_HIP_DECODE=kernels selects the latter at start. */
+enum { SCRY_DECODE_AUTO = 0, SCRY_DECODE_KERNELS = 1 };
+int scry_hip_set_decode_mode(int mode);
+/* *persistent = 1 when decode steps of this model run on the persistent kernel
+ * under the current mode. */
+int scry_hip_decode_mode_active(scry_llama m, int *persistent);
 
 /* ------------------------------------------------ measurement helpers */
 /* Decode-step session for benchmarks: binds a model and cache, feeds the
