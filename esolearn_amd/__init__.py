@@ -6,7 +6,7 @@ interface: ``HipBackend`` (backend trait methods), ``LlamaModel`` /
 ``LlamaKvCache`` / ``generate`` (llama.rs, kv_cache.rs, generate.rs).
 """
 from .backend import HipBackend, I8Storage, Storage, init  # noqa: F401
-from .llama import (DECODE_AUTO, DECODE_KERNELS, QUANT_BLOCK32, QUANT_PER_TENSOR,  # noqa: F401
+from .llama import (DECODE_KERNELS, DECODE_PERSISTENT, QUANT_BLOCK32, QUANT_PER_TENSOR,  # noqa: F401
                     LlamaConfig, LlamaKvCache, LlamaModel, SamplingConfig, bench_qgemv, generate,
                     set_decode_mode)
 from ._lib import ScryHipError  # noqa: F401

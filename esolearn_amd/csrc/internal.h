@@ -186,6 +186,7 @@ struct DecArgs {
     int n_heads, n_kv, hd, ns;  // ns: attention splits per query head
     int kp_h, kp_q, kp_f;       // packed row strides for k = h, q_dim, ffn
     int nch_max, part_cap;      // LDS activation chunks / partial slots per workgroup
+    int qkv_pairs;              // LDS RoPE slots: qkv row pairs per workgroup (multiple of 8)
     const uint8_t *w_lm;
     float s_lm;
     const float *norm_final;
@@ -196,21 +197,29 @@ struct DecArgs {
     int advance;
     const float2 *rope_cs;
     float q_scale, eps;
-    float *ws;                  // per-layer activations, ws_stride floats per layer
+    // Activations exchanged between workgroups (floats): per layer ws_stride
+    // floats at these offsets.
+    float *ws;
     size_t ws_stride;
-    int o_xq, o_xa, o_xo, o_xg, o_xd, o_apo, o_apm;
+    int o_xq, o_xk, o_xv, o_xa, o_xo, o_xg, o_xd, o_apo, o_apm;
+    // Attention split partials: O at o_apo + head*apo_hs + split*hd, (M, L) at
+    // o_apm + head*64 + 2*split.  Each head's block starts on its own 256-byte
+    // boundary: a head's merge reads its block once its splits are published,
+    // and an L2 line read early must not hold another head's later writes.
+    int apo_hs;
+    unsigned *lm_part;          // [n_wg][8] LM-head argmax partials
     float *logits;
-    float *lm_pv;
-    int *lm_pi, *lm_pn;
-    unsigned *ctr;              // [5L+1][16] stage counters, then [L][n_heads] head counters
+    // Completion counters: [5L+1][8] per (stage, XCD), then [L][n_heads] per
+    // head; after launch number `tag` they hold tag x (workgroups counted).
+    unsigned *ctr;
     int *abort_flag;
-    unsigned epoch;             // launches completed on this counter set
+    unsigned tag;               // this launch's number (1, 2, ...)
     unsigned spin_limit;
 };
 
 constexpr int DEC_THREADS = 512;
 // Dynamic LDS bytes for a configuration (before the one-workgroup-per-CU floor).
-size_t decode_lds_bytes(int nch_max, int part_cap);
+size_t decode_lds_bytes(int nch_max, int part_cap, int h, int qkv_pairs);
 // Checks that the kernel for this head_dim can run n_wg co-resident workgroups
 // with `lds` bytes each; sets the LDS attribute.
 int decode_prepare(int hd, size_t lds, int n_wg);

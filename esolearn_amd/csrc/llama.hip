@@ -58,21 +58,62 @@ struct HostStage {
     int abort;
 };
 
+// Uncached device memory for the data the persistent decode kernel's
+// workgroups exchange (activations, partials, counters): a store that has
+// completed is then in memory, so no cache write-back orders it.  Blocks are
+// never returned to the runtime (memory of this kind that a kernel has read
+// must not be freed while the process runs): a released block goes to a pool
+// that later sessions reuse.
+struct UcBlock {
+    void *p;
+    size_t bytes;
+};
+std::vector<UcBlock> &uc_pool() {
+    static std::vector<UcBlock> pool;
+    return pool;
+}
+
+int uc_take(size_t bytes, UcBlock *out) {
+    auto &pool = uc_pool();
+    size_t best = pool.size();
+    for (size_t i = 0; i < pool.size(); i++)
+        if (pool[i].bytes >= bytes && (best == pool.size() || pool[i].bytes < pool[best].bytes)) best = i;
+    if (best < pool.size()) {
+        *out = pool[best];
+        pool.erase(pool.begin() + (long)best);
+        return SCRY_OK;
+    }
+    void *p = nullptr;
+    const hipError_t e = hipExtMallocWithFlags(&p, bytes, hipDeviceMallocUncached);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(SCRY_ERR_OOM, "uncached allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+    }
+    *out = UcBlock{p, bytes};
+    return SCRY_OK;
+}
+
+void uc_give(UcBlock &b) {
+    if (b.p) uc_pool().push_back(b);
+    b = UcBlock{nullptr, 0};
+}
+
 // Resources of the persistent decode kernel (decode.hip) for one session.
 struct DecodeRes {
+    bool tried = false;     // decode_setup has run
     bool ok = false;        // the configuration runs on the persistent kernel
     int n_wg = 0;
     size_t lds = 0;
     DecArgs args{};
     DecLayer *layers = nullptr;  // device table
     unsigned version = ~0u;      // model version the table was built for
-    float *ws = nullptr;
-    unsigned *ctr = nullptr;
+    UcBlock uc{nullptr, 0};      // holds the four buffers below
+    float *ws = nullptr;         // activations exchanged between workgroups
+    unsigned *lm_part = nullptr; // LM-head argmax partials
+    unsigned *ctr = nullptr;     // completion counters
     size_t ctr_n = 0;
     int *abort_flag = nullptr;
-    float *pv = nullptr;
-    int *pi = nullptr, *pn = nullptr;
-    unsigned epoch = 0;
+    unsigned launches = 0;       // launches since the counters were zeroed
 };
 
 struct scry_kv_cache_s {
@@ -313,12 +354,7 @@ void cache_free(scry_kv_cache c) {
     dev_free(c->lp_nan);
     dev_free(c->amax);
     dev_free(c->dr.layers);
-    dev_free(c->dr.ws);
-    dev_free(c->dr.ctr);
-    dev_free(c->dr.abort_flag);
-    dev_free(c->dr.pv);
-    dev_free(c->dr.pi);
-    dev_free(c->dr.pn);
+    uc_give(c->dr.uc);
     if (c->hs) (void)hipHostFree(c->hs);
     if (c->m) c->m->live_caches--;
     delete c;
@@ -372,7 +408,6 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e != hipSuccess) rc = hip_fail(e, "rope table upload", __FILE__, __LINE__);
     }
-    if (!rc) rc = decode_setup(c);
     if (rc) {
         cache_free(c);
         return rc;
@@ -382,13 +417,13 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
 }
 
 // ------------------------------------------------------ persistent decode
-// 0: persistent kernel where the configuration allows it; 1: per-kernel graph
+// SCRY_DECODE_KERNELS (default) or SCRY_DECODE_PERSISTENT
 int g_decode_mode = -1;
 
 int decode_mode() {
     if (g_decode_mode < 0) {
         const char *e = std::getenv("SCRY_HIP_DECODE");
-        g_decode_mode = (e && std::strcmp(e, "kernels") == 0) ? 1 : 0;
+        g_decode_mode = (e && std::strcmp(e, "persistent") == 0) ? SCRY_DECODE_PERSISTENT : SCRY_DECODE_KERNELS;
     }
     return g_decode_mode;
 }
@@ -427,15 +462,16 @@ int decode_tables(scry_kv_cache c) {
 }
 
 // Resources for the persistent decode kernel.  Configurations it does not
-// cover (block-32 scales, more heads than CUs, head_dim > 256, an LDS stage
-// that does not fit) keep the per-kernel path: dr.ok stays false.
+// cover (block-32 scales, more heads than CUs, head_dim > 256, hidden size
+// > 4096, an LDS stage that does not fit) keep the per-kernel path: dr.ok
+// stays false.
 int decode_setup(scry_kv_cache c) {
     scry_llama m = c->m;
     DecodeRes &d = c->dr;
     d.ok = false;
     const int nwg = ctx().cu_count;
-    if (m->quant_mode != SCRY_QUANT_PER_TENSOR || nwg <= 0 || m->nh > nwg || m->hd > 256 ||
-        m->h % 4 || m->ffn % 4 || m->q_dim % 4)
+    if (m->quant_mode != SCRY_QUANT_PER_TENSOR || nwg <= 0 || nwg > 256 || m->nh > nwg || m->hd > 256 ||
+        m->h > 4096 || m->h % 4 || m->ffn % 4 || m->q_dim % 4)
         return SCRY_OK;
     const int ns = std::max(1, std::min(16, nwg / m->nh));
     auto nch = [](int k) { return (k + 1023) / 1024; };
@@ -451,10 +487,11 @@ int decode_setup(scry_kv_cache c) {
         if (P->bytes() >= 0x7fffffffull) return SCRY_OK;
     int max_lds = 0;
     SCRY_HIP(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, ctx().device));
-    size_t lds = decode_lds_bytes(nch_max, part_cap);
-    if (lds > (size_t)max_lds) return SCRY_OK;
+    const int qkv_pairs = (((m->qkv_dim + 3) / 4 + nwg - 1) / nwg * 2 + 7) / 8 * 8;
+    size_t lds = decode_lds_bytes(nch_max, part_cap, m->h, qkv_pairs);
+    if (lds + 1024 > (size_t)max_lds) return SCRY_OK;
     // ask for more than half the CU's LDS so no two workgroups share a CU
-    lds = std::max(lds, std::min<size_t>((size_t)max_lds, 96 * 1024));
+    lds = std::max(lds, std::min<size_t>((size_t)max_lds - 1024, 96 * 1024));
     if (decode_prepare(m->hd, lds, nwg) != SCRY_OK) return SCRY_OK;
     DecArgs &a = d.args;
     a = DecArgs{};
@@ -474,6 +511,7 @@ int decode_setup(scry_kv_cache c) {
     a.kp_f = m->layers[0].down.kp;
     a.nch_max = nch_max;
     a.part_cap = part_cap;
+    a.qkv_pairs = qkv_pairs;
     a.w_lm = m->lm.d;
     a.norm_final = m->norm_final();
     a.embed = m->embed;
@@ -484,39 +522,44 @@ int decode_setup(scry_kv_cache c) {
     a.rope_cs = c->rope_cs;
     a.q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
     a.eps = 1e-5f;  // RMSNorm::new (rmsnorm.rs:17-22)
+    // per-layer offsets (floats), 64-float aligned
     int o = 0;
     a.o_xq = o; o += align64(m->q_dim);
+    a.o_xk = o; o += align64(m->kv_dim);
+    a.o_xv = o; o += align64(m->kv_dim);
     a.o_xa = o; o += align64(m->q_dim);
     a.o_xo = o; o += align64(m->h);
     a.o_xg = o; o += align64(m->ffn);
     a.o_xd = o; o += align64(m->h);
-    a.o_apo = o; o += align64(m->nh * ns * m->hd);
-    a.o_apm = o; o += align64(m->nh * ns * 2);
+    a.apo_hs = align64(ns * m->hd);
+    a.o_apo = o; o += m->nh * a.apo_hs;
+    a.o_apm = o; o += m->nh * 64;  // ns <= 16: 2*ns <= 32 floats per head
     a.ws_stride = (size_t)o;
     a.logits = c->logits;
     a.spin_limit = 1u << 21;
-    d.ctr_n = (size_t)(5 * m->L + 1) * 16 + (size_t)m->L * m->nh;
+    d.ctr_n = (size_t)(5 * m->L + 1) * 8 + (size_t)m->L * m->nh;
     hipStream_t s = ctx().stream;
-    SCRY_TRY(dev_alloc((void **)&d.ws, sizeof(float) * a.ws_stride * m->L));
+    auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t b_ws = al(sizeof(float) * a.ws_stride * m->L), b_lm = al(sizeof(unsigned) * 8 * nwg),
+                 b_ctr = al(sizeof(unsigned) * d.ctr_n);
+    SCRY_TRY(uc_take(b_ws + b_lm + b_ctr + 256, &d.uc));
+    char *base = (char *)d.uc.p;
+    d.ws = (float *)base;
+    d.lm_part = (unsigned *)(base + b_ws);
+    d.ctr = (unsigned *)(base + b_ws + b_lm);
+    d.abort_flag = (int *)(base + b_ws + b_lm + b_ctr);
     SCRY_TRY(launch_fill_f32(d.ws, a.ws_stride * m->L, 0.f, s));
-    SCRY_TRY(dev_alloc((void **)&d.ctr, sizeof(unsigned) * d.ctr_n));
     SCRY_TRY(launch_fill_u32(d.ctr, d.ctr_n, 0u, s));
-    SCRY_TRY(dev_alloc((void **)&d.abort_flag, sizeof(int)));
     SCRY_TRY(launch_fill_u32((unsigned *)d.abort_flag, 1, 0u, s));
-    SCRY_TRY(dev_alloc((void **)&d.pv, sizeof(float) * nwg));
-    SCRY_TRY(dev_alloc((void **)&d.pi, sizeof(int) * nwg));
-    SCRY_TRY(dev_alloc((void **)&d.pn, sizeof(int) * nwg));
     SCRY_TRY(dev_alloc((void **)&d.layers, sizeof(DecLayer) * m->L));
     a.layers = d.layers;
     a.ws = d.ws;
+    a.lm_part = d.lm_part;
     a.ctr = d.ctr;
     a.abort_flag = d.abort_flag;
-    a.lm_pv = d.pv;
-    a.lm_pi = d.pi;
-    a.lm_pn = d.pn;
     d.n_wg = nwg;
     d.lds = lds;
-    d.epoch = 0;
+    d.launches = 0;
     SCRY_TRY(decode_tables(c));
     d.ok = true;
     return SCRY_OK;
@@ -526,32 +569,45 @@ int decode_launch(scry_kv_cache c) {
     DecodeRes &d = c->dr;
     hipStream_t s = ctx().stream;
     if (d.version != c->m->version) SCRY_TRY(decode_tables(c));
-    if (d.epoch >= (1u << 26)) {  // keep (epoch + 1) * 16 far from wrapping
+    if (d.launches >= (1u << 26)) {  // keep launch x 256 far from wrapping
         SCRY_TRY(sync_stream());
         SCRY_TRY(launch_fill_u32(d.ctr, d.ctr_n, 0u, s));
-        d.epoch = 0;
+        d.launches = 0;
     }
-    d.args.epoch = d.epoch;
-    SCRY_TRY(launch_decode(d.args, d.n_wg, d.lds, s));
-    d.epoch++;
-    return SCRY_OK;
+    d.args.tag = ++d.launches;
+    return launch_decode(d.args, d.n_wg, d.lds, s);
 }
 
 // After a synchronisation: report (and clear) an aborted persistent launch.
 int decode_check(scry_kv_cache c) {
     DecodeRes &d = c->dr;
-    if (!d.ok || d.epoch == 0) return SCRY_OK;
+    if (!d.ok || d.launches == 0) return SCRY_OK;
     hipStream_t s = ctx().stream;
     SCRY_HIP(hipMemcpyAsync(&c->hs->abort, d.abort_flag, sizeof(int), hipMemcpyDeviceToHost, s));
     SCRY_TRY(sync_stream());
     if (!c->hs->abort) return SCRY_OK;
+    // an aborted launch leaves counters part-way: restart them from zero
     SCRY_TRY(launch_fill_u32(d.ctr, d.ctr_n, 0u, s));
     SCRY_TRY(launch_fill_u32((unsigned *)d.abort_flag, 1, 0u, s));
     SCRY_TRY(sync_stream());
-    d.epoch = 0;
+    d.launches = 0;
     return set_error(SCRY_ERR_HIP,
                      "decode: the persistent kernel timed out waiting for other workgroups "
                      "(not all co-resident?); results of this call are invalid");
+}
+
+// Whether this session's decode steps run on the persistent kernel: the mode
+// asks for it and the configuration allows it.  Its resources are set up on
+// first use.
+int decode_use_persistent(scry_kv_cache c, bool *use) {
+    *use = false;
+    if (decode_mode() != SCRY_DECODE_PERSISTENT) return SCRY_OK;
+    if (!c->dr.tried) {
+        c->dr.tried = true;
+        SCRY_TRY(decode_setup(c));
+    }
+    *use = c->dr.ok;
+    return SCRY_OK;
 }
 
 GemvArgs qkv_args(scry_kv_cache c, int l) {
@@ -675,7 +731,9 @@ int record_step(scry_kv_cache c, hipStream_t s) {
 // SCRY_HIP_NO_GRAPH=1 forces direct launches (same kernels), for tools that
 // do not follow graph launches.
 int run_step(scry_kv_cache c) {
-    if (c->dr.ok && decode_mode() == 0) return decode_launch(c);
+    bool persistent = false;
+    SCRY_TRY(decode_use_persistent(c, &persistent));
+    if (persistent) return decode_launch(c);
     hipStream_t s = ctx().stream;
     static const bool no_graph = std::getenv("SCRY_HIP_NO_GRAPH") != nullptr;
     if (no_graph) return record_step(c, s);
@@ -980,9 +1038,9 @@ int scry_hip_llama_generate_greedy(scry_llama m, const int64_t *prompt, int n_pr
 
 int scry_hip_set_decode_mode(int mode) {
     API_LOCK;
-    if (mode != SCRY_DECODE_AUTO && mode != SCRY_DECODE_KERNELS)
+    if (mode != SCRY_DECODE_KERNELS && mode != SCRY_DECODE_PERSISTENT)
         return set_error(SCRY_ERR_INVALID, "unknown decode mode %d", mode);
-    g_decode_mode = mode == SCRY_DECODE_AUTO ? 0 : 1;
+    g_decode_mode = mode;
     return SCRY_OK;
 }
 
@@ -992,9 +1050,11 @@ int scry_hip_decode_mode_active(scry_llama m, int *persistent) {
     if (!m || !persistent) return set_error(SCRY_ERR_INVALID, "null argument");
     scry_kv_cache c = nullptr;
     SCRY_TRY(cache_new(m, 16, &c));
-    *persistent = (c->dr.ok && decode_mode() == 0) ? 1 : 0;
+    bool p = false;
+    const int rc = decode_use_persistent(c, &p);
     cache_free(c);
-    return SCRY_OK;
+    *persistent = p ? 1 : 0;
+    return rc;
 }
 
 // ------------------------------------------------------------ measurement

@@ -18,8 +18,8 @@ from ._lib import LlamaConfigC, call, load
 QUANT_PER_TENSOR = 0
 QUANT_BLOCK32 = 1
 T_EMBED, T_QKV, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(7)
-DECODE_AUTO = 0      # persistent decode kernel where the configuration allows it
-DECODE_KERNELS = 1   # captured per-kernel graph
+DECODE_KERNELS = 0     # captured per-kernel graph (default)
+DECODE_PERSISTENT = 1  # persistent decode kernel where the configuration allows it
 
 
 def set_decode_mode(mode: int) -> None:

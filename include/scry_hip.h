@@ -210,13 +210,14 @@ int scry_hip_llama_generate_greedy(scry_llama m, const int64_t *prompt, int n_pr
                                    float *step_logits);
 
 /* Decode-step implementation (no counterpart in the reference: a backend
- * choice).  SCRY_DECODE_AUTO runs each token as one launch of the persistent
- * decode kernel when the configuration allows it (per-tensor int8 scales,
- * head_dim <= 256, n_heads <= CU count) and as the captured per-kernel graph
- * otherwise; SCRY_DECODE_KERNELS always uses the per-kernel graph.  Both give
- * the same tokens; logits agree to float rounding.  Process-wide; the
- * environment variable SCRY_HIP_DECODE=kernels selects the latter at start. */
-enum { SCRY_DECODE_AUTO = 0, SCRY_DECODE_KERNELS = 1 };
+ * choice).  SCRY_DECODE_KERNELS (the default) runs each token as one replay of
+ * the captured per-kernel graph.  SCRY_DECODE_PERSISTENT runs each token as
+ * one launch of the persistent decode kernel where the configuration allows it
+ * (per-tensor int8 scales, head_dim <= 256, n_heads <= CU count) and as the
+ * per-kernel graph otherwise.  Both give the same tokens; logits agree to
+ * float rounding.  Process-wide; the environment variable
+ * SCRY_HIP_DECODE=persistent selects the persistent kernel at start. */
+enum { SCRY_DECODE_KERNELS = 0, SCRY_DECODE_PERSISTENT = 1 };
 int scry_hip_set_decode_mode(int mode);
 /* *persistent = 1 when decode steps of this model run on the persistent kernel
  * under the current mode. */

@@ -26,25 +26,29 @@ def rel_err(g, c):
 
 def run_both(hip, hm, prompt, n):
     """(tokens, logits) from the persistent kernel and from the per-kernel graph."""
-    hip.set_decode_mode(hip.DECODE_AUTO)
-    assert hm.decode_persistent()
+    hip.set_decode_mode(hip.DECODE_PERSISTENT)
     try:
+        assert hm.decode_persistent()
         p = hm.generate_greedy(prompt, n, want_logits=True)
-        hip.set_decode_mode(hip.DECODE_KERNELS)
-        assert not hm.decode_persistent()
-        k = hm.generate_greedy(prompt, n, want_logits=True)
     finally:
-        hip.set_decode_mode(hip.DECODE_AUTO)
+        hip.set_decode_mode(hip.DECODE_KERNELS)
+    assert not hm.decode_persistent()
+    k = hm.generate_greedy(prompt, n, want_logits=True)
     return p, k
 
 
 def test_path_selection(hip):
     cfg = hip.LlamaConfig(**{**TINY, "n_layers": 1})
     m = hip.LlamaModel.new_random(cfg, 0)
-    assert m.decode_persistent()
-    m.free()
-    m = hip.LlamaModel.new_random(cfg, 0, hip.QUANT_BLOCK32)
-    assert not m.decode_persistent()  # block-32 scales: per-kernel graph
+    assert not m.decode_persistent()  # default: per-kernel graph
+    hip.set_decode_mode(hip.DECODE_PERSISTENT)
+    try:
+        assert m.decode_persistent()
+        b = hip.LlamaModel.new_random(cfg, 0, hip.QUANT_BLOCK32)
+        assert not b.decode_persistent()  # block-32 scales: per-kernel graph
+        b.free()
+    finally:
+        hip.set_decode_mode(hip.DECODE_KERNELS)
     m.free()
 
 
@@ -63,7 +67,11 @@ def test_tiny_paths_agree_with_oracle(orc, hip):
     assert ep < LOGIT_TOL and ek < LOGIT_TOL and epk < PATH_TOL
     assert (pt == ref_t).all() and (kt == ref_t).all()
     # deterministic: a second persistent run reproduces the logits bit for bit
-    pt2, pl2 = hm.generate_greedy(prompt, 64, want_logits=True)
+    hip.set_decode_mode(hip.DECODE_PERSISTENT)
+    try:
+        pt2, pl2 = hm.generate_greedy(prompt, 64, want_logits=True)
+    finally:
+        hip.set_decode_mode(hip.DECODE_KERNELS)
     assert (pt2 == pt).all() and np.array_equal(pl2, pl)
     hm.free()
     om.close()
