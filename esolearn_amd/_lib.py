@@ -88,6 +88,10 @@ SIGNATURES = {
     "scry_hip_kv_cache_layer_to_vec": [vp, i32, vp, vp, sz],
     "scry_hip_llama_forward_with_cache": [vp, vp, i64, i32, vp, P(i64)],
     "scry_hip_llama_generate_greedy": [vp, vp, i32, i32, vp, P(i32), vp],
+    "scry_hip_llama_generate_greedy_prefill": [vp, vp, i32, i32, vp, P(i32), vp],
+    "scry_hip_llama_forward": [vp, vp, i32, vp],
+    "scry_hip_llama_prefill": [vp, vp, i32, vp, i32, vp],
+    "scry_hip_llama_bench_prefill": [vp, vp, i32, i32, i32, vp, P(f64), P(f64)],
     "scry_hip_set_decode_mode": [i32],
     "scry_hip_decode_mode_active": [vp, P(i32)],
     "scry_hip_llama_bench_decode": [vp, vp, i32, i32, i32, vp, P(f64)],

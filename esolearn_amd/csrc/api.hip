@@ -132,15 +132,37 @@ int qmatmul(scry_buf a, scry_i8buf bq, float scale, const float *scales32, const
     w.scale = scale;
     w.s32 = const_cast<float *>(scales32);
     w.nb = (k + 31) / 32;
-    GemvArgs g;
-    g.w = &w;
-    g.x = a->d;
-    g.ldx = k;
-    g.m = m;
-    g.y = o->d;
-    g.ldy = n;
-    g.bias = bias;
-    int rc = launch_qgemv(EPI_STORE, g, ctx().stream);
+    int rc;
+    if (m <= GEMV_MAX_M) {
+        GemvArgs g;
+        g.w = &w;
+        g.x = a->d;
+        g.ldx = k;
+        g.m = m;
+        g.y = o->d;
+        g.ldy = n;
+        g.bias = bias;
+        rc = launch_qgemv(EPI_STORE, g, ctx().stream);
+    } else {
+        // prefill shapes: the activations as bf16 planes, then the MFMA GEMM
+        const int mp = prefill_rows_pad(m), ld = round_up(k, 32);
+        unsigned short *pl = nullptr;
+        rc = dev_alloc((void **)&pl, sizeof(unsigned short) * 2 * (size_t)mp * ld);
+        if (!rc) rc = launch_fill_u32((unsigned *)pl, (size_t)mp * ld, 0u, ctx().stream);  // 2 planes of u16
+        if (!rc) rc = launch_split(a->d, k, m, k, pl, pl + (size_t)mp * ld, ld, ctx().stream);
+        PrefillGemm g;
+        g.w = &w;
+        g.ahi = pl;
+        g.alo = pl + (size_t)mp * ld;
+        g.lda = ld;
+        g.M = m;
+        g.c = o->d;
+        g.ldc = n;
+        g.bias = bias;
+        if (!rc) rc = launch_gemm(PF_STORE, g, ctx().stream);
+        if (!rc) rc = sync();  // the planes are freed below
+        dev_free(pl);
+    }
     if (rc) {
         del_buf(o);
         return rc;

@@ -137,6 +137,8 @@ struct GemvArgs {
 };
 
 int launch_qgemv(int epi, const GemvArgs &a, hipStream_t s);
+// matmul_i8_f32 with more activation rows than this runs as the MFMA GEMM
+constexpr int GEMV_MAX_M = 16;
 int launch_logits_finish(const GemvArgs &a, hipStream_t s);
 
 // attn.hip
@@ -224,6 +226,42 @@ size_t decode_lds_bytes(int nch_max, int part_cap, int h, int qkv_pairs);
 // with `lds` bytes each; sets the LDS attribute.
 int decode_prepare(int hd, size_t lds, int n_wg);
 int launch_decode(const DecArgs &a, int n_wg, size_t lds, hipStream_t s);
+
+// prefill.hip -- batched prefill (GEMMs on the matrix cores)
+constexpr int PF_MAX_SEQS = 16;
+struct PrefillSeqs {  // per sequence: its KV cache and first position
+    float *k[PF_MAX_SEQS], *v[PF_MAX_SEQS];  // layer-0 K / V rows [max_seq][kv_dim]
+    size_t ls[PF_MAX_SEQS];                  // floats from one layer's K (V) to the next
+    const float2 *rope[PF_MAX_SEQS];         // (cos, sin) [max_seq][hd/2]
+    int p0[PF_MAX_SEQS];
+};
+struct PrefillGemm {
+    const Packed *w = nullptr;
+    const unsigned short *ahi = nullptr, *alo = nullptr;  // bf16 planes [Mp][lda]
+    int lda = 0, M = 0;
+    float *c = nullptr;  // PF_STORE / PF_RESID output [M][ldc]
+    int ldc = 0;
+    const float *bias = nullptr;  // PF_STORE: + bias[n]
+    unsigned short *ohi = nullptr, *olo = nullptr;  // GE_SWIGLU output planes
+    int ldo = 0, opad = 0;
+};
+struct PrefillAttn {
+    const float *qkv = nullptr;  // rows [M][ldq], q part RoPE'd
+    int ldq = 0, seq = 0, hd = 0, nh = 0, nkv = 0, kvd = 0;
+    float scale = 1.f;
+    unsigned short *ohi = nullptr, *olo = nullptr;  // o_proj input planes
+    int ldo = 0, opad = 0;
+};
+enum { PF_STORE = 0, PF_RESID = 1, PF_SWIGLU = 2 };
+int prefill_rows_pad(int M);
+int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, const float *w, int k, float eps,
+                      unsigned short *hi, unsigned short *lo, int ldp, float *outf, int ldf, hipStream_t s);
+int launch_split(const float *x, int ldx, int rows, int k, unsigned short *hi, unsigned short *lo, int ldp,
+                 hipStream_t s);
+int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s);
+int launch_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, const PrefillSeqs &t, int l,
+                   hipStream_t s);
+int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hipStream_t s);
 
 // init.cpp -- host restatement of LlamaModel::new's random init (threaded)
 void host_normal_vec(uint64_t seed, uint64_t start_call, size_t n, float mean, float stdv,

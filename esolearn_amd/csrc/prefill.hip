@@ -1,0 +1,537 @@
+// Batched prefill for gfx950: LlamaModel::forward (llama.rs:683-700) with its
+// attention (llama.rs:162-266), run over n_seq sequences of seq tokens at once
+// so every projection is one GEMM on the matrix cores.  The K/V rows of the
+// processed positions are appended to each sequence's KV cache, so decode can
+// continue from them.
+//
+// GEMM numerics.  The int8 weights are exact in bf16.  Each f32 activation x
+// is held as two bf16 values hi = bf16(x) and lo = bf16(x - hi), so
+// |x - hi - lo| <= 2^-17 |x|, and two bf16 MFMAs (hi x W, then lo x W)
+// accumulate in f32.  The products are exact, so the result is the
+// f32-accumulated dot product of x (to 2^-17) with the int8 weights, scaled
+// once per output (per-tensor) or once per 32-wide k block (block-32).  The
+// reference accumulates f64(a) * f64(q * scale) into f32 in k order
+// (cpu.rs:1128-1160): the differences are summation order and the 2^-17 split,
+// far inside the 1e-3 logit bar.
+//
+// Data layout.  GEMM inputs are two bf16 planes [Mp][ld] (hi, lo): Mp = rows
+// rounded up to the M tile, ld = k rounded up to 32; the columns past k and
+// the rows past M are zero.  The kernel that produces an activation writes
+// its planes directly (RMSNorm, attention, SwiGLU), so no f32 copy of a GEMM
+// input exists.  Weights are the GEMV stream layout (one row of kp bytes per
+// output, byte = q + 128); the GEMM converts them to bf16 while staging.
+#include <cmath>
+
+#include "internal.h"
+#include "kdev.h"
+
+namespace scry {
+namespace {
+
+using namespace dev;
+
+typedef unsigned short u16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define PF_LAUNCH_CHECK() SCRY_HIP(hipGetLastError()); return SCRY_OK
+
+// bf16 with round-to-nearest-even (NaN stays NaN)
+__device__ __forceinline__ u16 bf16_rn(float f) {
+    unsigned b = __float_as_uint(f);
+    if ((b & 0x7f800000u) == 0x7f800000u) return (u16)((b >> 16) | ((b & 0xffffu) ? 0x40u : 0u));
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return (u16)(b >> 16);
+}
+__device__ __forceinline__ float bf16_f(u16 h) { return __uint_as_float((unsigned)h << 16); }
+__device__ __forceinline__ void split_bf16(float x, u16 &hi, u16 &lo) {
+    hi = bf16_rn(x);
+    lo = bf16_rn(x - bf16_f(hi));
+}
+
+// ------------------------------------------------------------------ RMSNorm
+// cpu.rs:574-599 on the rows r*rstep + roff of x: rstd = 1/sqrt(mean(x^2)+eps)
+// in f64, out = f32(x * rstd * w).  Writes the bf16 planes of row r (columns
+// [k, ld) zeroed) and/or an f32 copy.
+__global__ __launch_bounds__(256) void k_norm_split(const float *__restrict__ x, int ldx, int rstep, int roff,
+                                                    const float *__restrict__ w, int k, float eps, u16 *hi,
+                                                    u16 *lo, int ldp, int kpad, float *outf, int ldf) {
+    __shared__ double red[4];
+    const int r = blockIdx.x;
+    const float *src = x + ((size_t)r * rstep + roff) * ldx;
+    double ss = 0.0;
+    for (int j = threadIdx.x; j < k; j += 256) ss += (double)src[j] * (double)src[j];
+    const double rstd = 1.0 / sqrt(block_sum_d(ss, red) / (double)k + (double)eps);
+    for (int j = threadIdx.x; j < kpad; j += 256) {
+        const float v = j < k ? (float)((double)src[j] * rstd * (double)w[j]) : 0.f;
+        if (hi) {
+            u16 a, b;
+            split_bf16(v, a, b);
+            hi[(size_t)r * ldp + j] = a;
+            lo[(size_t)r * ldp + j] = b;
+        }
+        if (outf && j < k) outf[(size_t)r * ldf + j] = v;
+    }
+}
+
+// f32 rows -> bf16 planes (columns [k, kpad) zeroed)
+__global__ void k_split(const float *__restrict__ x, int ldx, int rows, int k, int kpad, u16 *hi, u16 *lo, int ldp) {
+    const size_t total = (size_t)rows * kpad;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(g / kpad), j = (int)(g % kpad);
+        u16 a = 0, b = 0;
+        if (j < k) split_bf16(x[(size_t)r * ldx + j], a, b);
+        hi[(size_t)r * ldp + j] = a;
+        lo[(size_t)r * ldp + j] = b;
+    }
+}
+
+// ------------------------------------------------------------------ GEMM
+// C[m][n] = sum_k (hi + lo)[m][k] * q[n][k], q the int8 weight of output n.
+// Workgroup tile BM x BN, k step BK; 4 waves in 2 x 2, each 64 x 128 as 4 x 8
+// tiles of v_mfma_f32_16x16x32_bf16.  Operand lane layouts of that
+// instruction (16 x 32 A, 32 x 16 B, 16 x 16 D): lane l holds
+// A[l % 16][8 (l / 16) + e] and B[8 (l / 16) + e][l % 16] for e = 0..7, and
+// D[4 (l / 16) + r][l % 16] for r = 0..3.
+constexpr int BM = 128, BN = 256, BK = 32;
+constexpr int LDT = 40;  // LDS row stride in bf16 (80 B): 16-byte row reads hit distinct banks
+constexpr int G_THREADS = 256;
+constexpr size_t A_TILE = (size_t)BM * LDT, B_TILE = (size_t)BN * LDT;  // u16 elements
+// dynamic LDS: [2 buffers] x (A hi, A lo, B) + [2][BN] block-32 scales
+constexpr size_t GEMM_LDS = 2 * (2 * A_TILE + B_TILE) * sizeof(u16) + 2 * BN * sizeof(float);
+
+enum { GE_STORE = PF_STORE, GE_RESID = PF_RESID, GE_SWIGLU = PF_SWIGLU };
+
+struct GemmP {
+    const u16 *ahi, *alo;
+    int lda;
+    const uint8_t *w;
+    int kp, N;
+    const float *s32;  // block-32 scales [N][nb] (packed-row order) or null
+    int nb;
+    int M, nk;         // rows, k steps (k rounded up to 32, / 32)
+    int n_mb, n_nb;    // tiles along M and N
+    int n_super;       // super-tiles (4 M tiles x 8 N tiles)
+    float scale, scale2;
+    const float *bias;  // GE_STORE: + bias[n] (f32, after scaling)
+    float *c;
+    int ldc;
+    u16 *ohi, *olo;
+    int ldo, opad;     // SwiGLU planes: row stride, columns written (with zero pad)
+};
+
+// Workgroup -> tile: workgroup b runs on XCD b % 8.  Tiles are grouped in
+// super-tiles of 4 M tiles x 8 N tiles; an XCD works through whole
+// super-tiles, so the workgroups it runs together share A rows and weight
+// rows in its L2.
+__device__ __forceinline__ bool gemm_tile(const GemmP &p, int &mb, int &nb) {
+    const int b = blockIdx.x, xcd = b & 7, loc = b >> 3;
+    const int sup = (loc >> 5) * 8 + xcd, in = loc & 31;
+    if (sup >= p.n_super) return false;
+    const int n_msup = (p.n_mb + 3) >> 2;
+    mb = (sup % n_msup) * 4 + (in & 3);
+    nb = (sup / n_msup) * 8 + (in >> 2);
+    return mb < p.n_mb && nb < p.n_nb;
+}
+
+// 16 weight bytes (q + 128) -> 16 bf16 of q, as 8 words
+__device__ __forceinline__ void bytes_to_bf16(u32x4 v, u32x4 &o0, u32x4 &o1) {
+    unsigned r[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const unsigned wd = v[i];
+        const float f0 = (float)(int)(wd & 0xffu) - 128.f, f1 = (float)(int)((wd >> 8) & 0xffu) - 128.f;
+        const float f2 = (float)(int)((wd >> 16) & 0xffu) - 128.f, f3 = (float)(int)(wd >> 24) - 128.f;
+        r[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+        r[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+    }
+    o0 = u32x4{r[0], r[1], r[2], r[3]};
+    o1 = u32x4{r[4], r[5], r[6], r[7]};
+}
+
+template <int EPI, bool B32>
+__global__ __launch_bounds__(G_THREADS) void k_gemm(GemmP p) {
+    extern __shared__ float4 gsm[];
+    u16 *lds = reinterpret_cast<u16 *>(gsm);
+    float *s_sc = reinterpret_cast<float *>(lds + 2 * (2 * A_TILE + B_TILE));
+    int mb, nbk;
+    if (!gemm_tile(p, mb, nbk)) return;
+    const int m0 = mb * BM, n0 = nbk * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // global -> LDS assignment: A chunk c = tid + 256 i (row c / 4, 8 bf16 at
+    // 8 (c % 4)); B chunk c = tid + 256 i (row c / 2, 16 bytes at 16 (c % 2))
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (size_t)p.N * p.kp);
+    const u16 *ga[2][2];
+    unsigned boff[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int c = tid + 256 * i;
+        ga[0][i] = p.ahi + (size_t)(m0 + (c >> 2)) * p.lda + ((c & 3) << 3);
+        ga[1][i] = p.alo + (size_t)(m0 + (c >> 2)) * p.lda + ((c & 3) << 3);
+        const int n = n0 + (c >> 1);
+        boff[i] = n < p.N ? (unsigned)((size_t)n * p.kp + ((c & 1) << 4)) : 0x80000000u;
+    }
+    const bool s_ld = B32 && n0 + tid < p.N;
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(p.s32, B32 ? (size_t)p.N * p.nb * sizeof(float) : 0);
+
+    u32x4 ra[2][2], rb[2];
+    float rs = 0.f;
+    auto gload = [&](int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int pl = 0; pl < 2; pl++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) ra[pl][i] = *(const u32x4 *)(ga[pl][i] + k0);
+#pragma unroll
+        for (int i = 0; i < 2; i++) rb[i] = bload16(wr, boff[i] + (unsigned)k0);
+        if (B32)
+            rs = s_ld ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                      sr, (int)(((n0 + tid) * p.nb + kt) * 4), 0, 0))
+                      : 0.f;
+    };
+    auto lstore = [&](int buf) {
+        u16 *sa = lds + (size_t)buf * (2 * A_TILE + B_TILE);
+        u16 *sb = sa + 2 * A_TILE;
+#pragma unroll
+        for (int pl = 0; pl < 2; pl++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int c = tid + 256 * i;
+                *(u32x4 *)(sa + pl * A_TILE + (c >> 2) * LDT + ((c & 3) << 3)) = ra[pl][i];
+            }
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = tid + 256 * i;
+            u32x4 o0, o1;
+            bytes_to_bf16(rb[i], o0, o1);
+            u16 *d = sb + (c >> 1) * LDT + ((c & 1) << 4);
+            *(u32x4 *)d = o0;
+            *(u32x4 *)(d + 8) = o1;
+        }
+        if (B32) s_sc[buf * BN + tid] = rs;
+    };
+
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    const int fr = lane & 15, fk = (lane >> 4) << 3;
+    for (int kt = 0; kt < p.nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < p.nk) gload(kt + 1);
+        const u16 *sa = lds + (size_t)buf * (2 * A_TILE + B_TILE);
+        const u16 *sb = sa + 2 * A_TILE;
+        bf16x8 ah[4], al[4];
+#pragma unroll
+        for (int tm = 0; tm < 4; tm++) {
+            const int r = wm * 64 + tm * 16 + fr;
+            ah[tm] = *(const bf16x8 *)(sa + r * LDT + fk);
+            al[tm] = *(const bf16x8 *)(sa + A_TILE + r * LDT + fk);
+        }
+#pragma unroll
+        for (int tn = 0; tn < 8; tn++) {
+            const int cn = wn * 128 + tn * 16 + fr;
+            const bf16x8 bv = *(const bf16x8 *)(sb + cn * LDT + fk);
+            if (B32) {
+                const float sc = s_sc[buf * BN + cn];
+#pragma unroll
+                for (int tm = 0; tm < 4; tm++) {
+                    f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bv, t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bv, t, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[tm][tn][r] = fmaf(sc, t[r], acc[tm][tn][r]);
+                }
+            } else {
+#pragma unroll
+                for (int tm = 0; tm < 4; tm++) {
+                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bv, acc[tm][tn], 0, 0, 0);
+                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bv, acc[tm][tn], 0, 0, 0);
+                }
+            }
+        }
+        if (kt + 1 < p.nk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: D[4 (l / 16) + r][l % 16] of each tile
+    const float s_a = B32 ? 1.f : p.scale, s_b = B32 ? 1.f : p.scale2;
+#pragma unroll
+    for (int tn = 0; tn < 8; tn++) {
+        const int n = n0 + wn * 128 + tn * 16 + fr;
+#pragma unroll
+        for (int tm = 0; tm < 4; tm++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 64 + tm * 16 + ((lane >> 4) << 2) + r;
+                if (EPI == GE_SWIGLU) {
+                    // fused gate/up rows of a group of 4: gate[2t], gate[2t+1], up[2t], up[2t+1]
+                    const bool gate = (n & 2) == 0;
+                    const float v = acc[tm][tn][r] * (gate ? s_a : s_b);
+                    const float o = __shfl_xor(v, 2);
+                    if (gate && m < p.M && n < p.N) {
+                        const int col = ((n >> 2) << 1) | (n & 1);
+                        u16 a, b;
+                        split_bf16(silu_f(v) * o, a, b);  // cpu.rs:666-678
+                        p.ohi[(size_t)m * p.ldo + col] = a;
+                        p.olo[(size_t)m * p.ldo + col] = b;
+                    }
+                } else if (m < p.M && n < p.N) {
+                    float v = acc[tm][tn][r] * s_a;
+                    float *cp = p.c + (size_t)m * p.ldc + n;
+                    if (EPI == GE_STORE && p.bias) v += p.bias[n];  // cpu.rs:553-570
+                    *cp = EPI == GE_RESID ? *cp + v : v;  // cpu.rs:104-113 add
+                }
+            }
+        }
+    }
+    if (EPI == GE_SWIGLU && wave == 0 && nbk == p.n_nb - 1) {
+        // zero the plane columns past the SwiGLU output (k padding of the next GEMM)
+        const int c0 = p.N >> 1;
+        for (int idx = lane; idx < BM * (p.opad - c0); idx += 64) {
+            const int m = m0 + idx / (p.opad - c0), col = c0 + idx % (p.opad - c0);
+            p.ohi[(size_t)m * p.ldo + col] = 0;
+            p.olo[(size_t)m * p.ldo + col] = 0;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ RoPE + KV append
+// Row m = s * seq + i is position p0[s] + i of sequence s.  q pairs are rotated
+// in place (llama.rs:208-216 without a pre-scale: forward scales the scores),
+// k pairs are rotated into the cache row, v is copied into the cache row
+// (kv_cache.rs:99-118).  cpu.rs:655-658 in f32, no contraction.
+__global__ void k_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, PrefillSeqs t, int l) {
+    const int hh = hd >> 1;
+    const int per_row = (qd >> 1) + (kvd >> 1) + kvd;
+    const size_t total = (size_t)M * per_row;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(g / per_row), e = (int)(g % per_row);
+        const int s = m / seq, i = m - s * seq;
+        const int pos = t.p0[s] + i;
+        float *row = qkv + (size_t)m * ldq;
+        float *kc = t.k[s] + (size_t)l * t.ls[s] + (size_t)pos * kvd;
+        float *vc = t.v[s] + (size_t)l * t.ls[s] + (size_t)pos * kvd;
+        if (e < (qd >> 1) + (kvd >> 1)) {
+            const bool isq = e < (qd >> 1);
+            const int j = isq ? 2 * e : 2 * (e - (qd >> 1));  // element index within q or k
+            const float2 cs = t.rope[s][(size_t)pos * hh + ((j % hd) >> 1)];
+            float *x = isq ? row + j : row + qd + j;
+            const float x0 = x[0], x1 = x[1];
+            const float r0 = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
+            const float r1 = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+            if (isq) {
+                x[0] = r0;
+                x[1] = r1;
+            } else {
+                kc[j] = r0;
+                kc[j + 1] = r1;
+            }
+        } else {
+            const int j = e - (qd >> 1) - (kvd >> 1);
+            vc[j] = row[qd + kvd + j];
+        }
+    }
+}
+
+// ------------------------------------------------------------------ attention
+// Causal attention of the processed rows over their cache (llama.rs:218-250:
+// scores = q.k, x scale, mask keys after the query position, softmax, P.V),
+// online over 32-key tiles.  Workgroup: 128 query rows of one (head, sequence);
+// two threads per row, each holding half of head_dim (HT >= hd / 2 values).
+// The output row goes straight into the bf16 planes of the o_proj input.
+constexpr int AQ = 128, AK = 32;
+
+template <int HT>
+__global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttn a, PrefillSeqs t, int l) {
+    extern __shared__ float4 asm4[];
+    float *sk = reinterpret_cast<float *>(asm4);  // [AK][hd]
+    float *sv = sk + AK * a.hd;
+    const int tid = threadIdx.x, row = tid >> 1, half = tid & 1;
+    const int qb = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+    const int i = qb * AQ + row;
+    const bool valid = i < a.seq;
+    const int p0 = t.p0[s], pos = p0 + i;
+    const int ht = a.hd >> 1, kvh = h / (a.nh / a.nkv);
+    const size_t m = (size_t)s * a.seq + i;
+    float q[HT], o[HT];
+#pragma unroll
+    for (int d = 0; d < HT; d++) {
+        q[d] = (valid && d < ht) ? a.qkv[m * a.ldq + h * a.hd + half * ht + d] : 0.f;
+        o[d] = 0.f;
+    }
+    float mx = -INFINITY, lsum = 0.f;
+    const int kend = p0 + min(a.seq, (qb + 1) * AQ);  // keys [0, kend) cover this block
+    const float *kc = t.k[s] + (size_t)l * t.ls[s] + (size_t)kvh * a.hd;
+    const float *vc = t.v[s] + (size_t)l * t.ls[s] + (size_t)kvh * a.hd;
+    for (int k0 = 0; k0 < kend; k0 += AK) {
+        __syncthreads();
+        for (int idx = tid; idx < AK * a.hd; idx += 256) {
+            const int j = idx / a.hd, d = idx - j * a.hd;
+            const bool in = k0 + j < kend;
+            sk[idx] = in ? kc[(size_t)(k0 + j) * a.kvd + d] : 0.f;
+            sv[idx] = in ? vc[(size_t)(k0 + j) * a.kvd + d] : 0.f;
+        }
+        __syncthreads();
+        float sc[AK];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < AK; j++) {
+            const float *kr = sk + j * a.hd + half * ht;
+            float dt = 0.f;
+#pragma unroll
+            for (int d = 0; d < HT; d++)
+                if (d < ht) dt = fmaf(q[d], kr[d], dt);
+            dt += __shfl_xor(dt, 1);
+            const float v = k0 + j <= pos ? dt * a.scale : -INFINITY;
+            sc[j] = v;
+            bm = fmaxf(bm, v);
+        }
+        const float mn = fmaxf(mx, bm);
+        if (mn == -INFINITY) continue;  // every key so far masked (rows past seq)
+        const float alpha = expf(mx - mn);
+        lsum *= alpha;
+#pragma unroll
+        for (int d = 0; d < HT; d++) o[d] *= alpha;
+#pragma unroll
+        for (int j = 0; j < AK; j++) {
+            const float pj = expf(sc[j] - mn);
+            lsum += pj;
+            const float *vr = sv + j * a.hd + half * ht;
+#pragma unroll
+            for (int d = 0; d < HT; d++)
+                if (d < ht) o[d] = fmaf(pj, vr[d], o[d]);
+        }
+        mx = mn;
+    }
+    if (!valid) return;
+    const float inv = 1.f / lsum;
+    u16 *ph = a.ohi + m * a.ldo + h * a.hd + half * ht;
+    u16 *pl = a.olo + m * a.ldo + h * a.hd + half * ht;
+#pragma unroll
+    for (int d = 0; d < HT; d++)
+        if (d < ht) {
+            u16 x0, x1;
+            split_bf16(o[d] * inv, x0, x1);
+            ph[d] = x0;
+            pl[d] = x1;
+        }
+    if (h == a.nh - 1 && half == 1)  // zero the k padding of the o_proj input
+        for (int c = a.nh * a.hd; c < a.opad; c++) {
+            a.ohi[m * a.ldo + c] = 0;
+            a.olo[m * a.ldo + c] = 0;
+        }
+}
+
+template <int EPI, bool B32>
+int gemm_t(const GemmP &p, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<EPI, B32>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)GEMM_LDS));
+        attr = true;
+    }
+    const int grid = (p.n_super + 7) / 8 * 8 * 32;
+    hipLaunchKernelGGL((k_gemm<EPI, B32>), dim3(grid), dim3(G_THREADS), GEMM_LDS, s, p);
+    PF_LAUNCH_CHECK();
+}
+
+}  // namespace
+
+int prefill_rows_pad(int M) { return (M + BM - 1) / BM * BM; }
+
+int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, const float *w, int k, float eps,
+                      u16 *hi, u16 *lo, int ldp, float *outf, int ldf, hipStream_t s) {
+    if (rows <= 0) return SCRY_OK;
+    const int kpad = hi ? (k + 31) / 32 * 32 : k;
+    if (hi && kpad > ldp) return set_error(SCRY_ERR_INVALID, "norm_split: k %d exceeds plane stride %d", k, ldp);
+    hipLaunchKernelGGL(k_norm_split, dim3(rows), dim3(256), 0, s, x, ldx, rstep, roff, w, k, eps, hi, lo, ldp,
+                       kpad, outf, ldf);
+    PF_LAUNCH_CHECK();
+}
+
+int launch_split(const float *x, int ldx, int rows, int k, u16 *hi, u16 *lo, int ldp, hipStream_t s) {
+    const int kpad = (k + 31) / 32 * 32;
+    if (kpad > ldp) return set_error(SCRY_ERR_INVALID, "split: k %d exceeds plane stride %d", k, ldp);
+    const size_t total = (size_t)rows * kpad;
+    if (total == 0) return SCRY_OK;
+    const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_split, dim3(grid), dim3(256), 0, s, x, ldx, rows, k, kpad, hi, lo, ldp);
+    PF_LAUNCH_CHECK();
+}
+
+int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
+    const Packed &w = *g.w;
+    if (w.kp % 16 || w.k > w.kp) return set_error(SCRY_ERR_INVALID, "gemm: bad packed layout");
+    const int kpad = (w.k + 31) / 32 * 32;
+    if (kpad > g.lda || g.lda % 8) return set_error(SCRY_ERR_INVALID, "gemm: plane stride %d < k %d", g.lda, w.k);
+    if (epi == GE_SWIGLU && (w.fused != 1 || w.rows % 4 || (w.rows >> 1) > g.ldo || g.opad > g.ldo))
+        return set_error(SCRY_ERR_INVALID, "gemm: swiglu needs the fused gate/up layout");
+    if (w.s32 && w.nb * 32 < kpad) return set_error(SCRY_ERR_INVALID, "gemm: block-32 scales too short");
+    GemmP p{};
+    p.ahi = g.ahi;
+    p.alo = g.alo;
+    p.lda = g.lda;
+    p.w = w.d;
+    p.kp = w.kp;
+    p.N = w.rows;
+    p.s32 = w.s32;
+    p.nb = w.nb;
+    p.M = g.M;
+    p.nk = kpad / BK;
+    p.n_mb = (g.M + BM - 1) / BM;
+    p.n_nb = (w.rows + BN - 1) / BN;
+    p.n_super = ((p.n_mb + 3) / 4) * ((p.n_nb + 7) / 8);
+    p.scale = w.scale;
+    p.scale2 = w.scale2;
+    p.bias = g.bias;
+    p.c = g.c;
+    p.ldc = g.ldc;
+    p.ohi = g.ohi;
+    p.olo = g.olo;
+    p.ldo = g.ldo;
+    p.opad = g.opad;
+    const bool b32 = w.s32 != nullptr;
+    switch (epi) {
+        case GE_STORE: return b32 ? gemm_t<GE_STORE, true>(p, s) : gemm_t<GE_STORE, false>(p, s);
+        case GE_RESID: return b32 ? gemm_t<GE_RESID, true>(p, s) : gemm_t<GE_RESID, false>(p, s);
+        case GE_SWIGLU: return b32 ? gemm_t<GE_SWIGLU, true>(p, s) : gemm_t<GE_SWIGLU, false>(p, s);
+    }
+    return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
+}
+
+int launch_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, const PrefillSeqs &t, int l,
+                   hipStream_t s) {
+    if (hd % 2 || qd % hd || kvd % hd) return set_error(SCRY_ERR_INVALID, "rope_kv: bad head dims");
+    const size_t total = (size_t)M * ((qd >> 1) + (kvd >> 1) + kvd);
+    if (total == 0) return SCRY_OK;
+    const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_rope_kv, dim3(grid), dim3(256), 0, s, qkv, ldq, M, seq, qd, kvd, hd, t, l);
+    PF_LAUNCH_CHECK();
+}
+
+int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hipStream_t s) {
+    if (a.hd % 2 || a.hd > 128 || a.nkv <= 0 || a.nh % a.nkv)
+        return set_error(SCRY_ERR_UNSUPPORTED, "attn_prefill: head_dim %d / heads %d,%d", a.hd, a.nh, a.nkv);
+    const dim3 grid((a.seq + AQ - 1) / AQ, a.nh, n_seq);
+    const size_t lds = 2 * (size_t)AK * a.hd * sizeof(float);
+    const int ht = a.hd / 2;
+    if (ht <= 8)
+        hipLaunchKernelGGL(k_attn_prefill<8>, grid, dim3(256), lds, s, a, t, l);
+    else if (ht <= 16)
+        hipLaunchKernelGGL(k_attn_prefill<16>, grid, dim3(256), lds, s, a, t, l);
+    else if (ht <= 32)
+        hipLaunchKernelGGL(k_attn_prefill<32>, grid, dim3(256), lds, s, a, t, l);
+    else
+        hipLaunchKernelGGL(k_attn_prefill<64>, grid, dim3(256), lds, s, a, t, l);
+    PF_LAUNCH_CHECK();
+}
+
+}  // namespace scry

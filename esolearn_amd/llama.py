@@ -166,17 +166,52 @@ class LlamaModel:
              lg.ctypes.data if lg is not None else None, C.byref(am))
         return lg, int(am.value)
 
-    def generate_greedy(self, prompt, max_tokens: int, want_logits: bool = False):
+    def generate_greedy(self, prompt, max_tokens: int, want_logits: bool = False,
+                        prefill: bool = False):
+        """generate() at temperature 0; prefill=True runs the prompt (all but its
+        last token) through one batched prefill instead of token by token."""
         p = np.ascontiguousarray(prompt, dtype=np.int64)
         nout = max(1, max_tokens)
         toks = np.empty(nout, np.int64)
         n = C.c_int()
         lg = np.empty(nout * self.cfg.vocab_size, np.float32) if want_logits else None
-        call("scry_hip_llama_generate_greedy", self.h, p.ctypes.data, p.size, max_tokens,
+        fn = "scry_hip_llama_generate_greedy_prefill" if prefill else "scry_hip_llama_generate_greedy"
+        call(fn, self.h, p.ctypes.data, p.size, max_tokens,
              toks.ctypes.data, C.byref(n), lg.ctypes.data if lg is not None else None)
         if want_logits:
             return toks[: n.value], lg.reshape(nout, -1)[: n.value]
         return toks[: n.value]
+
+    def forward(self, tokens) -> np.ndarray:
+        """LlamaModel::forward: logits [seq, V] for every position (no cache)."""
+        t = np.ascontiguousarray(tokens, dtype=np.int64)
+        lg = np.empty((t.size, self.cfg.vocab_size), np.float32)
+        call("scry_hip_llama_forward", self.h, t.ctypes.data, t.size, lg.ctypes.data)
+        return lg
+
+    def prefill(self, caches, tokens, want_logits: bool = True):
+        """Batched prefill of tokens [n_seq, seq] into the given caches (one per
+        sequence); returns the last position's logits [n_seq, V] or None."""
+        t = np.ascontiguousarray(np.atleast_2d(tokens), dtype=np.int64)
+        n_seq, seq = t.shape
+        if len(caches) != n_seq:
+            raise ValueError("one cache per sequence")
+        hs = (C.c_void_p * n_seq)(*[c.h for c in caches])
+        lg = np.empty((n_seq, self.cfg.vocab_size), np.float32) if want_logits else None
+        call("scry_hip_llama_prefill", self.h, hs, n_seq, t.ctypes.data, seq,
+             lg.ctypes.data if lg is not None else None)
+        return lg
+
+    def bench_prefill(self, prompts, decode_steps: int):
+        """(prefill ms, decode ms, tokens [n_seq, decode_steps]) for prompts
+        [n_seq, n_prompt]: batched prefill, then greedy decode per sequence."""
+        p = np.ascontiguousarray(prompts, dtype=np.int64)
+        n_seq, n_prompt = p.shape
+        toks = np.empty((n_seq, decode_steps), np.int64)
+        pm, dm = C.c_double(), C.c_double()
+        call("scry_hip_llama_bench_prefill", self.h, p.ctypes.data, n_seq, n_prompt, decode_steps,
+             toks.ctypes.data, C.byref(pm), C.byref(dm))
+        return pm.value, dm.value, toks
 
     def decode_persistent(self) -> bool:
         """True when this model's decode steps run on the persistent kernel."""

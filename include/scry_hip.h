@@ -209,6 +209,30 @@ int scry_hip_llama_generate_greedy(scry_llama m, const int64_t *prompt, int n_pr
                                    int max_tokens, int64_t *out_tokens, int *n_out,
                                    float *step_logits);
 
+/* generate() as above, with the prompt prefilled: its first n_prompt - 1
+ * tokens go through one batched prefill (GEMMs on the matrix cores), then the
+ * decode loop starts at the last prompt token.  Same tokens as
+ * scry_hip_llama_generate_greedy; logits agree within float rounding.  (No
+ * counterpart in the reference, whose generate feeds the prompt token by
+ * token, generate.rs:69-76.) */
+int scry_hip_llama_generate_greedy_prefill(scry_llama m, const int64_t *prompt, int n_prompt,
+                                           int max_tokens, int64_t *out_tokens, int *n_out,
+                                           float *step_logits);
+
+/* LlamaModel::forward (llama.rs:683-700; attention llama.rs:162-266): logits
+ * [seq, V] (host) for every position of one sequence, causal attention, no
+ * cache kept.  Projections run as GEMMs on the matrix cores. */
+int scry_hip_llama_forward(scry_llama m, const int64_t *tokens, int seq, float *logits);
+
+/* Batched prefill (the forward above over several sequences, continuing KV
+ * caches; the reference has no batched cache path): tokens [n_seq, seq] run
+ * at positions caches[s]->seq_len .. of their caches, whose K/V rows are
+ * appended (seq_len advances by seq).  last_logits (host, may be NULL)
+ * receives [n_seq, V]: each sequence's last position.  1 <= n_seq <= 16,
+ * distinct caches, head_dim <= 128. */
+int scry_hip_llama_prefill(scry_llama m, scry_kv_cache *caches, int n_seq, const int64_t *tokens,
+                           int seq, float *last_logits);
+
 /* Decode-step implementation (no counterpart in the reference: a backend
  * choice).  SCRY_DECODE_KERNELS (the default) runs each token as one replay of
  * the captured per-kernel graph.  SCRY_DECODE_PERSISTENT runs each token as
@@ -234,6 +258,14 @@ int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_promp
  * step uses.  tensor_id: SCRY_T_QKV / O / GATE (fused gate+up) / DOWN / LM_HEAD. */
 int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int iters,
                                    double *avg_us, double *bytes_per_launch);
+/* Prefill then decode, timed: prompts [n_seq, n_prompt]; the first
+ * n_prompt - 1 tokens of every sequence go through one batched prefill
+ * (*prefill_ms, after an untimed pass), then each sequence runs decode_steps
+ * greedy steps in turn (*decode_ms, all sequences).  out_tokens (may be NULL)
+ * receives [n_seq, decode_steps]. */
+int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq, int n_prompt,
+                                 int decode_steps, int64_t *out_tokens, double *prefill_ms,
+                                 double *decode_ms);
 /* Average device time of matmul_i8_f32 at m,k,n rotating over `n_bufs`
  * distinct weight copies (defeats the 256 MB Infinity Cache). */
 int scry_hip_bench_qgemv(int m, int k, int n, int quant_mode, int n_bufs, int warmup, int iters,
