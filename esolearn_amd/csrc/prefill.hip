@@ -430,6 +430,136 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttn a, PrefillSeqs
         }
 }
 
+// The same attention on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: lane
+// l holds A[l % 16][l / 16], B[l / 16][l % 16] and D[4 (l / 16) + r][l % 16]).
+// Workgroup: MQ query rows of one (head, sequence), one wave per 16 rows; K/V
+// tiles of MK keys in LDS.  Per wave and 16-key sub-tile:
+//   S^T = K Q^T in HD/4 MFMAs; chunk c, position j holds head dim (HD/4) j + c,
+//     so a lane's K and Q values are contiguous.  Lane l receives the scores
+//     of query row l % 16 against keys 4 (l / 16) + r, r = 0..3;
+//   online softmax per query row, reduced over the 4 lanes l % 16 + 16 g;
+//   O^T += V^T P^T in HD/16 x 4 MFMAs; chunk r takes keys 4 j + r, so P^T is
+//     the lane's own scores, and lane l accumulates query row l % 16 at head
+//     dims 16 t + 4 (l / 16) + r.
+// fp32 products and accumulation: the arithmetic of the VALU kernel above,
+// in another summation order.
+constexpr int MQ = 64, MK = 64;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_mfma(PrefillAttn a, PrefillSeqs t, int l) {
+    constexpr int NC = HD / 4, NT = HD / 16, LD = HD + 4;
+    extern __shared__ float4 am4[];
+    float *sk = reinterpret_cast<float *>(am4);  // [MK][LD]
+    float *sv = sk + MK * LD;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
+    const int h = blockIdx.y, s = blockIdx.z;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int i = qb * MQ + w * 16 + lr;
+    const bool valid = i < a.seq;
+    const int p0 = t.p0[s], pos = p0 + i;
+    const int kvh = h / (a.nh / a.nkv);
+    const size_t m = (size_t)s * a.seq + i;
+    float q[NC];
+    {
+        const float *qr = a.qkv + m * a.ldq + h * HD + NC * lg;
+#pragma unroll
+        for (int c = 0; c < NC; c++) q[c] = valid ? qr[c] : 0.f;
+    }
+    f32x4 o[NT];
+#pragma unroll
+    for (int dt = 0; dt < NT; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float mrow = -INFINITY, lrow = 0.f;
+    const int kend = p0 + min(a.seq, (qb + 1) * MQ);                 // keys of the workgroup
+    const int wlast = p0 + min(a.seq, qb * MQ + w * 16 + 16) - 1;    // last key of this wave's rows
+    const float *kc = t.k[s] + (size_t)l * t.ls[s] + (size_t)kvh * HD;
+    const float *vc = t.v[s] + (size_t)l * t.ls[s] + (size_t)kvh * HD;
+    for (int k0 = 0; k0 < kend; k0 += MK) {
+        __syncthreads();
+        for (int idx = tid; idx < MK * (HD / 4); idx += 256) {
+            const int j = idx / (HD / 4), c4 = idx - j * (HD / 4);
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (k0 + j < kend) {
+                kv = *(const float4 *)(kc + (size_t)(k0 + j) * a.kvd + 4 * c4);
+                vv = *(const float4 *)(vc + (size_t)(k0 + j) * a.kvd + 4 * c4);
+            }
+            *(float4 *)(sk + j * LD + 4 * c4) = kv;
+            *(float4 *)(sv + j * LD + 4 * c4) = vv;
+        }
+        __syncthreads();
+        for (int sb = 0; sb < MK; sb += 16) {
+            const int kb = k0 + sb;
+            if (kb > wlast) break;  // wave-uniform: masked for every row of the wave
+            f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+            const float *kr = sk + (sb + lr) * LD + NC * lg;
+#pragma unroll
+            for (int c = 0; c < NC; c++) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[c], q[c], st, 0, 0, 0);
+            float p[4];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                p[r] = kb + 4 * lg + r <= pos ? st[r] * a.scale : -INFINITY;  // llama.rs:225-234
+                tmax = fmaxf(tmax, p[r]);
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const float mn = fmaxf(mrow, tmax);  // finite: key 0 is visible to every row
+            const float alpha = expf(mrow - mn);
+            float ps = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                p[r] = expf(p[r] - mn);
+                ps += p[r];
+            }
+            ps += __shfl_xor(ps, 16);
+            ps += __shfl_xor(ps, 32);
+            lrow = lrow * alpha + ps;
+            mrow = mn;
+#pragma unroll
+            for (int dt = 0; dt < NT; dt++) o[dt] *= alpha;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float *vr = sv + (sb + 4 * lg + r) * LD + lr;
+#pragma unroll
+                for (int dt = 0; dt < NT; dt++)
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[dt * 16], p[r], o[dt], 0, 0, 0);
+            }
+        }
+    }
+    if (!valid) return;
+    const float inv = 1.f / lrow;
+    u16 *ph = a.ohi + m * a.ldo + h * HD, *pl = a.olo + m * a.ldo + h * HD;
+#pragma unroll
+    for (int dt = 0; dt < NT; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int d = dt * 16 + 4 * lg + r;
+            u16 x0, x1;
+            split_bf16(o[dt][r] * inv, x0, x1);
+            ph[d] = x0;
+            pl[d] = x1;
+        }
+    if (h == a.nh - 1 && lg == 0)  // zero the k padding of the o_proj input
+        for (int c = a.nh * HD; c < a.opad; c++) {
+            a.ohi[m * a.ldo + c] = 0;
+            a.olo[m * a.ldo + c] = 0;
+        }
+}
+
+template <int HD>
+int attn_mfma_t(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hipStream_t s) {
+    constexpr size_t lds = 2 * (size_t)MK * (HD + 4) * sizeof(float);
+    static bool attr = false;
+    if (!attr) {
+        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_mfma<HD>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    const dim3 grid((a.seq + MQ - 1) / MQ, a.nh, n_seq);
+    hipLaunchKernelGGL(k_attn_mfma<HD>, grid, dim3(256), lds, s, a, t, l);
+    PF_LAUNCH_CHECK();
+}
+
 template <int EPI, bool B32>
 int gemm_t(const GemmP &p, hipStream_t s) {
     static bool attr = false;
@@ -520,6 +650,13 @@ int launch_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd,
 int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hipStream_t s) {
     if (a.hd % 2 || a.hd > 128 || a.nkv <= 0 || a.nh % a.nkv)
         return set_error(SCRY_ERR_UNSUPPORTED, "attn_prefill: head_dim %d / heads %d,%d", a.hd, a.nh, a.nkv);
+    switch (a.hd) {  // matrix-core kernel for the common head sizes
+        case 32: return attn_mfma_t<32>(a, n_seq, t, l, s);
+        case 48: return attn_mfma_t<48>(a, n_seq, t, l, s);
+        case 64: return attn_mfma_t<64>(a, n_seq, t, l, s);
+        case 128: return attn_mfma_t<128>(a, n_seq, t, l, s);
+        default: break;
+    }
     const dim3 grid((a.seq + AQ - 1) / AQ, a.nh, n_seq);
     const size_t lds = 2 * (size_t)AK * a.hd * sizeof(float);
     const int ht = a.hd / 2;
