@@ -16,10 +16,19 @@ Also reported:
   roofline      the dominant projection kernel (largest device time per token),
                 timed with HIP events over launches that rotate through all 32
                 layers' weights (so they stream from HBM, not the 256 MB MALL);
-                achieved = algorithmic bytes per launch / average launch time
+                achieved = algorithmic bytes per launch / average launch time;
+                traffic = HBM bytes per launch from the committed rocprofv3
+                FETCH_SIZE / WRITE_SIZE summary (profiles/)
   cpu_baseline  the oracle (C restatement of the reference CPU path) on the same
                 int8 weights, reference-faithful single-threaded
                 matmul_i8_f32_tiled, timed over a few decode steps on the host
+  prefill       BASELINE config 5 (Llama-3-8B shape, 4 x 2048-token prompts):
+                batched prefill of the first 2047 tokens of each prompt on the
+                matrix cores, then 64 greedy decode steps per sequence
+
+Profiling modes (no JSON line): --pmc-probe runs a 256 MiB device copy (the
+counter calibration) and each decode projection kernel over all layers;
+--prefill-only runs the config-5 measurement alone.
 """
 from __future__ import annotations
 
@@ -34,6 +43,79 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # dense
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_projections_pmc_traffic.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of a decode projection kernel, from the committed
+    rocprofv3 PMC summary (None when it has no figure for it)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int = 64) -> dict:
+    """BASELINE config 5 on the GPU: batched prefill, then greedy decode."""
+    cfg = E.LlamaConfig.llama3_8b()
+    t0 = time.perf_counter()
+    m = E.LlamaModel.new_random(cfg, seed=0)
+    t_init = time.perf_counter() - t0
+    prompts = [E.synth.prompt_ids(s + 1, n_prompt, cfg.vocab_size) for s in range(n_seq)]
+    import numpy as np
+    pm, dm, toks = m.bench_prefill(np.stack(prompts), decode_steps)
+    m.free()
+    h, ffn, L = cfg.hidden_size, cfg.intermediate_size, cfg.n_layers
+    hd = h // cfg.n_heads
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    rows = n_seq * (n_prompt - 1)
+    proj = 2.0 * rows * L * (h * (qd + 2 * kvd) + qd * h + 2 * h * ffn + ffn * h)
+    s = n_prompt - 1
+    attn = 4.0 * n_seq * L * cfg.n_heads * (s * (s + 1) / 2) * hd
+    tf = proj / (pm / 1e3) / 1e12
+    print(f"[bench] prefill {n_seq}x{s}: {pm:.1f} ms ({rows / pm * 1e3:.0f} tok/s, projections "
+          f"{tf:.1f} TFLOP/s); decode {n_seq}x{decode_steps}: {dm:.1f} ms; init {t_init:.1f} s",
+          file=sys.stderr, flush=True)
+    return {
+        "workload": "llama3-8b-shape int8: 4 x 2048-token prompts, batched prefill of the first "
+                    "2047 tokens each (GEMMs on MFMA, split-bf16 activations), then 64 greedy "
+                    "decode steps per sequence (BASELINE config 5)",
+        "prefill_ms": round(pm, 2),
+        "prefill_tok_s": round(rows / (pm / 1e3), 1),
+        "projection_tflop": round(proj / 1e12, 2),
+        "attention_tflop_causal": round(attn / 1e12, 2),
+        "projection_tflops": round(tf, 1),
+        "mfma_peak_tflops_bf16": BF16_MFMA_PEAK_TFLOPS,
+        "mfma_frac_useful": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+        "mfma_frac_issued": round(2 * tf / BF16_MFMA_PEAK_TFLOPS, 4),
+        "decode_ms": round(dm, 2),
+        "decode_tok_s": round(n_seq * decode_steps / (dm / 1e3), 1),
+        "greedy_tokens_head": [[int(t) for t in row[:4]] for row in toks],
+    }
+
+
+def pmc_probe(E) -> None:
+    """The workload of the committed PMC summary: calibration copy + projections."""
+    import esolearn_amd.llama as EL
+    B = E.HipBackend
+    src = B.zeros(64 * 1024 * 1024)  # 256 MiB
+    B.synchronize()
+    for _ in range(3):
+        dst = B.clone_storage(src)
+        B.synchronize()
+        dst.free()
+    src.free()
+    m = E.LlamaModel.new_random(E.LlamaConfig.llama2_7b(), seed=0)
+    for name, tid in (("qkv", EL.T_QKV), ("o", EL.T_O), ("gate_up", EL.T_GATE),
+                      ("down", EL.T_DOWN), ("lm_head", EL.T_LM_HEAD)):
+        us, b = m.time_projection(tid, 32)
+        print(f"[probe] {name} {us:.2f} us {b:.0f} B", flush=True)
+    m.free()
 
 
 def weight_bytes(cfg) -> int:
@@ -93,6 +175,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--host-init", action="store_true",
                     help="draw the random weights on the host (slow) instead of the GPU")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill line")
+    ap.add_argument("--pmc-probe", action="store_true", help="profiling workload only (see above)")
+    ap.add_argument("--prefill-only", action="store_true", help="config-5 measurement only")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -106,6 +191,12 @@ def main() -> int:
     import esolearn_amd.llama as EL
 
     E.init(0)
+    if args.pmc_probe:
+        pmc_probe(E)
+        return 0
+    if args.prefill_only:
+        print(json.dumps(prefill_config5(E)), flush=True)
+        return 0
     info = E.HipBackend.device_info()
     cfg = E.LlamaConfig.llama2_7b()
     t0 = time.perf_counter()
@@ -143,7 +234,7 @@ def main() -> int:
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(proj[dom]["gbs"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": measured_traffic(dom),
         "kernel": f"k_qgemv ({dom} projection, decode epilogue)",
         "bytes_per_launch": proj[dom]["bytes"],
         "avg_launch_us": proj[dom]["avg_us"],
@@ -153,6 +244,8 @@ def main() -> int:
     if not args.no_cpu_baseline:
         print(f"[bench] cpu baseline: {args.cpu_tokens} tokens", file=sys.stderr, flush=True)
         cpu = cpu_baseline(model, cfg, prompt, args.cpu_tokens)
+    model.free()
+    pre = None if args.no_prefill else prefill_config5(E)
 
     line = {
         "metric": "decode tok/s, Llama-7B-shape int8 batch 1; quant-GEMV achieved HBM GB/s",
@@ -181,9 +274,9 @@ def main() -> int:
         "cpu_baseline": cpu,
         "projections": proj,
         "greedy_tokens_head": [int(t) for t in toks[:8]],
+        "prefill": pre,
     }
     print(json.dumps(line), flush=True)
-    model.free()
     return 0
 
 

@@ -8,11 +8,14 @@
 // The cache is read in place ([max_seq, n_kv*hd] rows, no repeat_kv copy):
 // workgroup (g, s) handles KV head g and position split s for all n_rep query
 // heads of the group, so each K/V row is read once per group.  Splits write
-// (max, sum, unnormalised output) with plain stores -- no fences or atomics;
-// the consumer (the o_proj GEMV prologue, next kernel on the stream) merges
-// them with the usual log-sum-exp rescaling.  The split count is fixed per
-// cache, so the launch shape does not depend on the current length and the
-// kernel can live in a replayed graph; the length comes from the device state.
+// (max, sum, unnormalised output); the last split of a group to finish merges
+// the group's splits (log-sum-exp rescaling, in split order) into the
+// attention output row.  The partials and the per-group arrival counters live
+// in uncached device memory: a split's stores are complete in memory before
+// its counter increment, so the last arrival reads them without cache
+// maintenance.  The split count is fixed per cache, so the launch shape does
+// not depend on the current length and the kernel can live in a replayed
+// graph; the length comes from the device state.
 #include "internal.h"
 #include "kdev.h"
 
@@ -20,6 +23,14 @@ namespace scry {
 namespace {
 
 using namespace dev;
+
+// load from the uncached exchange memory (a vector load: scalar loads would
+// go through the scalar cache)
+__device__ __forceinline__ float cload(const float *p) {
+    return __builtin_bit_cast(float, __hip_atomic_load((const unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+constexpr int MAX_SPLITS = 16;  // attn_pick_splits never picks more
 
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
@@ -142,6 +153,45 @@ __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
             a.part_ml[ph * 2 + 1] = lsum;
         }
     }
+    // count this split in once its partial stores are complete
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ int s_last;
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(a.merge_ctr + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(a.n_splits - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // last split of group g: x[h*hd + d] = sum_s O_s[d] e^(M_s - M) / sum_s L_s e^(M_s - M),
+    // every load issued before the first use (one memory round trip)
+    const int ns = a.n_splits;
+    for (int idx = tid; idx < nrep * hd; idx += TPB) {
+        const int r = idx / hd, d = idx % hd, h = g * nrep + r;
+        const float *ml = a.part_ml + (size_t)h * ns * 2;
+        const float *po = a.part_o + (size_t)h * ns * hd + d;
+        float mq[MAX_SPLITS], lq[MAX_SPLITS], oq[MAX_SPLITS];
+#pragma unroll
+        for (int q = 0; q < MAX_SPLITS; q++) {
+            mq[q] = q < ns ? cload(ml + 2 * q) : -INFINITY;
+            lq[q] = q < ns ? cload(ml + 2 * q + 1) : 0.f;
+            oq[q] = q < ns ? cload(po + (size_t)q * hd) : 0.f;
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < MAX_SPLITS; q++) M = fmaxf(M, mq[q]);
+        float Ls = 0.f;
+#pragma unroll
+        for (int q = 0; q < MAX_SPLITS; q++)
+            if (mq[q] != -INFINITY) Ls += lq[q] * expf(mq[q] - M);
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < MAX_SPLITS; q++) {
+            const float w = mq[q] == -INFINITY ? 0.f : expf(mq[q] - M) / Ls;
+            v += w * oq[q];
+        }
+        a.xa[(size_t)h * hd + d] = v;
+    }
+    if (tid == 0) a.merge_ctr[g] = 0;  // ready for the next launch on the stream
 }
 
 template <int G>
@@ -180,6 +230,10 @@ int attn_pick_splits(int n_kv, int max_seq, int *n_splits, int *max_chunk) {
 }
 
 int launch_attn_decode(const AttnArgs &a, hipStream_t s) {
+    if (!a.merge_ctr || !a.xa || !a.part_o || !a.part_ml)
+        return set_error(SCRY_ERR_INVALID, "attention: missing partial / merge buffers");
+    if (a.n_splits < 1 || a.n_splits > MAX_SPLITS)
+        return set_error(SCRY_ERR_INVALID, "attention: %d splits (1..%d)", a.n_splits, MAX_SPLITS);
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0)
         return set_error(SCRY_ERR_INVALID, "attention: n_heads %% n_kv != 0");
     if (a.head_dim % 4 != 0 || a.head_dim > 256)

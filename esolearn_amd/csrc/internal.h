@@ -131,9 +131,6 @@ struct GemvArgs {
     int64_t *tokens_rw = nullptr;
     int64_t *argmax_out = nullptr;
     int advance = 0;
-    // attention-merge prologue (o_proj): split partials of the decode attention
-    const float *attn_part_o = nullptr, *attn_part_ml = nullptr;
-    int attn_nh = 0, attn_ns = 0, attn_hd = 0;
 };
 
 int launch_qgemv(int epi, const GemvArgs &a, hipStream_t s);
@@ -145,7 +142,11 @@ int launch_logits_finish(const GemvArgs &a, hipStream_t s);
 struct AttnArgs {
     const float *q = nullptr;     // [n_heads*hd] pre-scaled
     const float *k_cache = nullptr, *v_cache = nullptr;  // [max_seq, n_kv*hd]
-    float *part_o = nullptr, *part_ml = nullptr;  // per (head, split) partials
+    // per (head, split) partials and per-KV-group arrival counters (zero
+    // between launches), in uncached device memory
+    float *part_o = nullptr, *part_ml = nullptr;
+    unsigned *merge_ctr = nullptr;
+    float *xa = nullptr;          // merged output [n_heads*hd]
     const DevState *state = nullptr;
     int n_heads = 0, n_kv = 0, head_dim = 0, n_splits = 1, max_chunk = 0;
     int fixed_len = -1;  // >= 0: use this length instead of state->cache_len + 1

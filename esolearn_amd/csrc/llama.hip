@@ -12,13 +12,15 @@
 // Decode step, per layer (5 kernels):
 //   qkv   : RMSNorm(x) -> int8 GEMV -> RoPE(Q)*1/sqrt(hd), RoPE(K), K/V row append
 //           (layer 0 reads the embedding row of the current token directly)
-//   attn  : split-L attention over the cache in place -> per-split partials
-//   o     : merge of the attention partials (prologue) -> int8 GEMV + residual add into x
+//   attn  : split-L attention over the cache in place -> per-split partials,
+//           merged by the last split of each KV group into the attention row
+//   o     : int8 GEMV of the attention row + residual add into x
 //   gateup: RMSNorm(x) -> fused gate/up int8 GEMV -> silu(g)*u
 //   down  : int8 GEMV + residual add into x
 // then lm_head: RMSNorm(x) -> int8 GEMV -> logits + per-workgroup argmax, and a
-// one-workgroup finish kernel: ordered argmax -> next token, position advance.  The current position and token live in device
-// memory, so the same captured graph replays for every token.
+// one-workgroup finish kernel: ordered argmax -> next token, position advance.
+// The current position and token live in device memory, so the same captured
+// graph replays for every token.
 #include <algorithm>
 #include <climits>
 #include <cstdlib>
@@ -136,7 +138,12 @@ struct scry_kv_cache_s {
     int64_t *tokens = nullptr;
     int tokens_len = 0;
     float *x = nullptr, *xq = nullptr, *act = nullptr, *logits = nullptr;
+    // decode attention split partials and per-KV-group arrival counters
+    // (uncached: the last split merges them), and the merged output row
+    UcBlock att_uc{nullptr, 0};
     float *ap_o = nullptr, *ap_ml = nullptr;
+    unsigned *att_ctr = nullptr;
+    float *xa = nullptr;
     float *lp_val = nullptr;
     int *lp_idx = nullptr, *lp_nan = nullptr;
     int64_t *amax = nullptr;
@@ -364,8 +371,8 @@ void cache_free(scry_kv_cache c) {
     dev_free(c->xq);
     dev_free(c->act);
     dev_free(c->logits);
-    dev_free(c->ap_o);
-    dev_free(c->ap_ml);
+    uc_give(c->att_uc);
+    dev_free(c->xa);
     dev_free(c->lp_val);
     dev_free(c->lp_idx);
     dev_free(c->lp_nan);
@@ -400,8 +407,20 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
     if (!rc) rc = dev_alloc((void **)&c->xq, sizeof(float) * m->q_dim);
     if (!rc) rc = dev_alloc((void **)&c->act, sizeof(float) * m->ffn);
     if (!rc) rc = dev_alloc((void **)&c->logits, sizeof(float) * m->V);
-    if (!rc) rc = dev_alloc((void **)&c->ap_o, sizeof(float) * (size_t)m->nh * c->n_splits * m->hd);
-    if (!rc) rc = dev_alloc((void **)&c->ap_ml, sizeof(float) * (size_t)m->nh * c->n_splits * 2);
+    if (!rc) rc = dev_alloc((void **)&c->xa, sizeof(float) * m->q_dim);
+    if (!rc) {
+        auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+        const size_t b_o = al(sizeof(float) * (size_t)m->nh * c->n_splits * m->hd);
+        const size_t b_ml = al(sizeof(float) * (size_t)m->nh * c->n_splits * 2);
+        rc = uc_take(b_o + b_ml + al(sizeof(unsigned) * m->nkv), &c->att_uc);
+        if (!rc) {
+            char *base = (char *)c->att_uc.p;
+            c->ap_o = (float *)base;
+            c->ap_ml = (float *)(base + b_o);
+            c->att_ctr = (unsigned *)(base + b_o + b_ml);
+            rc = launch_fill_u32(c->att_ctr, m->nkv, 0u, s);
+        }
+    }
     if (!rc) rc = dev_alloc((void **)&c->lp_val, sizeof(float) * nparts);
     if (!rc) rc = dev_alloc((void **)&c->lp_idx, sizeof(int) * nparts);
     if (!rc) rc = dev_alloc((void **)&c->lp_nan, sizeof(int) * nparts);
@@ -657,6 +676,8 @@ AttnArgs attn_args(scry_kv_cache c, int l) {
     a.v_cache = c->Vc(l);
     a.part_o = c->ap_o;
     a.part_ml = c->ap_ml;
+    a.merge_ctr = c->att_ctr;
+    a.xa = c->xa;
     a.state = c->state;
     a.n_heads = m->nh;
     a.n_kv = m->nkv;
@@ -670,12 +691,8 @@ GemvArgs o_args(scry_kv_cache c, int l) {
     scry_llama m = c->m;
     GemvArgs g;
     g.w = &m->layers[l].o;
+    g.x = c->xa;  // the attention output row (merged by the attention kernel)
     g.ldx = m->q_dim;
-    g.attn_part_o = c->ap_o;
-    g.attn_part_ml = c->ap_ml;
-    g.attn_nh = m->nh;
-    g.attn_ns = c->n_splits;
-    g.attn_hd = m->hd;
     g.y = c->x;
     g.ldy = m->h;
     g.resid = l == 0 ? nullptr : c->x;  // layer 0: residual is the embedding row
@@ -1397,8 +1414,7 @@ int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int i
     SCRY_TRY(cache_new(m, 16, &c));
     hipStream_t s = ctx().stream;
     int rc = launch_fill_f32(c->x, m->h, 1.0f, s);
-    if (!rc) rc = launch_fill_f32(c->ap_ml, (size_t)m->nh * c->n_splits * 2, 1.0f, s);
-    if (!rc) rc = launch_fill_f32(c->ap_o, (size_t)m->nh * c->n_splits * m->hd, 0.5f, s);
+    if (!rc) rc = launch_fill_f32(c->xa, m->q_dim, 0.5f, s);
     if (!rc) rc = launch_fill_f32(c->act, m->ffn, 0.25f, s);
     if (!rc) {
         c->hs->tok = 0;

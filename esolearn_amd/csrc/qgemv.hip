@@ -56,12 +56,10 @@ struct KArgs {
     float q_scale;
     float *part_val;
     int *part_idx, *part_nan;
-    const float *at_o, *at_ml;  // PRO_ATTN: attention split partials
-    int at_nh, at_ns, at_hd;
 };
 
 // activation prologues
-enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ATTN = 2 };
+enum { PRO_PLAIN = 0, PRO_NORM = 1 };
 
 // Activation row source for row mr (nullptr if mr >= m).
 __device__ __forceinline__ const float *act_row(const KArgs &a, int mr) {
@@ -127,7 +125,7 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
     // ---- 1. activation loads first, then the first PF weight chunks: waiting
     // for the activations then leaves the weight stream in flight.
     float4 xr[XP];
-    if (PRO != PRO_ATTN) load_x<XP>(act_row(a, m0), a.k, xr);
+    load_x<XP>(act_row(a, m0), a.k, xr);
     float4 nw[NORM ? XP : 1];
     if (NORM) load_x<XP>(a.norm_w, a.k, reinterpret_cast<float4(&)[XP]>(nw));
 
@@ -143,41 +141,6 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
         for (int r = 0; r < RW; r++) wb[d][r] = bload16(wr, woff[r] + (d << 10));
 
     // ---- 2. stage the activation rows (optionally RMSNorm'd) into LDS
-    if (PRO == PRO_ATTN) {
-        // Merge the attention splits (log-sum-exp rescaling) into the input
-        // row: x[h*hd + d] = sum_s O_s[d] e^(M_s - M) / sum_s L_s e^(M_s - M).
-        float *wm = xs + MT * kc + (B32 ? MT * (kc >> 4) : 0);  // [nh][ns]
-        const int nh = a.at_nh, ns = a.at_ns, hd = a.at_hd;
-        for (int h = tid; h < nh; h += TPB) {
-            const float *ml = a.at_ml + (size_t)h * ns * 2;
-            float M = -INFINITY;
-            for (int q = 0; q < ns; q++) M = fmaxf(M, ml[2 * q]);
-            float Ls = 0.f;
-            for (int q = 0; q < ns; q++)
-                if (ml[2 * q] != -INFINITY) Ls += ml[2 * q + 1] * expf(ml[2 * q] - M);
-            for (int q = 0; q < ns; q++)
-                wm[h * ns + q] = ml[2 * q] == -INFINITY ? 0.f : expf(ml[2 * q] - M) / Ls;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int p = 0; p < XP; p++) {
-            const int idx = (p << 10) + (tid << 2);
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (idx < a.k) {
-                const int h = idx / hd, d = idx - h * hd;
-                const float *po = a.at_o + (size_t)h * ns * hd + d;
-                for (int q = 0; q < ns; q++) {
-                    const float w = wm[h * ns + q];
-                    const float4 o4 = *(const float4 *)(po + (size_t)q * hd);
-                    v.x += w * o4.x;
-                    v.y += w * o4.y;
-                    v.z += w * o4.z;
-                    v.w += w * o4.w;
-                }
-            }
-            xr[p] = v;
-        }
-    }
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         if (mi > 0) load_x<XP>(act_row(a, m0 + mi), a.k, xr);
@@ -386,7 +349,6 @@ template <int EPI, int PRO, bool B32, int MT, int NCH>
 int launch_t(const KArgs &ka, hipStream_t s) {
     const int kc = ka.nch << 10;
     size_t lds = (size_t)MT * kc * sizeof(float) + (B32 ? (size_t)MT * (kc >> 4) * sizeof(float) : 0);
-    if (PRO == PRO_ATTN) lds += (size_t)ka.at_nh * ka.at_ns * sizeof(float);
     dim3 grid((ka.rows + RPB - 1) / RPB, (ka.m + MT - 1) / MT);
     hipLaunchKernelGGL((k_qgemv<EPI, PRO, B32, MT, NCH>), grid, dim3(TPB), lds, s, ka);
     SCRY_HIP(hipGetLastError());
@@ -419,21 +381,15 @@ int launch_mt(const KArgs &ka, hipStream_t s) {
 }
 
 template <int EPI>
-int launch_e(const KArgs &ka, bool norm, bool attn, bool b32, hipStream_t s) {
-    // decode epilogues QKV/SWIGLU/LOGITS always take the fused RMSNorm; the
-    // attention-merge prologue feeds only the residual epilogue (o_proj)
+int launch_e(const KArgs &ka, bool norm, bool b32, hipStream_t s) {
+    // decode epilogues QKV/SWIGLU/LOGITS always take the fused RMSNorm
     constexpr bool kNorm = (EPI == EPI_QKV || EPI == EPI_SWIGLU || EPI == EPI_LOGITS);
     if (norm != kNorm)
         return set_error(SCRY_ERR_INVALID, "qgemv: epilogue %d %s a fused RMSNorm", EPI,
                          kNorm ? "requires" : "does not take");
     if constexpr (kNorm) {
         return b32 ? launch_mt<EPI, PRO_NORM, true>(ka, s) : launch_mt<EPI, PRO_NORM, false>(ka, s);
-    } else if constexpr (EPI == EPI_RESID) {
-        if (attn)
-            return b32 ? launch_mt<EPI, PRO_ATTN, true>(ka, s) : launch_mt<EPI, PRO_ATTN, false>(ka, s);
-        return b32 ? launch_mt<EPI, PRO_PLAIN, true>(ka, s) : launch_mt<EPI, PRO_PLAIN, false>(ka, s);
     } else {
-        if (attn) return set_error(SCRY_ERR_INVALID, "qgemv: attention merge needs the residual epilogue");
         return b32 ? launch_mt<EPI, PRO_PLAIN, true>(ka, s) : launch_mt<EPI, PRO_PLAIN, false>(ka, s);
     }
 }
@@ -484,22 +440,14 @@ int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     ka.part_val = g.part_val;
     ka.part_idx = g.part_idx;
     ka.part_nan = g.part_nan;
-    ka.at_o = g.attn_part_o;
-    ka.at_ml = g.attn_part_ml;
-    ka.at_nh = g.attn_nh;
-    ka.at_ns = g.attn_ns;
-    ka.at_hd = g.attn_hd;
     const bool norm = g.norm_w != nullptr;
-    const bool attn = g.attn_part_o != nullptr;
     const bool b32 = w.s32 != nullptr;
-    if (attn && (g.attn_nh * g.attn_hd != w.k || g.attn_hd % 4 || g.m != 1))
-        return set_error(SCRY_ERR_INVALID, "qgemv: attention merge shape mismatch");
     switch (epi) {
-        case EPI_STORE: return launch_e<EPI_STORE>(ka, norm, attn, b32, s);
-        case EPI_RESID: return launch_e<EPI_RESID>(ka, norm, attn, b32, s);
-        case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(ka, norm, attn, b32, s);
-        case EPI_QKV: return launch_e<EPI_QKV>(ka, norm, attn, b32, s);
-        case EPI_LOGITS: return launch_e<EPI_LOGITS>(ka, norm, attn, b32, s);
+        case EPI_STORE: return launch_e<EPI_STORE>(ka, norm, b32, s);
+        case EPI_RESID: return launch_e<EPI_RESID>(ka, norm, b32, s);
+        case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(ka, norm, b32, s);
+        case EPI_QKV: return launch_e<EPI_QKV>(ka, norm, b32, s);
+        case EPI_LOGITS: return launch_e<EPI_LOGITS>(ka, norm, b32, s);
     }
     return set_error(SCRY_ERR_INVALID, "qgemv: unknown epilogue %d", epi);
 }
