@@ -145,7 +145,7 @@ int qmatmul(scry_buf a, scry_i8buf bq, float scale, const float *scales32, const
         rc = launch_qgemv(EPI_STORE, g, ctx().stream);
     } else {
         // prefill shapes: the activations as bf16 planes, then the MFMA GEMM
-        const int mp = prefill_rows_pad(m), ld = round_up(k, 32);
+        const int mp = prefill_rows_pad(m), ld = prefill_k_pad(k);
         unsigned short *pl = nullptr;
         rc = dev_alloc((void **)&pl, sizeof(unsigned short) * 2 * (size_t)mp * ld);
         if (!rc) rc = launch_fill_u32((unsigned *)pl, (size_t)mp * ld, 0u, ctx().stream);  // 2 planes of u16

@@ -238,7 +238,7 @@ struct PrefillSeqs {  // per sequence: its KV cache and first position
 };
 struct PrefillGemm {
     const Packed *w = nullptr;
-    const unsigned short *ahi = nullptr, *alo = nullptr;  // bf16 planes [Mp][lda]
+    const unsigned short *ahi = nullptr, *alo = nullptr;  // bf16 planes [Mp][lda], lda >= prefill_k_pad(k)
     int lda = 0, M = 0;
     float *c = nullptr;  // PF_STORE / PF_RESID output [M][ldc]
     int ldc = 0;
@@ -254,7 +254,8 @@ struct PrefillAttn {
     int ldo = 0, opad = 0;
 };
 enum { PF_STORE = 0, PF_RESID = 1, PF_SWIGLU = 2 };
-int prefill_rows_pad(int M);
+int prefill_rows_pad(int M);  // GEMM input plane rows for M activation rows
+int prefill_k_pad(int k);     // GEMM input plane columns (and zero padding) for k
 int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, const float *w, int k, float eps,
                       unsigned short *hi, unsigned short *lo, int ldp, float *outf, int ldf, hipStream_t s);
 int launch_split(const float *x, int ldx, int rows, int k, unsigned short *hi, unsigned short *lo, int ldp,

@@ -826,7 +826,7 @@ int check_ids(scry_llama m, const int64_t *ids, int n) {
 int prefill_ws(scry_llama m, int M, int n_seq) {
     auto &P = m->pf;
     const int Mp = prefill_rows_pad(M);
-    const int ld0 = round_up(std::max(m->h, m->q_dim), 32), ld1 = round_up(m->ffn, 32);
+    const int ld0 = prefill_k_pad(std::max(m->h, m->q_dim)), ld1 = prefill_k_pad(m->ffn);
     if (Mp <= P.Mp && P.ld0 == ld0 && P.ld1 == ld1) return SCRY_OK;
     dev_free(P.p0);
     dev_free(P.p1);
@@ -915,7 +915,7 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         at.ohi = h0;
         at.olo = l0;
         at.ldo = P.ld0;
-        at.opad = round_up(m->q_dim, 32);
+        at.opad = prefill_k_pad(m->q_dim);
         SCRY_TRY(launch_attn_prefill(at, n_seq, t, l, s));
         g.w = &Ly.o;
         g.c = P.x;
@@ -927,7 +927,7 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         g.ohi = h1;
         g.olo = l1;
         g.ldo = P.ld1;
-        g.opad = round_up(m->ffn, 32);
+        g.opad = prefill_k_pad(m->ffn);
         SCRY_TRY(launch_gemm(PF_SWIGLU, g, s));
         PrefillGemm d;
         d.ahi = h1;

@@ -15,7 +15,7 @@
 // far inside the 1e-3 logit bar.
 //
 // Data layout.  GEMM inputs are two bf16 planes [Mp][ld] (hi, lo): Mp = rows
-// rounded up to the M tile, ld = k rounded up to 32; the columns past k and
+// rounded up to the M tile, ld = k rounded up to the k step (64); the columns past k and
 // the rows past M are zero.  The kernel that produces an activation writes
 // its planes directly (RMSNorm, attention, SwiGLU), so no f32 copy of a GEMM
 // input exists.  Weights are the GEMV stream layout (one row of kp bytes per
@@ -93,12 +93,19 @@ __global__ void k_split(const float *__restrict__ x, int ldx, int rows, int k, i
 // instruction (16 x 32 A, 32 x 16 B, 16 x 16 D): lane l holds
 // A[l % 16][8 (l / 16) + e] and B[8 (l / 16) + e][l % 16] for e = 0..7, and
 // D[4 (l / 16) + r][l % 16] for r = 0..3.
-constexpr int BM = 128, BN = 256, BK = 32;
-constexpr int LDT = 40;  // LDS row stride in bf16 (80 B): 16-byte row reads hit distinct banks
+// One LDS stage (the next k step is held in registers while the current one
+// is consumed) keeps a workgroup at ~75 KB, so two fit on a CU: two waves per
+// SIMD hide each other's LDS and barrier latency (measured: 45-48% of the
+// bf16 issue rate, against 29-35% for a double-buffered stage at one wave
+// per SIMD).
+constexpr int BM = 128, BN = 256, BK = 64;
+constexpr int LDT = BK + 8;  // LDS row stride in bf16 (144 B): 16-byte row reads hit distinct banks
 constexpr int G_THREADS = 256;
 constexpr size_t A_TILE = (size_t)BM * LDT, B_TILE = (size_t)BN * LDT;  // u16 elements
-// dynamic LDS: [2 buffers] x (A hi, A lo, B) + [2][BN] block-32 scales
-constexpr size_t GEMM_LDS = 2 * (2 * A_TILE + B_TILE) * sizeof(u16) + 2 * BN * sizeof(float);
+constexpr int AC = BM * BK / 8 / G_THREADS;   // 16-byte A chunks per thread and plane
+constexpr int BC = BN * BK / 16 / G_THREADS;  // 16-byte weight chunks per thread
+// dynamic LDS: A hi, A lo, B + [BK/32][BN] block-32 scales
+constexpr size_t GEMM_LDS = (2 * A_TILE + B_TILE) * sizeof(u16) + (BK / 32) * BN * sizeof(float);
 
 enum { GE_STORE = PF_STORE, GE_RESID = PF_RESID, GE_SWIGLU = PF_SWIGLU };
 
@@ -149,68 +156,81 @@ __device__ __forceinline__ void bytes_to_bf16(u32x4 v, u32x4 &o0, u32x4 &o1) {
     o1 = u32x4{r[4], r[5], r[6], r[7]};
 }
 
+// (block-32: the per-block scaling needs a second accumulator tile, so one
+// workgroup per CU keeps it in registers)
 template <int EPI, bool B32>
-__global__ __launch_bounds__(G_THREADS) void k_gemm(GemmP p) {
+__global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
     extern __shared__ float4 gsm[];
-    u16 *lds = reinterpret_cast<u16 *>(gsm);
-    float *s_sc = reinterpret_cast<float *>(lds + 2 * (2 * A_TILE + B_TILE));
+    u16 *sa = reinterpret_cast<u16 *>(gsm);
+    u16 *sb = sa + 2 * A_TILE;
+    float *s_sc = reinterpret_cast<float *>(sb + B_TILE);  // [BK/32][BN]
     int mb, nbk;
     if (!gemm_tile(p, mb, nbk)) return;
     const int m0 = mb * BM, n0 = nbk * BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
-    // global -> LDS assignment: A chunk c = tid + 256 i (row c / 4, 8 bf16 at
-    // 8 (c % 4)); B chunk c = tid + 256 i (row c / 2, 16 bytes at 16 (c % 2))
+    // global -> LDS assignment: A chunk c = tid + 256 i (row c / (BK/8), 8 bf16
+    // at 8 (c % (BK/8))); B chunk c = tid + 256 i (row c / (BK/16), 16 bytes at
+    // 16 (c % (BK/16)))
+    constexpr int CPR = BK / 8, BPR = BK / 16;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (size_t)p.N * p.kp);
-    const u16 *ga[2][2];
-    unsigned boff[2];
+    const u16 *ga[2][AC];
+    unsigned boff[BC];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < AC; i++) {
         const int c = tid + 256 * i;
-        ga[0][i] = p.ahi + (size_t)(m0 + (c >> 2)) * p.lda + ((c & 3) << 3);
-        ga[1][i] = p.alo + (size_t)(m0 + (c >> 2)) * p.lda + ((c & 3) << 3);
-        const int n = n0 + (c >> 1);
-        boff[i] = n < p.N ? (unsigned)((size_t)n * p.kp + ((c & 1) << 4)) : 0x80000000u;
+        ga[0][i] = p.ahi + (size_t)(m0 + c / CPR) * p.lda + (c % CPR) * 8;
+        ga[1][i] = p.alo + (size_t)(m0 + c / CPR) * p.lda + (c % CPR) * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < BC; i++) {
+        const int c = tid + 256 * i;
+        const int n = n0 + c / BPR;
+        boff[i] = n < p.N ? (unsigned)((size_t)n * p.kp + (c % BPR) * 16) : 0x80000000u;
     }
     const bool s_ld = B32 && n0 + tid < p.N;
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(p.s32, B32 ? (size_t)p.N * p.nb * sizeof(float) : 0);
 
-    u32x4 ra[2][2], rb[2];
-    float rs = 0.f;
+    u32x4 ra[2][AC], rb[BC];
+    float rs[BK / 32];
     auto gload = [&](int kt) {
         const int k0 = kt * BK;
 #pragma unroll
         for (int pl = 0; pl < 2; pl++)
 #pragma unroll
-            for (int i = 0; i < 2; i++) ra[pl][i] = *(const u32x4 *)(ga[pl][i] + k0);
+            for (int i = 0; i < AC; i++) ra[pl][i] = *(const u32x4 *)(ga[pl][i] + k0);
 #pragma unroll
-        for (int i = 0; i < 2; i++) rb[i] = bload16(wr, boff[i] + (unsigned)k0);
-        if (B32)
-            rs = s_ld ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                      sr, (int)(((n0 + tid) * p.nb + kt) * 4), 0, 0))
-                      : 0.f;
+        for (int i = 0; i < BC; i++) rb[i] = bload16(wr, boff[i] + (unsigned)k0);
+        if (B32) {
+#pragma unroll
+            for (int j = 0; j < BK / 32; j++)  // blocks past the scales read as 0 (their A is 0)
+                rs[j] = s_ld ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                             sr, (int)(((n0 + tid) * p.nb + kt * (BK / 32) + j) * 4), 0, 0))
+                             : 0.f;
+        }
     };
-    auto lstore = [&](int buf) {
-        u16 *sa = lds + (size_t)buf * (2 * A_TILE + B_TILE);
-        u16 *sb = sa + 2 * A_TILE;
+    auto lstore = [&]() {
 #pragma unroll
         for (int pl = 0; pl < 2; pl++)
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
+            for (int i = 0; i < AC; i++) {
                 const int c = tid + 256 * i;
-                *(u32x4 *)(sa + pl * A_TILE + (c >> 2) * LDT + ((c & 3) << 3)) = ra[pl][i];
+                *(u32x4 *)(sa + pl * A_TILE + (c / CPR) * LDT + (c % CPR) * 8) = ra[pl][i];
             }
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < BC; i++) {
             const int c = tid + 256 * i;
             u32x4 o0, o1;
             bytes_to_bf16(rb[i], o0, o1);
-            u16 *d = sb + (c >> 1) * LDT + ((c & 1) << 4);
+            u16 *d = sb + (c / BPR) * LDT + (c % BPR) * 16;
             *(u32x4 *)d = o0;
             *(u32x4 *)(d + 8) = o1;
         }
-        if (B32) s_sc[buf * BN + tid] = rs;
+        if (B32) {
+#pragma unroll
+            for (int j = 0; j < BK / 32; j++) s_sc[j * BN + tid] = rs[j];
+        }
     };
 
     f32x4 acc[4][8];
@@ -220,44 +240,47 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm(GemmP p) {
         for (int j = 0; j < 8; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     gload(0);
-    lstore(0);
+    lstore();
     __syncthreads();
     const int fr = lane & 15, fk = (lane >> 4) << 3;
     for (int kt = 0; kt < p.nk; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < p.nk) gload(kt + 1);
-        const u16 *sa = lds + (size_t)buf * (2 * A_TILE + B_TILE);
-        const u16 *sb = sa + 2 * A_TILE;
-        bf16x8 ah[4], al[4];
+        if (kt + 1 < p.nk) gload(kt + 1);  // in flight while this step is consumed
 #pragma unroll
-        for (int tm = 0; tm < 4; tm++) {
-            const int r = wm * 64 + tm * 16 + fr;
-            ah[tm] = *(const bf16x8 *)(sa + r * LDT + fk);
-            al[tm] = *(const bf16x8 *)(sa + A_TILE + r * LDT + fk);
-        }
+        for (int ks = 0; ks < BK / 32; ks++) {
+            bf16x8 ah[4], al[4];
 #pragma unroll
-        for (int tn = 0; tn < 8; tn++) {
-            const int cn = wn * 128 + tn * 16 + fr;
-            const bf16x8 bv = *(const bf16x8 *)(sb + cn * LDT + fk);
-            if (B32) {
-                const float sc = s_sc[buf * BN + cn];
+            for (int tm = 0; tm < 4; tm++) {
+                const int r = wm * 64 + tm * 16 + fr;
+                ah[tm] = *(const bf16x8 *)(sa + r * LDT + ks * 32 + fk);
+                al[tm] = *(const bf16x8 *)(sa + A_TILE + r * LDT + ks * 32 + fk);
+            }
 #pragma unroll
-                for (int tm = 0; tm < 4; tm++) {
-                    f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bv, t, 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bv, t, 0, 0, 0);
+            for (int tn = 0; tn < 8; tn++) {
+                const int cn = wn * 128 + tn * 16 + fr;
+                const bf16x8 bv = *(const bf16x8 *)(sb + cn * LDT + ks * 32 + fk);
+                if (B32) {
+                    const float sc = s_sc[ks * BN + cn];
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[tm][tn][r] = fmaf(sc, t[r], acc[tm][tn][r]);
-                }
-            } else {
+                    for (int tm = 0; tm < 4; tm++) {
+                        f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+                        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bv, t, 0, 0, 0);
+                        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bv, t, 0, 0, 0);
 #pragma unroll
-                for (int tm = 0; tm < 4; tm++) {
-                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bv, acc[tm][tn], 0, 0, 0);
-                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bv, acc[tm][tn], 0, 0, 0);
+                        for (int r = 0; r < 4; r++) acc[tm][tn][r] = fmaf(sc, t[r], acc[tm][tn][r]);
+                    }
+                } else {
+#pragma unroll
+                    for (int tm = 0; tm < 4; tm++) {
+                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bv, acc[tm][tn], 0, 0, 0);
+                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bv, acc[tm][tn], 0, 0, 0);
+                    }
                 }
             }
         }
-        if (kt + 1 < p.nk) lstore(buf ^ 1);
+        if (kt + 1 < p.nk) {
+            __syncthreads();  // every wave is done with this step's LDS
+            lstore();
+        }
         __syncthreads();
     }
 
@@ -576,11 +599,12 @@ int gemm_t(const GemmP &p, hipStream_t s) {
 }  // namespace
 
 int prefill_rows_pad(int M) { return (M + BM - 1) / BM * BM; }
+int prefill_k_pad(int k) { return (k + BK - 1) / BK * BK; }
 
 int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, const float *w, int k, float eps,
                       u16 *hi, u16 *lo, int ldp, float *outf, int ldf, hipStream_t s) {
     if (rows <= 0) return SCRY_OK;
-    const int kpad = hi ? (k + 31) / 32 * 32 : k;
+    const int kpad = hi ? prefill_k_pad(k) : k;
     if (hi && kpad > ldp) return set_error(SCRY_ERR_INVALID, "norm_split: k %d exceeds plane stride %d", k, ldp);
     hipLaunchKernelGGL(k_norm_split, dim3(rows), dim3(256), 0, s, x, ldx, rstep, roff, w, k, eps, hi, lo, ldp,
                        kpad, outf, ldf);
@@ -588,7 +612,7 @@ int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, co
 }
 
 int launch_split(const float *x, int ldx, int rows, int k, u16 *hi, u16 *lo, int ldp, hipStream_t s) {
-    const int kpad = (k + 31) / 32 * 32;
+    const int kpad = prefill_k_pad(k);
     if (kpad > ldp) return set_error(SCRY_ERR_INVALID, "split: k %d exceeds plane stride %d", k, ldp);
     const size_t total = (size_t)rows * kpad;
     if (total == 0) return SCRY_OK;
@@ -600,11 +624,11 @@ int launch_split(const float *x, int ldx, int rows, int k, u16 *hi, u16 *lo, int
 int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
     const Packed &w = *g.w;
     if (w.kp % 16 || w.k > w.kp) return set_error(SCRY_ERR_INVALID, "gemm: bad packed layout");
-    const int kpad = (w.k + 31) / 32 * 32;
+    const int kpad = prefill_k_pad(w.k);
     if (kpad > g.lda || g.lda % 8) return set_error(SCRY_ERR_INVALID, "gemm: plane stride %d < k %d", g.lda, w.k);
     if (epi == GE_SWIGLU && (w.fused != 1 || w.rows % 4 || (w.rows >> 1) > g.ldo || g.opad > g.ldo))
         return set_error(SCRY_ERR_INVALID, "gemm: swiglu needs the fused gate/up layout");
-    if (w.s32 && w.nb * 32 < kpad) return set_error(SCRY_ERR_INVALID, "gemm: block-32 scales too short");
+    if (w.s32 && w.nb * 32 < w.k) return set_error(SCRY_ERR_INVALID, "gemm: block-32 scales too short");
     GemmP p{};
     p.ahi = g.ahi;
     p.alo = g.alo;
