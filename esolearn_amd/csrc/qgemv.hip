@@ -29,8 +29,8 @@ namespace {
 
 using namespace dev;
 
-constexpr int RW = 4;    // rows per wave
-constexpr int RPB = 16;  // rows per workgroup
+constexpr int RW = 4;    // rows per wave (default; the residual GEMVs pick fewer)
+constexpr int RPB = 16;  // rows per workgroup at RW
 constexpr int PF4 = 4;   // chunks in flight per row (runtime-chunk path, k <= 4096)
 
 struct KArgs {
@@ -76,11 +76,11 @@ __device__ __forceinline__ void load_x(const float *src, int k, float4 (&xr)[XP]
 }
 
 
-// One 1024-wide k chunk for RW rows and MT activation rows.
-template <int MT, bool B32>
-__device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RW], int c, const float *xs, int kc,
+// One 1024-wide k chunk for RWT rows and MT activation rows.
+template <int MT, bool B32, int RWT>
+__device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RWT], int c, const float *xs, int kc,
                                           const float *xg, __amdgpu_buffer_rsrc_t sr, int nb,
-                                          int row0, int lane, float (&acc)[MT][RW]) {
+                                          int row0, int lane, float (&acc)[MT][RWT]) {
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         const float *xb = xs + mi * kc + (c << 10) + (lane << 2);
@@ -90,13 +90,13 @@ __device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RW], int c, const flo
         const float4 x3 = *(const float4 *)(xb + 768);
         if (!B32) {
 #pragma unroll
-            for (int r = 0; r < RW; r++) acc[mi][r] = dot16(w[r], x0, x1, x2, x3, acc[mi][r]);
+            for (int r = 0; r < RWT; r++) acc[mi][r] = dot16(w[r], x0, x1, x2, x3, acc[mi][r]);
         } else {
             // block-32: this lane's 16 bytes are half of k-block blk
             const float gs = xg[mi * (kc >> 4) + (c << 6) + lane];
             const int blk = ((c << 10) + (lane << 4)) >> 5;
 #pragma unroll
-            for (int r = 0; r < RW; r++) {
+            for (int r = 0; r < RWT; r++) {
                 const float p = dot16(w[r], x0, x1, x2, x3, 0.f);
                 const float sc = __builtin_bit_cast(
                     float, __builtin_amdgcn_raw_buffer_load_b32(sr, ((row0 + r) * nb + blk) * 4, 0, 0));
@@ -106,11 +106,14 @@ __device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RW], int c, const flo
     }
 }
 
-template <int EPI, int PRO, bool B32, int MT, int NCH>
+// RWT rows per wave (4 * RWT per workgroup), PFT chunks in flight per row.
+template <int EPI, int PRO, bool B32, int MT, int NCH, int RWT = RW, int PFT = PF4>
 __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
+    static_assert(RWT == RW || EPI == EPI_RESID || EPI == EPI_STORE,
+                  "the SwiGLU, QKV and logits epilogues work on 4-row groups");
     constexpr bool NORM = PRO == PRO_NORM;
     constexpr int XP = NCH > 0 ? NCH : 16;
-    constexpr int PF = PF4;
+    constexpr int PF = PFT;
     extern __shared__ float4 dyn4[];
     float *xs = reinterpret_cast<float *>(dyn4);
     const int kc = (NCH > 0 ? NCH : a.nch) << 10;
@@ -119,7 +122,7 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
     __shared__ float sx_sh[MT];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row0 = blockIdx.x * RPB + wave * RW;
+    const int row0 = blockIdx.x * (4 * RWT) + wave * RWT;
     const int m0 = blockIdx.y * MT;
 
     // ---- 1. activation loads first, then the first PF weight chunks: waiting
@@ -130,15 +133,15 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
     if (NORM) load_x<XP>(a.norm_w, a.k, reinterpret_cast<float4(&)[XP]>(nw));
 
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.W, (size_t)a.rows * a.kp);
-    unsigned woff[RW];
+    unsigned woff[RWT];
 #pragma unroll
-    for (int r = 0; r < RW; r++)  // rows past the end read zeros (never stored)
+    for (int r = 0; r < RWT; r++)  // rows past the end read zeros (never stored)
         woff[r] = (row0 + r) < a.rows ? (unsigned)((row0 + r) * a.kp + (lane << 4)) : 0x80000000u;
-    u32x4 wb[PF][RW];
+    u32x4 wb[PF][RWT];
 #pragma unroll
     for (int d = 0; d < PF; d++)
 #pragma unroll
-        for (int r = 0; r < RW; r++) wb[d][r] = bload16(wr, woff[r] + (d << 10));
+        for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + (d << 10));
 
     // ---- 2. stage the activation rows (optionally RMSNorm'd) into LDS
 #pragma unroll
@@ -195,11 +198,11 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
     }
 
     // ---- 3. stream the weights
-    float acc[MT][RW];
+    float acc[MT][RWT];
 #pragma unroll
     for (int mi = 0; mi < MT; mi++)
 #pragma unroll
-        for (int r = 0; r < RW; r++) acc[mi][r] = 0.f;
+        for (int r = 0; r < RWT; r++) acc[mi][r] = 0.f;
     const __amdgpu_buffer_rsrc_t sr =
         make_rsrc(a.s32, B32 ? (size_t)a.rows * a.nb * sizeof(float) : 0);
 
@@ -207,10 +210,10 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
         // straight-line stream: chunk c computes from wb[c % PF], then refills it
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
-            chunk_fma<MT, B32>(wb[c % PF], c, xs, kc, xg, sr, a.nb, row0, lane, acc);
+            chunk_fma<MT, B32, RWT>(wb[c % PF], c, xs, kc, xg, sr, a.nb, row0, lane, acc);
             if (c + PF < NCH) {
 #pragma unroll
-                for (int r = 0; r < RW; r++) wb[c % PF][r] = bload16(wr, woff[r] + ((c + PF) << 10));
+                for (int r = 0; r < RWT; r++) wb[c % PF][r] = bload16(wr, woff[r] + ((c + PF) << 10));
             }
         }
     } else {
@@ -219,10 +222,10 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
             for (int d = 0; d < PF; d++) {
                 const int c = c0 + d;
                 if (c < a.nch) {
-                    chunk_fma<MT, B32>(wb[d], c, xs, kc, xg, sr, a.nb, row0, lane, acc);
+                    chunk_fma<MT, B32, RWT>(wb[d], c, xs, kc, xg, sr, a.nb, row0, lane, acc);
                     if (c + PF < a.nch) {
 #pragma unroll
-                        for (int r = 0; r < RW; r++) wb[d][r] = bload16(wr, woff[r] + ((c + PF) << 10));
+                        for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + ((c + PF) << 10));
                     }
                 }
             }
@@ -230,12 +233,12 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
     }
 
     // ---- 4. reduce over the wave, remove the +128 bias, apply the scale
-    float val[MT][RW];
+    float val[MT][RWT];
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         const float corr = 128.f * sx_sh[mi];
 #pragma unroll
-        for (int r = 0; r < RW; r++) {
+        for (int r = 0; r < RWT; r++) {
             const float s = wave_sum(acc[mi][r]);
             if (B32) {
                 val[mi][r] = s;
@@ -253,7 +256,7 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
             const int mr = m0 + mi;
             // lane r stores row r (static indices: no private-array select)
 #pragma unroll
-            for (int r = 0; r < RW; r++) {
+            for (int r = 0; r < RWT; r++) {
                 const int row = row0 + r;
                 if (lane == r && mr < a.m && row < a.rows) {
                     float v = val[mi][r];
@@ -345,25 +348,39 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
     }
 }
 
-template <int EPI, int PRO, bool B32, int MT, int NCH>
+template <int EPI, int PRO, bool B32, int MT, int NCH, int RWT = RW, int PFT = PF4>
 int launch_t(const KArgs &ka, hipStream_t s) {
     const int kc = ka.nch << 10;
     size_t lds = (size_t)MT * kc * sizeof(float) + (B32 ? (size_t)MT * (kc >> 4) * sizeof(float) : 0);
-    dim3 grid((ka.rows + RPB - 1) / RPB, (ka.m + MT - 1) / MT);
-    hipLaunchKernelGGL((k_qgemv<EPI, PRO, B32, MT, NCH>), grid, dim3(TPB), lds, s, ka);
+    dim3 grid((ka.rows + 4 * RWT - 1) / (4 * RWT), (ka.m + MT - 1) / MT);
+    hipLaunchKernelGGL((k_qgemv<EPI, PRO, B32, MT, NCH, RWT, PFT>), grid, dim3(TPB), lds, s, ka);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }
 
 // NCH = compile-time chunk count (straight-line stream) for the k on the
 // Llama path; 0 = runtime loop for any other k <= 16384.
+// The residual GEMVs of the decode step (o_proj, down_proj: 4096 outputs)
+// have few rows per launch: fewer rows per wave put more waves on each CU,
+// and for long rows every chunk is requested at once (measured on the 7B
+// shapes: o 5.6 -> 5.3 us with 2 rows per wave, down 12.9 -> 10.5 us with one
+// row per wave and all 11 chunks in flight).
 template <int EPI, int PRO, bool B32, int MT>
 int launch_nch(const KArgs &ka, hipStream_t s) {
+    constexpr bool resid1 = EPI == EPI_RESID && MT == 1;
     switch (ka.nch) {
         case 1: return launch_t<EPI, PRO, B32, MT, 1>(ka, s);
-        case 4: return launch_t<EPI, PRO, B32, MT, 4>(ka, s);
-        case 11: if (MT == 1) return launch_t<EPI, PRO, B32, MT, 11>(ka, s); break;
-        case 14: if (MT == 1) return launch_t<EPI, PRO, B32, MT, 14>(ka, s); break;
+        case 4:
+            if constexpr (resid1) return launch_t<EPI, PRO, B32, MT, 4, 2, 4>(ka, s);
+            return launch_t<EPI, PRO, B32, MT, 4>(ka, s);
+        case 11:
+            if constexpr (resid1) return launch_t<EPI, PRO, B32, MT, 11, 1, 11>(ka, s);
+            if (MT == 1) return launch_t<EPI, PRO, B32, MT, 11>(ka, s);
+            break;
+        case 14:
+            if constexpr (resid1) return launch_t<EPI, PRO, B32, MT, 14, 1, 14>(ka, s);
+            if (MT == 1) return launch_t<EPI, PRO, B32, MT, 14>(ka, s);
+            break;
         default: break;
     }
     return launch_t<EPI, PRO, B32, MT, 0>(ka, s);
