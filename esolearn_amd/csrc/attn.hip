@@ -50,7 +50,7 @@ __device__ __forceinline__ float group_sum(float v) {
 template <int G, int NR>
 __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
     constexpr int P = 64 / G;  // positions per load instruction
-    constexpr int U = 4;       // load instructions per step
+    constexpr int U = 12;      // load instructions per step (all of a split in one round at ~770 positions)
     constexpr int PI = P * U;  // positions per wave step
     constexpr int SLOTS = 4 * P;
     extern __shared__ float sm[];

@@ -195,3 +195,88 @@ def test_7b_dims_prefill_vs_decode(hip):
     assert e < LOGIT_TOL
     assert (pt == kt).all()
     hm.free()
+
+
+def test_forward_block32_vs_oracle(orc, hip):
+    """Block-32 scales through the prefill GEMM (the per-block scaled MFMA path)."""
+    cfg = dict(TINY, n_layers=2)
+    om = orc.Llama(orc.LlamaConfig(**cfg), 0, quantize=True, block32=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), 0, hip.QUANT_BLOCK32)
+    toks = orc.prompt_ids(2, 24, cfg["vocab_size"])
+    orc.set_threads(8)
+    ref = om.forward(toks, mode=2)  # mode 2: the oracle's block-32 arithmetic
+    orc.set_threads(0)
+    got = hm.forward(toks)
+    err = row_err(got, ref)
+    print(f"[err] block-32 forward {err:.3e}", flush=True)
+    assert err < LOGIT_TOL
+    hm.free()
+    om.close()
+
+
+@pytest.mark.parametrize("seq", [1, 129])
+def test_forward_single_and_ragged_rows(orc, hip, seq):
+    """seq = 1 (one GEMM row) and 129 (one row past the 128-row tile)."""
+    cfg = dict(vocab_size=96, hidden_size=256, intermediate_size=320, n_layers=2, n_heads=4,
+               n_kv_heads=2, max_seq_len=256, rope_theta=10000.0, tie_word_embeddings=False)
+    om = orc.Llama(orc.LlamaConfig(**cfg), 5, quantize=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), 5)
+    toks = orc.prompt_ids(4, seq, 96)
+    assert row_err(hm.forward(toks), om.forward(toks)) < LOGIT_TOL
+    hm.free()
+    om.close()
+
+
+def test_prefill_after_decode_positions(orc, hip):
+    """A cache filled token by token for 5 positions, then 20 more by prefill:
+    the last logits equal the oracle's all-token-by-token path."""
+    cfg = dict(vocab_size=80, hidden_size=192, intermediate_size=256, n_layers=2, n_heads=6,
+               n_kv_heads=3, max_seq_len=64, rope_theta=10000.0, tie_word_embeddings=False)
+    om = orc.Llama(orc.LlamaConfig(**cfg), 9, quantize=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), 9)
+    toks = orc.prompt_ids(6, 25, 80)
+    oc = om.new_cache(32)
+    for p, t in enumerate(toks):
+        ref = om.forward_with_cache(oc, t, p)
+    c = hm.new_llama_kv_cache(32)
+    for p in range(5):
+        hm.forward_with_llama_cache(int(toks[p]), p, c)
+    last = hm.prefill([c], toks[None, 5:])[0]
+    assert c.seq_len == 25
+    assert rel_err(last, ref) < LOGIT_TOL
+    c.free()
+    hm.free()
+    om.close()
+
+
+def test_prefill_argument_errors(hip):
+    cfg = hip.LlamaConfig(vocab_size=64, hidden_size=128, intermediate_size=128, n_layers=1,
+                          n_heads=2, n_kv_heads=2, max_seq_len=32, rope_theta=10000.0,
+                          tie_word_embeddings=False)
+    hm = hip.LlamaModel.new_random(cfg, 1)
+    c = hm.new_llama_kv_cache(16)
+    with pytest.raises(hip.ScryHipError) as ei:  # past the cache capacity
+        hm.prefill([c], np.zeros((1, 17), np.int64))
+    assert "exceed" in str(ei.value)
+    with pytest.raises(hip.ScryHipError):  # token id out of range
+        hm.prefill([c], np.full((1, 4), 64, np.int64))
+    with pytest.raises(hip.ScryHipError):  # the same cache twice
+        hm.prefill([c, c], np.zeros((2, 4), np.int64))
+    many = [hm.new_llama_kv_cache(8) for _ in range(17)]
+    with pytest.raises(hip.ScryHipError):  # more sequences than one prefill takes
+        hm.prefill(many, np.zeros((17, 2), np.int64))
+    assert c.seq_len == 0  # failed calls leave the cache untouched
+    for x in many:
+        x.free()
+    c.free()
+    hm.free()
+
+
+def test_generate_prefill_one_token_prompt(hip):
+    """A one-token prompt has nothing to prefill: both paths are the same run."""
+    cfg = hip.LlamaConfig(**TINY)
+    hm = hip.LlamaModel.new_random(cfg, 0)
+    a = hm.generate_greedy([17], 12, prefill=True)
+    b = hm.generate_greedy([17], 12)
+    assert (a == b).all()
+    hm.free()
