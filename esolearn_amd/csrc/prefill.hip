@@ -295,16 +295,20 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + wm * 64 + tm * 16 + ((lane >> 4) << 2) + r;
                 if (EPI == GE_SWIGLU) {
-                    // fused gate/up rows of a group of 4: gate[2t], gate[2t+1], up[2t], up[2t+1]
+                    // fused gate/up rows of a group of 4: gate[2t], gate[2t+1],
+                    // up[2t], up[2t+1] in lanes 4q .. 4q+3; lane 4q stores the
+                    // two outputs 2t, 2t+1 of its group as one 32-bit word per plane
                     const bool gate = (n & 2) == 0;
                     const float v = acc[tm][tn][r] * (gate ? s_a : s_b);
                     const float o = __shfl_xor(v, 2);
-                    if (gate && m < p.M && n < p.N) {
-                        const int col = ((n >> 2) << 1) | (n & 1);
-                        u16 a, b;
-                        split_bf16(silu_f(v) * o, a, b);  // cpu.rs:666-678
-                        p.ohi[(size_t)m * p.ldo + col] = a;
-                        p.olo[(size_t)m * p.ldo + col] = b;
+                    u16 a = 0, b = 0;
+                    if (gate) split_bf16(silu_f(v) * o, a, b);  // cpu.rs:666-678
+                    const unsigned hw = (unsigned)a | ((unsigned)__shfl_xor((int)a, 1) << 16);
+                    const unsigned lw = (unsigned)b | ((unsigned)__shfl_xor((int)b, 1) << 16);
+                    if ((n & 3) == 0 && m < p.M && n < p.N) {  // N is a multiple of 4
+                        const size_t at = (size_t)m * p.ldo + (n >> 1);
+                        *(unsigned *)(p.ohi + at) = hw;
+                        *(unsigned *)(p.olo + at) = lw;
                     }
                 } else if (m < p.M && n < p.N) {
                     float v = acc[tm][tn][r] * s_a;
@@ -626,7 +630,7 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
     if (w.kp % 16 || w.k > w.kp) return set_error(SCRY_ERR_INVALID, "gemm: bad packed layout");
     const int kpad = prefill_k_pad(w.k);
     if (kpad > g.lda || g.lda % 8) return set_error(SCRY_ERR_INVALID, "gemm: plane stride %d < k %d", g.lda, w.k);
-    if (epi == GE_SWIGLU && (w.fused != 1 || w.rows % 4 || (w.rows >> 1) > g.ldo || g.opad > g.ldo))
+    if (epi == GE_SWIGLU && (w.fused != 1 || w.rows % 4 || (w.rows >> 1) > g.ldo || g.opad > g.ldo || g.ldo % 2))
         return set_error(SCRY_ERR_INVALID, "gemm: swiglu needs the fused gate/up layout");
     if (w.s32 && w.nb * 32 < w.k) return set_error(SCRY_ERR_INVALID, "gemm: block-32 scales too short");
     GemmP p{};
