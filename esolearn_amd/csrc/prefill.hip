@@ -470,10 +470,10 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttn a, PrefillSeqs
 //     dims 16 t + 4 (l / 16) + r.
 // fp32 products and accumulation: the arithmetic of the VALU kernel above,
 // in another summation order.
-constexpr int MQ = 64, MK = 64;
+constexpr int MQW = 8, MQ = 16 * MQW, MK = 64;  // waves (16 query rows each) per workgroup; keys per tile
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_mfma(PrefillAttn a, PrefillSeqs t, int l) {
+__global__ __launch_bounds__(64 * MQW) void k_attn_mfma(PrefillAttn a, PrefillSeqs t, int l) {
     constexpr int NC = HD / 4, NT = HD / 16, LD = HD + 4;
     extern __shared__ float4 am4[];
     float *sk = reinterpret_cast<float *>(am4);  // [MK][LD]
@@ -503,7 +503,7 @@ __global__ __launch_bounds__(256) void k_attn_mfma(PrefillAttn a, PrefillSeqs t,
     const float *vc = t.v[s] + (size_t)l * t.ls[s] + (size_t)kvh * HD;
     for (int k0 = 0; k0 < kend; k0 += MK) {
         __syncthreads();
-        for (int idx = tid; idx < MK * (HD / 4); idx += 256) {
+        for (int idx = tid; idx < MK * (HD / 4); idx += 64 * MQW) {
             const int j = idx / (HD / 4), c4 = idx - j * (HD / 4);
             float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
             if (k0 + j < kend) {
@@ -583,7 +583,7 @@ int attn_mfma_t(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hi
         attr = true;
     }
     const dim3 grid((a.seq + MQ - 1) / MQ, a.nh, n_seq);
-    hipLaunchKernelGGL(k_attn_mfma<HD>, grid, dim3(256), lds, s, a, t, l);
+    hipLaunchKernelGGL(k_attn_mfma<HD>, grid, dim3(64 * MQW), lds, s, a, t, l);
     PF_LAUNCH_CHECK();
 }
 

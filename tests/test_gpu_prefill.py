@@ -97,7 +97,7 @@ def test_forward_tiny_vs_oracle(orc, hip):
     orc.set_threads(0)
 
 
-@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 4), (4, 1, 128), (16, 4, 64), (6, 6, 48)])
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 4), (4, 1, 128), (16, 4, 64), (6, 6, 48), (8, 8, 32)])
 def test_prefill_cache_matches_decode(orc, hip, nh, nkv, hd):
     """Prefill of 70 tokens: K/V rows equal the token-by-token path's, the last
     logits match the oracle's cache path."""
