@@ -171,7 +171,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=16, help="untimed decode steps (W)")
     ap.add_argument("--prompt-len", type=int, default=512)
     ap.add_argument("--proj-iters", type=int, default=96)
-    ap.add_argument("--cpu-tokens", type=int, default=3)
+    ap.add_argument("--cpu-tokens", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--host-init", action="store_true",
                     help="draw the random weights on the host (slow) instead of the GPU")
