@@ -280,3 +280,21 @@ def test_generate_prefill_one_token_prompt(hip):
     b = hm.generate_greedy([17], 12)
     assert (a == b).all()
     hm.free()
+
+
+def test_llama3_rope_scaling_decode_and_forward(orc, hip):
+    """Llama-3 RoPE frequency scaling (compute_rope_freqs, llama.rs:1035-1067)
+    with GQA: greedy decode and the batched forward against the oracle."""
+    cfg = dict(vocab_size=128, hidden_size=256, intermediate_size=384, n_layers=2, n_heads=4,
+               n_kv_heads=1, max_seq_len=128, rope_theta=500000.0, tie_word_embeddings=False,
+               rope_scaling=(8.0, 1.0, 4.0, 64))
+    om = orc.Llama(orc.LlamaConfig(**cfg), 13, quantize=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), 13)
+    prompt = orc.prompt_ids(7, 40, 128)
+    ref_t, ref_l = om.generate_greedy(prompt, 16, mode=1, want_logits=True)
+    got_t, got_l = hm.generate_greedy(prompt, 16, want_logits=True, prefill=True)
+    assert max(rel_err(got_l[i], ref_l[i]) for i in range(16)) < LOGIT_TOL
+    assert (got_t == ref_t).all()
+    assert row_err(hm.forward(prompt), om.forward(prompt)) < LOGIT_TOL
+    hm.free()
+    om.close()
