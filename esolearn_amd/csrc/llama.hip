@@ -79,17 +79,22 @@ struct HostStage {
 struct UcBlock {
     void *p;
     size_t bytes;
+    int device;
 };
 std::vector<UcBlock> &uc_pool() {
     static std::vector<UcBlock> pool;
     return pool;
 }
 
+// A block of at least `bytes` on the current device: the smallest pooled one
+// that fits, else a new allocation.
 int uc_take(size_t bytes, UcBlock *out) {
     auto &pool = uc_pool();
+    const int dev = ctx().device;
     size_t best = pool.size();
     for (size_t i = 0; i < pool.size(); i++)
-        if (pool[i].bytes >= bytes && (best == pool.size() || pool[i].bytes < pool[best].bytes)) best = i;
+        if (pool[i].device == dev && pool[i].bytes >= bytes && (best == pool.size() || pool[i].bytes < pool[best].bytes))
+            best = i;
     if (best < pool.size()) {
         *out = pool[best];
         pool.erase(pool.begin() + (long)best);
@@ -101,13 +106,13 @@ int uc_take(size_t bytes, UcBlock *out) {
         (void)hipGetLastError();
         return set_error(SCRY_ERR_OOM, "uncached allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
     }
-    *out = UcBlock{p, bytes};
+    *out = UcBlock{p, bytes, dev};
     return SCRY_OK;
 }
 
 void uc_give(UcBlock &b) {
     if (b.p) uc_pool().push_back(b);
-    b = UcBlock{nullptr, 0};
+    b = UcBlock{nullptr, 0, -1};
 }
 
 // Resources of the persistent decode kernel (decode.hip) for one session.
@@ -119,7 +124,7 @@ struct DecodeRes {
     DecArgs args{};
     DecLayer *layers = nullptr;  // device table
     unsigned version = ~0u;      // model version the table was built for
-    UcBlock uc{nullptr, 0};      // holds the four buffers below
+    UcBlock uc{nullptr, 0, -1};  // holds the four buffers below
     float *ws = nullptr;         // activations exchanged between workgroups
     unsigned *lm_part = nullptr; // LM-head argmax partials
     unsigned *ctr = nullptr;     // completion counters
@@ -140,7 +145,7 @@ struct scry_kv_cache_s {
     float *x = nullptr, *xq = nullptr, *act = nullptr, *logits = nullptr;
     // decode attention split partials and per-KV-group arrival counters
     // (uncached: the last split merges them), and the merged output row
-    UcBlock att_uc{nullptr, 0};
+    UcBlock att_uc{nullptr, 0, -1};
     float *ap_o = nullptr, *ap_ml = nullptr;
     unsigned *att_ctr = nullptr;
     float *xa = nullptr;

@@ -628,6 +628,8 @@ int launch_split(const float *x, int ldx, int rows, int k, u16 *hi, u16 *lo, int
 int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
     const Packed &w = *g.w;
     if (w.kp % 16 || w.k > w.kp) return set_error(SCRY_ERR_INVALID, "gemm: bad packed layout");
+    if (w.bytes() >= 0x7fffffffull)  // buffer offsets are 32-bit
+        return set_error(SCRY_ERR_UNSUPPORTED, "gemm: %zu weight bytes (limit 2 GiB per tensor)", w.bytes());
     const int kpad = prefill_k_pad(w.k);
     if (kpad > g.lda || g.lda % 8) return set_error(SCRY_ERR_INVALID, "gemm: plane stride %d < k %d", g.lda, w.k);
     if (epi == GE_SWIGLU && (w.fused != 1 || w.rows % 4 || (w.rows >> 1) > g.ldo || g.opad > g.ldo || g.ldo % 2))

@@ -416,6 +416,8 @@ int launch_e(const KArgs &ka, bool norm, bool b32, hipStream_t s) {
 int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     const Packed &w = *g.w;
     if (w.kp % 16 != 0 || w.k > w.kp) return set_error(SCRY_ERR_INVALID, "qgemv: bad packed layout");
+    if (w.bytes() >= 0x7fffffffull)  // buffer offsets are 32-bit
+        return set_error(SCRY_ERR_UNSUPPORTED, "qgemv: %zu weight bytes (limit 2 GiB per tensor)", w.bytes());
     const int nch = (w.k + 1023) / 1024;
     if (nch > 16 || (size_t)nch * 1024 * sizeof(float) * (w.s32 ? 17 : 16) / 16 > 64 * 1024)
         return set_error(SCRY_ERR_UNSUPPORTED, "qgemv: k=%d exceeds the LDS activation stage", w.k);
