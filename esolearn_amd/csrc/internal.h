@@ -114,11 +114,20 @@ struct GemvArgs {
     DevState *state = nullptr;
     const float *norm_w = nullptr;  // RMSNorm weight -> fused RMSNorm prologue
     float eps = 1e-5f;
+    // pre-scaled RMSNorm input: x holds x*g, and the residual GEMV that wrote
+    // it left n_ss per-workgroup partial sums of x^2 (x itself) in ss_in
+    const double *ss_in = nullptr;
+    int n_ss = 0;
     // outputs
     float *y = nullptr;
     int ldy = 0;
     const float *resid = nullptr;   // EPI_RESID source (may alias y); nullptr -> embed row
     const float *bias = nullptr;    // EPI_STORE optional bias
+    // EPI_RESID, for the next RMSNorm'd GEMV: y*g_next and per-workgroup
+    // sums of y^2 (qgemv_blocks entries)
+    float *xg_out = nullptr;
+    const float *g_next = nullptr;
+    double *ss_out = nullptr;
     // EPI_QKV
     float *q_out = nullptr, *k_cache = nullptr, *v_cache = nullptr;
     const float2 *rope_cs = nullptr;  // [max_pos][head_dim/2] (cos, sin)
@@ -134,6 +143,9 @@ struct GemvArgs {
 };
 
 int launch_qgemv(int epi, const GemvArgs &a, hipStream_t s);
+// workgroups of one launch_qgemv launch (= EPI_LOGITS argmax partials, EPI_RESID
+// sum-of-squares partials)
+int qgemv_blocks(int epi, const Packed &w, int m);
 // matmul_i8_f32 with more activation rows than this runs as the MFMA GEMM
 constexpr int GEMV_MAX_M = 16;
 int launch_logits_finish(const GemvArgs &a, hipStream_t s);

@@ -45,6 +45,28 @@ __device__ __forceinline__ double wave_sum_d(double v) {
     return v;
 }
 
+// f64 wave sum over DPP row operations (no LDS permutes); the total is valid
+// in lane 63 (returned to every lane by readlane)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(u & 0xffffffffu), CTRL, ROW_MASK, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(u >> 32), CTRL, ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ double wave_sum_d_dpp(double v) {
+    v += dpp_d<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v += dpp_d<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v += dpp_d<0x141, 0xf>(v);  // row_half_mirror
+    v += dpp_d<0x140, 0xf>(v);  // row_mirror: every lane holds its row's sum
+    v += dpp_d<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_d<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = __builtin_amdgcn_readlane((int)(u & 0xffffffffu), 63);
+    const unsigned hi = __builtin_amdgcn_readlane((int)(u >> 32), 63);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
 // block-wide f64 sum (all 256 threads call it; result valid in every thread)
 __device__ __forceinline__ double block_sum_d(double v, double *red) {
     v = wave_sum_d(v);

@@ -143,6 +143,10 @@ struct scry_kv_cache_s {
     int64_t *tokens = nullptr;
     int tokens_len = 0;
     float *x = nullptr, *xq = nullptr, *act = nullptr, *logits = nullptr;
+    // the residual row times the next RMSNorm weight, and the per-workgroup
+    // sums of squares of the residual row (written by the residual GEMVs)
+    float *xg = nullptr;
+    double *ss = nullptr;
     // decode attention split partials and per-KV-group arrival counters
     // (uncached: the last split merges them), and the merged output row
     UcBlock att_uc{nullptr, 0, -1};
@@ -373,6 +377,8 @@ void cache_free(scry_kv_cache c) {
     dev_free(c->state);
     dev_free(c->tokens);
     dev_free(c->x);
+    dev_free(c->xg);
+    dev_free(c->ss);
     dev_free(c->xq);
     dev_free(c->act);
     dev_free(c->logits);
@@ -402,13 +408,16 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
     attn_pick_splits(m->nkv, max_seq, &c->n_splits, &c->max_chunk);
     hipStream_t s = ctx().stream;
     const size_t kvn = (size_t)m->L * 2 * max_seq * m->kv_dim;
-    const int nparts = (m->V + 15) / 16;
+    const int nparts = qgemv_blocks(EPI_LOGITS, m->lm, 1);
+    const int n_ss = std::max(qgemv_blocks(EPI_RESID, m->layers[0].o, 1), qgemv_blocks(EPI_RESID, m->layers[0].down, 1));
     int rc = dev_alloc((void **)&c->kv, sizeof(float) * kvn);
     if (!rc) rc = launch_fill_f32(c->kv, kvn, 0.f, s);  // LlamaLayerKvCache::new zeros
     if (!rc) rc = dev_alloc((void **)&c->rope_cs, sizeof(float2) * (size_t)max_seq * (m->hd / 2));
     if (!rc) rc = dev_alloc((void **)&c->state, sizeof(DevState));
     if (!rc) rc = dev_alloc((void **)&c->tokens, sizeof(int64_t) * c->tokens_len);
     if (!rc) rc = dev_alloc((void **)&c->x, sizeof(float) * m->h);
+    if (!rc) rc = dev_alloc((void **)&c->xg, sizeof(float) * m->h);
+    if (!rc) rc = dev_alloc((void **)&c->ss, sizeof(double) * n_ss);
     if (!rc) rc = dev_alloc((void **)&c->xq, sizeof(float) * m->q_dim);
     if (!rc) rc = dev_alloc((void **)&c->act, sizeof(float) * m->ffn);
     if (!rc) rc = dev_alloc((void **)&c->logits, sizeof(float) * m->V);
@@ -651,17 +660,36 @@ int decode_use_persistent(scry_kv_cache c, bool *use) {
     return SCRY_OK;
 }
 
+// Input of an RMSNorm'd GEMV that follows the residual GEMV on weights w: the
+// row it left pre-multiplied by this norm's weight, and its partial sums of squares.
+void pre_normed(scry_kv_cache c, const Packed &w, GemvArgs *g) {
+    g->x = c->xg;
+    g->ss_in = c->ss;
+    g->n_ss = qgemv_blocks(EPI_RESID, w, 1);
+}
+
+// Residual GEMV outputs for the RMSNorm'd GEMV that follows it.
+void next_norm(scry_kv_cache c, const float *g_next, GemvArgs *g) {
+    g->xg_out = c->xg;
+    g->g_next = g_next;
+    g->ss_out = c->ss;
+}
+
 GemvArgs qkv_args(scry_kv_cache c, int l) {
     scry_llama m = c->m;
     GemvArgs g;
     g.w = &m->layers[l].qkv;
-    g.x = l == 0 ? nullptr : c->x;  // layer 0: embedding row fused into the prologue
     g.ldx = m->h;
     g.embed = m->embed;
     g.tokens = c->tokens;
     g.state = c->state;
-    g.norm_w = m->norm_in(l);
     g.eps = 1e-5f;  // RMSNorm::new (rmsnorm.rs:17-22)
+    if (l == 0) {
+        g.x = nullptr;  // the embedding row, RMSNorm'd in the prologue
+        g.norm_w = m->norm_in(0);
+    } else {
+        pre_normed(c, m->layers[l - 1].down, &g);
+    }
     g.q_out = c->xq;
     g.k_cache = c->K(l);
     g.v_cache = c->Vc(l);
@@ -704,6 +732,7 @@ GemvArgs o_args(scry_kv_cache c, int l) {
     g.embed = m->embed;
     g.tokens = c->tokens;
     g.state = c->state;
+    next_norm(c, m->norm_post(l), &g);
     return g;
 }
 
@@ -711,9 +740,8 @@ GemvArgs gu_args(scry_kv_cache c, int l) {
     scry_llama m = c->m;
     GemvArgs g;
     g.w = &m->layers[l].gu;
-    g.x = c->x;
+    pre_normed(c, m->layers[l].o, &g);
     g.ldx = m->h;
-    g.norm_w = m->norm_post(l);
     g.eps = 1e-5f;
     g.y = c->act;
     g.ldy = m->ffn;
@@ -729,6 +757,7 @@ GemvArgs down_args(scry_kv_cache c, int l) {
     g.y = c->x;
     g.ldy = m->h;
     g.resid = c->x;
+    next_norm(c, l + 1 < m->L ? m->norm_in(l + 1) : m->norm_final(), &g);
     return g;
 }
 
@@ -736,9 +765,8 @@ GemvArgs lm_args(scry_kv_cache c, int advance) {
     scry_llama m = c->m;
     GemvArgs g;
     g.w = &m->lm;
-    g.x = c->x;
+    pre_normed(c, m->layers[m->L - 1].down, &g);
     g.ldx = m->h;
-    g.norm_w = m->norm_final();
     g.eps = 1e-5f;
     g.y = c->logits;
     g.ldy = m->V;
@@ -1454,6 +1482,11 @@ int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int i
         bytes = (double)P->rows * P->k + scales + 4.0 * P->k + 4.0 * out_n;
     }
     const int nl = tensor_id == SCRY_T_LM_HEAD ? 1 : m->L;
+    // the RMSNorm'd GEMVs read the pre-scaled row and partial sums that the
+    // residual GEMV before them leaves
+    if (!rc && (tensor_id == SCRY_T_QKV || tensor_id == SCRY_T_LM_HEAD))
+        rc = launch_qgemv(EPI_RESID, down_args(c, m->L - 1), s);
+    if (!rc && tensor_id == SCRY_T_GATE) rc = launch_qgemv(EPI_RESID, o_args(c, 0), s);
     for (int i = 0; i < std::min(iters, 8) && !rc; i++) rc = launch(i % nl);  // warm-up
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (!rc) {

@@ -4,23 +4,38 @@
 //   y[j] = scale * sum_p x[p] * q[p, j]            (matmul_i8_f32, cpu.rs:1128-1160)
 // from the GEMV stream layout (one row of kp bytes per output j, byte = q + 128).
 //
-// Work split: a 256-thread workgroup owns 16 output rows, each wave 4 rows
-// over the whole k range.  Per 1024-wide k chunk a lane loads 16 consecutive
-// weight bytes of each of its 4 rows (global_load_dwordx4; one wave-wide load
-// reads 1 KiB contiguous) and four float4 activation fragments from LDS.
-// The activation row is staged in LDS once per workgroup with a permutation
-// that makes those float4 reads conflict-free.  Each byte is converted with a
-// single byte-select convert (v_cvt_f32_ubyte*) and FMA'd; the +128 bias is
-// removed once per row as 128 * sum(x).  The first PF chunks of weights are
-// requested before the activation staging, so the weight stream starts while
-// the (optional fused RMSNorm) prologue runs.
+// Work split: a workgroup of NW waves owns NW * RWT consecutive output rows,
+// each wave RWT rows over the whole k range.  Per 1024-wide k chunk a lane
+// loads 16 consecutive weight bytes of each of its rows (one wave-wide
+// buffer_load_dwordx4 reads 1 KiB contiguous) and four float4 activation
+// fragments from LDS.  Each byte is converted with a single byte-select
+// convert (v_cvt_f32_ubyte*) and FMA'd.
+//
+// Prologue (one barrier): the activation row is staged in LDS with a
+// permutation that makes the float4 reads conflict-free; while staging, each
+// quad of threads also writes the sum of the 16 values a consumer lane reads
+// per chunk.  Those per-lane sums remove the +128 bias inside the final wave
+// reduction (sum_p (q+128) x - 128 sum_p x) and are the block-32 group sums.
+// The first PF chunks of every row are requested before the staging, so the
+// weight stream is in flight during it.  Rows past the end load a valid row
+// (and are never stored): a load that is out of range for every lane can
+// complete out of order and release a partial vmcnt wait too early.
+//
+// RMSNorm (rmsnorm.rs, cpu.rs:574-599) is applied as y = rstd * (W (x*g)):
+//   PRO_NORM   stages x*g and reduces sum(x^2) itself (the first layer, whose
+//              activation is the embedding row);
+//   PRO_NORMP  stages x*g written by the producing residual GEMV, with rstd
+//              from that GEMV's per-workgroup sum(x^2) partials.
+// Both sums of squares are reduced after the staging barrier, in a fixed order.
 //
 // Epilogues fused into the same pass (llama.rs:371-511):
 //   EPI_STORE   y = acc (+ bias)                     -- matmul_i8_f32[_bias]
-//   EPI_RESID   y = resid + acc                      -- o_proj / down_proj + residual add
+//   EPI_RESID   y = resid + acc; optionally x*g_next and sum(y^2) per workgroup
+//               for the next RMSNorm'd GEMV          -- o_proj / down_proj + residual add
 //   EPI_SWIGLU  h = silu(gate) * up on interleaved rows -- gate/up + swiglu
 //   EPI_QKV     RoPE(Q)*1/sqrt(hd), RoPE(K), K/V appended to the cache row
-//   EPI_LOGITS  logits + device argmax (last-arriving workgroup) + step advance
+//   EPI_LOGITS  logits + this workgroup's ordered argmax partial
+// The row-combining epilogues exchange row values through LDS.
 #include "internal.h"
 #include "kdev.h"
 
@@ -28,10 +43,6 @@ namespace scry {
 namespace {
 
 using namespace dev;
-
-constexpr int RW = 4;    // rows per wave (default; the residual GEMVs pick fewer)
-constexpr int RPB = 16;  // rows per workgroup at RW
-constexpr int PF4 = 4;   // chunks in flight per row (runtime-chunk path, k <= 4096)
 
 struct KArgs {
     const uint8_t *W;
@@ -46,10 +57,15 @@ struct KArgs {
     DevState *state;
     const float *norm_w;
     float eps;
+    const double *ss_in;
+    int n_ss;
     float *y;
     int ldy;
     const float *resid;
     const float *bias;
+    float *xg_out;
+    const float *g_next;
+    double *ss_out;
     float *q_out, *k_cache, *v_cache;
     const float2 *rope_cs;
     int q_dim, kv_dim, head_dim;
@@ -59,7 +75,25 @@ struct KArgs {
 };
 
 // activation prologues
-enum { PRO_PLAIN = 0, PRO_NORM = 1 };
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_NORMP = 2 };
+constexpr int SSW = 2;  // PRO_NORMP partial sums per thread (n_ss <= SSW * threads)
+
+// Launch shape for a chunk count (0: runtime loop) and activation rows per
+// pass.  Measured on the Llama-2-7B decode shapes (one launch of 4096 x 22016
+// int8 weights: 4 rows per wave x 4 waves 17.7 us, 1 row per wave x 8 waves
+// 15.0 us): single-row waves keep more loads in flight per CU and finish
+// evenly.  The MT > 1 and runtime-k paths keep 4 rows per wave, which shares
+// each LDS activation read between 4 rows.
+struct Shape {
+    int rwt, nw, pf;  // rows per wave, waves per workgroup, chunks in flight per row
+};
+constexpr Shape shape_for(int nch, int mt) {
+    return mt > 1      ? Shape{4, 4, 4}
+           : nch == 4  ? Shape{1, 8, 4}
+           : nch == 11 ? Shape{1, 8, 8}
+           : nch == 14 ? Shape{1, 8, 7}
+                       : Shape{4, 4, 4};
+}
 
 // Activation row source for row mr (nullptr if mr >= m).
 __device__ __forceinline__ const float *act_row(const KArgs &a, int mr) {
@@ -67,20 +101,25 @@ __device__ __forceinline__ const float *act_row(const KArgs &a, int mr) {
     return a.x ? a.x + (size_t)mr * a.ldx : a.embed + (size_t)a.tokens[a.state->pos] * a.k;
 }
 
-// Thread t loads x[p*1024 + 4t .. +3] for p < XP (zero past k).
-template <int XP>
-__device__ __forceinline__ void load_x(const float *src, int k, float4 (&xr)[XP]) {
+// Thread t loads the float4s f4 = p*NT + t (p < XP) of a k-vector.  A wave
+// whose float4s all lie past k loads nothing (zeros).
+template <int XP, int NT>
+__device__ __forceinline__ void load_vec(const float *src, int k, int nch, float4 (&v)[XP]) {
     const __amdgpu_buffer_rsrc_t r = make_rsrc(src, src ? (size_t)k * 4 : 0);
+    const int tid = threadIdx.x;
 #pragma unroll
-    for (int p = 0; p < XP; p++) xr[p] = bload16f(r, (unsigned)((p << 12) + (threadIdx.x << 4)));
+    for (int p = 0; p < XP; p++) {
+        const int f4 = p * NT + tid;
+        v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (src && f4 < nch * 256 && (f4 & ~63) * 4 < k) v[p] = bload16f(r, (unsigned)f4 << 4);
+    }
 }
-
 
 // One 1024-wide k chunk for RWT rows and MT activation rows.
 template <int MT, bool B32, int RWT>
 __device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RWT], int c, const float *xs, int kc,
-                                          const float *xg, __amdgpu_buffer_rsrc_t sr, int nb,
-                                          int row0, int lane, float (&acc)[MT][RWT]) {
+                                          const float *xsum, __amdgpu_buffer_rsrc_t sr, int nb,
+                                          const int (&wrow)[RWT], int lane, float (&acc)[MT][RWT]) {
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         const float *xb = xs + mi * kc + (c << 10) + (lane << 2);
@@ -93,108 +132,116 @@ __device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RWT], int c, const fl
             for (int r = 0; r < RWT; r++) acc[mi][r] = dot16(w[r], x0, x1, x2, x3, acc[mi][r]);
         } else {
             // block-32: this lane's 16 bytes are half of k-block blk
-            const float gs = xg[mi * (kc >> 4) + (c << 6) + lane];
+            const float gs = xsum[mi * (kc >> 4) + (c << 6) + lane];
             const int blk = ((c << 10) + (lane << 4)) >> 5;
 #pragma unroll
             for (int r = 0; r < RWT; r++) {
                 const float p = dot16(w[r], x0, x1, x2, x3, 0.f);
                 const float sc = __builtin_bit_cast(
-                    float, __builtin_amdgcn_raw_buffer_load_b32(sr, ((row0 + r) * nb + blk) * 4, 0, 0));
+                    float, __builtin_amdgcn_raw_buffer_load_b32(sr, (wrow[r] * nb + blk) * 4, 0, 0));
                 acc[mi][r] = fmaf(sc, fmaf(-128.f, gs, p), acc[mi][r]);
             }
         }
     }
 }
 
-// RWT rows per wave (4 * RWT per workgroup), PFT chunks in flight per row.
-template <int EPI, int PRO, bool B32, int MT, int NCH, int RWT = RW, int PFT = PF4>
-__global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
-    static_assert(RWT == RW || EPI == EPI_RESID || EPI == EPI_STORE,
-                  "the SwiGLU, QKV and logits epilogues work on 4-row groups");
-    constexpr bool NORM = PRO == PRO_NORM;
-    constexpr int XP = NCH > 0 ? NCH : 16;
-    constexpr int PF = PFT;
+template <int EPI, int PRO, bool B32, int MT, int NCH>
+__global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
+    constexpr Shape S = shape_for(NCH, MT);
+    constexpr int RWT = S.rwt, NW = S.nw, PF = S.pf, RPW = RWT * NW, NT = 64 * NW;
+    constexpr int XP = ((NCH > 0 ? NCH : 16) * 256 + NT - 1) / NT;  // float4 per thread per row
+    constexpr bool NORM = PRO != PRO_PLAIN;
+    static_assert(!NORM || MT == 1, "the RMSNorm prologues take one activation row");
+    static_assert(EPI == EPI_STORE || MT == 1, "only the store epilogue takes several rows");
+    static_assert(EPI == EPI_STORE || EPI == EPI_RESID || RPW % 4 == 0,
+                  "the SwiGLU, QKV and logits epilogues combine rows in groups of 4");
     extern __shared__ float4 dyn4[];
-    float *xs = reinterpret_cast<float *>(dyn4);
-    const int kc = (NCH > 0 ? NCH : a.nch) << 10;
-    float *xg = xs + MT * kc;  // B32: per-16 group sums
-    __shared__ double red_d[4];
-    __shared__ float sx_sh[MT];
+    const int nch = NCH > 0 ? NCH : a.nch;
+    const int kc = nch << 10;
+    float *xs = reinterpret_cast<float *>(dyn4);  // [MT][kc] permuted activation rows
+    float *xsum = xs + MT * kc;                    // [MT][nch][64] per-lane 16-value sums
+    __shared__ double s_ss[NW];  // per-wave sums of squares for the RMSNorm
+    __shared__ float s_rstd;
+    __shared__ float s_val[MT * RPW];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row0 = blockIdx.x * (4 * RWT) + wave * RWT;
+    const int rb = blockIdx.x * RPW, row0 = rb + wave * RWT;
     const int m0 = blockIdx.y * MT;
 
-    // ---- 1. activation loads first, then the first PF weight chunks: waiting
-    // for the activations then leaves the weight stream in flight.
+    // ---- 1. activation loads (and the RMSNorm inputs), then the first PF
+    // chunks of every row: waiting for the activations leaves the weight
+    // stream in flight
     float4 xr[XP];
-    load_x<XP>(act_row(a, m0), a.k, xr);
-    float4 nw[NORM ? XP : 1];
-    if (NORM) load_x<XP>(a.norm_w, a.k, reinterpret_cast<float4(&)[XP]>(nw));
+    load_vec<XP, NT>(act_row(a, m0), a.k, nch, xr);
+    float4 gw[PRO == PRO_NORM ? XP : 1];
+    if constexpr (PRO == PRO_NORM) load_vec<XP, NT>(a.norm_w, a.k, nch, gw);
+    // PRO_NORMP: this thread's share of the producer's partial sums
+    // (unconditional clamped loads: no wait inside a branch)
+    double ssv[PRO == PRO_NORMP ? SSW : 1];
+    if constexpr (PRO == PRO_NORMP) {
+#pragma unroll
+        for (int j = 0; j < SSW; j++) ssv[j] = a.ss_in[min(tid + NT * j, a.n_ss - 1)];
+    }
 
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.W, (size_t)a.rows * a.kp);
+    int wrow[RWT];
     unsigned woff[RWT];
 #pragma unroll
-    for (int r = 0; r < RWT; r++)  // rows past the end read zeros (never stored)
-        woff[r] = (row0 + r) < a.rows ? (unsigned)((row0 + r) * a.kp + (lane << 4)) : 0x80000000u;
+    for (int r = 0; r < RWT; r++) {
+        wrow[r] = min(row0 + r, a.rows - 1);
+        woff[r] = (unsigned)(wrow[r] * a.kp + (lane << 4));
+    }
     u32x4 wb[PF][RWT];
 #pragma unroll
     for (int d = 0; d < PF; d++)
+        if (NCH > 0 || d < nch) {
 #pragma unroll
-        for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + (d << 10));
+            for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + (d << 10));
+        }
 
-    // ---- 2. stage the activation rows (optionally RMSNorm'd) into LDS
+    // ---- 2. stage the activation rows into LDS with the per-lane sums
+    double ssp = 0.0;
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
-        if (mi > 0) load_x<XP>(act_row(a, m0 + mi), a.k, xr);
-        float *xrow = xs + mi * kc;
-        double acc2 = 0.0;
+        if (mi > 0) load_vec<XP, NT>(act_row(a, m0 + mi), a.k, nch, xr);
 #pragma unroll
         for (int p = 0; p < XP; p++) {
-            const float4 v = xr[p];
-            if (NORM)
-                acc2 += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-            else
-                acc2 += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
-        }
-        double tot = block_sum_d(acc2, red_d);
-        if (NORM) {
-            // cpu.rs:574-599: rstd = 1/sqrt(mean(x^2) + eps) in f64; out = f32(x*rstd*w)
-            const double rstd = 1.0 / sqrt(tot / (double)a.k + (double)a.eps);
-            double sx = 0.0;
-#pragma unroll
-            for (int p = 0; p < XP; p++) {
-                const float4 w4 = nw[NORM ? p : 0];
+            const int f4 = p * NT + tid;
+            if (f4 < nch * 256) {  // whole waves: nch * 256 is a multiple of 64
                 float4 v = xr[p];
-                v.x = (float)((double)v.x * rstd * (double)w4.x);
-                v.y = (float)((double)v.y * rstd * (double)w4.y);
-                v.z = (float)((double)v.z * rstd * (double)w4.z);
-                v.w = (float)((double)v.w * rstd * (double)w4.w);
-                xr[p] = v;
-                sx += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
+                if constexpr (PRO == PRO_NORM) {
+                    ssp += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+                    v.x *= gw[p].x;
+                    v.y *= gw[p].y;
+                    v.z *= gw[p].z;
+                    v.w *= gw[p].w;
+                }
+                *(float4 *)(xs + mi * kc + xslot(f4 >> 8, f4 & 255)) = v;
+                // consumer lane L of chunk c reads float4s c*256 + 4L .. 4L+3:
+                // the quad of threads staging them sums its 16 values
+                float s = (v.x + v.y) + (v.z + v.w);
+                s += __shfl_xor(s, 1);
+                s += __shfl_xor(s, 2);
+                if ((tid & 3) == 0) xsum[mi * (kc >> 4) + ((f4 >> 8) << 6) + ((f4 & 255) >> 2)] = s;
             }
-            tot = block_sum_d(sx, red_d);
         }
+    }
+    if constexpr (NORM) {
+        if constexpr (PRO == PRO_NORMP) {
 #pragma unroll
-        for (int p = 0; p < XP; p++)
-            if (NCH > 0 || p < a.nch) *(float4 *)(xrow + xslot(p, tid)) = xr[p];
-        if (tid == 0) sx_sh[mi] = (float)tot;
+            for (int j = 0; j < SSW; j++)
+                if (tid + NT * j < a.n_ss) ssp += ssv[j];
+        }
+        ssp = wave_sum_d_dpp(ssp);
+        if (lane == 0) s_ss[wave] = ssp;
     }
     __syncthreads();
-    if (B32) {
-        const int ng = kc >> 4;
-        for (int t = tid; t < MT * ng; t += TPB) {
-            const int mi = t / ng, g = t % ng;
-            const int c = g >> 6, L = g & 63;
-            const float *xq = xs + mi * kc + (c << 10) + (L << 2);
-            float s = 0.f;
+    if (NORM && wave == 0) {
+        // cpu.rs:574-599: rstd = 1/sqrt(mean(x^2) + eps) in f64 (waves in order)
+        double t = 0.0;
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) s += xq[(q << 8) + e];
-            xg[t] = s;
-        }
-        __syncthreads();
+        for (int w = 0; w < NW; w++) t += s_ss[w];
+        if (lane == 0) s_rstd = (float)(1.0 / sqrt(t / (double)a.k + (double)a.eps));
     }
 
     // ---- 3. stream the weights
@@ -210,20 +257,20 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
         // straight-line stream: chunk c computes from wb[c % PF], then refills it
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
-            chunk_fma<MT, B32, RWT>(wb[c % PF], c, xs, kc, xg, sr, a.nb, row0, lane, acc);
+            chunk_fma<MT, B32, RWT>(wb[c % PF], c, xs, kc, xsum, sr, a.nb, wrow, lane, acc);
             if (c + PF < NCH) {
 #pragma unroll
                 for (int r = 0; r < RWT; r++) wb[c % PF][r] = bload16(wr, woff[r] + ((c + PF) << 10));
             }
         }
     } else {
-        for (int c0 = 0; c0 < a.nch; c0 += PF) {
+        for (int c0 = 0; c0 < nch; c0 += PF) {
 #pragma unroll
             for (int d = 0; d < PF; d++) {
                 const int c = c0 + d;
-                if (c < a.nch) {
-                    chunk_fma<MT, B32, RWT>(wb[d], c, xs, kc, xg, sr, a.nb, row0, lane, acc);
-                    if (c + PF < a.nch) {
+                if (c < nch) {
+                    chunk_fma<MT, B32, RWT>(wb[d], c, xs, kc, xsum, sr, a.nb, wrow, lane, acc);
+                    if (c + PF < nch) {
 #pragma unroll
                         for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + ((c + PF) << 10));
                     }
@@ -232,25 +279,25 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
         }
     }
 
-    // ---- 4. reduce over the wave, remove the +128 bias, apply the scale
+
+    // ---- 4. remove the +128 bias inside the wave reduction, apply the scales
     float val[MT][RWT];
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
-        const float corr = 128.f * sx_sh[mi];
+        float sxl = 0.f;
+        if (!B32)
+            for (int c = 0; c < nch; c++) sxl += xsum[mi * (kc >> 4) + (c << 6) + lane];
 #pragma unroll
         for (int r = 0; r < RWT; r++) {
-            const float s = wave_sum(acc[mi][r]);
-            if (B32) {
-                val[mi][r] = s;
-            } else {
-                const float sc = (EPI == EPI_SWIGLU && r >= 2) ? a.scale2 : a.scale;
-                val[mi][r] = sc * (s - corr);
-            }
+            const float s = wave_sum(B32 ? acc[mi][r] : fmaf(-128.f, sxl, acc[mi][r]));
+            // fused gate/up rows come as gate, gate, up, up
+            const float sc = B32 ? 1.f : (EPI == EPI_SWIGLU && ((row0 + r) & 2)) ? a.scale2 : a.scale;
+            val[mi][r] = sc * s;
         }
     }
 
     // ---- 5. epilogues
-    if (EPI == EPI_STORE || EPI == EPI_RESID) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {
 #pragma unroll
         for (int mi = 0; mi < MT; mi++) {
             const int mr = m0 + mi;
@@ -260,78 +307,81 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
                 const int row = row0 + r;
                 if (lane == r && mr < a.m && row < a.rows) {
                     float v = val[mi][r];
-                    if (EPI == EPI_STORE) {
+                    if constexpr (EPI == EPI_STORE) {
                         if (a.bias) v = v + a.bias[row];
-                        a.y[(size_t)mr * a.ldy + row] = v;
                     } else {
                         const float *R = a.resid ? a.resid + (size_t)mr * a.ldy
                                                  : a.embed + (size_t)a.tokens[a.state->pos] * a.rows;
-                        a.y[(size_t)mr * a.ldy + row] = R[row] + v;
+                        v = R[row] + v;
+                        if (a.xg_out) a.xg_out[row] = v * a.g_next[row];
+                        s_val[wave * RWT + r] = v;
                     }
+                    a.y[(size_t)mr * a.ldy + row] = v;
                 }
             }
         }
-    } else if (EPI == EPI_SWIGLU) {
-        // wave rows = gate[2t], gate[2t+1], up[2t], up[2t+1]
+        if constexpr (EPI == EPI_RESID) {
+            if (a.ss_out) {  // uniform: the next RMSNorm's sum of squares, in row order
+                __syncthreads();
+                if (tid == 0) {
+                    double t = 0.0;
+                    for (int i = 0; i < RPW && rb + i < a.rows; i++) t += (double)s_val[i] * s_val[i];
+                    a.ss_out[blockIdx.x] = t;
+                }
+            }
+        }
+        return;
+    } else {
 #pragma unroll
-        for (int mi = 0; mi < MT; mi++) {
-            const int mr = m0 + mi;
-            if (lane < 2 && mr < a.m && row0 < a.rows) {
-                const float g = lane ? val[mi][1] : val[mi][0];
-                const float u = lane ? val[mi][3] : val[mi][2];
-                const int t = (row0 >> 1) + lane;  // (row0/4)*2 + lane
-                a.y[(size_t)mr * a.ldy + t] = silu_f(g) * u;
-            }
+        for (int r = 0; r < RWT; r++)
+            if (lane == r) s_val[wave * RWT + r] = val[0][r];
+        __syncthreads();
+    }
+    const float rs = NORM ? s_rstd : 1.f;
+    if constexpr (EPI == EPI_SWIGLU) {
+        // rows 4i..4i+3 = gate[2i], gate[2i+1], up[2i], up[2i+1]
+        if (tid < RPW / 2 && rb + 2 * tid < a.rows) {
+            const int q = (tid >> 1) * 4 + (tid & 1);
+            a.y[(rb >> 1) + tid] = silu_f(s_val[q] * rs) * (s_val[q + 2] * rs);
         }
-    } else if (EPI == EPI_QKV) {
-        if (lane < 2) {
-            const int j = row0 + 2 * lane;
-            if (j < a.rows) {
-                const float x0 = lane ? val[0][2] : val[0][0];
-                const float x1 = lane ? val[0][3] : val[0][1];
-                const int pos = a.state->pos, crow = a.state->cache_len;
-                const int hh = a.head_dim >> 1;
-                if (j < a.q_dim + a.kv_dim) {
-                    const bool isq = j < a.q_dim;
-                    const int jj = isq ? j : j - a.q_dim;
-                    const float2 cs = a.rope_cs[(size_t)pos * hh + ((jj % a.head_dim) >> 1)];
-                    // cpu.rs:655-658 in f32, no contraction
-                    const float r0 = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
-                    const float r1 = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
-                    if (isq) {
-                        a.q_out[jj] = __fmul_rn(r0, a.q_scale);
-                        a.q_out[jj + 1] = __fmul_rn(r1, a.q_scale);
-                    } else {
-                        float *kr = a.k_cache + (size_t)crow * a.kv_dim;
-                        kr[jj] = r0;
-                        kr[jj + 1] = r1;
-                    }
+    } else if constexpr (EPI == EPI_QKV) {
+        const int j = rb + 2 * tid;
+        if (tid < RPW / 2 && j < a.rows) {
+            const float x0 = s_val[2 * tid] * rs, x1 = s_val[2 * tid + 1] * rs;
+            const int pos = a.state->pos, crow = a.state->cache_len;
+            const int hh = a.head_dim >> 1;
+            if (j < a.q_dim + a.kv_dim) {
+                const bool isq = j < a.q_dim;
+                const int jj = isq ? j : j - a.q_dim;
+                const float2 cs = a.rope_cs[(size_t)pos * hh + ((jj % a.head_dim) >> 1)];
+                // cpu.rs:655-658 in f32, no contraction
+                const float r0 = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
+                const float r1 = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+                if (isq) {
+                    a.q_out[jj] = __fmul_rn(r0, a.q_scale);
+                    a.q_out[jj + 1] = __fmul_rn(r1, a.q_scale);
                 } else {
-                    const int jj = j - a.q_dim - a.kv_dim;
-                    float *vr = a.v_cache + (size_t)crow * a.kv_dim;
-                    vr[jj] = x0;
-                    vr[jj + 1] = x1;
+                    float *kr = a.k_cache + (size_t)crow * a.kv_dim;
+                    kr[jj] = r0;
+                    kr[jj + 1] = r1;
                 }
+            } else {
+                const int jj = j - a.q_dim - a.kv_dim;
+                float *vr = a.v_cache + (size_t)crow * a.kv_dim;
+                vr[jj] = x0;
+                vr[jj + 1] = x1;
             }
         }
-    } else if (EPI == EPI_LOGITS) {
+    } else if constexpr (EPI == EPI_LOGITS) {
         // logits + this workgroup's ordered argmax partial (no fences: the
         // finish kernel that reduces the partials is the next launch)
-        __shared__ float s_v[RPB];
-#pragma unroll
-        for (int r = 0; r < RW; r++) {
-            if (lane == r) {
-                if (row0 + r < a.rows) a.y[row0 + r] = val[0][r];
-                s_v[wave * RW + r] = val[0][r];
-            }
-        }
-        __syncthreads();
+        if (tid < RPW && rb + tid < a.rows) a.y[rb + tid] = s_val[tid] * rs;
         if (tid == 0) {
             ArgAcc p{0.f, -1, -1};
-            for (int t = 0; t < RPB; t++) {
-                const int row = blockIdx.x * RPB + t;
+            for (int t = 0; t < RPW; t++) {
+                const int row = rb + t;
                 if (row >= a.rows) break;
-                const float v = s_v[t];
+                const float v = s_val[t] * rs;
                 if (isnan(v)) {
                     p.nan = row;
                     continue;
@@ -348,84 +398,121 @@ __global__ __launch_bounds__(TPB) void k_qgemv(KArgs a) {
     }
 }
 
-template <int EPI, int PRO, bool B32, int MT, int NCH, int RWT = RW, int PFT = PF4>
+// Compile-time chunk count (straight-line stream) for the k on the Llama
+// paths; 0 = runtime loop.  Several activation rows share a weight pass only
+// in the store epilogue with k <= 4096.
+struct Sel {
+    int nch_t, mt;
+};
+Sel select_cfg(int epi, int nch, int m) {
+    int mt = 1;
+    if (epi == EPI_STORE && nch <= 4) mt = m >= 4 ? 4 : (m >= 2 ? 2 : 1);
+    int nt = 0;
+    if (nch == 1 || nch == 4) nt = nch;
+    if ((nch == 11 || nch == 14) && mt == 1 && (epi == EPI_STORE || epi == EPI_RESID)) nt = nch;
+    return {nt, mt};
+}
+
+size_t lds_bytes(int epi, int nch, int mt, int pro) {
+    const Shape S = shape_for(select_cfg(epi, nch, mt).nch_t, mt);
+    const size_t dyn = (size_t)mt * nch * 1024 * sizeof(float) * 17 / 16;
+    (void)pro;
+    const size_t stat = S.nw * sizeof(double) +
+                        (size_t)mt * S.rwt * S.nw * sizeof(float);
+    return dyn + stat;
+}
+
+constexpr size_t kLdsMax = 160 * 1024;  // gfx950 LDS per workgroup
+
+template <int EPI, int PRO, bool B32, int MT, int NCH>
 int launch_t(const KArgs &ka, hipStream_t s) {
-    const int kc = ka.nch << 10;
-    size_t lds = (size_t)MT * kc * sizeof(float) + (B32 ? (size_t)MT * (kc >> 4) * sizeof(float) : 0);
-    dim3 grid((ka.rows + 4 * RWT - 1) / (4 * RWT), (ka.m + MT - 1) / MT);
-    hipLaunchKernelGGL((k_qgemv<EPI, PRO, B32, MT, NCH, RWT, PFT>), grid, dim3(TPB), lds, s, ka);
+    constexpr Shape S = shape_for(NCH, MT);
+    const size_t lds = (size_t)MT * (ka.nch << 10) * sizeof(float) * 17 / 16;
+    if (lds > 64 * 1024) {  // above the default dynamic LDS limit
+        static bool attr = false;
+        if (!attr) {
+            const size_t stat = lds_bytes(EPI, ka.nch, MT, PRO) - lds;
+            SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_qgemv<EPI, PRO, B32, MT, NCH>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kLdsMax - stat)));
+            attr = true;
+        }
+    }
+    dim3 grid((ka.rows + S.rwt * S.nw - 1) / (S.rwt * S.nw), (ka.m + MT - 1) / MT);
+    hipLaunchKernelGGL((k_qgemv<EPI, PRO, B32, MT, NCH>), grid, dim3(64 * S.nw), lds, s, ka);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }
 
-// NCH = compile-time chunk count (straight-line stream) for the k on the
-// Llama path; 0 = runtime loop for any other k <= 16384.
-// The residual GEMVs of the decode step (o_proj, down_proj: 4096 outputs)
-// have few rows per launch: fewer rows per wave put more waves on each CU,
-// and for long rows every chunk is requested at once (measured on the 7B
-// shapes: o 5.6 -> 5.3 us with 2 rows per wave, down 12.9 -> 10.5 us with one
-// row per wave and all 11 chunks in flight).
 template <int EPI, int PRO, bool B32, int MT>
-int launch_nch(const KArgs &ka, hipStream_t s) {
-    constexpr bool resid1 = EPI == EPI_RESID && MT == 1;
-    switch (ka.nch) {
+int launch_nch(const KArgs &ka, int nch_t, hipStream_t s) {
+    switch (nch_t) {
         case 1: return launch_t<EPI, PRO, B32, MT, 1>(ka, s);
-        case 4:
-            if constexpr (resid1) return launch_t<EPI, PRO, B32, MT, 4, 2, 4>(ka, s);
-            return launch_t<EPI, PRO, B32, MT, 4>(ka, s);
-        case 11:
-            if constexpr (resid1) return launch_t<EPI, PRO, B32, MT, 11, 1, 11>(ka, s);
-            if (MT == 1) return launch_t<EPI, PRO, B32, MT, 11>(ka, s);
-            break;
-        case 14:
-            if constexpr (resid1) return launch_t<EPI, PRO, B32, MT, 14, 1, 14>(ka, s);
-            if (MT == 1) return launch_t<EPI, PRO, B32, MT, 14>(ka, s);
-            break;
+        case 4: return launch_t<EPI, PRO, B32, MT, 4>(ka, s);
         default: break;
+    }
+    if constexpr (MT == 1 && (EPI == EPI_STORE || EPI == EPI_RESID)) {
+        if (nch_t == 11) return launch_t<EPI, PRO, B32, MT, 11>(ka, s);
+        if (nch_t == 14) return launch_t<EPI, PRO, B32, MT, 14>(ka, s);
     }
     return launch_t<EPI, PRO, B32, MT, 0>(ka, s);
 }
 
 template <int EPI, int PRO, bool B32>
-int launch_mt(const KArgs &ka, hipStream_t s) {
-    // skinny GEMM: MT activation rows share one weight pass (k <= 4096 keeps
-    // MT * k floats within the 64 KiB LDS stage)
+int launch_mt(const KArgs &ka, Sel sel, hipStream_t s) {
     if constexpr (EPI == EPI_STORE) {
-        if (ka.m >= 4 && ka.nch <= 4) return launch_nch<EPI, PRO, B32, 4>(ka, s);
-        if (ka.m >= 2 && ka.nch <= 4) return launch_nch<EPI, PRO, B32, 2>(ka, s);
+        if (sel.mt == 4) return launch_nch<EPI, PRO, B32, 4>(ka, sel.nch_t, s);
+        if (sel.mt == 2) return launch_nch<EPI, PRO, B32, 2>(ka, sel.nch_t, s);
     }
-    return launch_nch<EPI, PRO, B32, 1>(ka, s);
+    return launch_nch<EPI, PRO, B32, 1>(ka, sel.nch_t, s);
 }
 
 template <int EPI>
-int launch_e(const KArgs &ka, bool norm, bool b32, hipStream_t s) {
-    // decode epilogues QKV/SWIGLU/LOGITS always take the fused RMSNorm
+int launch_e(const KArgs &ka, int pro, bool b32, Sel sel, hipStream_t s) {
+    // the decode epilogues QKV/SWIGLU/LOGITS always take a fused RMSNorm
     constexpr bool kNorm = (EPI == EPI_QKV || EPI == EPI_SWIGLU || EPI == EPI_LOGITS);
-    if (norm != kNorm)
+    if ((pro != PRO_PLAIN) != kNorm)
         return set_error(SCRY_ERR_INVALID, "qgemv: epilogue %d %s a fused RMSNorm", EPI,
                          kNorm ? "requires" : "does not take");
     if constexpr (kNorm) {
-        return b32 ? launch_mt<EPI, PRO_NORM, true>(ka, s) : launch_mt<EPI, PRO_NORM, false>(ka, s);
+        if (pro == PRO_NORMP)
+            return b32 ? launch_mt<EPI, PRO_NORMP, true>(ka, sel, s) : launch_mt<EPI, PRO_NORMP, false>(ka, sel, s);
+        return b32 ? launch_mt<EPI, PRO_NORM, true>(ka, sel, s) : launch_mt<EPI, PRO_NORM, false>(ka, sel, s);
     } else {
-        return b32 ? launch_mt<EPI, PRO_PLAIN, true>(ka, s) : launch_mt<EPI, PRO_PLAIN, false>(ka, s);
+        return b32 ? launch_mt<EPI, PRO_PLAIN, true>(ka, sel, s) : launch_mt<EPI, PRO_PLAIN, false>(ka, sel, s);
     }
 }
 
 }  // namespace
+
+int qgemv_blocks(int epi, const Packed &w, int m) {
+    const Sel sel = select_cfg(epi, (w.k + 1023) / 1024, m);
+    const Shape S = shape_for(sel.nch_t, sel.mt);
+    return (w.rows + S.rwt * S.nw - 1) / (S.rwt * S.nw);
+}
 
 int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     const Packed &w = *g.w;
     if (w.kp % 16 != 0 || w.k > w.kp) return set_error(SCRY_ERR_INVALID, "qgemv: bad packed layout");
     if (w.bytes() >= 0x7fffffffull)  // buffer offsets are 32-bit
         return set_error(SCRY_ERR_UNSUPPORTED, "qgemv: %zu weight bytes (limit 2 GiB per tensor)", w.bytes());
+    if (g.m < 1) return set_error(SCRY_ERR_INVALID, "qgemv: m must be >= 1");
     const int nch = (w.k + 1023) / 1024;
-    if (nch > 16 || (size_t)nch * 1024 * sizeof(float) * (w.s32 ? 17 : 16) / 16 > 64 * 1024)
+    const int pro = g.ss_in ? PRO_NORMP : g.norm_w ? PRO_NORM : PRO_PLAIN;
+    const Sel sel = select_cfg(epi, nch, g.m);
+    if (nch > 16 || lds_bytes(epi, nch, sel.mt, pro) > kLdsMax)
         return set_error(SCRY_ERR_UNSUPPORTED, "qgemv: k=%d exceeds the LDS activation stage", w.k);
     if (epi == EPI_SWIGLU && (w.fused != 1 || w.rows % 4 != 0))
         return set_error(SCRY_ERR_INVALID, "qgemv: swiglu epilogue needs the fused gate/up layout");
-    if ((epi == EPI_QKV || epi == EPI_LOGITS) && g.m != 1)
+    if ((epi == EPI_QKV || epi == EPI_LOGITS || epi == EPI_SWIGLU || epi == EPI_RESID) && g.m != 1)
         return set_error(SCRY_ERR_INVALID, "qgemv: decode epilogues take one activation row");
-    if (g.m < 1) return set_error(SCRY_ERR_INVALID, "qgemv: m must be >= 1");
+    if (epi == EPI_QKV && (w.rows % 2 != 0 || g.head_dim % 2 != 0 || g.q_dim % 2 != 0 || g.kv_dim % 2 != 0))
+        return set_error(SCRY_ERR_INVALID, "qgemv: qkv epilogue needs even head, q and kv sizes");
+    const int max_ss = SSW * 64 * shape_for(sel.nch_t, sel.mt).nw;
+    if (g.ss_in && (g.n_ss < 1 || g.n_ss > max_ss || g.norm_w))
+        return set_error(SCRY_ERR_INVALID,
+                         "qgemv: pre-scaled RMSNorm input needs 1..%d partial sums and no norm weight", max_ss);
+    if (epi == EPI_RESID && (!g.xg_out != !g.g_next || !g.xg_out != !g.ss_out))
+        return set_error(SCRY_ERR_INVALID, "qgemv: residual RMSNorm outputs come together");
     KArgs ka{};
     ka.W = w.d;
     ka.k = w.k;
@@ -444,10 +531,15 @@ int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     ka.state = g.state;
     ka.norm_w = g.norm_w;
     ka.eps = g.eps;
+    ka.ss_in = g.ss_in;
+    ka.n_ss = g.n_ss;
     ka.y = g.y;
     ka.ldy = g.ldy;
     ka.resid = g.resid;
     ka.bias = g.bias;
+    ka.xg_out = g.xg_out;
+    ka.g_next = g.g_next;
+    ka.ss_out = g.ss_out;
     ka.q_out = g.q_out;
     ka.k_cache = g.k_cache;
     ka.v_cache = g.v_cache;
@@ -459,14 +551,13 @@ int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     ka.part_val = g.part_val;
     ka.part_idx = g.part_idx;
     ka.part_nan = g.part_nan;
-    const bool norm = g.norm_w != nullptr;
     const bool b32 = w.s32 != nullptr;
     switch (epi) {
-        case EPI_STORE: return launch_e<EPI_STORE>(ka, norm, b32, s);
-        case EPI_RESID: return launch_e<EPI_RESID>(ka, norm, b32, s);
-        case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(ka, norm, b32, s);
-        case EPI_QKV: return launch_e<EPI_QKV>(ka, norm, b32, s);
-        case EPI_LOGITS: return launch_e<EPI_LOGITS>(ka, norm, b32, s);
+        case EPI_STORE: return launch_e<EPI_STORE>(ka, pro, b32, sel, s);
+        case EPI_RESID: return launch_e<EPI_RESID>(ka, pro, b32, sel, s);
+        case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(ka, pro, b32, sel, s);
+        case EPI_QKV: return launch_e<EPI_QKV>(ka, pro, b32, sel, s);
+        case EPI_LOGITS: return launch_e<EPI_LOGITS>(ka, pro, b32, sel, s);
     }
     return set_error(SCRY_ERR_INVALID, "qgemv: unknown epilogue %d", epi);
 }
@@ -510,7 +601,7 @@ __global__ __launch_bounds__(TPB) void k_logits_finish(const float *__restrict__
 }  // namespace
 
 int launch_logits_finish(const GemvArgs &g, hipStream_t s) {
-    const int np = (g.w->rows + RPB - 1) / RPB;
+    const int np = qgemv_blocks(EPI_LOGITS, *g.w, 1);
     hipLaunchKernelGGL(k_logits_finish, dim3(1), dim3(TPB), 0, s, g.y, g.w->rows, g.part_val,
                        g.part_idx, g.part_nan, np, g.state, g.tokens_rw, g.argmax_out, g.advance);
     SCRY_HIP(hipGetLastError());
