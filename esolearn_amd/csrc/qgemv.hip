@@ -44,21 +44,21 @@ namespace {
 
 using namespace dev;
 
+// The fields the prologue needs come first: the kernel fetches them together.
 struct KArgs {
     const uint8_t *W;
+    const float *x;
+    const double *ss_in;
+    const float *norm_w;
     int k, kp, rows, nch;
+    int ldx, m, n_ss;
+    float eps;
     const float *s32;
     int nb;
     float scale, scale2;
-    const float *x;
-    int ldx, m;
     const float *embed;
     const int64_t *tokens;
     DevState *state;
-    const float *norm_w;
-    float eps;
-    const double *ss_in;
-    int n_ss;
     float *y;
     int ldy;
     const float *resid;
@@ -95,10 +95,16 @@ constexpr Shape shape_for(int nch, int mt) {
                        : Shape{4, 4, 4};
 }
 
-// Activation row source for row mr (nullptr if mr >= m).
+// Activation row source for row mr (nullptr if mr >= m).  Only the
+// self-contained RMSNorm prologue (the first layer) reads the embedding row of
+// the current token when x is null; with one row per pass the grid has
+// exactly m rows of workgroups.  Both keep argument-dependent branches (and
+// their serialized argument fetches) off the common paths.
+template <int PRO, int MT>
 __device__ __forceinline__ const float *act_row(const KArgs &a, int mr) {
-    if (mr >= a.m) return nullptr;
-    return a.x ? a.x + (size_t)mr * a.ldx : a.embed + (size_t)a.tokens[a.state->pos] * a.k;
+    if (MT > 1 && mr >= a.m) return nullptr;
+    if (PRO == PRO_NORM && !a.x) return a.embed + (size_t)a.tokens[a.state->pos] * a.k;
+    return a.x + (size_t)mr * a.ldx;
 }
 
 // Thread t loads the float4s f4 = p*NT + t (p < XP) of a k-vector.  A wave
@@ -172,7 +178,7 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
     // chunks of every row: waiting for the activations leaves the weight
     // stream in flight
     float4 xr[XP];
-    load_vec<XP, NT>(act_row(a, m0), a.k, nch, xr);
+    load_vec<XP, NT>(act_row<PRO, MT>(a, m0), a.k, nch, xr);
     float4 gw[PRO == PRO_NORM ? XP : 1];
     if constexpr (PRO == PRO_NORM) load_vec<XP, NT>(a.norm_w, a.k, nch, gw);
     // PRO_NORMP: this thread's share of the producer's partial sums
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
     double ssp = 0.0;
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
-        if (mi > 0) load_vec<XP, NT>(act_row(a, m0 + mi), a.k, nch, xr);
+        if (mi > 0) load_vec<XP, NT>(act_row<PRO, MT>(a, m0 + mi), a.k, nch, xr);
 #pragma unroll
         for (int p = 0; p < XP; p++) {
             const int f4 = p * NT + tid;
@@ -496,6 +502,8 @@ int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     if (w.bytes() >= 0x7fffffffull)  // buffer offsets are 32-bit
         return set_error(SCRY_ERR_UNSUPPORTED, "qgemv: %zu weight bytes (limit 2 GiB per tensor)", w.bytes());
     if (g.m < 1) return set_error(SCRY_ERR_INVALID, "qgemv: m must be >= 1");
+    if (!g.x && !(g.norm_w && g.embed && g.tokens && g.state && g.m == 1))
+        return set_error(SCRY_ERR_INVALID, "qgemv: no activation (only the fused RMSNorm reads the embedding row)");
     const int nch = (w.k + 1023) / 1024;
     const int pro = g.ss_in ? PRO_NORMP : g.norm_w ? PRO_NORM : PRO_PLAIN;
     const Sel sel = select_cfg(epi, nch, g.m);
