@@ -6,14 +6,18 @@
 // Q arrives pre-scaled by 1/sqrt(hd) and RoPE'd (fused into the QKV GEMV).
 //
 // The cache is read in place ([max_seq, n_kv*hd] rows, no repeat_kv copy):
-// workgroup (g, s) handles KV head g and position split s for all n_rep query
+// one workgroup handles KV head g and position split s for all n_rep query
 // heads of the group, so each K/V row is read once per group.  Splits write
 // (max, sum, unnormalised output); the last split of a group to finish merges
 // the group's splits (log-sum-exp rescaling, in split order) into the
-// attention output row.  The partials and the per-group arrival counters live
-// in uncached device memory: a split's stores are complete in memory before
-// its counter increment, so the last arrival reads them without cache
-// maintenance.  The split count is fixed per cache, so the launch shape does
+// attention output row.
+//
+// The exchange stays inside one XCD's L2: workgroups are dispatched to the
+// XCDs round-robin by linear block id, and the 1-D grid gives every split of
+// group g the same block id mod 8, so all of them (their partial stores, the
+// group's arrival counter, and the last arrival's L1-bypassing loads) meet in
+// the same L2.  A split's stores are complete in L2 before its counter
+// increment.  The split count is fixed per cache, so the launch shape does
 // not depend on the current length and the kernel can live in a replayed
 // graph; the length comes from the device state.
 #include "internal.h"
@@ -24,8 +28,8 @@ namespace {
 
 using namespace dev;
 
-// load from the uncached exchange memory (a vector load: scalar loads would
-// go through the scalar cache)
+// device-scope load: misses the CU's L1 and reads the L2 the other splits
+// stored to (a vector load: scalar loads would go through the scalar cache)
 __device__ __forceinline__ float cload(const float *p) {
     return __builtin_bit_cast(float, __hip_atomic_load((const unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
@@ -40,23 +44,28 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 // G = lanes per cached position (each lane holds 4 of the hd values);
-// NR = max query heads per KV head handled by one workgroup.
+// NR = max query heads per KV head handled by one workgroup; NW = waves.
 //
 // Each wave walks its positions U*P at a time: the K and V rows of a step are
 // requested together (one memory round trip per step), the scores are reduced
 // over the G lanes of a position, and an online softmax keeps (max, sum, out)
-// per lane group.  The 4*P lane groups of the workgroup are merged through LDS
-// into one partial per (query head, split).
-template <int G, int NR>
-__global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
+// per lane group.  The NW*P lane groups of the workgroup are merged through
+// LDS into one partial per (query head, split); with a single split that is
+// the attention row itself.
+template <int G, int NR, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_decode(AttnArgs a) {
+    constexpr int NT = 64 * NW;
     constexpr int P = 64 / G;  // positions per load instruction
-    constexpr int U = 12;      // load instructions per step (all of a split in one round at ~770 positions)
+    constexpr int U = 12;      // load instructions per step
     constexpr int PI = P * U;  // positions per wave step
-    constexpr int SLOTS = 4 * P;
+    constexpr int SLOTS = NW * P;
     extern __shared__ float sm[];
     float *s_o = sm;                    // [SLOTS][NR][hd]
     __shared__ float s_m[SLOTS][NR], s_l[SLOTS][NR];
-    const int g = blockIdx.x, split = blockIdx.y;
+    // block b: group (b % 8) + 8 * ((b / 8) / n_splits), split (b / 8) % n_splits
+    const int bi = blockIdx.x >> 3;
+    const int g = (blockIdx.x & 7) + 8 * (bi / a.n_splits), split = bi % a.n_splits;
+    if (g >= a.n_kv) return;  // padding of the last row of 8 groups
     const int nrep = a.n_heads / a.n_kv, hd = a.head_dim, kv_dim = a.n_kv * hd;
     const int L = a.fixed_len >= 0 ? a.fixed_len : a.state->cache_len + 1;
     const int chunk = (L + a.n_splits - 1) / a.n_splits;
@@ -80,7 +89,7 @@ __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
         l[r] = 0.f;
         o[r] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (int tb = t0 + wave * PI; tb < t1; tb += 4 * PI) {
+    for (int tb = t0 + wave * PI; tb < t1; tb += NW * PI) {
         float4 kv[U], vv[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -131,7 +140,8 @@ __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
         if (dact) *(float4 *)(s_o + ((size_t)slot * NR + r) * hd + gl * 4) = o[r];
     }
     __syncthreads();
-    for (int idx = tid; idx < nrep * hd; idx += TPB) {
+    const bool single = a.n_splits == 1;
+    for (int idx = tid; idx < nrep * hd; idx += NT) {
         const int r = idx / hd, d = idx % hd;
         float M = -INFINITY;
 #pragma unroll
@@ -146,6 +156,10 @@ __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
                 osum += s_o[((size_t)q * NR + r) * hd + d] * f;
             }
         }
+        if (single) {  // the whole sequence: softmax-normalised row
+            a.xa[(size_t)(g * nrep + r) * hd + d] = M == -INFINITY ? 0.f : osum / lsum;
+            continue;
+        }
         const size_t ph = (size_t)(g * nrep + r) * a.n_splits + split;
         a.part_o[ph * hd + d] = osum;
         if (d == 0) {
@@ -153,6 +167,7 @@ __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
             a.part_ml[ph * 2 + 1] = lsum;
         }
     }
+    if (single) return;
     // count this split in once its partial stores are complete
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -165,7 +180,7 @@ __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
     // last split of group g: x[h*hd + d] = sum_s O_s[d] e^(M_s - M) / sum_s L_s e^(M_s - M),
     // every load issued before the first use (one memory round trip)
     const int ns = a.n_splits;
-    for (int idx = tid; idx < nrep * hd; idx += TPB) {
+    for (int idx = tid; idx < nrep * hd; idx += NT) {
         const int r = idx / hd, d = idx % hd, h = g * nrep + r;
         const float *ml = a.part_ml + (size_t)h * ns * 2;
         const float *po = a.part_o + (size_t)h * ns * hd + d;
@@ -179,39 +194,46 @@ __global__ __launch_bounds__(TPB) void k_attn_decode(AttnArgs a) {
         float M = -INFINITY;
 #pragma unroll
         for (int q = 0; q < MAX_SPLITS; q++) M = fmaxf(M, mq[q]);
-        float Ls = 0.f;
-#pragma unroll
-        for (int q = 0; q < MAX_SPLITS; q++)
-            if (mq[q] != -INFINITY) Ls += lq[q] * expf(mq[q] - M);
-        float v = 0.f;
+        float Ls = 0.f, v = 0.f;
 #pragma unroll
         for (int q = 0; q < MAX_SPLITS; q++) {
-            const float w = mq[q] == -INFINITY ? 0.f : expf(mq[q] - M) / Ls;
-            v += w * oq[q];
+            if (q < ns && mq[q] != -INFINITY) {
+                const float e = expf(mq[q] - M);
+                Ls += lq[q] * e;
+                v += oq[q] * e;
+            }
         }
-        a.xa[(size_t)h * hd + d] = v;
+        a.xa[(size_t)h * hd + d] = M == -INFINITY ? 0.f : v / Ls;
     }
     if (tid == 0) a.merge_ctr[g] = 0;  // ready for the next launch on the stream
 }
 
-template <int G>
-int launch_g(const AttnArgs &a, int nrep, hipStream_t s) {
+template <int G, int NW>
+int launch_gw(const AttnArgs &a, int nrep, hipStream_t s) {
     const int P = 64 / G;
-    auto lds = [&](int nr) { return (size_t)4 * P * nr * a.head_dim * 4; };
-    dim3 grid(a.n_kv, a.n_splits);
+    auto lds = [&](int nr) { return (size_t)NW * P * nr * a.head_dim * 4; };
+    dim3 grid(8 * ((a.n_kv + 7) / 8) * a.n_splits);
+    dim3 block(64 * NW);
     if (nrep <= 1) {
-        hipLaunchKernelGGL((k_attn_decode<G, 1>), grid, dim3(TPB), lds(1), s, a);
+        hipLaunchKernelGGL((k_attn_decode<G, 1, NW>), grid, block, lds(1), s, a);
     } else if (nrep <= 2) {
-        hipLaunchKernelGGL((k_attn_decode<G, 2>), grid, dim3(TPB), lds(2), s, a);
+        hipLaunchKernelGGL((k_attn_decode<G, 2, NW>), grid, block, lds(2), s, a);
     } else if (nrep <= 4) {
-        hipLaunchKernelGGL((k_attn_decode<G, 4>), grid, dim3(TPB), lds(4), s, a);
+        hipLaunchKernelGGL((k_attn_decode<G, 4, NW>), grid, block, lds(4), s, a);
     } else if (nrep <= 8) {
-        hipLaunchKernelGGL((k_attn_decode<G, 8>), grid, dim3(TPB), lds(8), s, a);
+        hipLaunchKernelGGL((k_attn_decode<G, 8, NW>), grid, block, lds(8), s, a);
     } else {
         return set_error(SCRY_ERR_UNSUPPORTED, "attention: n_heads/n_kv = %d > 8", nrep);
     }
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
+}
+
+// 16 waves when one workgroup covers a whole KV group's sequence (more loads
+// in flight per CU), 4 when the sequence is split over workgroups.
+template <int G>
+int launch_g(const AttnArgs &a, int nrep, hipStream_t s) {
+    return a.n_splits == 1 ? launch_gw<G, 16>(a, nrep, s) : launch_gw<G, 4>(a, nrep, s);
 }
 
 }  // namespace
@@ -230,8 +252,8 @@ int attn_pick_splits(int n_kv, int max_seq, int *n_splits, int *max_chunk) {
 }
 
 int launch_attn_decode(const AttnArgs &a, hipStream_t s) {
-    if (!a.merge_ctr || !a.xa || !a.part_o || !a.part_ml)
-        return set_error(SCRY_ERR_INVALID, "attention: missing partial / merge buffers");
+    if (!a.xa || (a.n_splits > 1 && (!a.merge_ctr || !a.part_o || !a.part_ml)))
+        return set_error(SCRY_ERR_INVALID, "attention: missing output / partial / merge buffers");
     if (a.n_splits < 1 || a.n_splits > MAX_SPLITS)
         return set_error(SCRY_ERR_INVALID, "attention: %d splits (1..%d)", a.n_splits, MAX_SPLITS);
     if (a.n_kv <= 0 || a.n_heads % a.n_kv != 0)

@@ -147,9 +147,9 @@ struct scry_kv_cache_s {
     // sums of squares of the residual row (written by the residual GEMVs)
     float *xg = nullptr;
     double *ss = nullptr;
-    // decode attention split partials and per-KV-group arrival counters
-    // (uncached: the last split merges them), and the merged output row
-    UcBlock att_uc{nullptr, 0, -1};
+    // decode attention split partials and per-KV-group arrival counters (the
+    // last split merges them), and the merged output row
+    void *att_buf = nullptr;
     float *ap_o = nullptr, *ap_ml = nullptr;
     unsigned *att_ctr = nullptr;
     float *xa = nullptr;
@@ -382,7 +382,7 @@ void cache_free(scry_kv_cache c) {
     dev_free(c->xq);
     dev_free(c->act);
     dev_free(c->logits);
-    uc_give(c->att_uc);
+    dev_free(c->att_buf);
     dev_free(c->xa);
     dev_free(c->lp_val);
     dev_free(c->lp_idx);
@@ -426,9 +426,9 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
         auto al = [](size_t b) { return (b + 255) / 256 * 256; };
         const size_t b_o = al(sizeof(float) * (size_t)m->nh * c->n_splits * m->hd);
         const size_t b_ml = al(sizeof(float) * (size_t)m->nh * c->n_splits * 2);
-        rc = uc_take(b_o + b_ml + al(sizeof(unsigned) * m->nkv), &c->att_uc);
+        rc = dev_alloc(&c->att_buf, b_o + b_ml + al(sizeof(unsigned) * m->nkv));
         if (!rc) {
-            char *base = (char *)c->att_uc.p;
+            char *base = (char *)c->att_buf;
             c->ap_o = (float *)base;
             c->ap_ml = (float *)(base + b_o);
             c->att_ctr = (unsigned *)(base + b_o + b_ml);
