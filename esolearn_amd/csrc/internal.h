@@ -115,8 +115,8 @@ struct GemvArgs {
     const float *norm_w = nullptr;  // RMSNorm weight -> fused RMSNorm prologue
     float eps = 1e-5f;
     // pre-scaled RMSNorm input: x holds x*g, and the residual GEMV that wrote
-    // it left n_ss per-workgroup partial sums of x^2 (x itself) in ss_in
-    const double *ss_in = nullptr;
+    // it left n_ss per-workgroup partial sums of x^2 (x itself, f32) in ss_in
+    const float *ss_in = nullptr;
     int n_ss = 0;
     // outputs
     float *y = nullptr;
@@ -127,7 +127,7 @@ struct GemvArgs {
     // sums of y^2 (qgemv_blocks entries)
     float *xg_out = nullptr;
     const float *g_next = nullptr;
-    double *ss_out = nullptr;
+    float *ss_out = nullptr;
     // EPI_QKV
     float *q_out = nullptr, *k_cache = nullptr, *v_cache = nullptr;
     const float2 *rope_cs = nullptr;  // [max_pos][head_dim/2] (cos, sin)

@@ -103,18 +103,24 @@ __device__ __forceinline__ ArgAcc arg_combine(ArgAcc l, ArgAcc r) {  // l preced
 
 // All 256 threads: ordered reduction of per-thread accumulators (thread t
 // covers an index range preceding thread t+1's).  Result in every thread.
+// In-order combines over wave shuffles (lane i joins lane i + off, which
+// covers the indices after its own), then the four wave results in order
+// through sh[0..3] (one barrier).
 __device__ inline ArgAcc block_argmax(ArgAcc a, ArgAcc *sh) {
-    const int tid = threadIdx.x;
-    sh[tid] = a;
-    __syncthreads();
-    for (int off = 1; off < TPB; off <<= 1) {
-        ArgAcc mine = sh[tid];
-        ArgAcc other = (tid + off < TPB) ? sh[tid + off] : ArgAcc{0.f, -1, -1};
-        __syncthreads();
-        if ((tid & (2 * off - 1)) == 0) sh[tid] = arg_combine(mine, other);
-        __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        ArgAcc o;
+        o.v = __shfl_down(a.v, off);
+        o.i = __shfl_down(a.i, off);
+        o.nan = __shfl_down(a.nan, off);
+        if (lane + off < 64) a = arg_combine(a, o);
     }
+    if (lane == 0) sh[wave] = a;
+    __syncthreads();
     ArgAcc r = sh[0];
+#pragma unroll
+    for (int w = 1; w < TPB / 64; w++) r = arg_combine(r, sh[w]);
     __syncthreads();
     return r;
 }

@@ -146,7 +146,7 @@ struct scry_kv_cache_s {
     // the residual row times the next RMSNorm weight, and the per-workgroup
     // sums of squares of the residual row (written by the residual GEMVs)
     float *xg = nullptr;
-    double *ss = nullptr;
+    float *ss = nullptr;
     // decode attention split partials and per-KV-group arrival counters (the
     // last split merges them), and the merged output row
     void *att_buf = nullptr;
@@ -417,7 +417,7 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
     if (!rc) rc = dev_alloc((void **)&c->tokens, sizeof(int64_t) * c->tokens_len);
     if (!rc) rc = dev_alloc((void **)&c->x, sizeof(float) * m->h);
     if (!rc) rc = dev_alloc((void **)&c->xg, sizeof(float) * m->h);
-    if (!rc) rc = dev_alloc((void **)&c->ss, sizeof(double) * n_ss);
+    if (!rc) rc = dev_alloc((void **)&c->ss, sizeof(float) * n_ss);
     if (!rc) rc = dev_alloc((void **)&c->xq, sizeof(float) * m->q_dim);
     if (!rc) rc = dev_alloc((void **)&c->act, sizeof(float) * m->ffn);
     if (!rc) rc = dev_alloc((void **)&c->logits, sizeof(float) * m->V);

@@ -48,7 +48,7 @@ using namespace dev;
 struct KArgs {
     const uint8_t *W;
     const float *x;
-    const double *ss_in;
+    const float *ss_in;
     const float *norm_w;
     int k, kp, rows, nch;
     int ldx, m, n_ss;
@@ -65,7 +65,7 @@ struct KArgs {
     const float *bias;
     float *xg_out;
     const float *g_next;
-    double *ss_out;
+    float *ss_out;
     float *q_out, *k_cache, *v_cache;
     const float2 *rope_cs;
     int q_dim, kv_dim, head_dim;
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
     if constexpr (PRO == PRO_NORM) load_vec<XP, NT>(a.norm_w, a.k, nch, gw);
     // PRO_NORMP: this thread's share of the producer's partial sums
     // (unconditional clamped loads: no wait inside a branch)
-    double ssv[PRO == PRO_NORMP ? SSW : 1];
+    float ssv[PRO == PRO_NORMP ? SSW : 1];
     if constexpr (PRO == PRO_NORMP) {
 #pragma unroll
         for (int j = 0; j < SSW; j++) ssv[j] = a.ss_in[min(tid + NT * j, a.n_ss - 1)];
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
                 if (tid == 0) {
                     double t = 0.0;
                     for (int i = 0; i < RPW && rb + i < a.rows; i++) t += (double)s_val[i] * s_val[i];
-                    a.ss_out[blockIdx.x] = t;
+                    a.ss_out[blockIdx.x] = (float)t;
                 }
             }
         }
@@ -591,9 +591,23 @@ __global__ __launch_bounds__(TPB) void k_logits_finish(const float *__restrict__
                                                        int64_t *argmax_out, int advance) {
     __shared__ ArgAcc sh[TPB];
     const int tid = threadIdx.x;
+    // thread t combines partials [t*per, t*per + per) in order, FP at a time
+    // with every load of a batch issued before the first combine
+    constexpr int FP = 16;
     const int per = (np + TPB - 1) / TPB;
+    const int b0 = min(np, tid * per), b1 = min(np, b0 + per);
     ArgAcc acc{0.f, -1, -1};
-    for (int t = tid * per; t < min(np, tid * per + per); t++) acc = arg_combine(acc, ArgAcc{pv[t], pi[t], pn[t]});
+    for (int t0 = b0; t0 < b1; t0 += FP) {
+        ArgAcc q[FP];
+#pragma unroll
+        for (int j = 0; j < FP; j++) {
+            const int t = min(t0 + j, np - 1);  // clamped: unconditional loads
+            q[j] = ArgAcc{pv[t], pi[t], pn[t]};
+        }
+#pragma unroll
+        for (int j = 0; j < FP; j++)
+            if (t0 + j < b1) acc = arg_combine(acc, q[j]);
+    }
     const ArgAcc r = block_argmax(acc, sh);
     const int tok = argmax_finish(r, logits, V, sh);
     if (tid == 0) {
