@@ -89,23 +89,24 @@ struct ArgAcc {
     int nan;  // largest NaN index seen, -1 if none
 };
 
-__device__ __forceinline__ ArgAcc arg_combine(ArgAcc l, ArgAcc r) {  // l precedes r
+// Order-independent: the larger value, ties to the larger index (the last of
+// equal maxima), the largest NaN index.  Accumulators over any partition of
+// the indices combine in any order to the sequential scan's result.
+__device__ __forceinline__ ArgAcc arg_combine(ArgAcc l, ArgAcc r) {
     ArgAcc o;
     if (l.i < 0)
         o = r;
     else if (r.i < 0)
         o = l;
     else
-        o = (l.v > r.v) ? l : r;
+        o = (l.v > r.v || (l.v == r.v && l.i > r.i)) ? l : r;
     o.nan = max(l.nan, r.nan);
     return o;
 }
 
-// All 256 threads: ordered reduction of per-thread accumulators (thread t
-// covers an index range preceding thread t+1's).  Result in every thread.
-// In-order combines over wave shuffles (lane i joins lane i + off, which
-// covers the indices after its own), then the four wave results in order
-// through sh[0..3] (one barrier).
+// All 256 threads: reduction of per-thread accumulators over wave shuffles,
+// then the four wave results through sh[0..3] (one barrier).  Result in every
+// thread.
 __device__ inline ArgAcc block_argmax(ArgAcc a, ArgAcc *sh) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -127,11 +128,8 @@ __device__ inline ArgAcc block_argmax(ArgAcc a, ArgAcc *sh) {
 
 // sequential-semantics argmax over x[lo, hi) by the whole block
 __device__ inline ArgAcc block_argmax_range(const float *x, int lo, int hi, ArgAcc *sh) {
-    const int n = hi - lo;
-    const int per = (n + TPB - 1) / TPB;
-    const int b = lo + threadIdx.x * per, e = min(hi, b + per);
     ArgAcc a{0.f, -1, -1};
-    for (int i = b; i < e; i++) {
+    for (int i = lo + (int)threadIdx.x; i < hi; i += TPB) {  // coalesced; arg_combine is order-free
         float v = x[i];
         if (isnan(v)) {
             a.nan = i;

@@ -591,22 +591,20 @@ __global__ __launch_bounds__(TPB) void k_logits_finish(const float *__restrict__
                                                        int64_t *argmax_out, int advance) {
     __shared__ ArgAcc sh[TPB];
     const int tid = threadIdx.x;
-    // thread t combines partials [t*per, t*per + per) in order, FP at a time
-    // with every load of a batch issued before the first combine
+    // thread t combines partials t, t + TPB, ... (coalesced; arg_combine is
+    // order-free), FP at a time with every load of a batch issued first
     constexpr int FP = 16;
-    const int per = (np + TPB - 1) / TPB;
-    const int b0 = min(np, tid * per), b1 = min(np, b0 + per);
     ArgAcc acc{0.f, -1, -1};
-    for (int t0 = b0; t0 < b1; t0 += FP) {
+    for (int t0 = tid; t0 < np; t0 += FP * TPB) {
         ArgAcc q[FP];
 #pragma unroll
         for (int j = 0; j < FP; j++) {
-            const int t = min(t0 + j, np - 1);  // clamped: unconditional loads
+            const int t = min(t0 + j * TPB, np - 1);  // clamped: unconditional loads
             q[j] = ArgAcc{pv[t], pi[t], pn[t]};
         }
 #pragma unroll
         for (int j = 0; j < FP; j++)
-            if (t0 + j < b1) acc = arg_combine(acc, q[j]);
+            if (t0 + j * TPB < np) acc = arg_combine(acc, q[j]);
     }
     const ArgAcc r = block_argmax(acc, sh);
     const int tok = argmax_finish(r, logits, V, sh);
