@@ -155,7 +155,7 @@ struct AttnArgs {
     const float *q = nullptr;     // [n_heads*hd] pre-scaled
     const float *k_cache = nullptr, *v_cache = nullptr;  // [max_seq, n_kv*hd]
     // per (head, split) partials and per-KV-group arrival counters (zero
-    // between launches), in uncached device memory
+    // between launches)
     float *part_o = nullptr, *part_ml = nullptr;
     unsigned *merge_ctr = nullptr;
     float *xa = nullptr;          // merged output [n_heads*hd]
