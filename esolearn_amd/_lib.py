@@ -78,6 +78,7 @@ SIGNATURES = {
     "scry_hip_scatter_rows": [vp, vp, i32, i32, i32, i32],
     "scry_hip_argmax": [vp, P(i64)],
     "scry_hip_llama_new_random": [P(LlamaConfigC), u64, i32, i32, P(vp)],
+    "scry_hip_llama_from_safetensors": [P(LlamaConfigC), P(C.c_char_p), i32, i32, P(vp)],
     "scry_hip_llama_free": [vp],
     "scry_hip_llama_set_tensor": [vp, i32, i32, vp, sz],
     "scry_hip_llama_get_qtensor": [vp, i32, i32, vp, sz, P(f32)],

@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/scry_hip.h"
 
@@ -149,6 +150,22 @@ int qgemv_blocks(int epi, const Packed &w, int m);
 // matmul_i8_f32 with more activation rows than this runs as the MFMA GEMM
 constexpr int GEMV_MAX_M = 16;
 int launch_logits_finish(const GemvArgs &a, hipStream_t s);
+
+// safetensors.hip: memory-mapped safetensors shards and the device dtype
+// widening of the checkpoint loader
+enum { ST_OTHER = 0, ST_F32 = 1, ST_BF16 = 2, ST_F16 = 3 };
+struct StTensor {
+    std::string name, dtype_name;
+    int dtype = ST_OTHER;
+    std::vector<int64_t> shape;
+    size_t numel = 0, bytes = 0;
+    const uint8_t *data = nullptr;  // inside the mapping
+};
+struct StShards;
+int st_open(const char *const *paths, int n_paths, StShards **out);
+void st_close(StShards *sh);
+const StTensor *st_find(const StShards *sh, const char *name);  // nullptr if absent
+int launch_widen(const void *src, int dtype, size_t n, float *dst, hipStream_t s);
 
 // attn.hip
 struct AttnArgs {

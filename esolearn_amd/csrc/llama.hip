@@ -38,6 +38,9 @@ struct scry_llama_s {
     int quant_mode = 0;
     float *embed = nullptr;  // [V, h] f32
     float *norms = nullptr;  // [2L+1][h] RMSNorm weights (RMSNorm::new: ones)
+    // RMSNorm eps: 1e-5 from RMSNorm::new (rmsnorm.rs:17-22), which ignores
+    // config.rms_norm_eps; a loaded checkpoint uses the config's (llama.rs:880-914)
+    float eps = 1e-5f;
     std::vector<float> freqs;  // [hd/2] f32 (llama.rs:618-622)
     struct Layer {
         Packed qkv, o, gu, down;
@@ -571,7 +574,7 @@ int decode_setup(scry_kv_cache c) {
     a.advance = 1;
     a.rope_cs = c->rope_cs;
     a.q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
-    a.eps = 1e-5f;  // RMSNorm::new (rmsnorm.rs:17-22)
+    a.eps = m->eps;
     // per-layer offsets (floats), 64-float aligned
     int o = 0;
     a.o_xq = o; o += align64(m->q_dim);
@@ -683,7 +686,7 @@ GemvArgs qkv_args(scry_kv_cache c, int l) {
     g.embed = m->embed;
     g.tokens = c->tokens;
     g.state = c->state;
-    g.eps = 1e-5f;  // RMSNorm::new (rmsnorm.rs:17-22)
+    g.eps = m->eps;
     if (l == 0) {
         g.x = nullptr;  // the embedding row, RMSNorm'd in the prologue
         g.norm_w = m->norm_in(0);
@@ -742,7 +745,7 @@ GemvArgs gu_args(scry_kv_cache c, int l) {
     g.w = &m->layers[l].gu;
     pre_normed(c, m->layers[l].o, &g);
     g.ldx = m->h;
-    g.eps = 1e-5f;
+    g.eps = m->eps;
     g.y = c->act;
     g.ldy = m->ffn;
     return g;
@@ -767,7 +770,7 @@ GemvArgs lm_args(scry_kv_cache c, int advance) {
     g.w = &m->lm;
     pre_normed(c, m->layers[m->L - 1].down, &g);
     g.ldx = m->h;
-    g.eps = 1e-5f;
+    g.eps = m->eps;
     g.y = c->logits;
     g.ldy = m->V;
     g.state = c->state;
@@ -922,7 +925,7 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
     unsigned short *h1 = P.p1, *l1 = P.p1 + (size_t)P.Mp * P.ld1;
     SCRY_HIP(hipMemcpyAsync(P.ids, tokens, sizeof(int64_t) * M, hipMemcpyHostToDevice, s));
     SCRY_TRY(launch_embedding(m->embed, P.ids, M, m->h, P.x, s));  // cpu.rs:485-498
-    const float eps = 1e-5f;  // RMSNorm::new (rmsnorm.rs:17-22)
+    const float eps = m->eps;
     for (int l = 0; l < m->L; l++) {
         const auto &Ly = m->layers[l];
         SCRY_TRY(launch_norm_split(P.x, m->h, M, 1, 0, m->norm_in(l), m->h, eps, h0, l0, P.ld0, nullptr, 0, s));
@@ -1112,6 +1115,97 @@ int scry_hip_llama_new_random(const scry_llama_config *cfg, uint64_t seed, int q
         if (!rc) rc = quant_into(m, m->stage, h, V, 1, m->lm, 1, 1, 0, false);
     }
     if (!rc) rc = sync_stream();
+    if (rc) {
+        model_free(m);
+        return rc;
+    }
+    *out = m;
+    return SCRY_OK;
+}
+
+// LlamaModel::from_safetensors (llama.rs:765-958) with the int8 composition.
+// Tensors are looked up by their HF names in the shards (the first shard
+// holding a name wins), widened to f32 on the device and quantized with the
+// same path as the random init.  HF stores projections as [out, in], the
+// GEMV stream's row-per-output order, so they are packed from that layout
+// directly (the reference transposes them to [in, out] on the host first,
+// llama.rs:832-839; per-tensor absmax and per-element rounding give the same
+// int8 values either way).  Unlike the reference, a tensor whose shape does
+// not match the config is an error.
+int scry_hip_llama_from_safetensors(const scry_llama_config *cfg, const char *const *paths, int n_paths,
+                                    int quant_mode, scry_llama *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!out) return set_error(SCRY_ERR_INVALID, "null argument");
+    scry_llama m = nullptr;
+    SCRY_TRY(model_alloc(cfg, quant_mode, &m));
+    StShards *sh = nullptr;
+    int rc = st_open(paths, n_paths, &sh);
+    hipStream_t s = ctx().stream;
+    void *raw = nullptr;
+    size_t raw_n = 0;
+    const int h = m->h, V = m->V, ffn = m->ffn, qd = m->q_dim, kvd = m->kv_dim;
+    // tensor `name` ([rows, cols], or [cols] when rows == 0) into dst as f32
+    auto fetch = [&](const std::string &name, int rows, int cols, float *dst) -> int {
+        const StTensor *t = st_find(sh, name.c_str());
+        if (!t) return set_error(SCRY_ERR_INVALID, "tensor '%s' not found in any shard", name.c_str());
+        if (t->dtype == ST_OTHER)
+            return set_error(SCRY_ERR_UNSUPPORTED, "unsupported dtype %s for tensor '%s'", t->dtype_name.c_str(),
+                             name.c_str());
+        const bool ok = rows > 0 ? t->shape.size() == 2 && t->shape[0] == rows && t->shape[1] == cols
+                                 : t->shape.size() == 1 && t->shape[0] == cols;
+        if (!ok) {
+            std::string sh_s;
+            for (size_t i = 0; i < t->shape.size(); i++) sh_s += (i ? ", " : "") + std::to_string(t->shape[i]);
+            return rows > 0 ? set_error(SCRY_ERR_INVALID, "tensor '%s': shape [%s], expected [%d, %d]", name.c_str(),
+                                        sh_s.c_str(), rows, cols)
+                            : set_error(SCRY_ERR_INVALID, "tensor '%s': shape [%s], expected [%d]", name.c_str(),
+                                        sh_s.c_str(), cols);
+        }
+        if (t->bytes > raw_n) {  // the previous tensor's kernels are ordered before the free on the stream
+            SCRY_TRY(sync_stream());
+            dev_free(raw);
+            raw = nullptr;
+            raw_n = 0;
+            SCRY_TRY(dev_alloc(&raw, t->bytes));
+            raw_n = t->bytes;
+        }
+        SCRY_HIP(hipMemcpyAsync(raw, t->data, t->bytes, hipMemcpyHostToDevice, s));
+        return launch_widen(raw, t->dtype, t->numel, dst, s);
+    };
+    // llama.rs:826-827 embed_tokens; a tied lm_head is quantized from it
+    if (!rc) rc = fetch("model.embed_tokens.weight", V, h, m->embed);
+    if (!rc && m->cfg.tie_word_embeddings) rc = quant_into(m, m->embed, h, V, 1, m->lm, 1, 1, 0, false);
+    for (int l = 0; l < m->L && !rc; l++) {
+        auto &Ly = m->layers[l];
+        const std::string p = "model.layers." + std::to_string(l);
+        // llama.rs:833-883: q, k, v fused along the outputs (fuse_qkv_weights) as rows of [qkv_dim][h]
+        rc = fetch(p + ".self_attn.q_proj.weight", qd, h, m->stage);
+        if (!rc) rc = fetch(p + ".self_attn.k_proj.weight", kvd, h, m->stage + (size_t)qd * h);
+        if (!rc) rc = fetch(p + ".self_attn.v_proj.weight", kvd, h, m->stage + (size_t)(qd + kvd) * h);
+        if (!rc) rc = quant_into(m, m->stage, h, m->qkv_dim, 1, Ly.qkv, 1, 1, 0, false);
+        if (!rc) rc = fetch(p + ".self_attn.o_proj.weight", h, qd, m->stage);
+        if (!rc) rc = quant_into(m, m->stage, qd, h, 1, Ly.o, 1, 1, 0, false);
+        if (!rc) rc = fetch(p + ".mlp.gate_proj.weight", ffn, h, m->stage);
+        if (!rc) rc = quant_into(m, m->stage, h, ffn, 1, Ly.gu, 2, 4, 0, false);
+        if (!rc) rc = fetch(p + ".mlp.up_proj.weight", ffn, h, m->stage);
+        if (!rc) rc = quant_into(m, m->stage, h, ffn, 1, Ly.gu, 2, 4, 2, true);
+        if (!rc) rc = fetch(p + ".mlp.down_proj.weight", h, ffn, m->stage);
+        if (!rc) rc = quant_into(m, m->stage, ffn, h, 1, Ly.down, 1, 1, 0, false);
+        // llama.rs:880-881, 901-904, 912-915: the loaded norm weights
+        if (!rc) rc = fetch(p + ".input_layernorm.weight", 0, h, m->norms + (size_t)(2 * l) * h);
+        if (!rc) rc = fetch(p + ".post_attention_layernorm.weight", 0, h, m->norms + (size_t)(2 * l + 1) * h);
+    }
+    if (!rc) rc = fetch("model.norm.weight", 0, h, m->norms + (size_t)(2 * m->L) * h);  // llama.rs:936-940
+    if (!rc && !m->cfg.tie_word_embeddings) {                                          // llama.rs:942-953
+        rc = fetch("lm_head.weight", V, h, m->stage);
+        if (!rc) rc = quant_into(m, m->stage, h, V, 1, m->lm, 1, 1, 0, false);
+    }
+    m->eps = cfg->rms_norm_eps;  // RMSNorm { eps: config.rms_norm_eps } (llama.rs:903, 914, 939)
+    const int rs = sync_stream();
+    if (!rc) rc = rs;
+    dev_free(raw);
+    st_close(sh);
     if (rc) {
         model_free(m);
         return rc;

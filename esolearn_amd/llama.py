@@ -130,6 +130,18 @@ class LlamaModel:
              C.byref(h))
         return LlamaModel(h.value, cfg, quant_mode)
 
+    @staticmethod
+    def from_safetensors(cfg: LlamaConfig, paths, quant_mode: int = QUANT_PER_TENSOR):
+        """LlamaModel::from_safetensors (llama.rs:765-958): HF safetensors shards
+        (F32 / BF16 / F16), then the int8 layout step; the RMSNorms use the
+        loaded weights and cfg.rms_norm_eps."""
+        enc = [str(p).encode() for p in ([paths] if isinstance(paths, (str, bytes)) else paths)]
+        arr = (C.c_char_p * len(enc))(*enc)
+        c = cfg.to_c()
+        h = C.c_void_p()
+        call("scry_hip_llama_from_safetensors", C.byref(c), arr, len(enc), quant_mode, C.byref(h))
+        return LlamaModel(h.value, cfg, quant_mode)
+
     def set_tensor(self, tensor_id: int, layer: int, data) -> None:
         a = np.ascontiguousarray(data, dtype=np.float32).ravel()
         call("scry_hip_llama_set_tensor", self.h, tensor_id, layer, a.ctypes.data, a.size)

@@ -172,6 +172,18 @@ enum {
  * device libm (identical except where the two libms differ in the last bit). */
 int scry_hip_llama_new_random(const scry_llama_config *cfg, uint64_t seed, int quant_mode,
                               int init_on_device, scry_llama *out);
+/* LlamaModel::from_safetensors (llama.rs:765-958): weights from HuggingFace
+ * safetensors shards (F32 / BF16 / F16; the first shard holding a name wins):
+ * model.embed_tokens.weight, model.layers.{i}.self_attn.{q,k,v,o}_proj.weight,
+ * model.layers.{i}.mlp.{gate,up,down}_proj.weight,
+ * model.layers.{i}.{input,post_attention}_layernorm.weight, model.norm.weight
+ * and, when not tied, lm_head.weight, in HF's [out, in] layout.  The
+ * projections are quantized with quant_mode as by new_random; the RMSNorms
+ * use the loaded weights and cfg->rms_norm_eps.  Errors (status, message):
+ * a missing tensor, an unsupported dtype, a shape that does not match cfg, an
+ * unreadable or malformed shard. */
+int scry_hip_llama_from_safetensors(const scry_llama_config *cfg, const char *const *paths, int n_paths,
+                                    int quant_mode, scry_llama *out);
 int scry_hip_llama_free(scry_llama m);
 /* Replace one tensor from host f32 data in the reference layout ([in,out]
  * row-major; embed/lm_head [V,h]); it is quantized and repacked on device.

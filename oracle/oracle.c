@@ -575,7 +575,25 @@ struct orc_llama {
     orc_proj *proj; /* n_layers * 5: qkv, o, gate, up, down */
     orc_proj lm;
     int lm_tied_f32; /* lm.w aliases embed */
+    /* RMSNorm weights, (2 n_layers + 1) x h: input and post-attention per
+     * layer, then the final norm.  RMSNorm::new (rmsnorm.rs:17-22) gives ones
+     * and eps 1e-5; from_safetensors (llama.rs:880-914, 936-940) loads the
+     * checkpoint's weights with config.rms_norm_eps. */
+    float *norms;
+    float norm_eps;
 };
+
+static void norms_init(orc_llama *m) {
+    const size_t n = (size_t)(2 * m->cfg.n_layers + 1) * m->cfg.hidden_size;
+    m->norms = (float *)malloc(sizeof(float) * n);
+    for (size_t i = 0; i < n; i++) m->norms[i] = 1.0f;
+    m->norm_eps = 1e-5f;
+}
+
+static const float *norm_w(const orc_llama *m, int which, int layer) {
+    const int h = m->cfg.hidden_size;
+    return m->norms + (which == 2 ? (size_t)(2 * m->cfg.n_layers) * h : (size_t)(2 * layer + which) * h);
+}
 
 struct orc_cache {
     int n_layers, max_seq, kv_dim;
@@ -623,6 +641,7 @@ orc_llama *orc_llama_new(const orc_llama_config *cfg, uint64_t seed, int quantiz
     m->q_dim = cfg->n_heads * m->hd;
     m->kv_dim = cfg->n_kv_heads * m->hd;
     m->qkv_dim = m->q_dim + 2 * m->kv_dim;
+    norms_init(m);
     uint64_t calls = 0;
     /* llama.rs:602-605 embed_tokens first */
     m->embed = gen(seed, &calls, (size_t)V * h);
@@ -702,6 +721,7 @@ void orc_llama_free(orc_llama *m) {
     proj_free(&m->lm);
     free(m->embed);
     free(m->freqs);
+    free(m->norms);
     free(m);
 }
 
@@ -794,6 +814,7 @@ orc_llama *orc_llama_new_empty(const orc_llama_config *cfg) {
     m->q_dim = cfg->n_heads * m->hd;
     m->kv_dim = cfg->n_kv_heads * m->hd;
     m->qkv_dim = m->q_dim + 2 * m->kv_dim;
+    norms_init(m);
     m->embed = (float *)calloc((size_t)V * h, sizeof(float));
     int np = m->hd / 2;
     double *fd = (double *)malloc(sizeof(double) * np);
@@ -829,6 +850,13 @@ int orc_llama_set_qtensor(orc_llama *m, int id, int layer, const int8_t *q, floa
 
 int orc_llama_set_embed(orc_llama *m, const float *w) {
     memcpy(m->embed, w, sizeof(float) * (size_t)m->cfg.vocab_size * m->cfg.hidden_size);
+    return 0;
+}
+
+int orc_llama_set_norm(orc_llama *m, int which, int layer, const float *w, float eps) {
+    if (which < 0 || which > 2 || (which < 2 && (layer < 0 || layer >= m->cfg.n_layers))) return -1;
+    memcpy((float *)norm_w(m, which, layer), w, sizeof(float) * m->cfg.hidden_size);
+    m->norm_eps = eps;
     return 0;
 }
 
@@ -878,8 +906,6 @@ int orc_llama_forward_with_cache(const orc_llama *m, orc_cache *c, int64_t token
     int nh = cf->n_heads, nkv = cf->n_kv_heads, hd = m->hd;
     int qd = m->q_dim, kvd = m->kv_dim, qkvd = m->qkv_dim;
     (void)pos;
-    float *ones = ALLOC(h);
-    for (int i = 0; i < h; i++) ones[i] = 1.0f;
     float *x = ALLOC(h), *xn = ALLOC(h), *qkv = ALLOC(qkvd), *qr = ALLOC(qd), *qs = ALLOC(qd),
           *kr = ALLOC(kvd), *att = ALLOC(qd), *proj = ALLOC(h), *tmp = ALLOC(h), *g = ALLOC(ffn),
           *u = ALLOC(ffn), *act = ALLOC(ffn);
@@ -895,7 +921,7 @@ int orc_llama_forward_with_cache(const orc_llama *m, orc_cache *c, int64_t token
             rc = -2;
             goto done;
         }
-        orc_rmsnorm(x, ones, 1, h, 1e-5f, xn); /* RMSNorm::new eps (rmsnorm.rs:17-22) */
+        orc_rmsnorm(x, norm_w(m, 0, l), 1, h, m->norm_eps, xn);
         if ((rc = run_proj(&P[0], xn, 1, mode, qkv)) != 0) goto done;
         /* gather_columns (mod.rs:316-331) are slices of the fused row */
         orc_rope_with_freqs_preloaded(qkv, 1, nh, hd, pos, m->freqs, qr);
@@ -922,7 +948,7 @@ int orc_llama_forward_with_cache(const orc_llama *m, orc_cache *c, int64_t token
         if ((rc = run_proj(&P[1], att, 1, mode, proj)) != 0) goto done;
         orc_add(x, proj, (size_t)h, tmp);
         memcpy(x, tmp, sizeof(float) * h);
-        orc_rmsnorm(x, ones, 1, h, 1e-5f, xn);
+        orc_rmsnorm(x, norm_w(m, 1, l), 1, h, m->norm_eps, xn);
         if ((rc = run_proj(&P[2], xn, 1, mode, g)) != 0) goto done;
         if ((rc = run_proj(&P[3], xn, 1, mode, u)) != 0) goto done;
         orc_swiglu(g, u, (size_t)ffn, act);
@@ -930,10 +956,9 @@ int orc_llama_forward_with_cache(const orc_llama *m, orc_cache *c, int64_t token
         orc_add(x, proj, (size_t)h, tmp);
         memcpy(x, tmp, sizeof(float) * h);
     }
-    orc_rmsnorm(x, ones, 1, h, 1e-5f, xn);
+    orc_rmsnorm(x, norm_w(m, 2, 0), 1, h, m->norm_eps, xn);
     rc = run_proj(&m->lm, xn, 1, mode, logits);
 done:
-    free(ones);
     free(x);
     free(xn);
     free(qkv);
@@ -961,8 +986,6 @@ int orc_llama_forward(const orc_llama *m, const int64_t *tokens, int seq, int mo
     int nh = cf->n_heads, nkv = cf->n_kv_heads, hd = m->hd;
     int qd = m->q_dim, kvd = m->kv_dim, qkvd = m->qkv_dim;
     size_t S = (size_t)seq;
-    float *ones = ALLOC(h);
-    for (int i = 0; i < h; i++) ones[i] = 1.0f;
     float *x = ALLOC(S * h), *xn = ALLOC(S * h), *qkv = ALLOC(S * qkvd), *q = ALLOC(S * qd),
           *k = ALLOC(S * kvd), *v = ALLOC(S * kvd), *qr = ALLOC(S * qd), *kr = ALLOC(S * kvd),
           *qh = ALLOC(S * qd), *kh = ALLOC(S * kvd), *vh = ALLOC(S * kvd),
@@ -973,7 +996,7 @@ int orc_llama_forward(const orc_llama *m, const int64_t *tokens, int seq, int mo
     if (rc != 0) goto done;
     for (int l = 0; l < cf->n_layers; l++) {
         const orc_proj *P = m->proj + (size_t)l * 5;
-        orc_rmsnorm(x, ones, seq, h, 1e-5f, xn);
+        orc_rmsnorm(x, norm_w(m, 0, l), seq, h, m->norm_eps, xn);
         if ((rc = run_proj(&P[0], xn, seq, mode, qkv)) != 0) goto done;
         for (int s = 0; s < seq; s++) {
             memcpy(q + (size_t)s * qd, qkv + (size_t)s * qkvd, sizeof(float) * qd);
@@ -1007,17 +1030,17 @@ int orc_llama_forward(const orc_llama *m, const int64_t *tokens, int seq, int mo
                        sizeof(float) * hd);
         if ((rc = run_proj(&P[1], ho, seq, mode, proj)) != 0) goto done;
         orc_add(x, proj, S * h, x);
-        orc_rmsnorm(x, ones, seq, h, 1e-5f, xn);
+        orc_rmsnorm(x, norm_w(m, 1, l), seq, h, m->norm_eps, xn);
         if ((rc = run_proj(&P[2], xn, seq, mode, g)) != 0) goto done;
         if ((rc = run_proj(&P[3], xn, seq, mode, u)) != 0) goto done;
         orc_swiglu(g, u, S * ffn, act);
         if ((rc = run_proj(&P[4], act, seq, mode, proj)) != 0) goto done;
         orc_add(x, proj, S * h, x);
     }
-    orc_rmsnorm(x, ones, seq, h, 1e-5f, xn);
+    orc_rmsnorm(x, norm_w(m, 2, 0), seq, h, m->norm_eps, xn);
     rc = run_proj(&m->lm, xn, seq, mode, logits);
 done:
-    free(ones); free(x); free(xn); free(qkv); free(q); free(k); free(v); free(qr); free(kr);
+    free(x); free(xn); free(qkv); free(q); free(k); free(v); free(qr); free(kr);
     free(qh); free(kh); free(vh); free(ke); free(ve); free(sc); free(pr); free(o); free(ho);
     free(proj); free(g); free(u); free(act);
     return rc;

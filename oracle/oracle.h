@@ -128,6 +128,9 @@ void orc_llama_free(orc_llama *m);
 orc_llama *orc_llama_new_empty(const orc_llama_config *cfg);
 int orc_llama_set_qtensor(orc_llama *m, int id, int layer, const int8_t *q, float scale);
 int orc_llama_set_embed(orc_llama *m, const float *w);
+/* RMSNorm weight `which` (0 input, 1 post-attention: of `layer`; 2 final) and
+ * the eps of every norm, as from_safetensors loads them (llama.rs:880-914). */
+int orc_llama_set_norm(orc_llama *m, int which, int layer, const float *w, float eps);
 uint64_t orc_llama_rng_calls(const orc_llama *m);
 /* copies a tensor out; returns element count (0 if absent) */
 size_t orc_llama_tensor(const orc_llama *m, int id, int layer, float *out);

@@ -76,6 +76,7 @@ def lib():
         "orc_llama_new_empty": (vp, [vp]),
         "orc_llama_set_qtensor": (i32, [vp, i32, i32, i8p, f32]),
         "orc_llama_set_embed": (i32, [vp, f32p]),
+        "orc_llama_set_norm": (i32, [vp, i32, i32, f32p, f32]),
         "orc_llama_rng_calls": (u64, [vp]),
         "orc_llama_tensor": (sz, [vp, i32, i32, vp]),
         "orc_llama_qtensor": (sz, [vp, i32, i32, vp, C.POINTER(C.c_float)]),
@@ -373,6 +374,11 @@ class Llama:
 
     def set_embed(self, w):
         lib().orc_llama_set_embed(self.h, _f32(w).ravel())
+
+    def set_norm(self, which, layer, w, eps):
+        """which: 0 input / 1 post-attention norm of `layer`, 2 the final norm."""
+        if lib().orc_llama_set_norm(self.h, which, layer, _f32(w).ravel(), float(eps)) != 0:
+            raise ValueError("set_norm: bad norm")
 
     def close(self):
         if self.h:

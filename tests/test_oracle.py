@@ -435,3 +435,28 @@ def test_llama_greedy_determinism_and_quant_error(orc):
     lf = m.forward([3, 7, 1], mode=0)
     lq = m.forward([3, 7, 1], mode=1)
     assert np.abs(lf - lq).max() < 0.05 * np.abs(lf).max()
+
+
+def test_llama_loaded_norm_weights_and_eps(orc):
+    """from_safetensors norms (llama.rs:880-914, 936-940): a final-norm weight
+    of 2 doubles every logit exactly (x2 commutes with each rounding on the
+    path: f64 RMSNorm product, f64 int8 products, f32 sums); eps and the
+    per-layer weights are used (the logits move)."""
+    m = _model(orc)
+    h = m.cfg.hidden_size
+    toks = [3, 7, 1, 9]
+    base = m.forward(toks, mode=1)
+    m.set_norm(2, 0, np.full(h, 2.0, np.float32), 1e-5)
+    assert np.array_equal(m.forward(toks, mode=1), 2 * base)
+    c = m.new_cache(16)
+    step = [m.forward_with_cache(c, t, p, mode=1) for p, t in enumerate(toks)]
+    assert np.abs(step[-1] - 2 * base[-1]).max() < 2e-3 * np.abs(base).max()
+    m.set_norm(2, 0, np.ones(h, np.float32), 1e-5)
+    assert np.array_equal(m.forward(toks, mode=1), base)
+    m.set_norm(0, 1, np.linspace(0.5, 1.5, h, dtype=np.float32), 1e-5)
+    moved = m.forward(toks, mode=1)
+    assert not np.array_equal(moved, base)
+    m.set_norm(0, 1, np.ones(h, np.float32), 0.25)  # eps alone
+    assert not np.array_equal(m.forward(toks, mode=1), base)
+    with pytest.raises(ValueError):
+        m.set_norm(0, 5, np.ones(h, np.float32), 1e-5)
