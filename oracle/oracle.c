@@ -25,6 +25,8 @@
  *   Llama decode/forward tests/llama_smoke.rs invariants: cache == full forward
  *                        (1e-3), greedy determinism, GQA ratios (pinned as
  *                        invariants; no reference logits exist)
+ *   loaded norms         llama.rs:880-914, 936-940 (set_norm): a final-norm
+ *                        weight of 2 doubles every logit exactly (pinned)
  *   fastrand / Box-Muller parity UNPINNED: no reference test fixes any value
  *                        of the fastrand 2.3.0 stream.
  */
