@@ -526,6 +526,93 @@ int64_t orc_argmax(const float *logits, int64_t n) {
     return best;
 }
 
+/* generate.rs:92-165 sample_token, with the fastrand restatement above as
+ * the rng (Rng::f64 once per sampled token, in weighted_sample).
+ *
+ * The reference sorts with sort_unstable_by (descending), whose order among
+ * equal values is unspecified.  Top-k only reads the k-th value, so ties do
+ * not matter there; top-p keeps the first cutoff entries of that order, so
+ * when the cutoff falls inside a run of equal probabilities the reference's
+ * choice of indices is unspecified.  This restatement breaks ties by the
+ * smaller index (a sort by (value desc, index asc)). */
+typedef struct {
+    double v;
+    int64_t i;
+} orc_vi;
+
+static int vi_desc(const void *a, const void *b) {
+    const orc_vi *x = (const orc_vi *)a, *y = (const orc_vi *)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return x->i < y->i ? -1 : (x->i > y->i);
+}
+
+int64_t orc_sample_token(const float *logits, int64_t n, float temperature, int64_t top_k, float top_p,
+                         uint64_t *rng_state) {
+    if (temperature < 1e-8f) return orc_argmax(logits, n); /* generate.rs:96-98 */
+    double *sc = (double *)malloc(sizeof(double) * (size_t)n);
+    for (int64_t i = 0; i < n; i++) sc[i] = (double)logits[i] / (double)temperature;
+    orc_vi *ix = (orc_vi *)malloc(sizeof(orc_vi) * (size_t)n);
+    if (top_k > 0 && top_k < n) { /* generate.rs:108-118 */
+        for (int64_t i = 0; i < n; i++) ix[i] = (orc_vi){sc[i], i};
+        qsort(ix, (size_t)n, sizeof(orc_vi), vi_desc);
+        const double thr = ix[top_k - 1].v;
+        for (int64_t i = 0; i < n; i++)
+            if (sc[i] < thr) sc[i] = -INFINITY;
+    }
+    /* generate.rs:120-131: softmax in f64, uniform when the sum is not > 0 */
+    double mx = -INFINITY;
+    for (int64_t i = 0; i < n; i++) mx = fmax(mx, sc[i]);
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; i++) {
+        sc[i] = exp(sc[i] - mx);
+        sum += sc[i];
+    }
+    if (sum > 0.0) {
+        for (int64_t i = 0; i < n; i++) sc[i] /= sum;
+    } else {
+        const double u = 1.0 / (double)n;
+        for (int64_t i = 0; i < n; i++) sc[i] = u;
+    }
+    if (top_p < 1.0f && top_p > 0.0f) { /* generate.rs:134-160 */
+        for (int64_t i = 0; i < n; i++) ix[i] = (orc_vi){sc[i], i};
+        qsort(ix, (size_t)n, sizeof(orc_vi), vi_desc);
+        double cum = 0.0;
+        int64_t cut = n;
+        for (int64_t j = 0; j < n; j++) {
+            cum += ix[j].v;
+            if (cum >= (double)top_p) {
+                cut = j + 1;
+                break;
+            }
+        }
+        unsigned char *keep = (unsigned char *)calloc((size_t)n, 1);
+        for (int64_t j = 0; j < cut; j++) keep[ix[j].i] = 1;
+        for (int64_t i = 0; i < n; i++)
+            if (!keep[i]) sc[i] = 0.0;
+        free(keep);
+        double sum2 = 0.0;
+        for (int64_t i = 0; i < n; i++) sum2 += sc[i];
+        if (sum2 > 0.0)
+            for (int64_t i = 0; i < n; i++) sc[i] /= sum2;
+    }
+    /* generate.rs:175-186 weighted_sample */
+    *rng_state += WY0;
+    const double r = wy_f64(wy_mix(*rng_state));
+    double cum = 0.0;
+    int64_t tok = n - 1;
+    for (int64_t i = 0; i < n; i++) {
+        cum += sc[i];
+        if (r < cum) {
+            tok = i;
+            break;
+        }
+    }
+    free(sc);
+    free(ix);
+    return tok;
+}
+
 /* llama.rs:1035-1067 compute_rope_freqs (f64, optional Llama-3 scaling). */
 void orc_compute_rope_freqs(int head_dim, float theta, int has_scaling, double factor,
                             double low_freq_factor, double high_freq_factor,
@@ -1051,6 +1138,34 @@ done:
 /* generate.rs:51-89 with temperature < 1e-8 (sample_token -> argmax).
  * Returns the number of tokens written: max(1, max_tokens), as the reference
  * pushes the prompt's sampled token before the generation loop. */
+/* generate.rs:51-89 generate() with sample_token and Rng::with_seed(seed). */
+int orc_generate(const orc_llama *m, const int64_t *prompt, int n_prompt, int max_tokens, float temperature,
+                 int64_t top_k, float top_p, uint64_t seed, int mode, int64_t *out_tokens, float *step_logits) {
+    if (n_prompt <= 0) return -1;
+    int V = m->cfg.vocab_size;
+    orc_cache *c = orc_cache_new(m, n_prompt + max_tokens);
+    float *lg = ALLOC(V);
+    uint64_t st = seed;
+    int ng = 0, rc = 0;
+    for (int pos = 0; pos < n_prompt; pos++) {
+        if ((rc = orc_llama_forward_with_cache(m, c, prompt[pos], pos, mode, lg)) != 0) goto done;
+        if (pos == n_prompt - 1) {
+            if (step_logits) memcpy(step_logits + (size_t)ng * V, lg, sizeof(float) * V);
+            out_tokens[ng++] = orc_sample_token(lg, V, temperature, top_k, top_p, &st);
+        }
+    }
+    for (int i = 1; i < max_tokens; i++) {
+        if ((rc = orc_llama_forward_with_cache(m, c, out_tokens[ng - 1], n_prompt + i - 1, mode, lg)) != 0) goto done;
+        if (step_logits) memcpy(step_logits + (size_t)ng * V, lg, sizeof(float) * V);
+        out_tokens[ng++] = orc_sample_token(lg, V, temperature, top_k, top_p, &st);
+    }
+    rc = ng;
+done:
+    free(lg);
+    orc_cache_free(c);
+    return rc;
+}
+
 int orc_generate_greedy(const orc_llama *m, const int64_t *prompt, int n_prompt, int max_tokens,
                         int mode, int64_t *out_tokens, float *step_logits) {
     if (n_prompt <= 0) return -1;

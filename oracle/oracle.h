@@ -88,6 +88,10 @@ void orc_scatter_rows(float *dst, const float *src, int total_rows, int cols, in
                       int row_count);
 void orc_causal_mask_scale(float *scores, int n_mat, int seq, float scale, float mask_value);
 int64_t orc_argmax(const float *logits, int64_t n);
+/* generate.rs:92-165 sample_token; *rng_state is a fastrand state
+ * (Rng::with_seed(s) starts at s), advanced once per sampled token. */
+int64_t orc_sample_token(const float *logits, int64_t n, float temperature, int64_t top_k, float top_p,
+                         uint64_t *rng_state);
 void orc_compute_rope_freqs(int head_dim, float theta, int has_scaling, double factor,
                             double low_freq_factor, double high_freq_factor,
                             int64_t original_max_pos, double *out);
@@ -150,6 +154,9 @@ int orc_llama_forward_with_cache(const orc_llama *m, orc_cache *c, int64_t token
 int orc_llama_forward(const orc_llama *m, const int64_t *tokens, int seq, int mode,
                       float *logits);
 /* generate() greedy (generate.rs:51-89 with temperature 0) */
+/* generate.rs:51-89 generate(): returns the token count or < 0 on error. */
+int orc_generate(const orc_llama *m, const int64_t *prompt, int n_prompt, int max_tokens, float temperature,
+                 int64_t top_k, float top_p, uint64_t seed, int mode, int64_t *out_tokens, float *step_logits);
 int orc_generate_greedy(const orc_llama *m, const int64_t *prompt, int n_prompt, int max_tokens,
                         int mode, int64_t *out_tokens, float *step_logits);
 

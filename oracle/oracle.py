@@ -88,6 +88,8 @@ def lib():
         "orc_llama_forward_with_cache": (i32, [vp, vp, C.c_int64, i32, i32, f32p]),
         "orc_llama_forward": (i32, [vp, i64p, i32, i32, f32p]),
         "orc_generate_greedy": (i32, [vp, i64p, i32, i32, i32, i64p, vp]),
+        "orc_generate": (i32, [vp, i64p, i32, i32, f32, C.c_int64, f32, u64, i32, i64p, vp]),
+        "orc_sample_token": (C.c_int64, [f32p, C.c_int64, f32, C.c_int64, f32, C.POINTER(u64)]),
         "orc_set_threads": (None, [i32]),
         "orc_get_threads": (i32, []),
     }
@@ -289,6 +291,14 @@ def causal_mask_scale(scores, n_mat, seq, scale_, mask_value):
     return s
 
 
+def sample_token(logits, temperature, top_k, top_p, rng_state: int):
+    """generate.rs:92-165; returns (token, the rng state after the call)."""
+    st = C.c_uint64(rng_state)
+    tok = lib().orc_sample_token(_f32(logits), len(logits), float(temperature), int(top_k),
+                                 float(top_p), C.byref(st))
+    return int(tok), int(st.value)
+
+
 def argmax(logits) -> int:
     x = _f32(logits).ravel()
     return int(lib().orc_argmax(x, x.size))
@@ -431,6 +441,22 @@ class Llama:
         if rc != 0:
             raise RuntimeError(f"oracle forward failed: {rc}")
         return out.reshape(t.size, self.cfg.vocab_size)
+
+    def generate(self, prompt, max_tokens, temperature, top_k, top_p, seed, mode=1,
+                 want_logits=False):
+        """generate() (generate.rs:51-89) with sample_token and Rng::with_seed(seed)."""
+        p = np.ascontiguousarray(prompt, np.int64)
+        nout = max(1, max_tokens)
+        toks = np.empty(nout, np.int64)
+        lg = np.empty(nout * self.cfg.vocab_size, np.float32) if want_logits else None
+        rc = lib().orc_generate(self.h, p, p.size, max_tokens, float(temperature), int(top_k),
+                                float(top_p), int(seed), mode, toks,
+                                lg.ctypes.data if lg is not None else None)
+        if rc < 0:
+            raise RuntimeError(f"oracle generate failed: {rc}")
+        if want_logits:
+            return toks[:rc], lg.reshape(nout, -1)[:rc]
+        return toks[:rc]
 
     def generate_greedy(self, prompt, max_tokens, mode=1, want_logits=False):
         p = np.ascontiguousarray(prompt, np.int64)

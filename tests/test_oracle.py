@@ -460,3 +460,73 @@ def test_llama_loaded_norm_weights_and_eps(orc):
     assert not np.array_equal(m.forward(toks, mode=1), base)
     with pytest.raises(ValueError):
         m.set_norm(0, 5, np.ones(h, np.float32), 1e-5)
+
+
+# ------------------------------------------------ sampling (generate.rs:92-186)
+def _sample_py(logits, t, k, p, r):
+    """generate.rs:92-186 in plain Python (f64, sequential sums), ties in the
+    sorts broken by the smaller index."""
+    n = len(logits)
+    sc = [float(x) / float(np.float32(t)) for x in logits]
+    if 0 < k < n:
+        thr = sorted(sc, reverse=True)[k - 1]
+        sc = [-math.inf if v < thr else v for v in sc]
+    mx = max(sc)
+    pr = [math.exp(v - mx) for v in sc]
+    s = 0.0
+    for v in pr:
+        s += v
+    pr = [v / s for v in pr] if s > 0 else [1.0 / n] * n
+    pf = float(np.float32(p))
+    if 0.0 < pf < 1.0:
+        order = sorted(range(n), key=lambda i: (-pr[i], i))
+        cum, cut = 0.0, n
+        for j, i in enumerate(order):
+            cum += pr[i]
+            if cum >= pf:
+                cut = j + 1
+                break
+        keep = set(order[:cut])
+        pr = [v if i in keep else 0.0 for i, v in enumerate(pr)]
+        s2 = 0.0
+        for v in pr:
+            s2 += v
+        if s2 > 0:
+            pr = [v / s2 for v in pr]
+    cum = 0.0
+    for i, v in enumerate(pr):
+        cum += v
+        if r < cum:
+            return i
+    return n - 1
+
+
+@pytest.mark.parametrize("t,k,p", [(1.0, 0, 1.0), (0.7, 3, 1.0), (1.3, 0, 0.6), (0.9, 4, 0.8),
+                                   (2.0, 7, 0.3), (1.0, 1, 1.0)])
+def test_sample_token_matches_plain_restatement(orc, t, k, p):
+    rng = np.random.default_rng(int(t * 100) + k)
+    for seed in range(40):
+        logits = rng.normal(0, 2, 9).astype(np.float32)
+        logits[seed % 9] = logits[(seed + 4) % 9]  # a tie somewhere
+        r = float(orc.rng_f64(seed, 0, 1)[0])
+        tok, st = orc.sample_token(logits, t, k, p, seed)
+        assert tok == _sample_py(logits, t, k, p, r), (seed, logits)
+        assert st == (seed + 0x2D358DCCAA6C78A5) % 2**64  # one rng call per sample
+
+
+def test_sample_token_edge_cases(orc):
+    lg = np.array([0.5, 2.0, -1.0, 2.0, 1.5], np.float32)
+    # temperature < 1e-8: argmax (last of equal maxima), no rng call
+    assert orc.sample_token(lg, 0.0, 0, 1.0, 5) == (3, 5)
+    assert orc.sample_token(lg, 9e-9, 3, 0.5, 5) == (3, 5)
+    # top_k = 1 keeps every value equal to the largest: only 1 and 3 remain
+    for seed in range(20):
+        assert orc.sample_token(lg, 1.0, 1, 1.0, seed)[0] in (1, 3)
+    # a tiny top_p keeps only the first entry of the descending order (index 1)
+    for seed in range(20):
+        assert orc.sample_token(lg, 1.0, 0, 1e-6, seed)[0] == 1
+    # every scaled logit -inf: the sum is NaN, not > 0, so the draw is uniform
+    ninf = np.full(4, -np.inf, np.float32)
+    for seed in range(20):
+        r = float(orc.rng_f64(seed, 0, 1)[0])
+        assert orc.sample_token(ninf, 1.0, 0, 1.0, seed)[0] == min(int(r * 4), 3)
