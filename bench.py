@@ -118,6 +118,25 @@ def pmc_probe(E) -> None:
     m.free()
 
 
+SAMPLING_SWEEP = [(0.8, 40, 0.95), (0.8, 0, 0.95), (1.0, 0, 1.0), (0.7, 0, 0.5)]
+
+
+def sampling_sweep(E, EL, model, prompt, warmup: int, steps: int) -> dict:
+    """Decode with the device sampler after each LM head (generate.rs:92-186)
+    against greedy decode, same session shape; device time of the steps."""
+    ms, _ = model.bench_decode(prompt, warmup, steps)
+    out = {"greedy_tok_s": round(steps / (ms / 1000.0), 2), "configs": []}
+    for T, k, p in SAMPLING_SWEEP:
+        sc = EL.SamplingConfig(temperature=T, top_k=k, top_p=p, max_tokens=steps)
+        ms_s, _ = model.bench_decode_sampled(prompt, warmup, steps, sc, seed=42)
+        out["configs"].append({"temperature": T, "top_k": k, "top_p": p,
+                               "tok_s": round(steps / (ms_s / 1000.0), 2),
+                               "extra_us_per_step": round((ms_s - ms) / steps * 1000.0, 2)})
+        print(f"[bench] sampled T={T} k={k} p={p}: {out['configs'][-1]['tok_s']} tok/s, "
+              f"+{out['configs'][-1]['extra_us_per_step']} us/step", file=sys.stderr, flush=True)
+    return out
+
+
 def weight_bytes(cfg) -> int:
     """int8 weight bytes + per-tensor scales read per decode token."""
     h, ffn, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.n_layers
@@ -178,6 +197,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill line")
     ap.add_argument("--pmc-probe", action="store_true", help="profiling workload only (see above)")
     ap.add_argument("--prefill-only", action="store_true", help="config-5 measurement only")
+    ap.add_argument("--sampling-only", action="store_true",
+                    help="greedy vs device-sampled decode over a few sampling configs only")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -206,6 +227,11 @@ def main() -> int:
     print(f"[bench] {info['name']} {info['arch']} CUs={info['cu_count']}; model init "
           f"{t_init:.1f} s", file=sys.stderr, flush=True)
 
+    if args.sampling_only:
+        print(json.dumps({"sampling": sampling_sweep(E, EL, model, prompt, args.warmup, args.steps),
+                          "prompt_tokens": args.prompt_len, "steps": args.steps}), flush=True)
+        model.free()
+        return 0
     E.HipBackend.synchronize()
     t0 = time.perf_counter()
     ms, toks = model.bench_decode(prompt, args.warmup, args.steps)
@@ -214,6 +240,17 @@ def main() -> int:
     tok_s = args.steps / (ms / 1000.0)
     print(f"[bench] decode {args.steps} steps in {ms:.2f} ms -> {tok_s:.1f} tok/s "
           f"(call wall {wall:.2f} s incl. prompt + warm-up)", file=sys.stderr, flush=True)
+
+    # the same decode with the device sampler (top-k 40, top-p 0.95, T 0.8)
+    # after each LM head instead of the argmax finish: its share of the step
+    sc = EL.SamplingConfig(temperature=0.8, top_k=40, top_p=0.95, max_tokens=args.steps)
+    ms_s, _ = model.bench_decode_sampled(prompt, args.warmup, args.steps, sc, seed=42)
+    sampled = {"config": {"temperature": 0.8, "top_k": 40, "top_p": 0.95},
+               "tok_s": round(args.steps / (ms_s / 1000.0), 2),
+               "ms_per_step": round(ms_s / args.steps, 4),
+               "extra_us_per_step_vs_greedy": round((ms_s - ms) / args.steps * 1000.0, 2)}
+    print(f"[bench] sampled decode {sampled['tok_s']} tok/s "
+          f"({sampled['extra_us_per_step_vs_greedy']} us/step over greedy)", file=sys.stderr, flush=True)
 
     # per-projection kernel timing (HIP events, rotating over layers)
     proj = {}
@@ -274,6 +311,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "projections": proj,
         "greedy_tokens_head": [int(t) for t in toks[:8]],
+        "sampled_decode": sampled,
         "prefill": pre,
     }
     print(json.dumps(line), flush=True)

@@ -36,6 +36,11 @@ class LlamaConfigC(C.Structure):
     ]
 
 
+class SamplingConfigC(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float),
+                ("max_tokens", C.c_int32)]
+
+
 vp, sz, i32, i64, u64, f32, f64 = (C.c_void_p, C.c_size_t, C.c_int, C.c_int64, C.c_uint64,
                                    C.c_float, C.c_double)
 P = C.POINTER
@@ -77,6 +82,7 @@ SIGNATURES = {
     "scry_hip_repeat_kv": [vp, i32, i32, i32, i32, P(vp)],
     "scry_hip_scatter_rows": [vp, vp, i32, i32, i32, i32],
     "scry_hip_argmax": [vp, P(i64)],
+    "scry_hip_sample_token": [vp, P(SamplingConfigC), P(u64), P(i64)],
     "scry_hip_llama_new_random": [P(LlamaConfigC), u64, i32, i32, P(vp)],
     "scry_hip_llama_from_safetensors": [P(LlamaConfigC), P(C.c_char_p), i32, i32, P(vp)],
     "scry_hip_llama_free": [vp],
@@ -90,12 +96,14 @@ SIGNATURES = {
     "scry_hip_llama_forward_with_cache": [vp, vp, i64, i32, vp, P(i64)],
     "scry_hip_llama_generate_greedy": [vp, vp, i32, i32, vp, P(i32), vp],
     "scry_hip_llama_generate_greedy_prefill": [vp, vp, i32, i32, vp, P(i32), vp],
+    "scry_hip_llama_generate": [vp, vp, i32, P(SamplingConfigC), P(u64), i32, vp, P(i32), vp],
     "scry_hip_llama_forward": [vp, vp, i32, vp],
     "scry_hip_llama_prefill": [vp, vp, i32, vp, i32, vp],
     "scry_hip_llama_bench_prefill": [vp, vp, i32, i32, i32, vp, P(f64), P(f64)],
     "scry_hip_set_decode_mode": [i32],
     "scry_hip_decode_mode_active": [vp, P(i32)],
     "scry_hip_llama_bench_decode": [vp, vp, i32, i32, i32, vp, P(f64)],
+    "scry_hip_llama_bench_decode_sampled": [vp, vp, i32, i32, i32, P(SamplingConfigC), u64, vp, P(f64)],
     "scry_hip_llama_time_projection": [vp, i32, i32, i32, P(f64), P(f64)],
     "scry_hip_bench_qgemv": [i32, i32, i32, i32, i32, i32, i32, P(f64), P(f64)],
 }

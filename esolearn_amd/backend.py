@@ -262,6 +262,18 @@ class HipBackend:
         call("scry_hip_argmax", logits.h, C.byref(out))
         return int(out.value)
 
+    @staticmethod
+    def sample_token(logits: Storage, config, rng) -> int:
+        """sample_token (generate.rs:92-186) on the device: config is a
+        SamplingConfig, rng an Rng whose state advances by the draw."""
+        sc = _lib.SamplingConfigC(float(config.temperature), int(config.top_k),
+                                  float(config.top_p), int(config.max_tokens))
+        st = C.c_uint64(rng.state)
+        out = C.c_int64()
+        call("scry_hip_sample_token", logits.h, C.byref(sc), C.byref(st), C.byref(out))
+        rng.state = int(st.value)
+        return int(out.value)
+
 
 def init(device: int = 0) -> None:
     HipBackend.init_gpu(device)

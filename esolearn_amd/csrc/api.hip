@@ -627,4 +627,43 @@ int scry_hip_argmax(scry_buf logits, int64_t *out) {
     return rc;
 }
 
+int scry_hip_sample_token(scry_buf logits, const scry_sampling_config *cfg, uint64_t *rng_state, int64_t *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(logits, "sample_token");
+    if (!cfg || !rng_state || !out) return set_error(SCRY_ERR_INVALID, "sample_token: null argument");
+    if (cfg->temperature != cfg->temperature || cfg->top_p != cfg->top_p || cfg->top_k < 0)
+        return set_error(SCRY_ERR_INVALID, "sample_token: NaN temperature / top_p or negative top_k");
+    if (logits->n > 0x7fffffff) return set_error(SCRY_ERR_UNSUPPORTED, "sample_token: vocabulary too large");
+    if (cfg->temperature < 1e-8f) return scry_hip_argmax(logits, out);  // generate.rs:96-98
+    hipStream_t s = ctx().stream;
+    // one block: DevState, tokens[2], the rng state, f64 scratch [n]
+    const size_t V = logits->n;
+    char *blk = nullptr;
+    SCRY_TRY(dev_alloc((void **)&blk, 64 + sizeof(double) * V));
+    DevState *st = (DevState *)blk;
+    int64_t *toks = (int64_t *)(blk + 16);
+    unsigned long long *rng = (unsigned long long *)(blk + 32);
+    double *ws = (double *)(blk + 64);
+    struct {
+        DevState st;
+        int64_t toks[2];
+        uint64_t rng;
+    } h{{0, 0, 1, 1}, {0, 0}, *rng_state};  // position 0 of a 1-token prompt: one draw
+    static_assert(sizeof(DevState) == 16, "DevState layout");
+    hipError_t e = hipMemcpyAsync(blk, &h, sizeof h, hipMemcpyHostToDevice, s);
+    int rc = e == hipSuccess ? SCRY_OK : hip_fail(e, "sample_token upload", __FILE__, __LINE__);
+    if (!rc) rc = launch_sample(logits->d, (int)V, *cfg, ws, rng, st, toks, s);
+    if (!rc) {
+        e = hipMemcpyAsync(&h, blk, sizeof h, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(e, "sample_token readback", __FILE__, __LINE__);
+    }
+    dev_free(blk);
+    if (rc) return rc;
+    *out = h.toks[1];
+    *rng_state = h.rng;
+    return SCRY_OK;
+}
+
 }  // extern "C"

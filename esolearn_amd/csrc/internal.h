@@ -150,6 +150,11 @@ int qgemv_blocks(int epi, const Packed &w, int m);
 // matmul_i8_f32 with more activation rows than this runs as the MFMA GEMM
 constexpr int GEMV_MAX_M = 16;
 int launch_logits_finish(const GemvArgs &a, hipStream_t s);
+// sample_token on the device (sample.hip): logits [V] -> tokens[pos + 1] when
+// the position draws a token, then the position advances.  ws: [V] f64
+// scratch; rng: the wyrand state.
+int launch_sample(const float *logits, int V, const scry_sampling_config &sc, double *ws,
+                  unsigned long long *rng, DevState *st, int64_t *tokens, hipStream_t s);
 
 // safetensors.hip: memory-mapped safetensors shards and the device dtype
 // widening of the checkpoint loader

@@ -159,6 +159,12 @@ struct scry_kv_cache_s {
     float *lp_val = nullptr;
     int *lp_idx = nullptr, *lp_nan = nullptr;
     int64_t *amax = nullptr;
+    // stochastic sampling (generate with temperature >= 1e-8): the config the
+    // step graph was captured with, f64 scratch [V] and the wyrand state
+    bool sampling = false;
+    scry_sampling_config samp{};
+    double *samp_ws = nullptr;
+    unsigned long long *rng = nullptr;
     int n_splits = 1, max_chunk = 16;
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
@@ -391,6 +397,8 @@ void cache_free(scry_kv_cache c) {
     dev_free(c->lp_idx);
     dev_free(c->lp_nan);
     dev_free(c->amax);
+    dev_free(c->samp_ws);
+    dev_free(c->rng);
     dev_free(c->dr.layers);
     uc_give(c->dr.uc);
     if (c->hs) (void)hipHostFree(c->hs);
@@ -794,6 +802,8 @@ int record_step(scry_kv_cache c, hipStream_t s) {
     }
     const GemvArgs lg = lm_args(c, 1);
     SCRY_TRY(launch_qgemv(EPI_LOGITS, lg, s));
+    if (c->sampling)
+        return launch_sample(c->logits, m->V, c->samp, c->samp_ws, c->rng, c->state, c->tokens, s);
     return launch_logits_finish(lg, s);
 }
 
@@ -802,7 +812,7 @@ int record_step(scry_kv_cache c, hipStream_t s) {
 // do not follow graph launches.
 int run_step(scry_kv_cache c) {
     bool persistent = false;
-    SCRY_TRY(decode_use_persistent(c, &persistent));
+    if (!c->sampling) SCRY_TRY(decode_use_persistent(c, &persistent));
     if (persistent) return decode_launch(c);
     hipStream_t s = ctx().stream;
     static const bool no_graph = std::getenv("SCRY_HIP_NO_GRAPH") != nullptr;
@@ -1004,12 +1014,13 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
     return SCRY_OK;
 }
 
-// generate() with temperature 0 (generate.rs:51-89): the prompt is fed token
-// by token through the decode step (or, with prefill, all but its last token
-// through one batched prefill), then greedy tokens follow; the token loop
-// runs on the device.
+// generate() (generate.rs:51-89): the prompt is fed token by token through
+// the decode step (or, with prefill, all but its last token through one
+// batched prefill), then tokens follow, greedy (samp == nullptr) or drawn by
+// the device sampler with rng state seed; the token loop runs on the device.
 int generate_impl(scry_llama m, const int64_t *prompt, int n_prompt, int max_tokens, int64_t *out_tokens,
-                  int *n_out, float *step_logits, bool prefill) {
+                  int *n_out, float *step_logits, bool prefill, const scry_sampling_config *samp = nullptr,
+                  uint64_t *rng_state = nullptr) {
     SCRY_REQUIRE_INIT();
     if (!m || !prompt || !out_tokens || !n_out) return set_error(SCRY_ERR_INVALID, "null argument");
     if (n_prompt <= 0) return set_error(SCRY_ERR_INVALID, "generate: prompt_tokens must not be empty");
@@ -1021,8 +1032,20 @@ int generate_impl(scry_llama m, const int64_t *prompt, int n_prompt, int max_tok
     SCRY_TRY(cache_new(m, n_prompt + max_tokens, &c));  // generate.rs:62-63
     hipStream_t s = ctx().stream;
     int rc = SCRY_OK;
-    hipError_t e = hipMemcpyAsync(c->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, s);
-    if (e != hipSuccess) rc = hip_fail(e, "prompt upload", __FILE__, __LINE__);
+    hipError_t e = hipSuccess;
+    if (samp) {
+        c->sampling = true;
+        c->samp = *samp;
+        rc = dev_alloc((void **)&c->samp_ws, sizeof(double) * (size_t)m->V);
+        if (!rc) rc = dev_alloc((void **)&c->rng, sizeof(unsigned long long));
+        if (!rc) {
+            e = hipMemcpyAsync(c->rng, rng_state, sizeof *rng_state, hipMemcpyHostToDevice, s);
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            if (e != hipSuccess) rc = hip_fail(e, "rng upload", __FILE__, __LINE__);
+        }
+    }
+    if (!rc) e = hipMemcpyAsync(c->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, s);
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "prompt upload", __FILE__, __LINE__);
     const int start = prefill ? n_prompt - 1 : 0;
     if (!rc && start > 0) rc = prefill_core(m, &c, 1, prompt, start, nullptr, nullptr);
     if (!rc) rc = set_state(c, start, start, n_prompt);
@@ -1037,6 +1060,7 @@ int generate_impl(scry_llama m, const int64_t *prompt, int n_prompt, int max_tok
     }
     if (!rc) {
         e = hipMemcpyAsync(out_tokens, c->tokens + n_prompt, sizeof(int64_t) * nout, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess && samp) e = hipMemcpyAsync(rng_state, c->rng, sizeof *rng_state, hipMemcpyDeviceToHost, s);
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e != hipSuccess) rc = hip_fail(e, "token readback", __FILE__, __LINE__);
     }
@@ -1362,6 +1386,19 @@ int scry_hip_llama_generate_greedy_prefill(scry_llama m, const int64_t *prompt, 
     return generate_impl(m, prompt, n_prompt, max_tokens, out_tokens, n_out, step_logits, true);
 }
 
+int scry_hip_llama_generate(scry_llama m, const int64_t *prompt, int n_prompt, const scry_sampling_config *cfg,
+                            uint64_t *rng_state, int prefill, int64_t *out_tokens, int *n_out, float *step_logits) {
+    API_LOCK;
+    if (!cfg || !rng_state) return set_error(SCRY_ERR_INVALID, "null argument");
+    if (cfg->temperature != cfg->temperature || cfg->top_p != cfg->top_p)
+        return set_error(SCRY_ERR_INVALID, "generate: temperature and top_p must not be NaN");
+    if (cfg->top_k < 0) return set_error(SCRY_ERR_INVALID, "generate: top_k < 0");
+    // generate.rs:96-98: below 1e-8 every token is the argmax; no rng draws
+    const bool greedy = cfg->temperature < 1e-8f;
+    return generate_impl(m, prompt, n_prompt, cfg->max_tokens, out_tokens, n_out, step_logits, prefill != 0,
+                         greedy ? nullptr : cfg, rng_state);
+}
+
 int scry_hip_llama_forward(scry_llama m, const int64_t *tokens, int seq, float *logits) {
     API_LOCK;
     SCRY_REQUIRE_INIT();
@@ -1480,9 +1517,12 @@ int scry_hip_decode_mode_active(scry_llama m, int *persistent) {
 }
 
 // ------------------------------------------------------------ measurement
-int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_prompt, int warmup,
-                                int steps, int64_t *out_tokens, double *ms) {
-    API_LOCK;
+}  // extern "C"
+
+namespace {
+
+int bench_decode_impl(scry_llama m, const int64_t *prompt, int n_prompt, int warmup, int steps,
+                      const scry_sampling_config *samp, uint64_t seed, int64_t *out_tokens, double *ms) {
     SCRY_REQUIRE_INIT();
     if (!m || !prompt || n_prompt <= 0 || steps <= 0 || warmup < 0 || !ms)
         return set_error(SCRY_ERR_INVALID, "bench_decode: bad arguments");
@@ -1492,8 +1532,17 @@ int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_promp
     hipStream_t s = ctx().stream;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     int rc = SCRY_OK;
-    hipError_t e = hipMemcpyAsync(c->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, s);
-    if (e != hipSuccess) rc = hip_fail(e, "prompt upload", __FILE__, __LINE__);
+    hipError_t e = hipSuccess;
+    if (samp) {  // as generate_impl: the device sampler after each LM head
+        c->sampling = true;
+        c->samp = *samp;
+        rc = dev_alloc((void **)&c->samp_ws, sizeof(double) * (size_t)m->V);
+        if (!rc) rc = dev_alloc((void **)&c->rng, sizeof(unsigned long long));
+        if (!rc) e = hipMemcpyAsync(c->rng, &seed, sizeof seed, hipMemcpyHostToDevice, s);
+        if (!rc && e != hipSuccess) rc = hip_fail(e, "rng upload", __FILE__, __LINE__);
+    }
+    if (!rc) e = hipMemcpyAsync(c->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, s);
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "prompt upload", __FILE__, __LINE__);
     if (!rc) rc = set_state(c, 0, 0, n_prompt);
     // the prompt through the cache path, as generate() does
     for (int t = 0; t < n_prompt && !rc; t++) rc = run_step(c);
@@ -1529,6 +1578,25 @@ int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_promp
     if (e1) (void)hipEventDestroy(e1);
     cache_free(c);
     return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_prompt, int warmup,
+                                int steps, int64_t *out_tokens, double *ms) {
+    API_LOCK;
+    return bench_decode_impl(m, prompt, n_prompt, warmup, steps, nullptr, 0, out_tokens, ms);
+}
+
+int scry_hip_llama_bench_decode_sampled(scry_llama m, const int64_t *prompt, int n_prompt, int warmup, int steps,
+                                        const scry_sampling_config *cfg, uint64_t seed, int64_t *out_tokens,
+                                        double *ms) {
+    API_LOCK;
+    if (!cfg || !(cfg->temperature >= 1e-8f) || cfg->top_k < 0 || cfg->top_p != cfg->top_p)
+        return set_error(SCRY_ERR_INVALID, "bench_decode_sampled: needs temperature >= 1e-8, top_k >= 0");
+    return bench_decode_impl(m, prompt, n_prompt, warmup, steps, cfg, seed, out_tokens, ms);
 }
 
 int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int iters,

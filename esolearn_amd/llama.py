@@ -13,7 +13,7 @@ from dataclasses import dataclass, fields
 
 import numpy as np
 
-from ._lib import LlamaConfigC, call, load
+from ._lib import LlamaConfigC, SamplingConfigC, call, load
 
 QUANT_PER_TENSOR = 0
 QUANT_BLOCK32 = 1
@@ -194,6 +194,25 @@ class LlamaModel:
             return toks[: n.value], lg.reshape(nout, -1)[: n.value]
         return toks[: n.value]
 
+    def generate(self, prompt, config: "SamplingConfig", rng: "Rng", want_logits: bool = False,
+                 prefill: bool = False):
+        """generate() (generate.rs:51-89) with sample_token on the device;
+        rng (fastrand::Rng state) advances by one draw per sampled token."""
+        p = np.ascontiguousarray(prompt, dtype=np.int64)
+        nout = max(1, config.max_tokens)
+        toks = np.empty(nout, np.int64)
+        n = C.c_int()
+        lg = np.empty(nout * self.cfg.vocab_size, np.float32) if want_logits else None
+        sc = SamplingConfigC(float(config.temperature), int(config.top_k), float(config.top_p),
+                             int(config.max_tokens))
+        st = C.c_uint64(rng.state)
+        call("scry_hip_llama_generate", self.h, p.ctypes.data, p.size, C.byref(sc), C.byref(st),
+             int(prefill), toks.ctypes.data, C.byref(n), lg.ctypes.data if lg is not None else None)
+        rng.state = int(st.value)
+        if want_logits:
+            return toks[: n.value], lg.reshape(nout, -1)[: n.value]
+        return toks[: n.value]
+
     def forward(self, tokens) -> np.ndarray:
         """LlamaModel::forward: logits [seq, V] for every position (no cache)."""
         t = np.ascontiguousarray(tokens, dtype=np.int64)
@@ -239,6 +258,18 @@ class LlamaModel:
              toks.ctypes.data, C.byref(ms))
         return ms.value, toks
 
+    def bench_decode_sampled(self, prompt, warmup: int, steps: int, config: "SamplingConfig",
+                             seed: int = 0):
+        """bench_decode with the device sampler after every LM head."""
+        p = np.ascontiguousarray(prompt, dtype=np.int64)
+        toks = np.empty(steps, np.int64)
+        ms = C.c_double()
+        sc = SamplingConfigC(float(config.temperature), int(config.top_k), float(config.top_p),
+                             int(config.max_tokens))
+        call("scry_hip_llama_bench_decode_sampled", self.h, p.ctypes.data, p.size, warmup, steps,
+             C.byref(sc), int(seed), toks.ctypes.data, C.byref(ms))
+        return ms.value, toks
+
     def time_projection(self, tensor_id: int, iters: int = 64):
         us, b = C.c_double(), C.c_double()
         call("scry_hip_llama_time_projection", self.h, tensor_id, 0, iters, C.byref(us),
@@ -270,14 +301,29 @@ class SamplingConfig:
     max_tokens: int = 128
 
 
-def generate(model: LlamaModel, prompt_tokens, config: SamplingConfig) -> np.ndarray:
-    """generate() (generate.rs:51-89).  Greedy decoding (temperature < 1e-8,
-    generate.rs:96-98) runs entirely on the device."""
+class Rng:
+    """fastrand::Rng (2.3.0, wyrand): the 64-bit state the device sampler
+    advances.  Rng.with_seed(s) starts at s, as Rng::with_seed."""
+
+    def __init__(self, state: int = 0):
+        self.state = int(state) & 0xFFFFFFFFFFFFFFFF
+
+    @classmethod
+    def with_seed(cls, seed: int) -> "Rng":
+        return cls(seed)
+
+
+def generate(model: LlamaModel, prompt_tokens, config: SamplingConfig, rng: Rng | None = None) -> np.ndarray:
+    """generate() (generate.rs:51-89) with sample_token (generate.rs:92-186):
+    greedy below temperature 1e-8, else top-k / softmax / top-p / weighted draw
+    by the device sampler; the token loop runs entirely on the device."""
     if len(prompt_tokens) == 0:
         raise ValueError("generate: prompt_tokens must not be empty")
     if config.temperature < 1e-8:
         return model.generate_greedy(prompt_tokens, config.max_tokens)
-    raise NotImplementedError("stochastic sampling (top-k / top-p) is not on the device path yet")
+    if rng is None:
+        raise ValueError("generate: sampling needs an rng (Rng.with_seed(seed))")
+    return model.generate(prompt_tokens, config, rng)
 
 
 def bench_qgemv(m: int, k: int, n: int, quant_mode: int = QUANT_PER_TENSOR, n_bufs: int = 32,

@@ -48,6 +48,15 @@ typedef struct scry_i8buf_s *scry_i8buf; /* int8 weight storage (I8Storage)    *
 typedef struct scry_llama_s *scry_llama; /* LlamaModel with int8 projections   */
 typedef struct scry_kv_cache_s *scry_kv_cache; /* LlamaKvCache (device)        */
 
+/* SamplingConfig (generate.rs:24-45): temperature (< 1e-8 means greedy),
+ * top_k (0 or >= vocab: off), top_p (outside (0, 1): off), max_tokens. */
+typedef struct {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    int32_t max_tokens;
+} scry_sampling_config;
+
 /* ---------------------------------------------------------------- runtime */
 /* replaces cuda.rs:39-52 init_gpu (context, stream, kernel set) */
 int scry_hip_init(int device);
@@ -138,6 +147,11 @@ int scry_hip_scatter_rows(scry_buf dst, scry_buf src, int total_rows, int cols, 
                           int row_count);
 /* generate.rs:167-173 argmax (Iterator::max_by semantics), on device */
 int scry_hip_argmax(scry_buf logits, int64_t *out);
+/* sample_token (generate.rs:92-186) on device: the step sampler of
+ * scry_hip_llama_generate on one logits vector (temperature < 1e-8: argmax).
+ * *rng_state is the fastrand::Rng state, advanced by the one draw. */
+int scry_hip_sample_token(scry_buf logits, const scry_sampling_config *cfg, uint64_t *rng_state,
+                          int64_t *out);
 
 /* ------------------------------------------------------ Llama (llama.rs) */
 typedef struct {
@@ -231,6 +245,21 @@ int scry_hip_llama_generate_greedy_prefill(scry_llama m, const int64_t *prompt, 
                                            int max_tokens, int64_t *out_tokens, int *n_out,
                                            float *step_logits);
 
+/* generate() (generate.rs:51-89) with sample_token (generate.rs:92-186) on the
+ * device.  *rng_state is the fastrand::Rng (wyrand) state, as the reference's
+ * `rng: &mut fastrand::Rng` (Rng::with_seed(s) sets it to s); it is advanced
+ * by the draws made (one Rng::f64 per sampled token, none when greedy).
+ * Temperature < 1e-8 is scry_hip_llama_generate_greedy.
+ * Otherwise each step's LM head is followed by one sampling workgroup (top-k
+ * by radix select, f64 softmax, top-p cut, weighted draw) inside the captured
+ * step graph; only the token ids come back.  prefill != 0 runs the first
+ * n_prompt - 1 prompt tokens through the batched prefill (as
+ * scry_hip_llama_generate_greedy_prefill).  Outputs as
+ * scry_hip_llama_generate_greedy. */
+int scry_hip_llama_generate(scry_llama m, const int64_t *prompt, int n_prompt,
+                            const scry_sampling_config *cfg, uint64_t *rng_state, int prefill,
+                            int64_t *out_tokens, int *n_out, float *step_logits);
+
 /* LlamaModel::forward (llama.rs:683-700; attention llama.rs:162-266): logits
  * [seq, V] (host) for every position of one sequence, causal attention, no
  * cache kept.  Projections run as GEMMs on the matrix cores. */
@@ -265,6 +294,12 @@ int scry_hip_decode_mode_active(scry_llama m, int *persistent);
  * the decode steps (HIP events on the launch stream) is returned in *ms. */
 int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_prompt, int warmup,
                                 int steps, int64_t *out_tokens, double *ms);
+/* The same session with the device sampler (scry_hip_llama_generate's step:
+ * LM head, then top-k / softmax / top-p / draw) after each LM head; rng state
+ * starts at seed.  For the sampler's share of the step time. */
+int scry_hip_llama_bench_decode_sampled(scry_llama m, const int64_t *prompt, int n_prompt, int warmup,
+                                        int steps, const scry_sampling_config *cfg, uint64_t seed,
+                                        int64_t *out_tokens, double *ms);
 /* Average device time (HIP events on the launch stream) of `iters` launches
  * of one projection kernel of the model, with the same arguments the decode
  * step uses.  tensor_id: SCRY_T_QKV / O / GATE (fused gate+up) / DOWN / LM_HEAD. */
