@@ -137,6 +137,28 @@ def sampling_sweep(E, EL, model, prompt, warmup: int, steps: int) -> dict:
     return out
 
 
+LINEAR_SHAPES = [("gpt2 c_attn", 768, 2304), ("gpt2 c_fc", 768, 3072), ("gpt2 c_proj", 3072, 768),
+                 ("whisper-base fc1", 512, 2048), ("whisper-base fc2", 2048, 512),
+                 ("whisper-large fc1", 1280, 5120), ("whisper-large fc2", 5120, 1280)]
+
+
+def linear_sweep(E) -> list:
+    """Quantized Linear::forward with bias (linear.rs:67-94) at one row: the
+    dequant-fused GEMV, bias in its store epilogue.  Each shape rotates over
+    about 1 GB of weight copies, so HBM (not the 256 MB Infinity Cache) serves
+    the weights."""
+    from esolearn_amd.linear import bench_linear_bias
+    out = []
+    for name, k, n in LINEAR_SHAPES:
+        n_bufs = max(64, (1 << 30) // (k * n))
+        us, b = bench_linear_bias(1, k, n, n_bufs=n_bufs, warmup=100, iters=2000)
+        gbs = b / us / 1e3
+        out.append({"layer": name, "in": k, "out": n, "rows": 1, "avg_us": round(us, 3),
+                    "bytes": int(b), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+        print(f"[bench] linear {name:18s} {k}x{n}: {us:7.2f} us {gbs:7.1f} GB/s", file=sys.stderr, flush=True)
+    return out
+
+
 def weight_bytes(cfg) -> int:
     """int8 weight bytes + per-tensor scales read per decode token."""
     h, ffn, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.n_layers
@@ -197,6 +219,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill line")
     ap.add_argument("--pmc-probe", action="store_true", help="profiling workload only (see above)")
     ap.add_argument("--prefill-only", action="store_true", help="config-5 measurement only")
+    ap.add_argument("--linear-only", action="store_true",
+                    help="quantized Linear (bias GEMV) at GPT-2 / Whisper shapes only")
     ap.add_argument("--sampling-only", action="store_true",
                     help="greedy vs device-sampled decode over a few sampling configs only")
     args = ap.parse_args()
@@ -214,6 +238,9 @@ def main() -> int:
     E.init(0)
     if args.pmc_probe:
         pmc_probe(E)
+        return 0
+    if args.linear_only:
+        print(json.dumps({"linear_bias_gemv": linear_sweep(E)}), flush=True)
         return 0
     if args.prefill_only:
         print(json.dumps(prefill_config5(E)), flush=True)

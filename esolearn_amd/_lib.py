@@ -83,6 +83,8 @@ SIGNATURES = {
     "scry_hip_scatter_rows": [vp, vp, i32, i32, i32, i32],
     "scry_hip_argmax": [vp, P(i64)],
     "scry_hip_sample_token": [vp, P(SamplingConfigC), P(u64), P(i64)],
+    "scry_hip_normal_vec": [P(u64), sz, f32, f32, P(vp)],
+    "scry_hip_bench_qgemv_bias": [i32, i32, i32, i32, i32, i32, P(f64), P(f64)],
     "scry_hip_llama_new_random": [P(LlamaConfigC), u64, i32, i32, P(vp)],
     "scry_hip_llama_from_safetensors": [P(LlamaConfigC), P(C.c_char_p), i32, i32, P(vp)],
     "scry_hip_llama_free": [vp],

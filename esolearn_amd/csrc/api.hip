@@ -627,6 +627,29 @@ int scry_hip_argmax(scry_buf logits, int64_t *out) {
     return rc;
 }
 
+int scry_hip_normal_vec(uint64_t *rng_state, size_t n, float mean, float stdv, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!rng_state || !out) return set_error(SCRY_ERR_INVALID, "normal_vec: null argument");
+    // init.rs:3-14: two Rng::f64 per sample (Box-Muller), glibc libm on the
+    // host as the reference; the wyrand state is additive, so sample i of a
+    // draw from state s uses the calls 2i+1 and 2i+2 after s
+    std::vector<float> h(n);
+    host_normal_vec(*rng_state, 0, n, mean, stdv, h.data(), host_threads());
+    SCRY_TRY(new_buf(n, out));
+    if (n) {
+        hipError_t e = hipMemcpyAsync((*out)->d, h.data(), sizeof(float) * n, hipMemcpyHostToDevice, ctx().stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx().stream);
+        if (e != hipSuccess) {
+            del_buf(*out);
+            *out = nullptr;
+            return hip_fail(e, "normal_vec upload", __FILE__, __LINE__);
+        }
+    }
+    *rng_state += 2ull * n * 0x2d358dccaa6c78a5ull;
+    return SCRY_OK;
+}
+
 int scry_hip_sample_token(scry_buf logits, const scry_sampling_config *cfg, uint64_t *rng_state, int64_t *out) {
     API_LOCK;
     SCRY_REQUIRE_INIT();

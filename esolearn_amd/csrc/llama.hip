@@ -1674,18 +1674,23 @@ int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int i
     return rc;
 }
 
-int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, int warmup,
-                         int iters, double *avg_us, double *bytes_per_launch) {
-    API_LOCK;
+}  // extern "C"
+
+namespace {
+
+int bench_qgemv_impl(int m_rows, int k, int n, int quant_mode, int n_bufs, int warmup, int iters, bool with_bias,
+                     double *avg_us, double *bytes_per_launch) {
     SCRY_REQUIRE_INIT();
     if (m_rows <= 0 || k <= 0 || n <= 0 || n_bufs <= 0 || iters <= 0 || !avg_us)
         return set_error(SCRY_ERR_INVALID, "bench_qgemv: bad arguments");
     hipStream_t s = ctx().stream;
     std::vector<Packed> W(n_bufs);
-    float *x = nullptr, *y = nullptr;
+    float *x = nullptr, *y = nullptr, *bias = nullptr;
     int rc = dev_alloc((void **)&x, sizeof(float) * (size_t)m_rows * k);
     if (!rc) rc = dev_alloc((void **)&y, sizeof(float) * (size_t)m_rows * n);
     if (!rc) rc = launch_fill_f32(x, (size_t)m_rows * k, 0.5f, s);
+    if (!rc && with_bias) rc = dev_alloc((void **)&bias, sizeof(float) * (size_t)n);
+    if (!rc && with_bias) rc = launch_fill_f32(bias, (size_t)n, 0.25f, s);
     for (int b = 0; b < n_bufs && !rc; b++) {
         Packed &P = W[b];
         P.k = k;
@@ -1709,6 +1714,7 @@ int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, i
         g.m = m_rows;
         g.y = y;
         g.ldy = n;
+        g.bias = bias;
         return launch_qgemv(EPI_STORE, g, s);
     };
     for (int i = 0; i < warmup && !rc; i++) rc = launch(i);
@@ -1730,7 +1736,7 @@ int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, i
     }
     if (bytes_per_launch) {
         const double scales = quant_mode == SCRY_QUANT_BLOCK32 ? 4.0 * n * ((k + 31) / 32) : 4.0;
-        *bytes_per_launch = (double)k * n + scales + 4.0 * m_rows * k + 4.0 * m_rows * n;
+        *bytes_per_launch = (double)k * n + scales + 4.0 * m_rows * k + 4.0 * m_rows * n + (with_bias ? 4.0 * n : 0.0);
     }
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
@@ -1738,7 +1744,25 @@ int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, i
     for (auto &P : W) packed_free(P);
     dev_free(x);
     dev_free(y);
+    dev_free(bias);
     return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, int warmup,
+                         int iters, double *avg_us, double *bytes_per_launch) {
+    API_LOCK;
+    return bench_qgemv_impl(m_rows, k, n, quant_mode, n_bufs, warmup, iters, false, avg_us, bytes_per_launch);
+}
+
+int scry_hip_bench_qgemv_bias(int m_rows, int k, int n, int n_bufs, int warmup, int iters, double *avg_us,
+                              double *bytes_per_launch) {
+    API_LOCK;
+    return bench_qgemv_impl(m_rows, k, n, SCRY_QUANT_PER_TENSOR, n_bufs, warmup, iters, true, avg_us,
+                            bytes_per_launch);
 }
 
 }  // extern "C"

@@ -92,6 +92,7 @@ constexpr Shape shape_for(int nch, int mt) {
            : nch == 4  ? Shape{1, 8, 4}
            : nch == 11 ? Shape{1, 8, 8}
            : nch == 14 ? Shape{1, 8, 7}
+           : nch == 0  ? Shape{1, 8, 4}  // any k, one row: 8 rows per workgroup
                        : Shape{4, 4, 4};
 }
 

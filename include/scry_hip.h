@@ -147,6 +147,11 @@ int scry_hip_scatter_rows(scry_buf dst, scry_buf src, int total_rows, int cols, 
                           int row_count);
 /* generate.rs:167-173 argmax (Iterator::max_by semantics), on device */
 int scry_hip_argmax(scry_buf logits, int64_t *out);
+/* init::normal_vec (init.rs:12-14): n samples of N(mean, std) by Box-Muller
+ * from the fastrand::Rng state *rng_state (two Rng::f64 per sample, advanced
+ * by 2n steps), computed on the host with glibc libm as the reference, then
+ * stored to new device storage (Linear::new, linear.rs:28-39). */
+int scry_hip_normal_vec(uint64_t *rng_state, size_t n, float mean, float std_dev, scry_buf *out);
 /* sample_token (generate.rs:92-186) on device: the step sampler of
  * scry_hip_llama_generate on one logits vector (temperature < 1e-8: argmax).
  * *rng_state is the fastrand::Rng state, advanced by the one draw. */
@@ -317,6 +322,11 @@ int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq
  * distinct weight copies (defeats the 256 MB Infinity Cache). */
 int scry_hip_bench_qgemv(int m, int k, int n, int quant_mode, int n_bufs, int warmup, int iters,
                          double *avg_us, double *bytes_per_launch);
+/* The same with a bias row (matmul_i8_f32_bias, cpu.rs:553-570; the quantized
+ * Linear::forward, linear.rs:67-94): per-tensor int8, bias added in the
+ * GEMV's store epilogue. */
+int scry_hip_bench_qgemv_bias(int m_rows, int k, int n, int n_bufs, int warmup, int iters,
+                              double *avg_us, double *bytes_per_launch);
 
 #ifdef __cplusplus
 }
