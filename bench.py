@@ -159,6 +159,29 @@ def linear_sweep(E) -> list:
     return out
 
 
+BF16_SHAPES = [("q/k/v/o", 4096, 4096), ("gate/up", 4096, 11008), ("down", 11008, 4096),
+               ("lm_head", 4096, 32000)]
+
+
+def bf16_sweep(E) -> list:
+    """bf16 mode (the reference's bf16 feature): matmul with bf16 weight rows at
+    one activation row, Llama-2-7B projection shapes; about 1 GB of weight
+    copies per shape."""
+    import ctypes as C
+    from esolearn_amd._lib import call
+    out = []
+    for name, k, n in BF16_SHAPES:
+        n_bufs = max(4, (1 << 30) // (2 * k * n))
+        us, b = C.c_double(), C.c_double()
+        call("scry_hip_bench_gemv_bf16", 1, k, n, n_bufs, 50, 500, C.byref(us), C.byref(b))
+        gbs = b.value / us.value / 1e3
+        out.append({"proj": name, "in": k, "out": n, "rows": 1, "avg_us": round(us.value, 3),
+                    "bytes": int(b.value), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+        print(f"[bench] bf16 gemv {name:8s} {k}x{n}: {us.value:7.2f} us {gbs:7.1f} GB/s",
+              file=sys.stderr, flush=True)
+    return out
+
+
 def weight_bytes(cfg) -> int:
     """int8 weight bytes + per-tensor scales read per decode token."""
     h, ffn, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.n_layers
@@ -219,6 +242,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill line")
     ap.add_argument("--pmc-probe", action="store_true", help="profiling workload only (see above)")
     ap.add_argument("--prefill-only", action="store_true", help="config-5 measurement only")
+    ap.add_argument("--bf16-only", action="store_true",
+                    help="bf16-mode GEMV (bf16 weights) at Llama-2-7B projection shapes only")
     ap.add_argument("--linear-only", action="store_true",
                     help="quantized Linear (bias GEMV) at GPT-2 / Whisper shapes only")
     ap.add_argument("--sampling-only", action="store_true",
@@ -238,6 +263,9 @@ def main() -> int:
     E.init(0)
     if args.pmc_probe:
         pmc_probe(E)
+        return 0
+    if args.bf16_only:
+        print(json.dumps({"bf16_gemv": bf16_sweep(E)}), flush=True)
         return 0
     if args.linear_only:
         print(json.dumps({"linear_bias_gemv": linear_sweep(E)}), flush=True)

@@ -84,7 +84,12 @@ SIGNATURES = {
     "scry_hip_argmax": [vp, P(i64)],
     "scry_hip_sample_token": [vp, P(SamplingConfigC), P(u64), P(i64)],
     "scry_hip_normal_vec": [P(u64), sz, f32, f32, P(vp)],
+    "scry_hip_init_bf16": [i32],
+    "scry_hip_set_bf16_mode": [i32],
+    "scry_hip_bf16_mode": [P(i32)],
+    "scry_hip_from_vec_with_bf16": [vp, vp, sz, P(vp)],
     "scry_hip_bench_qgemv_bias": [i32, i32, i32, i32, i32, i32, P(f64), P(f64)],
+    "scry_hip_bench_gemv_bf16": [i32, i32, i32, i32, i32, i32, P(f64), P(f64)],
     "scry_hip_llama_new_random": [P(LlamaConfigC), u64, i32, i32, P(vp)],
     "scry_hip_llama_from_safetensors": [P(LlamaConfigC), P(C.c_char_p), i32, i32, P(vp)],
     "scry_hip_llama_free": [vp],

@@ -114,6 +114,34 @@ class HipBackend:
         return _st(o, a.size)
 
     @staticmethod
+    def init_gpu_bf16(device: int = 0) -> None:
+        """init_gpu_bf16 (cuda.rs:55-59): init, then bf16 mode."""
+        call("scry_hip_init_bf16", device)
+
+    @staticmethod
+    def set_bf16_mode(on: bool) -> None:
+        call("scry_hip_set_bf16_mode", int(bool(on)))
+
+    @staticmethod
+    def bf16_mode() -> bool:
+        v = C.c_int()
+        call("scry_hip_bf16_mode", C.byref(v))
+        return bool(v.value)
+
+    @staticmethod
+    def from_vec_with_bf16(data, bf16_bytes) -> Storage:
+        """DeviceBackend::from_vec_with_bf16 (mod.rs:28-32): bf16_bytes are the
+        little-endian bf16 words of the same values (uint16 array or bytes)."""
+        a = _f32(data)
+        h = np.frombuffer(bytes(bf16_bytes), np.uint16) if isinstance(bf16_bytes, (bytes, bytearray)) \
+            else np.ascontiguousarray(bf16_bytes, np.uint16).ravel()
+        if h.size != a.size:
+            raise ValueError("from_vec_with_bf16: bf16 data and f32 data differ in length")
+        o = _out()
+        call("scry_hip_from_vec_with_bf16", a.ctypes.data, h.ctypes.data, a.size, C.byref(o))
+        return _st(o, a.size)
+
+    @staticmethod
     def to_vec(s: Storage) -> np.ndarray:
         return s.to_vec()
 

@@ -87,7 +87,19 @@ int new_buf(size_t n, scry_buf *out) {
 void del_buf(scry_buf b) {
     if (!b) return;
     dev_free(b->d);
+    dev_free(b->bf);
+    dev_free(b->pk);
     delete b;
+}
+
+// the f32 data changed in place: drop the bf16 copies made from it
+void bf16_stale(scry_buf b) {
+    if (!b->d) return;
+    dev_free(b->bf);
+    dev_free(b->pk);
+    b->bf = nullptr;
+    b->pk = nullptr;
+    b->pk_tb = -1;
 }
 
 int sync() {
@@ -95,10 +107,101 @@ int sync() {
     return SCRY_OK;
 }
 
-#define CHECK_BUF(b, what)                                                      \
-    do {                                                                        \
-        if (!(b) || !(b)->d) return set_error(SCRY_ERR_INVALID, "%s: null storage", what); \
+#define CHECK_BUF(b, what)                                                                          \
+    do {                                                                                            \
+        if ((b) && !(b)->d && (b)->bf)                                                              \
+            return set_error(SCRY_ERR_INVALID, "%s: the storage holds bf16 data only (bf16 mode)", what); \
+        if (!(b) || !(b)->d) return set_error(SCRY_ERR_INVALID, "%s: null storage", what);          \
     } while (0)
+// f32 or bf16-only storage
+#define CHECK_ANY(b, what)                                                                          \
+    do {                                                                                            \
+        if (!(b) || (!(b)->d && !(b)->bf)) return set_error(SCRY_ERR_INVALID, "%s: null storage", what); \
+    } while (0)
+
+// bf16 rows [n][kp] of b as the B operand of a bf16-mode matmul (logical
+// [k, n]; tb: stored [n][k]), built once per (k, n, tb)
+int bf16_rows(scry_buf b, int k, int n, int tb, const unsigned short **rows, int *kp) {
+    if (!(b->pk && b->pk_k == k && b->pk_n == n && b->pk_tb == tb)) {
+        dev_free(b->pk);
+        b->pk = nullptr;
+        b->pk_tb = -1;
+        const int p = bf16_row_pad(k);
+        SCRY_TRY(dev_alloc((void **)&b->pk, sizeof(unsigned short) * (size_t)n * p));
+        SCRY_TRY(launch_pack_rows_bf16(b->d ? nullptr : b->bf, b->d, k, n, tb, b->pk, p, ctx().stream));
+        b->pk_k = k;
+        b->pk_n = n;
+        b->pk_kp = p;
+        b->pk_tb = tb;
+    }
+    *rows = b->pk;
+    *kp = b->pk_kp;
+    return SCRY_OK;
+}
+
+// An f32 view of a (the f32 data, or its bf16 data widened into *tmp)
+int f32_of(scry_buf a, float **tmp, const float **x) {
+    if (a->d) {
+        *x = a->d;
+        return SCRY_OK;
+    }
+    SCRY_TRY(dev_alloc((void **)tmp, sizeof(float) * (a->n ? a->n : 1)));
+    SCRY_TRY(launch_widen_bf16(a->bf, a->n, *tmp, ctx().stream));
+    *x = *tmp;
+    return SCRY_OK;
+}
+
+// bf16_ops::matmul_bf16 (cuda.rs:1226-1290): C = bf16(A) bf16(B), f32
+// accumulation.  Untransposed A: the bf16 GEMV (1-16 rows) or the MFMA GEMM
+// over B's bf16 rows; transposed A: the f32 kernel on bf16-rounded copies
+// (the same exact products).
+int matmul_bf16(scry_buf a, scry_buf b, int m, int k, int n, int ta, int tb, scry_buf *out) {
+    hipStream_t s = ctx().stream;
+    SCRY_TRY(new_buf((size_t)m * n, out));
+    float *tmp = nullptr, *tb_f = nullptr;
+    unsigned short *plane = nullptr;
+    const float *x = nullptr;
+    int rc = SCRY_OK;
+    if (!ta) {
+        const unsigned short *rows = nullptr;
+        int kp = 0;
+        rc = bf16_rows(b, k, n, tb, &rows, &kp);
+        if (!rc) rc = f32_of(a, &tmp, &x);
+        if (!rc && m <= GEMV_MAX_M) {
+            rc = launch_gemv_bf16(rows, kp, n, x, k, k, m, (*out)->d, n, nullptr, s);
+        } else if (!rc) {
+            const int mp = prefill_rows_pad(m), lda = prefill_k_pad(k);
+            rc = dev_alloc((void **)&plane, sizeof(unsigned short) * (size_t)mp * lda);
+            if (!rc) rc = launch_fill_u32((unsigned *)plane, (size_t)mp * lda / 2, 0u, s);
+            if (!rc) rc = launch_plane_bf16(x, k, m, k, lda, plane, lda, s);
+            if (!rc) rc = launch_gemm_bf16(rows, kp, n, k, plane, lda, m, (*out)->d, n, nullptr, s);
+        }
+    } else {
+        // both operands as the f32 values of their bf16 roundings
+        float *ra = nullptr;
+        rc = f32_of(a, &tmp, &x);
+        if (!rc) rc = dev_alloc((void **)&ra, sizeof(float) * (size_t)m * k);
+        if (!rc) rc = launch_round_bf16(x, (size_t)m * k, ra, s);
+        const float *xb = nullptr;
+        float *tmpb = nullptr;
+        if (!rc) rc = f32_of(b, &tmpb, &xb);
+        if (!rc) rc = dev_alloc((void **)&tb_f, sizeof(float) * (size_t)k * n);
+        if (!rc) rc = launch_round_bf16(xb, (size_t)k * n, tb_f, s);
+        if (!rc) rc = launch_matmul_f32(ra, tb_f, 1, m, k, n, ta, tb, (*out)->d, s);
+        if (!rc) rc = sync();
+        dev_free(ra);
+        dev_free(tmpb);
+    }
+    if (!rc) rc = sync();  // temporaries are freed below
+    dev_free(tmp);
+    dev_free(tb_f);
+    dev_free(plane);
+    if (rc) {
+        del_buf(*out);
+        *out = nullptr;
+    }
+    return rc;
+}
 
 // Ensure the GEMV layout of an I8Storage for logical [k, n].
 int ensure_packed(scry_i8buf q, int k, int n) {
@@ -198,6 +301,7 @@ int scry_hip_init(int device) {
         return set_error(SCRY_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only",
                          device, prop.gcnArchName);
     SCRY_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    c.bf16 = false;
     c.device = device;
     c.cu_count = prop.multiProcessorCount;
     c.name = prop.name;
@@ -269,16 +373,88 @@ int scry_hip_from_vec(const float *host, size_t n, scry_buf *out) {
 int scry_hip_to_vec(scry_buf b, float *host, size_t n) {
     API_LOCK;
     SCRY_REQUIRE_INIT();
-    CHECK_BUF(b, "to_vec");
+    CHECK_ANY(b, "to_vec");
     if (n != b->n) return set_error(SCRY_ERR_INVALID, "to_vec: storage has %zu elements, asked %zu", b->n, n);
-    if (n) SCRY_HIP(hipMemcpyAsync(host, b->d, n * sizeof(float), hipMemcpyDeviceToHost, ctx().stream));
+    if (!n) return SCRY_OK;
+    if (!b->d) {  // cuda.rs:244-254: bf16-only storage widens to f32
+        float *t = nullptr;
+        SCRY_TRY(dev_alloc((void **)&t, n * sizeof(float)));
+        int rc = launch_widen_bf16(b->bf, n, t, ctx().stream);
+        hipError_t e = hipSuccess;
+        if (!rc) e = hipMemcpyAsync(host, t, n * sizeof(float), hipMemcpyDeviceToHost, ctx().stream);
+        if (!rc && e != hipSuccess) rc = hip_fail(e, "to_vec copy", __FILE__, __LINE__);
+        if (!rc) rc = sync();
+        dev_free(t);
+        return rc;
+    }
+    SCRY_HIP(hipMemcpyAsync(host, b->d, n * sizeof(float), hipMemcpyDeviceToHost, ctx().stream));
     return sync();
+}
+
+int scry_hip_init_bf16(int device) {
+    API_LOCK;
+    SCRY_TRY(scry_hip_init(device));
+    ctx().bf16 = true;
+    return SCRY_OK;
+}
+
+int scry_hip_set_bf16_mode(int on) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    ctx().bf16 = on != 0;
+    return SCRY_OK;
+}
+
+int scry_hip_bf16_mode(int *on) {
+    if (!on) return set_error(SCRY_ERR_INVALID, "bf16_mode: null argument");
+    *on = ctx().bf16 ? 1 : 0;
+    return SCRY_OK;
+}
+
+int scry_hip_from_vec_with_bf16(const float *host, const uint16_t *bf16, size_t n, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!ctx().bf16) return scry_hip_from_vec(host, n, out);  // mod.rs:28-32 default
+    if (!out || (!bf16 && n)) return set_error(SCRY_ERR_INVALID, "from_vec_with_bf16: null argument");
+    auto *b = new (std::nothrow) scry_buf_s;
+    if (!b) return set_error(SCRY_ERR_OOM, "host allocation failed");
+    b->n = n;
+    int rc = dev_alloc((void **)&b->bf, sizeof(uint16_t) * (n ? n : 1));
+    if (!rc && n) {
+        hipError_t e = hipMemcpyAsync(b->bf, bf16, sizeof(uint16_t) * n, hipMemcpyHostToDevice, ctx().stream);
+        if (e != hipSuccess) rc = hip_fail(e, "from_vec_with_bf16 upload", __FILE__, __LINE__);
+        if (!rc) rc = sync();
+    }
+    if (rc) {
+        del_buf(b);
+        return rc;
+    }
+    *out = b;
+    return SCRY_OK;
 }
 
 int scry_hip_clone_storage(scry_buf src, scry_buf *out) {
     API_LOCK;
     SCRY_REQUIRE_INIT();
-    CHECK_BUF(src, "clone_storage");
+    CHECK_ANY(src, "clone_storage");
+    if (!src->d) {  // bf16 only
+        if (!out) return set_error(SCRY_ERR_INVALID, "null output handle");
+        auto *b = new (std::nothrow) scry_buf_s;
+        if (!b) return set_error(SCRY_ERR_OOM, "host allocation failed");
+        b->n = src->n;
+        int rc = dev_alloc((void **)&b->bf, sizeof(uint16_t) * (src->n ? src->n : 1));
+        if (!rc && src->n) {
+            hipError_t e = hipMemcpyAsync(b->bf, src->bf, sizeof(uint16_t) * src->n, hipMemcpyDeviceToDevice,
+                                          ctx().stream);
+            if (e != hipSuccess) rc = hip_fail(e, "clone_storage", __FILE__, __LINE__);
+        }
+        if (rc) {
+            del_buf(b);
+            return rc;
+        }
+        *out = b;
+        return SCRY_OK;
+    }
     SCRY_TRY(new_buf(src->n, out));
     if (src->n)
         SCRY_HIP(hipMemcpyAsync((*out)->d, src->d, src->n * sizeof(float), hipMemcpyDeviceToDevice,
@@ -449,6 +625,12 @@ int scry_hip_matmul(scry_buf a, scry_buf b, int m, int k, int n, int trans_a, in
                     scry_buf *out) {
     API_LOCK;
     SCRY_REQUIRE_INIT();
+    if (ctx().bf16) {  // cuda.rs:274-277
+        CHECK_ANY(a, "matmul");
+        CHECK_ANY(b, "matmul");
+        SCRY_TRY(check_mkn(a->n, b->n, m, k, n));
+        return matmul_bf16(a, b, m, k, n, trans_a, trans_b, out);
+    }
     CHECK_BUF(a, "matmul");
     CHECK_BUF(b, "matmul");
     SCRY_TRY(check_mkn(a->n, b->n, m, k, n));
@@ -550,7 +732,7 @@ int scry_hip_embedding(scry_buf weight, const int64_t *ids, int n_ids, int vocab
                        scry_buf *out) {
     API_LOCK;
     SCRY_REQUIRE_INIT();
-    CHECK_BUF(weight, "embedding");
+    CHECK_ANY(weight, "embedding");
     if (n_ids < 0 || vocab <= 0 || dim <= 0 || weight->n != (size_t)vocab * dim || (n_ids && !ids))
         return set_error(SCRY_ERR_INVALID, "embedding: shape mismatch");
     for (int i = 0; i < n_ids; i++)
@@ -564,7 +746,9 @@ int scry_hip_embedding(scry_buf weight, const int64_t *ids, int n_ids, int vocab
         hipError_t e = hipMemcpyAsync(d_ids, ids, sizeof(int64_t) * n_ids, hipMemcpyHostToDevice,
                                       ctx().stream);
         if (e != hipSuccess) rc = hip_fail(e, "embedding ids upload", __FILE__, __LINE__);
-        if (!rc) rc = launch_embedding(weight->d, d_ids, n_ids, dim, (*out)->d, ctx().stream);
+        if (!rc)
+            rc = weight->d ? launch_embedding(weight->d, d_ids, n_ids, dim, (*out)->d, ctx().stream)
+                           : launch_embed_bf16((*out)->d, weight->bf, d_ids, n_ids, dim, ctx().stream);  // cuda.rs:480-503
         if (!rc) rc = sync();
     }
     dev_free(d_ids);
@@ -607,6 +791,7 @@ int scry_hip_scatter_rows(scry_buf dst, scry_buf src, int total_rows, int cols, 
         SCRY_HIP(hipMemcpyAsync(dst->d + (size_t)row_start * cols, src->d,
                                 sizeof(float) * (size_t)row_count * cols, hipMemcpyDeviceToDevice,
                                 ctx().stream));
+    bf16_stale(dst);  // (the reference's bf16 shadow would keep the old rows)
     return SCRY_OK;
 }
 

@@ -15,6 +15,7 @@ namespace scry {
 
 struct Ctx {
     bool init = false;
+    bool bf16 = false;  // bf16 mode (init_gpu_bf16, cuda.rs:55-59)
     int device = -1;
     hipStream_t stream = nullptr;
     int cu_count = 0;
@@ -299,6 +300,23 @@ int launch_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd,
                    hipStream_t s);
 int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hipStream_t s);
 
+// bf16.hip -- bf16 mode: the reference's cast, widening, B-operand rows
+// [n][kp] (kp = bf16_row_pad(k)), the GEMM activation plane, the bf16 GEMV
+int bf16_row_pad(int k);
+int launch_cast_bf16(const float *x, size_t n, unsigned short *y, hipStream_t s);
+int launch_round_bf16(const float *x, size_t n, float *y, hipStream_t s);
+int launch_widen_bf16(const unsigned short *x, size_t n, float *y, hipStream_t s);
+int launch_embed_bf16(float *out, const unsigned short *w, const int64_t *ids, int n_ids, int dim, hipStream_t s);
+int launch_pack_rows_bf16(const unsigned short *bs, const float *fs, int k, int n, int tb, unsigned short *pk,
+                          int kp, hipStream_t s);
+int launch_plane_bf16(const float *x, int ldx, int rows, int k, int kpad, unsigned short *hi, int ldp,
+                      hipStream_t s);
+int launch_gemv_bf16(const unsigned short *w, int kp, int n, const float *x, int ldx, int k, int m, float *y,
+                     int ldy, const float *bias, hipStream_t s);
+// prefill.hip: the MFMA GEMM over bf16 weight rows [N][kp] and one bf16 plane
+int launch_gemm_bf16(const unsigned short *w, int kp, int N, int k, const unsigned short *ahi, int lda, int M,
+                     float *c, int ldc, const float *bias, hipStream_t s);
+
 // init.cpp -- host restatement of LlamaModel::new's random init (threaded)
 void host_normal_vec(uint64_t seed, uint64_t start_call, size_t n, float mean, float stdv,
                      float *out, int threads);
@@ -307,8 +325,15 @@ int host_threads();
 }  // namespace scry
 
 struct scry_buf_s {
-    float *d = nullptr;
+    float *d = nullptr;  // f32 data; null when the storage holds bf16 only (bf16 mode)
     size_t n = 0;
+    // bf16 mode: the bf16 data of from_vec_with_bf16, or the f32 data rounded
+    // once for a matmul (cleared when the f32 data is written in place)
+    unsigned short *bf = nullptr;
+    // bf16 rows [pk_n][pk_kp] of this storage as a matmul B operand for
+    // logical (pk_k, pk_n, pk_tb), built on first use
+    unsigned short *pk = nullptr;
+    int pk_k = 0, pk_n = 0, pk_kp = 0, pk_tb = -1;
 };
 
 struct scry_i8buf_s {

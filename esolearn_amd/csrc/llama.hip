@@ -1758,6 +1758,51 @@ int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, i
     return bench_qgemv_impl(m_rows, k, n, quant_mode, n_bufs, warmup, iters, false, avg_us, bytes_per_launch);
 }
 
+int scry_hip_bench_gemv_bf16(int m_rows, int k, int n, int n_bufs, int warmup, int iters, double *avg_us,
+                             double *bytes_per_launch) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (m_rows <= 0 || m_rows > GEMV_MAX_M || k <= 0 || n <= 0 || n_bufs <= 0 || iters <= 0 || !avg_us)
+        return set_error(SCRY_ERR_INVALID, "bench_gemv_bf16: bad arguments");
+    hipStream_t s = ctx().stream;
+    const int kp = bf16_row_pad(k);
+    std::vector<unsigned short *> W(n_bufs, nullptr);
+    float *x = nullptr, *y = nullptr;
+    int rc = dev_alloc((void **)&x, sizeof(float) * (size_t)m_rows * k);
+    if (!rc) rc = dev_alloc((void **)&y, sizeof(float) * (size_t)m_rows * n);
+    if (!rc) rc = launch_fill_f32(x, (size_t)m_rows * k, 0.5f, s);
+    for (int b = 0; b < n_bufs && !rc; b++) {
+        rc = dev_alloc((void **)&W[b], sizeof(unsigned short) * (size_t)n * kp);
+        if (!rc) rc = launch_fill_u32((unsigned *)W[b], (size_t)n * kp / 2, 0x3c003c00u + b, s);  // finite bf16
+    }
+    auto launch = [&](int i) { return launch_gemv_bf16(W[i % n_bufs], kp, n, x, k, k, m_rows, y, n, nullptr, s); };
+    for (int i = 0; i < warmup && !rc; i++) rc = launch(i);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc) {
+        hipError_t e = hipEventCreate(&e0);
+        if (e == hipSuccess) e = hipEventCreate(&e1);
+        if (e == hipSuccess) e = hipEventRecord(e0, s);
+        if (e != hipSuccess) rc = hip_fail(e, "event setup", __FILE__, __LINE__);
+    }
+    for (int i = 0; i < iters && !rc; i++) rc = launch(i);
+    if (!rc) {
+        hipError_t e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float f = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&f, e0, e1);
+        if (e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
+        *avg_us = 1000.0 * f / iters;
+    }
+    if (bytes_per_launch) *bytes_per_launch = 2.0 * k * n + 4.0 * m_rows * k + 4.0 * m_rows * n;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(s);
+    for (auto *w : W) dev_free(w);
+    dev_free(x);
+    dev_free(y);
+    return rc;
+}
+
 int scry_hip_bench_qgemv_bias(int m_rows, int k, int n, int n_bufs, int warmup, int iters, double *avg_us,
                               double *bytes_per_launch) {
     API_LOCK;

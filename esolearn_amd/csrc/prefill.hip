@@ -158,8 +158,12 @@ __device__ __forceinline__ void bytes_to_bf16(u32x4 v, u32x4 &o0, u32x4 &o1) {
 
 // (block-32: the per-block scaling needs a second accumulator tile, so one
 // workgroup per CU keeps it in registers)
-template <int EPI, bool B32>
+// WBF: bf16 weight rows [N][kp] (2 bytes each, copied to LDS as they are) and
+// a single bf16 activation plane (bf16 mode: both operands rounded to bf16,
+// products exact, f32 accumulation); p.alo is not read.
+template <int EPI, bool B32, bool WBF = false>
 __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
+    static_assert(!(WBF && B32), "bf16 weights carry no block scales");
     extern __shared__ float4 gsm[];
     u16 *sa = reinterpret_cast<u16 *>(gsm);
     u16 *sb = sa + 2 * A_TILE;
@@ -173,35 +177,38 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
     // global -> LDS assignment: A chunk c = tid + 256 i (row c / (BK/8), 8 bf16
     // at 8 (c % (BK/8))); B chunk c = tid + 256 i (row c / (BK/16), 16 bytes at
     // 16 (c % (BK/16)))
-    constexpr int CPR = BK / 8, BPR = BK / 16;
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (size_t)p.N * p.kp);
+    constexpr int CPR = BK / 8, BPR = WBF ? BK / 8 : BK / 16;  // 16-byte chunks per row
+    constexpr int BCW = BN * BPR / G_THREADS;                    // weight chunks per thread
+    constexpr int NPL = WBF ? 1 : 2;                             // activation planes
+    constexpr unsigned WB = WBF ? 2 : 1;                         // bytes per weight
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (size_t)p.N * p.kp * WB);
     const u16 *ga[2][AC];
-    unsigned boff[BC];
+    unsigned boff[BCW];
 #pragma unroll
     for (int i = 0; i < AC; i++) {
         const int c = tid + 256 * i;
         ga[0][i] = p.ahi + (size_t)(m0 + c / CPR) * p.lda + (c % CPR) * 8;
-        ga[1][i] = p.alo + (size_t)(m0 + c / CPR) * p.lda + (c % CPR) * 8;
+        ga[1][i] = WBF ? ga[0][i] : p.alo + (size_t)(m0 + c / CPR) * p.lda + (c % CPR) * 8;
     }
 #pragma unroll
-    for (int i = 0; i < BC; i++) {
+    for (int i = 0; i < BCW; i++) {
         const int c = tid + 256 * i;
         const int n = n0 + c / BPR;
-        boff[i] = n < p.N ? (unsigned)((size_t)n * p.kp + (c % BPR) * 16) : 0x80000000u;
+        boff[i] = n < p.N ? (unsigned)((size_t)n * p.kp * WB + (c % BPR) * 16) : 0x80000000u;
     }
     const bool s_ld = B32 && n0 + tid < p.N;
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(p.s32, B32 ? (size_t)p.N * p.nb * sizeof(float) : 0);
 
-    u32x4 ra[2][AC], rb[BC];
+    u32x4 ra[2][AC], rb[BCW];
     float rs[BK / 32];
     auto gload = [&](int kt) {
         const int k0 = kt * BK;
 #pragma unroll
-        for (int pl = 0; pl < 2; pl++)
+        for (int pl = 0; pl < NPL; pl++)
 #pragma unroll
             for (int i = 0; i < AC; i++) ra[pl][i] = *(const u32x4 *)(ga[pl][i] + k0);
 #pragma unroll
-        for (int i = 0; i < BC; i++) rb[i] = bload16(wr, boff[i] + (unsigned)k0);
+        for (int i = 0; i < BCW; i++) rb[i] = bload16(wr, boff[i] + (unsigned)k0 * WB);
         if (B32) {
 #pragma unroll
             for (int j = 0; j < BK / 32; j++)  // blocks past the scales read as 0 (their A is 0)
@@ -212,20 +219,24 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
     };
     auto lstore = [&]() {
 #pragma unroll
-        for (int pl = 0; pl < 2; pl++)
+        for (int pl = 0; pl < NPL; pl++)
 #pragma unroll
             for (int i = 0; i < AC; i++) {
                 const int c = tid + 256 * i;
                 *(u32x4 *)(sa + pl * A_TILE + (c / CPR) * LDT + (c % CPR) * 8) = ra[pl][i];
             }
 #pragma unroll
-        for (int i = 0; i < BC; i++) {
+        for (int i = 0; i < BCW; i++) {
             const int c = tid + 256 * i;
-            u32x4 o0, o1;
-            bytes_to_bf16(rb[i], o0, o1);
-            u16 *d = sb + (c / BPR) * LDT + (c % BPR) * 16;
-            *(u32x4 *)d = o0;
-            *(u32x4 *)(d + 8) = o1;
+            if constexpr (WBF) {
+                *(u32x4 *)(sb + (c / BPR) * LDT + (c % BPR) * 8) = rb[i];
+            } else {
+                u32x4 o0, o1;
+                bytes_to_bf16(rb[i], o0, o1);
+                u16 *d = sb + (c / BPR) * LDT + (c % BPR) * 16;
+                *(u32x4 *)d = o0;
+                *(u32x4 *)(d + 8) = o1;
+            }
         }
         if (B32) {
 #pragma unroll
@@ -252,7 +263,7 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
             for (int tm = 0; tm < 4; tm++) {
                 const int r = wm * 64 + tm * 16 + fr;
                 ah[tm] = *(const bf16x8 *)(sa + r * LDT + ks * 32 + fk);
-                al[tm] = *(const bf16x8 *)(sa + A_TILE + r * LDT + ks * 32 + fk);
+                if (!WBF) al[tm] = *(const bf16x8 *)(sa + A_TILE + r * LDT + ks * 32 + fk);
             }
 #pragma unroll
             for (int tn = 0; tn < 8; tn++) {
@@ -272,7 +283,8 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
 #pragma unroll
                     for (int tm = 0; tm < 4; tm++) {
                         acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bv, acc[tm][tn], 0, 0, 0);
-                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bv, acc[tm][tn], 0, 0, 0);
+                        if (!WBF)
+                            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bv, acc[tm][tn], 0, 0, 0);
                     }
                 }
             }
@@ -587,16 +599,16 @@ int attn_mfma_t(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hi
     PF_LAUNCH_CHECK();
 }
 
-template <int EPI, bool B32>
+template <int EPI, bool B32, bool WBF = false>
 int gemm_t(const GemmP &p, hipStream_t s) {
     static bool attr = false;
     if (!attr) {
-        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<EPI, B32>),
+        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<EPI, B32, WBF>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)GEMM_LDS));
         attr = true;
     }
     const int grid = (p.n_super + 7) / 8 * 8 * 32;
-    hipLaunchKernelGGL((k_gemm<EPI, B32>), dim3(grid), dim3(G_THREADS), GEMM_LDS, s, p);
+    hipLaunchKernelGGL((k_gemm<EPI, B32, WBF>), dim3(grid), dim3(G_THREADS), GEMM_LDS, s, p);
     PF_LAUNCH_CHECK();
 }
 
@@ -665,6 +677,33 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
         case GE_SWIGLU: return b32 ? gemm_t<GE_SWIGLU, true>(p, s) : gemm_t<GE_SWIGLU, false>(p, s);
     }
     return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
+}
+
+int launch_gemm_bf16(const unsigned short *w, int kp, int N, int k, const unsigned short *ahi, int lda, int M,
+                     float *c, int ldc, const float *bias, hipStream_t s) {
+    const int kpad = prefill_k_pad(k);
+    if (kp < kpad || kp % BK) return set_error(SCRY_ERR_INVALID, "gemm_bf16: weight rows of %d < k %d", kp, k);
+    if (kpad > lda || lda % 8) return set_error(SCRY_ERR_INVALID, "gemm_bf16: plane stride %d < k %d", lda, k);
+    if ((size_t)N * kp * 2 >= 0x7fffffffull)
+        return set_error(SCRY_ERR_UNSUPPORTED, "gemm_bf16: weight bytes above 2 GiB");
+    GemmP p{};
+    p.ahi = ahi;
+    p.alo = nullptr;
+    p.lda = lda;
+    p.w = reinterpret_cast<const uint8_t *>(w);
+    p.kp = kp;
+    p.N = N;
+    p.M = M;
+    p.nk = kpad / BK;
+    p.n_mb = (M + BM - 1) / BM;
+    p.n_nb = (N + BN - 1) / BN;
+    p.n_super = ((p.n_mb + 3) / 4) * ((p.n_nb + 7) / 8);
+    p.scale = 1.f;
+    p.scale2 = 1.f;
+    p.bias = bias;
+    p.c = c;
+    p.ldc = ldc;
+    return gemm_t<GE_STORE, false, true>(p, s);
 }
 
 int launch_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, const PrefillSeqs &t, int l,

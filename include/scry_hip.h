@@ -74,6 +74,18 @@ int scry_hip_device_info(char *name, size_t name_len, int *cu_count, char *arch,
 int scry_hip_zeros(size_t n, scry_buf *out);
 /* DeviceBackend::from_vec (mod.rs:25) */
 int scry_hip_from_vec(const float *host, size_t n, scry_buf *out);
+/* bf16 mode (the `bf16` feature): init_gpu_bf16 (cuda.rs:55-59) is
+ * scry_hip_init + mode on.  In bf16 mode scry_hip_from_vec_with_bf16 keeps
+ * the bf16 bytes only; scry_hip_matmul rounds both operands to bf16 with the
+ * reference's cast and accumulates in f32 (bf16_ops::matmul_bf16,
+ * cuda.rs:1226-1290); to_vec and embedding widen bf16-only storage; other
+ * ops refuse it.  set_bf16_mode toggles the mode (tests). */
+int scry_hip_init_bf16(int device);
+int scry_hip_set_bf16_mode(int on);
+int scry_hip_bf16_mode(int *on);
+/* DeviceBackend::from_vec_with_bf16 (mod.rs:28-32, cuda.rs:230-240): bf16 is
+ * n little-endian bf16 words; outside bf16 mode it is from_vec(host). */
+int scry_hip_from_vec_with_bf16(const float *host, const uint16_t *bf16, size_t n, scry_buf *out);
 /* DeviceBackend::to_vec (mod.rs:33); n must equal the storage length */
 int scry_hip_to_vec(scry_buf b, float *host, size_t n);
 /* DeviceBackend::clone_storage (mod.rs:44) */
@@ -111,7 +123,8 @@ int scry_hip_matmul_i8_f32_block32(scry_buf a, scry_i8buf b_q, scry_buf scales, 
                                    int n, scry_buf *out);
 
 /* --------------------------------------- MathBackend glue on the path */
-/* MathBackend::matmul (mod.rs:54-63; cpu.rs:924-961): f32 GEMM/GEMV */
+/* MathBackend::matmul (mod.rs:54-63; cpu.rs:924-961): f32 GEMM/GEMV; in bf16
+ * mode bf16 operands, f32 accumulation (cuda.rs:274-277) */
 int scry_hip_matmul(scry_buf a, scry_buf b, int m, int k, int n, int trans_a, int trans_b,
                     scry_buf *out);
 /* MathBackend::matmul_strided_batched (mod.rs:561-591; cpu.rs:1321-1350) */
@@ -327,6 +340,10 @@ int scry_hip_bench_qgemv(int m, int k, int n, int quant_mode, int n_bufs, int wa
  * GEMV's store epilogue. */
 int scry_hip_bench_qgemv_bias(int m_rows, int k, int n, int n_bufs, int warmup, int iters,
                               double *avg_us, double *bytes_per_launch);
+/* The bf16-mode GEMV (1-16 rows, bf16 weight rows [n][kp]) over n_bufs
+ * weight copies: average device time and algorithmic bytes per launch. */
+int scry_hip_bench_gemv_bf16(int m_rows, int k, int n, int n_bufs, int warmup, int iters, double *avg_us,
+                             double *bytes_per_launch);
 
 #ifdef __cplusplus
 }

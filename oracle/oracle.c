@@ -363,6 +363,45 @@ void orc_matmul_f32(const float *a, const float *b, int m, int k, int n, int tra
     matmul_fallback(a, b, m, k, n, trans_a, trans_b, c);
 }
 
+/* kernels.rs:629-633 float_to_bf16 (the bf16 feature's cast): round to
+ * nearest even by adding 0x7fff + the lowest kept bit to the f32 bits, in
+ * 32-bit unsigned arithmetic (a NaN whose payload lies in the low 16 bits
+ * becomes inf; the all-ones negative NaN wraps to +0). */
+uint16_t orc_f32_to_bf16(float x) {
+    uint32_t b;
+    memcpy(&b, &x, 4);
+    return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
+void orc_f32_to_bf16_vec(const float *x, size_t n, uint16_t *out) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_f32_to_bf16(x[i]);
+}
+
+static float bf16_val(uint16_t h) {
+    uint32_t b = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+/* bf16_ops::matmul_bf16 (cuda.rs:1226-1290): C = bf16(A) bf16(B) with f32
+ * accumulation in cuBLAS (order unspecified).  The restatement rounds both
+ * operands with the cast above and sums the (exact) products in f64, rounded
+ * once: the value any f32 accumulation approximates. */
+void orc_matmul_bf16(const float *a, const float *b, int m, int k, int n, int trans_a, int trans_b,
+                     float *c) {
+    for (int i = 0; i < m; i++)
+        for (int j = 0; j < n; j++) {
+            double acc = 0.0;
+            for (int p = 0; p < k; p++) {
+                const float av = trans_a ? a[(size_t)p * m + i] : a[(size_t)i * k + p];
+                const float bv = trans_b ? b[(size_t)j * k + p] : b[(size_t)p * n + j];
+                acc += (double)bf16_val(orc_f32_to_bf16(av)) * (double)bf16_val(orc_f32_to_bf16(bv));
+            }
+            c[(size_t)i * n + j] = (float)acc;
+        }
+}
+
 /* cpu.rs:1321-1350 (+ fallback 1444-1468) matmul_strided_batched_impl */
 void orc_matmul_strided_batched(const float *a, const float *b, int batch, int m, int k, int n,
                                 int trans_a, int trans_b, float *c) {

@@ -69,6 +69,11 @@ void orc_matmul_f32(const float *a, const float *b, int m, int k, int n, int tra
                     int trans_b, float *c);
 void orc_matmul_strided_batched(const float *a, const float *b, int batch, int m, int k, int n,
                                 int trans_a, int trans_b, float *c);
+/* ---- the bf16 feature (kernels.rs:629-633, cuda.rs:1226-1290) ---- */
+uint16_t orc_f32_to_bf16(float x);
+void orc_f32_to_bf16_vec(const float *x, size_t n, uint16_t *out);
+void orc_matmul_bf16(const float *a, const float *b, int m, int k, int n, int trans_a, int trans_b,
+                     float *c);
 
 /* ---- cpu.rs glue ops ---- */
 void orc_rmsnorm(const float *x, const float *w, int rows, int d, float eps, float *out);

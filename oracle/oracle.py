@@ -56,6 +56,8 @@ def lib():
         "orc_gemv_trans_b": (None, [f32p, f32p, i32, i32, f32p]),
         "orc_gemv_into": (None, [f32p, f32p, i32, i32, f32p]),
         "orc_matmul_f32": (None, [f32p, f32p, i32, i32, i32, i32, i32, f32p]),
+        "orc_f32_to_bf16_vec": (None, [f32p, sz, C.c_void_p]),
+        "orc_matmul_bf16": (None, [f32p, f32p, i32, i32, i32, i32, i32, f32p]),
         "orc_matmul_strided_batched": (None, [f32p, f32p, i32, i32, i32, i32, i32, i32, f32p]),
         "orc_rmsnorm": (None, [f32p, f32p, i32, i32, f32, f32p]),
         "orc_rope_with_freqs_preloaded": (None, [f32p, i32, i32, i32, i32, f32p, f32p]),
@@ -190,6 +192,22 @@ def matmul_i8_f32_bias(a, bq, scale, bias, m, k, n):
 def matmul_f32(a, b, m, k, n, trans_a=False, trans_b=False):
     c = np.empty(m * n, np.float32)
     lib().orc_matmul_f32(_f32(a).ravel(), _f32(b).ravel(), m, k, n, int(trans_a), int(trans_b), c)
+    return c.reshape(m, n)
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    """kernels.rs:629-633 float_to_bf16 on every element (uint16 words)."""
+    a = _f32(x).ravel()
+    out = np.empty(a.size, np.uint16)
+    lib().orc_f32_to_bf16_vec(a, a.size, out.ctypes.data)
+    return out
+
+
+def matmul_bf16(a, b, m, k, n, trans_a=False, trans_b=False):
+    """bf16_ops::matmul_bf16 (cuda.rs:1226-1290): bf16 operands, exact
+    products summed in f64 and rounded once."""
+    c = np.empty(m * n, np.float32)
+    lib().orc_matmul_bf16(_f32(a).ravel(), _f32(b).ravel(), m, k, n, int(trans_a), int(trans_b), c)
     return c.reshape(m, n)
 
 

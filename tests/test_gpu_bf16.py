@@ -1,0 +1,123 @@
+"""bf16 mode (the reference's `bf16` feature) on the GPU against the oracle:
+init_gpu_bf16 / from_vec_with_bf16 (mod.rs:28-32, cuda.rs:55-59, 149-175,
+230-254), matmul on bf16 operands with f32 accumulation (bf16_ops,
+cuda.rs:1226-1290), the bf16 embedding (cuda.rs:480-503).
+
+Bars: the device cast equals the reference's (oracle `orc_f32_to_bf16`) bit
+for bit, seen through matmuls with an identity (GEMV and GEMM paths);
+integer-valued operands give exact results on every path and transpose
+combination; random operands stay within 2e-5 relative of the oracle's
+exact-product f64 sum (f32 accumulation order); bf16-only storage widens
+exactly in to_vec / embedding, and other ops refuse it.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+F = np.float32
+TOL = 2e-5
+
+
+def rel_err(g, c):
+    g = np.asarray(g, np.float64)
+    c = np.asarray(c, np.float64)
+    return np.abs(g - c).max() / max(np.abs(c).max(), 1e-6)
+
+
+def widen(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.fixture
+def bf16_mode(hip):
+    B = hip.HipBackend
+    B.set_bf16_mode(True)
+    try:
+        yield B
+    finally:
+        B.set_bf16_mode(False)
+
+
+def test_cast_matches_reference_through_identity(bf16_mode, orc):
+    B = bf16_mode
+    print("[case] bf16 cast: x @ I, GEMV (1 row) and GEMM (40 rows)", flush=True)
+    rng = np.random.default_rng(1)
+    k = 256
+    bits = rng.integers(0, 2**32, (40, k), dtype=np.uint64).astype(np.uint32)
+    bits[:, :32] = (bits[:, :32] & 0xFFFF0000) | 0x8000  # exact ties
+    x = bits.view(np.float32)
+    x[~np.isfinite(x)] = 1.5  # identity products stay finite
+    x[np.abs(x) > 1e30] = 2.5
+    x[np.abs(x) < 1e-30] = 0.75  # no zeros (the sum of +0 terms drops a -0) or subnormals
+    eye = np.eye(k, dtype=F)
+    for m in (1, 40):
+        y = B.matmul(B.from_vec(x[:m]), B.from_vec(eye), m, k, k).to_vec().reshape(m, k)
+        want = widen(orc.f32_to_bf16(x[:m])).reshape(m, k)
+        assert np.array_equal(y.view(np.uint32), want.view(np.uint32)), m
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb", [
+    (1, 4096, 4096, False, False), (3, 768, 3072, False, True), (16, 1000, 300, False, False),
+    (17, 4096, 1024, False, False), (200, 768, 2304, False, True), (8, 96, 40, True, False),
+    (33, 64, 50, True, True), (1, 11008, 4096, False, True),
+])
+def test_matmul_bf16(bf16_mode, orc, m, k, n, ta, tb):
+    B = bf16_mode
+    print(f"[case] bf16 matmul m={m} k={k} n={n} ta={ta} tb={tb}", flush=True)
+    rng = np.random.default_rng(m * 131 + k + n)
+    a = rng.normal(0, 1, (m, k)).astype(F)
+    w = rng.normal(0, 0.02, (k, n)).astype(F)
+    A = np.ascontiguousarray(a.T) if ta else a
+    W = np.ascontiguousarray(w.T) if tb else w
+    # the weight as bf16-only storage (from_vec_with_bf16), the activation f32
+    wb = B.from_vec_with_bf16(W, orc.f32_to_bf16(W))
+    out = B.matmul(B.from_vec(A), wb, m, k, n, ta, tb).to_vec().reshape(m, n)
+    ref = orc.matmul_bf16(A, W, m, k, n, ta, tb)
+    err = rel_err(out, ref)
+    print(f"[err] {err:.3e}", flush=True)
+    assert err < TOL
+    # both operands f32 (each rounded by the device cast): the same result
+    out2 = B.matmul(B.from_vec(A), B.from_vec(W), m, k, n, ta, tb).to_vec().reshape(m, n)
+    assert rel_err(out2, ref) < TOL
+    # integer values: exact on this path
+    ai = rng.integers(-8, 9, (m, k)).astype(F)
+    wi = rng.integers(-8, 9, (k, n)).astype(F)
+    Ai = np.ascontiguousarray(ai.T) if ta else ai
+    Wi = np.ascontiguousarray(wi.T) if tb else wi
+    oi = B.matmul(B.from_vec(Ai), B.from_vec(Wi), m, k, n, ta, tb).to_vec().reshape(m, n)
+    assert np.array_equal(oi, ai @ wi)
+
+
+def test_bf16_storage(bf16_mode, hip, orc):
+    B = bf16_mode
+    print("[case] bf16-only storage: to_vec, clone, embedding, refusals, stale caches", flush=True)
+    rng = np.random.default_rng(2)
+    vocab, dim = 300, 64
+    emb = rng.normal(0, 1, (vocab, dim)).astype(F)
+    h = orc.f32_to_bf16(emb)
+    s = B.from_vec_with_bf16(emb, h)
+    assert np.array_equal(s.to_vec().view(np.uint32), widen(h).view(np.uint32))
+    c = B.clone_storage(s)
+    assert np.array_equal(c.to_vec(), s.to_vec())
+    ids = np.array([0, 299, 17, 17, 5], np.int64)
+    e = B.embedding(s, ids, vocab, dim).to_vec().reshape(len(ids), dim)
+    assert np.array_equal(e, widen(h).reshape(vocab, dim)[ids])
+    with pytest.raises(hip.ScryHipError) as ei:
+        B.softmax(s, vocab, dim)
+    assert "bf16 data only" in str(ei.value)
+    # outside bf16 mode from_vec_with_bf16 keeps the f32 data
+    B.set_bf16_mode(False)
+    f = B.from_vec_with_bf16(emb, h)
+    assert np.array_equal(f.to_vec(), emb.ravel())
+    B.set_bf16_mode(True)
+    # scatter_rows writes in place: the next matmul sees the new rows
+    k, n = 64, 32
+    w = rng.integers(-4, 5, (k, n)).astype(F)
+    ws = B.from_vec(w)
+    x = np.ones((1, k), F)
+    y0 = B.matmul(B.from_vec(x), ws, 1, k, n).to_vec()
+    assert np.array_equal(y0, w.sum(0))
+    B.scatter_rows(ws, B.from_vec(np.full((2, n), 3.0, F)), k, n, 10, 2)
+    w[10:12] = 3.0
+    y1 = B.matmul(B.from_vec(x), ws, 1, k, n).to_vec()
+    assert np.array_equal(y1, w.sum(0))

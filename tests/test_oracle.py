@@ -530,3 +530,44 @@ def test_sample_token_edge_cases(orc):
     for seed in range(20):
         r = float(orc.rng_f64(seed, 0, 1)[0])
         assert orc.sample_token(ninf, 1.0, 0, 1.0, seed)[0] == min(int(r * 4), 3)
+
+
+def test_f32_to_bf16_matches_torch_rounding(orc):
+    """The bf16 feature's cast (kernels.rs:629-633) is round-to-nearest-even:
+    torch's independent f32 -> bfloat16 conversion gives the same words for
+    every non-NaN input (ties, subnormals, overflow to inf, signed zeros)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(17)
+    bits = rng.integers(0, 2**32, 20000, dtype=np.uint64).astype(np.uint32)
+    ties = (rng.integers(0, 2**16, 2000, dtype=np.uint64).astype(np.uint32) << 16) | 0x8000  # exact ties
+    special = np.array([0, 0x80000000, 1, 0x807FFFFF, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F8000, 0x7F800000,
+                        0xFF800000, 0x3F808000, 0x3F818000, 0x3F80FFFF, 0x00008000, 0x00018000], np.uint32)
+    x = np.concatenate([bits, ties, special]).view(np.float32)
+    x = x[~np.isnan(x)]
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(orc.f32_to_bf16(x), want)
+    # NaN inputs follow the reference's integer arithmetic (no NaN branch)
+    nan = np.array([0x7FC00000, 0x7F800001, 0xFFFFFFFF, 0x7FFF0000], np.uint32).view(np.float32)
+    assert orc.f32_to_bf16(nan).tolist() == [0x7FC0, 0x7F80, 0x0000, 0x7FFF]
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_matmul_bf16_oracle(orc, ta, tb):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(3 + 2 * ta + tb)
+    m, k, n = 5, 37, 11
+    # bf16-representable integers: every product and sum exact
+    ai = rng.integers(-100, 100, (m, k)).astype(np.float32)
+    bi = rng.integers(-100, 100, (k, n)).astype(np.float32)
+    A = ai.T.copy() if ta else ai
+    Bm = bi.T.copy() if tb else bi
+    assert np.array_equal(orc.matmul_bf16(A, Bm, m, k, n, ta, tb), ai @ bi)
+    # random values: torch's bf16 rounding, then an f64 product
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    b = rng.normal(0, 1, (k, n)).astype(np.float32)
+    ab = torch.from_numpy(a).to(torch.bfloat16).to(torch.float64).numpy()
+    bb = torch.from_numpy(b).to(torch.bfloat16).to(torch.float64).numpy()
+    want = (ab @ bb).astype(np.float32)
+    got = orc.matmul_bf16(a.T.copy() if ta else a, b.T.copy() if tb else b, m, k, n, ta, tb)
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
+    assert not np.array_equal(got, a @ b)  # the rounding of the operands is there
