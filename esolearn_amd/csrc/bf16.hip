@@ -13,7 +13,7 @@
 //   - the activation plane of the MFMA GEMM (rows rounded to bf16, zero
 //     padded);
 //   - a GEMV for 1-16 activation rows over those bf16 rows: 16-byte weight
-//     loads (8 bf16), 4 rows per wave, 2 k steps of 512 in flight, the
+//     loads (8 bf16), 2 rows per wave, 2-4 k steps of 512 in flight, the
 //     activations read from cache and rounded in the kernel.
 #include "internal.h"
 #include "kdev.h"
@@ -93,11 +93,12 @@ __global__ __launch_bounds__(256) void k_plane_bf16(const float *__restrict__ x,
     }
 }
 
-constexpr int GV_RW = 4, GV_NW = 4, GV_U = 2;  // rows per wave, waves, 512-wide k steps in flight
+constexpr int GV_RW = 2, GV_NW = 4;  // rows per wave, waves
 
 // y[m][n] = sum_k bf16(x[m][k]) * W[n][k] (+ bias[n]); W rows [n][kp] bf16.
-// Grid (ceil(n / 16), ceil(m / MT)).
-template <int MT>
+// GV_U 512-wide k steps in flight (4 up to k = 8192, else 2: measured).
+// Grid (ceil(n / 8), ceil(m / MT)).
+template <int MT, int GV_U>
 __global__ __launch_bounds__(64 * GV_NW) void k_gemv_bf16(const u16 *__restrict__ W, int kp, int n,
                                                           const float *__restrict__ x, int ldx, int k, int m,
                                                           float *__restrict__ y, int ldy,
@@ -227,13 +228,20 @@ int launch_gemv_bf16(const unsigned short *w, int kp, int n, const float *x, int
     if ((size_t)n * kp * 2 >= 0x7fffffffull) return set_error(SCRY_ERR_UNSUPPORTED, "gemv_bf16: weights above 2 GiB");
     const int rpb = GV_RW * GV_NW;
     const int mt = m >= 4 ? 4 : (m >= 2 ? 2 : 1);
-    const dim3 grid((n + rpb - 1) / rpb, (m + mt - 1) / mt);
-    if (mt == 4)
-        hipLaunchKernelGGL(k_gemv_bf16<4>, grid, dim3(64 * GV_NW), 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
+    const dim3 grid((n + rpb - 1) / rpb, (m + mt - 1) / mt), blk(64 * GV_NW);
+    const bool u4 = k <= 8192;
+    if (mt == 4 && u4)
+        hipLaunchKernelGGL((k_gemv_bf16<4, 4>), grid, blk, 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
+    else if (mt == 4)
+        hipLaunchKernelGGL((k_gemv_bf16<4, 2>), grid, blk, 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
+    else if (mt == 2 && u4)
+        hipLaunchKernelGGL((k_gemv_bf16<2, 4>), grid, blk, 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
     else if (mt == 2)
-        hipLaunchKernelGGL(k_gemv_bf16<2>, grid, dim3(64 * GV_NW), 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
+        hipLaunchKernelGGL((k_gemv_bf16<2, 2>), grid, blk, 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
+    else if (u4)
+        hipLaunchKernelGGL((k_gemv_bf16<1, 4>), grid, blk, 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
     else
-        hipLaunchKernelGGL(k_gemv_bf16<1>, grid, dim3(64 * GV_NW), 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
+        hipLaunchKernelGGL((k_gemv_bf16<1, 2>), grid, blk, 0, s, w, kp, n, x, ldx, k, m, y, ldy, bias);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }
