@@ -847,12 +847,15 @@ int scry_hip_sample_token(scry_buf logits, const scry_sampling_config *cfg, uint
     hipStream_t s = ctx().stream;
     // one block: DevState, tokens[2], the rng state, f64 scratch [n]
     const size_t V = logits->n;
+    const bool prep = sample_uses_prep(*cfg, (int)V);
+    const size_t pb = prep ? sample_prep_bytes((int)V) : 0;
     char *blk = nullptr;
-    SCRY_TRY(dev_alloc((void **)&blk, 64 + sizeof(double) * V));
+    SCRY_TRY(dev_alloc((void **)&blk, 64 + sizeof(double) * V + pb));
     DevState *st = (DevState *)blk;
     int64_t *toks = (int64_t *)(blk + 16);
     unsigned long long *rng = (unsigned long long *)(blk + 32);
     double *ws = (double *)(blk + 64);
+    void *pw = prep ? (void *)(blk + 64 + sizeof(double) * V) : nullptr;
     struct {
         DevState st;
         int64_t toks[2];
@@ -861,7 +864,8 @@ int scry_hip_sample_token(scry_buf logits, const scry_sampling_config *cfg, uint
     static_assert(sizeof(DevState) == 16, "DevState layout");
     hipError_t e = hipMemcpyAsync(blk, &h, sizeof h, hipMemcpyHostToDevice, s);
     int rc = e == hipSuccess ? SCRY_OK : hip_fail(e, "sample_token upload", __FILE__, __LINE__);
-    if (!rc) rc = launch_sample(logits->d, (int)V, *cfg, ws, rng, st, toks, s);
+    if (!rc && prep) rc = launch_fill_u32((unsigned *)pw, pb / 4, 0u, s);
+    if (!rc) rc = launch_sample(logits->d, (int)V, *cfg, ws, rng, st, toks, pw, s);
     if (!rc) {
         e = hipMemcpyAsync(&h, blk, sizeof h, hipMemcpyDeviceToHost, s);
         if (e == hipSuccess) e = hipStreamSynchronize(s);

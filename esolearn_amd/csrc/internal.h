@@ -154,8 +154,12 @@ int launch_logits_finish(const GemvArgs &a, hipStream_t s);
 // sample_token on the device (sample.hip): logits [V] -> tokens[pos + 1] when
 // the position draws a token, then the position advances.  ws: [V] f64
 // scratch; rng: the wyrand state.
+// prep: sample_prep_bytes(V) zeroed bytes when sample_uses_prep (top-k off and
+// a large vocabulary: statistics and exp values over all CUs first)
+bool sample_uses_prep(const scry_sampling_config &sc, int V);
+size_t sample_prep_bytes(int V);
 int launch_sample(const float *logits, int V, const scry_sampling_config &sc, double *ws,
-                  unsigned long long *rng, DevState *st, int64_t *tokens, hipStream_t s);
+                  unsigned long long *rng, DevState *st, int64_t *tokens, void *prep, hipStream_t s);
 
 // safetensors.hip: memory-mapped safetensors shards and the device dtype
 // widening of the checkpoint loader

@@ -165,6 +165,7 @@ struct scry_kv_cache_s {
     scry_sampling_config samp{};
     double *samp_ws = nullptr;
     unsigned long long *rng = nullptr;
+    void *samp_prep = nullptr;  // zeroed; sample_uses_prep configurations
     int n_splits = 1, max_chunk = 16;
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
@@ -399,6 +400,7 @@ void cache_free(scry_kv_cache c) {
     dev_free(c->amax);
     dev_free(c->samp_ws);
     dev_free(c->rng);
+    dev_free(c->samp_prep);
     dev_free(c->dr.layers);
     uc_give(c->dr.uc);
     if (c->hs) (void)hipHostFree(c->hs);
@@ -803,7 +805,7 @@ int record_step(scry_kv_cache c, hipStream_t s) {
     const GemvArgs lg = lm_args(c, 1);
     SCRY_TRY(launch_qgemv(EPI_LOGITS, lg, s));
     if (c->sampling)
-        return launch_sample(c->logits, m->V, c->samp, c->samp_ws, c->rng, c->state, c->tokens, s);
+        return launch_sample(c->logits, m->V, c->samp, c->samp_ws, c->rng, c->state, c->tokens, c->samp_prep, s);
     return launch_logits_finish(lg, s);
 }
 
@@ -1038,6 +1040,11 @@ int generate_impl(scry_llama m, const int64_t *prompt, int n_prompt, int max_tok
         c->samp = *samp;
         rc = dev_alloc((void **)&c->samp_ws, sizeof(double) * (size_t)m->V);
         if (!rc) rc = dev_alloc((void **)&c->rng, sizeof(unsigned long long));
+        if (!rc && sample_uses_prep(*samp, m->V)) {
+            const size_t pb = sample_prep_bytes(m->V);
+            rc = dev_alloc(&c->samp_prep, pb);
+            if (!rc) rc = launch_fill_u32((unsigned *)c->samp_prep, pb / 4, 0u, s);
+        }
         if (!rc) {
             e = hipMemcpyAsync(c->rng, rng_state, sizeof *rng_state, hipMemcpyHostToDevice, s);
             if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -1538,6 +1545,11 @@ int bench_decode_impl(scry_llama m, const int64_t *prompt, int n_prompt, int war
         c->samp = *samp;
         rc = dev_alloc((void **)&c->samp_ws, sizeof(double) * (size_t)m->V);
         if (!rc) rc = dev_alloc((void **)&c->rng, sizeof(unsigned long long));
+        if (!rc && sample_uses_prep(*samp, m->V)) {
+            const size_t pb = sample_prep_bytes(m->V);
+            rc = dev_alloc(&c->samp_prep, pb);
+            if (!rc) rc = launch_fill_u32((unsigned *)c->samp_prep, pb / 4, 0u, s);
+        }
         if (!rc) e = hipMemcpyAsync(c->rng, &seed, sizeof seed, hipMemcpyHostToDevice, s);
         if (!rc && e != hipSuccess) rc = hip_fail(e, "rng upload", __FILE__, __LINE__);
     }

@@ -74,7 +74,104 @@ struct SampleArgs {
     unsigned long long *rng;  // fastrand state
     DevState *st;
     int64_t *tokens;
+    // top-k off and V > LCAP: the statistics, exp values (ws) and 64-entry
+    // segment sums come from the two vocabulary-wide kernels below
+    unsigned *prep;  // [PREP_WORDS], cleared by k_sample for the next step
+    double *segsum;  // [ceil(V / 64)]
 };
+
+// prep words: the largest finite key, ~(smallest finite key), finite count,
+// NaN/+inf flag, ~(smallest key with e > 0) (atomic max of the complement:
+// all start at 0)
+enum { PR_MAXKEY = 0, PR_NKMIN = 1, PR_NFIN = 2, PR_BAD = 3, PR_NKMINP = 4, PREP_WORDS = 8 };
+
+__device__ __forceinline__ float key_f32(unsigned key) {  // inverse of okey
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+// the draw condition of k_sample (generate.rs:67-83), read before it advances
+__device__ __forceinline__ bool draws(const DevState *st) {
+    const int p = st->pos;
+    return p + 1 >= st->n_prompt && p + 1 <= st->max_tokens;
+}
+
+// Vocabulary-wide statistics for k_sample, over all CUs.
+__global__ __launch_bounds__(256) void k_prep_stats(const float *__restrict__ lg, int V, const DevState *st,
+                                                    unsigned *prep) {
+    if (!draws(st)) return;
+    unsigned kmax = 0, kmin = ~0u, nfin = 0, bad = 0;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < V; i += gridDim.x * 256) {
+        const float x = lg[i];
+        bad |= !(x < INFINITY);
+        if (x > -INFINITY && x < INFINITY) {
+            const unsigned k = okey(x);
+            kmax = max(kmax, k);
+            kmin = min(kmin, k);
+            nfin++;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        kmax = max(kmax, (unsigned)__shfl_xor((int)kmax, off));
+        kmin = min(kmin, (unsigned)__shfl_xor((int)kmin, off));
+        nfin += (unsigned)__shfl_xor((int)nfin, off);
+        bad |= (unsigned)__shfl_xor((int)bad, off);
+    }
+    // one set of atomics per workgroup (they meet on four words in L2)
+    __shared__ unsigned r[4][4];
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        r[0][wave] = kmax;
+        r[1][wave] = kmin;
+        r[2][wave] = nfin;
+        r[3][wave] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) {
+            kmax = max(kmax, r[0][w]);
+            kmin = min(kmin, r[1][w]);
+            nfin += r[2][w];
+            bad |= r[3][w];
+        }
+        atomicMax(prep + PR_MAXKEY, kmax);
+        atomicMax(prep + PR_NKMIN, ~kmin);
+        atomicAdd(prep + PR_NFIN, nfin);
+        if (bad) atomicOr(prep + PR_BAD, 1u);
+    }
+}
+
+// e = exp(f64(x)/f64(T) - max) for every entry (top-k off: every finite
+// logit is kept; -inf gives 0) into ws, one wave per 64-entry segment with
+// its sum, and the smallest key with e > 0.
+__global__ __launch_bounds__(256) void k_prep_exp(const float *__restrict__ lg, int V, float temperature,
+                                                  const DevState *st, unsigned *prep, double *__restrict__ ws,
+                                                  double *__restrict__ segsum) {
+    if (!draws(st)) return;
+    if (prep[PR_BAD] || prep[PR_NFIN] == 0) return;  // k_sample takes the uniform path
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, s = blockIdx.x * 4 + wave;
+    const int nseg = (V + 63) >> 6;
+    const double T = (double)temperature;
+    const double mxs = (double)key_f32(prep[PR_MAXKEY]) / T;
+    const int i = s * 64 + lane;  // (segments past the end: x = -inf, nothing stored)
+    const float x = i < V ? lg[i] : -INFINITY;
+    const double e = x != -INFINITY ? exp((double)x / T - mxs) : 0.0;
+    if (i < V) ws[i] = e;
+    const double t = dev::wave_sum_d_dpp(e);
+    unsigned km = e > 0.0 ? okey(x) : ~0u;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) km = min(km, (unsigned)__shfl_xor((int)km, off));
+    __shared__ unsigned r[4];
+    if (lane == 0) {
+        if (s < nseg) segsum[s] = t;
+        r[wave] = km;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        km = min(min(r[0], r[1]), min(r[2], r[3]));
+        if (km != ~0u) atomicMax(prep + PR_NKMINP, ~km);  // one per workgroup
+    }
+}
 
 struct Shared {
     unsigned hcnt[NB];
@@ -347,21 +444,16 @@ __device__ __forceinline__ int find_mth(const Src &src, F flag, unsigned m, Shar
     return S.i1;
 }
 
-// weighted_sample over prob(i, x, e): per-segment sums, a scan over
-// segments, the crossing segment scanned by one wave (prob must give the
-// same value for an entry in every call)
-template <bool NE, class P>
-__device__ __forceinline__ int draw_segments(const Src &src, P prob, Shared &S) {
+// The walk of weighted_sample over per-segment sums already in S.b.segq
+// (S.i0 = INT_MAX, synchronised): a scan over segments finds the first whose
+// cumulative sum exceeds r, then one wave scans that segment's values val(i)
+// (0 past V).  The segment sums may be summed in another order than that
+// scan: when r lies within that rounding of the segment's end, its last entry
+// with a value > 0.
+template <class VAL>
+__device__ __forceinline__ int draw_walk(int V, double r, VAL val, Shared &S) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int V = src.V, nseg = (V + 63) >> 6;
-    each<NE>(src, [&](int i, float x, double e, bool ok) {
-        const double tot = dev::wave_sum_d_dpp(ok ? prob(i, x, e) : 0.0);
-        const int s = i >> 6;
-        if (lane == 0 && s < nseg) S.b.segq[s] = tot;
-    });
-    if (tid == 0) S.i0 = INT_MAX;
-    __syncthreads();
-    const double r = S.r;
+    const int nseg = (V + 63) >> 6;
     const int spt = (nseg + SN - 1) / SN, s0 = tid * spt;
     double loc = 0.0;
     for (int u = 0; u < spt && s0 + u < nseg; u++) loc += S.b.segq[s0 + u];
@@ -382,14 +474,9 @@ __device__ __forceinline__ int draw_segments(const Src &src, P prob, Shared &S) 
     if (sx == INT_MAX) return V - 1;  // r beyond the total (generate.rs:185)
     if (wave == 0) {
         const int i = sx * 64 + lane;
-        float x;
-        double e;
-        load_one<NE>(src, i, x, e);
-        const double q = i < V ? prob(i, x, e) : 0.0;
+        const double q = i < V ? val(i) : 0.0;
         const double c = S.b.segq[sx] + wscan_incl(q);
         const unsigned long long mk = __ballot(r < c);
-        // the segment total was summed in another order: when r lies within
-        // that rounding of the segment's end, its last entry with q > 0
         const unsigned long long nz = __ballot(q > 0.0);
         if (lane == 0)
             S.i1 = mk ? sx * 64 + __ffsll((unsigned long long)mk) - 1
@@ -397,6 +484,28 @@ __device__ __forceinline__ int draw_segments(const Src &src, P prob, Shared &S) 
     }
     __syncthreads();
     return S.i1;
+}
+
+// weighted_sample over prob(i, x, e): per-segment sums (one wave per
+// segment), then the walk (prob must give the same value for an entry in
+// every call)
+template <bool NE, class P>
+__device__ __forceinline__ int draw_segments(const Src &src, P prob, Shared &S) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int V = src.V, nseg = (V + 63) >> 6;
+    each<NE>(src, [&](int i, float x, double e, bool ok) {
+        const double tot = dev::wave_sum_d_dpp(ok ? prob(i, x, e) : 0.0);
+        const int s = i >> 6;
+        if (lane == 0 && s < nseg) S.b.segq[s] = tot;
+    });
+    if (tid == 0) S.i0 = INT_MAX;
+    __syncthreads();
+    return draw_walk(V, S.r, [&](int i) {
+        float x;
+        double e;
+        load_one<NE>(src, i, x, e);
+        return prob(i, x, e);
+    }, S);
 }
 
 // At most LCAP kept entries (finite, key >= kk): gathered in index order,
@@ -545,13 +654,22 @@ __device__ __forceinline__ int finish_gather(const SampleArgs &a, const Src &src
 
 __device__ __forceinline__ int sample_body(const SampleArgs &a, Shared &S) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int V = a.V;
+    const int V = a.V, nseg = (V + 63) >> 6;
     const float *lg = a.logits;
     const double T = (double)a.temperature;
     const Src src{lg, a.ws, V, (V + SN - 1) / SN};
     // ---- 0. max, smallest finite key, finite count, NaN / +inf
     float mx = -INFINITY;
     unsigned kmin = ~0u, nfin = 0, bad = 0;
+    if (a.prep) {  // from k_prep_stats
+        const unsigned km = a.prep[PR_MAXKEY];
+        mx = km ? key_f32(km) : -INFINITY;
+        kmin = ~a.prep[PR_NKMIN];
+        nfin = a.prep[PR_NFIN];
+        bad = a.prep[PR_BAD];
+        if (tid == 0) S.r = wy_next_f64(a.rng);  // generate.rs:176
+        __syncthreads();
+    } else {
     float fmin = INFINITY;
     each<false>(src, [&](int, float x, double, bool ok) {
         // past V, x is -inf; NaN and +inf fail x < inf; fmaxf ignores NaN
@@ -587,6 +705,7 @@ __device__ __forceinline__ int sample_body(const SampleArgs &a, Shared &S) {
     nfin = 0;
     for (int w = 0; w < SW; w++) nfin += S.rn[w];
     __syncthreads();
+    }
     const bool topp = a.top_p < 1.0f && a.top_p > 0.0f;
     const unsigned long long Tp = topp ? (unsigned long long)((double)a.top_p * FX + 0.5) : 0ull;
     if (bad || nfin == 0) {
@@ -642,16 +761,28 @@ __device__ __forceinline__ int sample_body(const SampleArgs &a, Shared &S) {
     // ---- 2. softmax over the kept entries
     double part = 0.0;
     unsigned kminp = ~0u;
-    each<false>(src, [&](int i, float x, double, bool ok) {
-        if (!ok) return;
-        const unsigned key = okey(x);
-        const double e = (x != -INFINITY && key >= kk) ? exp((double)x / T - mxs) : 0.0;
-        a.ws[i] = e;
-        part += e;
-        if (e > 0.0) kminp = min(kminp, key);
-    });
+    if (a.prep) {  // exp values and segment sums from k_prep_exp
+        for (int sg = tid; sg < nseg; sg += SN) part += a.segsum[sg];
+        kminp = ~a.prep[PR_NKMINP];
+    } else {
+        each<false>(src, [&](int i, float x, double, bool ok) {
+            if (!ok) return;
+            const unsigned key = okey(x);
+            const double e = (x != -INFINITY && key >= kk) ? exp((double)x / T - mxs) : 0.0;
+            a.ws[i] = e;
+            part += e;
+            if (e > 0.0) kminp = min(kminp, key);
+        });
+    }
     const double sum = block_sum(part, S.rd);
-    kminp = block_min_u(kminp, S.rk);
+    if (!a.prep) kminp = block_min_u(kminp, S.rk);
+    if (a.prep && !(a.top_p < 1.0f && a.top_p > 0.0f)) {
+        // no top-p: r < sum(p up to i) is r * sum < sum(e up to i), up to rounding
+        for (int sg = tid; sg < nseg; sg += SN) S.b.segq[sg] = a.segsum[sg];
+        if (tid == 0) S.i0 = INT_MAX;
+        __syncthreads();
+        return draw_walk(V, S.r * sum, [&](int i) { return a.ws[i]; }, S);
+    }
     // p = e * (1 / sum) in the vocabulary-wide passes (within an ulp of e / sum)
     const double isum = 1.0 / sum, wsc = FX / sum;
     // ---- 3. top-p: entries above the cut key kp, and ties up to index cut
@@ -738,18 +869,37 @@ __global__ __launch_bounds__(SN) void k_sample(SampleArgs a) {
         if (draw) a.tokens[p + 1] = tok;
         a.st->pos = p + 1;
         a.st->cache_len = a.st->cache_len + 1;
+        if (a.prep)  // (every thread read it before the body's barriers)
+            for (int w = 0; w < PREP_WORDS; w++) a.prep[w] = 0u;
     }
 }
 
 }  // namespace
 
+bool sample_uses_prep(const scry_sampling_config &sc, int V) {
+    return (sc.top_k <= 0 || sc.top_k >= V) && V > LCAP;
+}
+
+size_t sample_prep_bytes(int V) { return sizeof(unsigned) * PREP_WORDS + sizeof(double) * ((V + 63) / 64); }
+
 int launch_sample(const float *logits, int V, const scry_sampling_config &sc, double *ws,
-                  unsigned long long *rng, DevState *st, int64_t *tokens, hipStream_t s) {
+                  unsigned long long *rng, DevState *st, int64_t *tokens, void *prep, hipStream_t s) {
     if (!logits || V <= 0 || !ws || !rng || !st || !tokens)
         return set_error(SCRY_ERR_INVALID, "sample: missing buffers");
     if (V > MAXV) return set_error(SCRY_ERR_UNSUPPORTED, "sample: vocabulary %d above %d", V, MAXV);
     if (!(sc.temperature >= 1e-8f)) return set_error(SCRY_ERR_INVALID, "sample: temperature < 1e-8 is greedy");
-    SampleArgs a{logits, V, sc.temperature, sc.top_k, sc.top_p, ws, rng, st, tokens};
+    const bool use = sample_uses_prep(sc, V);
+    if (use && !prep) return set_error(SCRY_ERR_INVALID, "sample: missing the prep buffer");
+    unsigned *pw = use ? (unsigned *)prep : nullptr;
+    double *seg = use ? (double *)((unsigned *)prep + PREP_WORDS) : nullptr;
+    SampleArgs a{logits, V, sc.temperature, sc.top_k, sc.top_p, ws, rng, st, tokens, pw, seg};
+    if (use) {
+        const int nseg = (V + 63) / 64;
+        hipLaunchKernelGGL(k_prep_stats, dim3(std::min(64, (V + 1023) / 1024)), dim3(256), 0, s, logits, V,
+                           (const DevState *)st, pw);
+        hipLaunchKernelGGL(k_prep_exp, dim3((nseg + 3) / 4), dim3(256), 0, s, logits, V, sc.temperature,
+                           (const DevState *)st, pw, ws, seg);
+    }
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(SN), 0, s, a);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
