@@ -205,6 +205,21 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
 #pragma unroll
             for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + (d << 10));
         }
+    // EPI_RESID: the residual and the next norm's weight of the row this lane
+    // stores, requested now (they are used after the weight stream; the row
+    // is read and written by this lane only)
+    float pre_r[RWT], pre_g[RWT];
+    if constexpr (EPI == EPI_RESID) {
+        const float *R = a.resid ? a.resid : a.embed + (size_t)a.tokens[a.state->pos] * a.rows;
+#pragma unroll
+        for (int r = 0; r < RWT; r++) {
+            pre_r[r] = pre_g[r] = 0.f;
+            if (lane == r) {
+                pre_r[r] = R[wrow[r]];
+                if (a.xg_out) pre_g[r] = a.g_next[wrow[r]];
+            }
+        }
+    }
 
     // ---- 2. stage the activation rows into LDS with the per-lane sums
     double ssp = 0.0;
@@ -317,10 +332,8 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
                     if constexpr (EPI == EPI_STORE) {
                         if (a.bias) v = v + a.bias[row];
                     } else {
-                        const float *R = a.resid ? a.resid + (size_t)mr * a.ldy
-                                                 : a.embed + (size_t)a.tokens[a.state->pos] * a.rows;
-                        v = R[row] + v;
-                        if (a.xg_out) a.xg_out[row] = v * a.g_next[row];
+                        v = pre_r[r] + v;  // (EPI_RESID has one activation row: mr == 0)
+                        if (a.xg_out) a.xg_out[row] = v * pre_g[r];
                         s_val[wave * RWT + r] = v;
                     }
                     a.y[(size_t)mr * a.ldy + row] = v;
