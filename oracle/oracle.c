@@ -976,6 +976,20 @@ int orc_llama_set_qtensor(orc_llama *m, int id, int layer, const int8_t *q, floa
     return 0;
 }
 
+/* Block-32 int8 weights of a projection (forward mode 2): q32 in the
+ * projection's storage layout ([k,n], or [n,k] for the LM head), scales
+ * [n][ceil(k/32)]. */
+int orc_llama_set_qtensor_b32(orc_llama *m, int id, int layer, const int8_t *q32, const float *s32) {
+    orc_proj *P = (orc_proj *)get_proj(m, id, layer);
+    if (!P) return -1;
+    const size_t cnt = (size_t)P->k * P->n, ns = (size_t)P->n * ((P->k + 31) / 32);
+    if (!P->q32) P->q32 = (int8_t *)malloc(cnt);
+    if (!P->s32) P->s32 = (float *)malloc(sizeof(float) * ns);
+    memcpy(P->q32, q32, cnt);
+    memcpy(P->s32, s32, sizeof(float) * ns);
+    return 0;
+}
+
 int orc_llama_set_embed(orc_llama *m, const float *w) {
     memcpy(m->embed, w, sizeof(float) * (size_t)m->cfg.vocab_size * m->cfg.hidden_size);
     return 0;

@@ -136,6 +136,7 @@ orc_llama *orc_llama_new(const orc_llama_config *cfg, uint64_t seed, int quantiz
 void orc_llama_free(orc_llama *m);
 orc_llama *orc_llama_new_empty(const orc_llama_config *cfg);
 int orc_llama_set_qtensor(orc_llama *m, int id, int layer, const int8_t *q, float scale);
+int orc_llama_set_qtensor_b32(orc_llama *m, int id, int layer, const int8_t *q32, const float *s32);
 int orc_llama_set_embed(orc_llama *m, const float *w);
 /* RMSNorm weight `which` (0 input, 1 post-attention: of `layer`; 2 final) and
  * the eps of every norm, as from_safetensors loads them (llama.rs:880-914). */

@@ -77,6 +77,7 @@ def lib():
         "orc_llama_free": (None, [vp]),
         "orc_llama_new_empty": (vp, [vp]),
         "orc_llama_set_qtensor": (i32, [vp, i32, i32, i8p, f32]),
+        "orc_llama_set_qtensor_b32": (C.c_int, [C.c_void_p, i32, i32, i8p, f32p]),
         "orc_llama_set_embed": (i32, [vp, f32p]),
         "orc_llama_set_norm": (i32, [vp, i32, i32, f32p, f32]),
         "orc_llama_rng_calls": (u64, [vp]),
@@ -399,6 +400,12 @@ class Llama:
         q = np.ascontiguousarray(q, np.int8).ravel()
         if lib().orc_llama_set_qtensor(self.h, tid, layer, q, float(scale)) != 0:
             raise ValueError("set_qtensor: bad tensor")
+
+    def set_qtensor_b32(self, tid, layer, q32, s32):
+        """Block-32 weights (forward mode 2): q32 in the projection's layout."""
+        q = np.ascontiguousarray(q32, np.int8).ravel()
+        if lib().orc_llama_set_qtensor_b32(self.h, tid, layer, q, _f32(s32).ravel()) != 0:
+            raise ValueError("set_qtensor_b32: bad tensor")
 
     def set_embed(self, w):
         lib().orc_llama_set_embed(self.h, _f32(w).ravel())

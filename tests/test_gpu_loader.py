@@ -76,8 +76,9 @@ def make_checkpoint(tmp_path, cfg, seed, tied, dtypes):
     return paths, tensors
 
 
-def oracle_model(orc, cfg, tensors, tied):
-    """The reference's from_safetensors + int8 layout step, on the oracle."""
+def oracle_model(orc, cfg, tensors, tied, block32=False):
+    """The reference's from_safetensors + int8 layout step, on the oracle
+    (block32: also the block-32 weights, for forward mode 2)."""
     c = dict(cfg, tie_word_embeddings=tied)
     om = orc.Llama(orc.LlamaConfig(**c), None)
     h, n_layers = cfg["hidden_size"], cfg["n_layers"]
@@ -92,12 +93,24 @@ def oracle_model(orc, cfg, tensors, tied):
                        (orc.T_DOWN, f[f"{p}.mlp.down_proj.weight"].T)):
             q, s = orc.quantize_symmetric(np.ascontiguousarray(w))
             om.set_qtensor(tid, i, q, s)
+            if block32:
+                q32, s32 = orc.quantize_block32(np.ascontiguousarray(w), w.shape[0], w.shape[1])
+                om.set_qtensor_b32(tid, i, q32, s32)
         om.set_norm(0, i, f[f"{p}.input_layernorm.weight"], cfg["rms_norm_eps"])
         om.set_norm(1, i, f[f"{p}.post_attention_layernorm.weight"], cfg["rms_norm_eps"])
     om.set_norm(2, 0, f["model.norm.weight"], cfg["rms_norm_eps"])
     lm = f["model.embed_tokens.weight"] if tied else f["lm_head.weight"]
     q, s = orc.quantize_symmetric(lm)
     om.set_qtensor(orc.T_LM_HEAD, 0, q, s)
+    if block32:  # the LM head is stored [V, h]: blocks of 32 along each row
+        V, h = lm.shape
+        nb = (h + 31) // 32
+        q32 = np.empty((V, h), np.int8)
+        s32 = np.empty((V, nb), np.float32)
+        for j in range(V):
+            for b in range(nb):
+                q32[j, 32 * b:32 * b + 32], s32[j, b] = orc.quantize_symmetric(lm[j, 32 * b:32 * b + 32])
+        om.set_qtensor_b32(orc.T_LM_HEAD, 0, q32, s32)
     return om
 
 
@@ -135,6 +148,25 @@ def test_loaded_model_matches_oracle(tmp_path, orc, hip, tied):
     ef = max(rel_err(fg[i], fr[i]) for i in range(len(toks)))
     print(f"[err] forward logits {ef:.3e}", flush=True)
     assert ef < LOGIT_TOL
+    hm.free()
+    om.close()
+
+
+def test_loaded_block32_model_matches_oracle(tmp_path, orc, hip):
+    """The loader with block-32 int8 weights (quant_mode 1): the oracle gets
+    the same block-32 quantization of the widened weights (forward mode 2)."""
+    print("[case] safetensors tiny Llama, block-32 int8", flush=True)
+    paths, tensors = make_checkpoint(tmp_path, BASE, 13, False, [torch.bfloat16, torch.float32])
+    cfg = hip.LlamaConfig(**dict(BASE, tie_word_embeddings=False))
+    hm = hip.LlamaModel.from_safetensors(cfg, paths, hip.QUANT_BLOCK32)
+    om = oracle_model(orc, BASE, tensors, False, block32=True)
+    prompt = orc.prompt_ids(4, 10, BASE["vocab_size"])
+    ref_t, ref_l = om.generate_greedy(prompt, 20, mode=2, want_logits=True)
+    gt, gl = hm.generate_greedy(prompt, 20, want_logits=True)
+    err = max(rel_err(gl[i], ref_l[i]) for i in range(len(ref_t)))
+    print(f"[err] block-32 decode logits {err:.3e}", flush=True)
+    assert err < LOGIT_TOL
+    assert (gt == ref_t).all()
     hm.free()
     om.close()
 
