@@ -88,13 +88,13 @@ class Linear:
         if self.quant is not None:
             return HipBackend.matmul_i8_f32_bias(x, self.quant.weight_q, self.quant.scale, self.bias,
                                                  seq, self.in_features, self.out_features)
-        # ops::matmul_bias: the product, then the bias row on every output row
-        # (broadcast as ones[seq, 1] @ bias[1, out] on the device)
+        # ops::matmul_bias: the product (bf16 operands in bf16 mode), then the
+        # f32 bias row added to every output row (the broadcast row is built
+        # on the host: a matmul would round the bias in bf16 mode)
         y = HipBackend.matmul(x, self.weight, seq, self.in_features, self.out_features)
-        ones = HipBackend.from_vec(np.ones(seq, np.float32))
-        rows = HipBackend.matmul(ones, self.bias, seq, 1, self.out_features)
+        rows = HipBackend.from_vec(np.tile(self.bias.to_vec(), seq))
         out = HipBackend.add(y, rows)
-        for t in (y, ones, rows):
+        for t in (y, rows):
             t.free()
         return out
 

@@ -104,6 +104,14 @@ def test_f32_forward_and_errors(hip, orc):
     out = lin.forward(hip.HipBackend.from_vec(x), seq).to_vec().reshape(seq, n)
     ref = orc.matmul_f32(x, w, seq, k, n) + bias
     assert rel_err(out, ref) < GEMV_TOL
+    # bf16 mode: bf16 product, the bias still added in f32 (ops::matmul_bias)
+    hip.HipBackend.set_bf16_mode(True)
+    try:
+        ob = lin.forward(hip.HipBackend.from_vec(x), seq).to_vec().reshape(seq, n)
+    finally:
+        hip.HipBackend.set_bf16_mode(False)
+    refb = orc.matmul_bf16(x, w, seq, k, n) + bias
+    assert rel_err(ob, refb) < GEMV_TOL
     with pytest.raises(ValueError):
         lin.forward(hip.HipBackend.from_vec(x), seq + 1)
     with pytest.raises(ValueError):
