@@ -69,6 +69,7 @@ SIGNATURES = {
     "scry_hip_matmul_i8_f32_bias": [vp, vp, f32, vp, i32, i32, i32, P(vp)],
     "scry_hip_matmul_i8_f32_block32": [vp, vp, vp, i32, i32, i32, P(vp)],
     "scry_hip_matmul": [vp, vp, i32, i32, i32, i32, i32, P(vp)],
+    "scry_hip_matmul_bias": [vp, vp, vp, i32, i32, i32, i32, i32, P(vp)],
     "scry_hip_matmul_strided_batched": [vp, vp, i32, i32, i32, i32, i32, i32, P(vp)],
     "scry_hip_rmsnorm": [vp, vp, i32, i32, f32, P(vp)],
     "scry_hip_rope_with_freqs_preloaded": [vp, i32, i32, i32, i32, vp, P(vp)],

@@ -209,6 +209,14 @@ class HipBackend:
         return _st(o, m * n)
 
     @staticmethod
+    def matmul_bias(a, b, bias, m, k, n, trans_a=False, trans_b=False) -> Storage:
+        """C = A @ B + bias, the bias row [n] added to every row (mod.rs:62-86)."""
+        o = _out()
+        call("scry_hip_matmul_bias", a.h, b.h, bias.h, m, k, n, int(trans_a), int(trans_b),
+             C.byref(o))
+        return _st(o, m * n)
+
+    @staticmethod
     def matmul_strided_batched(a, b, batch, m, k, n, trans_a=False, trans_b=False) -> Storage:
         o = _out()
         call("scry_hip_matmul_strided_batched", a.h, b.h, batch, m, k, n, int(trans_a),

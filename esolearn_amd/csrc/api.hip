@@ -638,6 +638,32 @@ int scry_hip_matmul(scry_buf a, scry_buf b, int m, int k, int n, int trans_a, in
     return launch_matmul_f32(a->d, b->d, 1, m, k, n, trans_a, trans_b, (*out)->d, ctx().stream);
 }
 
+// MathBackend::matmul_bias (mod.rs:62-86; the CUDA backend keeps the default):
+// the matmul above (bf16 operands in bf16 mode), then the f32 bias row added
+// to every output row on the device.  A bf16-only bias is widened first, as
+// the default's to_vec does.
+int scry_hip_matmul_bias(scry_buf a, scry_buf b, scry_buf bias, int m, int k, int n, int trans_a,
+                         int trans_b, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_ANY(bias, "matmul_bias");
+    if (n > 0 && bias->n < (size_t)n)
+        return set_error(SCRY_ERR_INVALID, "matmul_bias: bias holds %zu values, needs %d",
+                         bias->n, n);
+    SCRY_TRY(scry_hip_matmul(a, b, m, k, n, trans_a, trans_b, out));
+    float *tmp = nullptr;
+    const float *bv = nullptr;
+    int rc = f32_of(bias, &tmp, &bv);
+    if (!rc) rc = launch_add_bias_rows((*out)->d, bv, m, n, ctx().stream);
+    if (tmp && !rc) rc = sync();  // the widened copy is freed below
+    dev_free(tmp);
+    if (rc) {
+        del_buf(*out);
+        *out = nullptr;
+    }
+    return rc;
+}
+
 int scry_hip_matmul_strided_batched(scry_buf a, scry_buf b, int batch, int m, int k, int n,
                                     int trans_a, int trans_b, scry_buf *out) {
     API_LOCK;

@@ -103,6 +103,12 @@ __global__ void k_add(const float *__restrict__ a, const float *__restrict__ b, 
     GRID_STRIDE(i, n) out[i] = __fadd_rn(a[i], b[i]);
 }
 
+// mod.rs:76-83: the bias row added to every row of c [rows, n], in place
+__global__ void k_add_bias_rows(float *__restrict__ c, const float *__restrict__ bias,
+                                size_t total, int n) {
+    GRID_STRIDE(i, total) c[i] = __fadd_rn(c[i], bias[i % n]);
+}
+
 // cpu.rs:485-498 (ids validated on the host)
 __global__ void k_embedding(const float *__restrict__ w, const int64_t *__restrict__ ids,
                             int n_ids, int dim, float *__restrict__ out) {
@@ -205,6 +211,13 @@ int launch_swiglu(const float *g, const float *u, size_t n, float *out, hipStrea
 int launch_add(const float *a, const float *b, size_t n, float *out, hipStream_t s) {
     if (n == 0) return SCRY_OK;
     hipLaunchKernelGGL(k_add, dim3(grid1(n)), dim3(256), 0, s, a, b, n, out);
+    LAUNCH_CHECK();
+}
+
+int launch_add_bias_rows(float *c, const float *bias, int rows, int n, hipStream_t s) {
+    const size_t total = (size_t)rows * n;
+    if (total == 0) return SCRY_OK;
+    hipLaunchKernelGGL(k_add_bias_rows, dim3(grid1(total)), dim3(256), 0, s, c, bias, total, n);
     LAUNCH_CHECK();
 }
 

@@ -202,6 +202,7 @@ int launch_scale(const float *x, size_t n, float s_, float *out, hipStream_t s);
 int launch_softmax(const float *x, int rows, int cols, float *out, hipStream_t s);
 int launch_swiglu(const float *g, const float *u, size_t n, float *out, hipStream_t s);
 int launch_add(const float *a, const float *b, size_t n, float *out, hipStream_t s);
+int launch_add_bias_rows(float *c, const float *bias, int rows, int n, hipStream_t s);
 int launch_embedding(const float *w, const int64_t *ids, int n_ids, int dim, float *out,
                      hipStream_t s);
 int launch_gather_repeat_kv(const float *cache, int cached_len, int n_kv, int n_q, int hd,

@@ -89,14 +89,9 @@ class Linear:
             return HipBackend.matmul_i8_f32_bias(x, self.quant.weight_q, self.quant.scale, self.bias,
                                                  seq, self.in_features, self.out_features)
         # ops::matmul_bias: the product (bf16 operands in bf16 mode), then the
-        # f32 bias row added to every output row (the broadcast row is built
-        # on the host: a matmul would round the bias in bf16 mode)
-        y = HipBackend.matmul(x, self.weight, seq, self.in_features, self.out_features)
-        rows = HipBackend.from_vec(np.tile(self.bias.to_vec(), seq))
-        out = HipBackend.add(y, rows)
-        for t in (y, rows):
-            t.free()
-        return out
+        # f32 bias row added to every output row on the device
+        return HipBackend.matmul_bias(x, self.weight, self.bias, seq, self.in_features,
+                                      self.out_features)
 
     def parameters(self) -> list[Storage]:
         """Module::parameters (linear.rs:97-101)."""

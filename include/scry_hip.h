@@ -127,6 +127,10 @@ int scry_hip_matmul_i8_f32_block32(scry_buf a, scry_i8buf b_q, scry_buf scales, 
  * mode bf16 operands, f32 accumulation (cuda.rs:274-277) */
 int scry_hip_matmul(scry_buf a, scry_buf b, int m, int k, int n, int trans_a, int trans_b,
                     scry_buf *out);
+/* MathBackend::matmul_bias (mod.rs:62-86; ops::matmul_bias, ops.rs:21-35):
+ * scry_hip_matmul, then the f32 bias row [n] added to every row of [m, n] */
+int scry_hip_matmul_bias(scry_buf a, scry_buf b, scry_buf bias, int m, int k, int n, int trans_a,
+                         int trans_b, scry_buf *out);
 /* MathBackend::matmul_strided_batched (mod.rs:561-591; cpu.rs:1321-1350) */
 int scry_hip_matmul_strided_batched(scry_buf a, scry_buf b, int batch, int m, int k, int n,
                                     int trans_a, int trans_b, scry_buf *out);

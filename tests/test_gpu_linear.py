@@ -117,3 +117,39 @@ def test_f32_forward_and_errors(hip, orc):
     with pytest.raises(ValueError):
         hip.Linear(lin.weight, hip.HipBackend.zeros(n + 1), k, n)
     lin.free()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_matmul_bias_backend(hip, orc, bf16):
+    """MathBackend::matmul_bias (mod.rs:62-86): the matmul, then the f32 bias
+    row added to every output row; every transpose pairing, GEMV and GEMM row
+    counts, f32 and bf16 mode."""
+    rng = np.random.default_rng(11)
+    k, n = 200, 72
+    bias = rng.normal(0, 1, n).astype(F)
+    bs = hip.HipBackend.from_vec(bias)
+    hip.HipBackend.set_bf16_mode(bf16)
+    try:
+        for m in (1, 7, 150):
+            for ta in (False, True):
+                for tb in (False, True):
+                    print(f"[case] matmul_bias bf16={bf16} m={m} ta={ta} tb={tb}", flush=True)
+                    a = rng.normal(0, 1, (k, m) if ta else (m, k)).astype(F)
+                    b = rng.normal(0, 0.1, (n, k) if tb else (k, n)).astype(F)
+                    av, bv = hip.HipBackend.from_vec(a.ravel()), hip.HipBackend.from_vec(b.ravel())
+                    got = hip.HipBackend.matmul_bias(av, bv, bs, m, k, n, ta, tb).to_vec()
+                    mm = orc.matmul_bf16 if bf16 else orc.matmul_f32
+                    ref = mm(a, b, m, k, n, ta, tb) + bias
+                    # only the bf16 MFMA GEMM (untransposed A, > 16 rows)
+                    # sums in another order than f32 / f64 accumulation
+                    tol = GEMM_TOL if (bf16 and m > 16 and not ta) else GEMV_TOL
+                    assert rel_err(got.reshape(m, n), ref) < tol, (m, ta, tb)
+                    av.free()
+                    bv.free()
+        with pytest.raises(RuntimeError, match="bias holds"):
+            hip.HipBackend.matmul_bias(hip.HipBackend.from_vec(np.ones(2 * k, F)),
+                                       hip.HipBackend.from_vec(np.ones(k * (n + 1), F)),
+                                       bs, 2, k, n + 1)
+    finally:
+        hip.HipBackend.set_bf16_mode(False)
+    bs.free()
