@@ -91,6 +91,25 @@ SIGNATURES = {
     "scry_hip_from_vec_with_bf16": [vp, vp, sz, P(vp)],
     "scry_hip_bench_qgemv_bias": [i32, i32, i32, i32, i32, i32, P(f64), P(f64)],
     "scry_hip_bench_gemv_bf16": [i32, i32, i32, i32, i32, i32, P(f64), P(f64)],
+    "scry_hip_ones": [sz, P(vp)],
+    "scry_hip_add_broadcast": [vp, P(sz), i32, vp, P(sz), i32, P(sz), i32, P(vp)],
+    "scry_hip_add_inplace": [vp, vp],
+    "scry_hip_scaled_softmax": [vp, f32, i32, i32, P(vp)],
+    "scry_hip_layernorm": [vp, vp, vp, i32, i32, f32, P(vp), P(vp), P(vp)],
+    "scry_hip_layernorm_inference": [vp, vp, vp, i32, i32, f32, P(vp)],
+    "scry_hip_gelu": [vp, P(vp)],
+    "scry_hip_sum": [vp, P(f32)],
+    "scry_hip_mul_elementwise": [vp, vp, P(vp)],
+    "scry_hip_concat_rows": [vp, vp, i32, i32, i32, P(vp)],
+    "scry_hip_rope": [vp, sz, i32, i32, i32, f32, P(vp)],
+    "scry_hip_gather_columns": [vp, i32, i32, i32, i32, P(vp)],
+    "scry_hip_scatter_columns": [vp, vp, i32, i32, i32, i32],
+    "scry_hip_gather_rows": [vp, i32, i32, i32, i32, P(vp)],
+    "scry_hip_apply_causal_mask_and_scale": [vp, i32, f32, f32],
+    "scry_hip_apply_batched_causal_mask_and_scale": [vp, i32, i32, f32, f32],
+    "scry_hip_split_qkv_reshape_heads": [vp, i32, i32, i32, P(vp), P(vp), P(vp)],
+    "scry_hip_reshape_for_heads": [vp, i32, i32, i32, i32, P(vp)],
+    "scry_hip_reshape_from_heads": [vp, i32, i32, i32, i32, P(vp)],
     "scry_hip_llama_new_random": [P(LlamaConfigC), u64, i32, i32, P(vp)],
     "scry_hip_llama_from_safetensors": [P(LlamaConfigC), P(C.c_char_p), i32, i32, P(vp)],
     "scry_hip_llama_free": [vp],
@@ -108,8 +127,6 @@ SIGNATURES = {
     "scry_hip_llama_forward": [vp, vp, i32, vp],
     "scry_hip_llama_prefill": [vp, vp, i32, vp, i32, vp],
     "scry_hip_llama_bench_prefill": [vp, vp, i32, i32, i32, vp, P(f64), P(f64)],
-    "scry_hip_set_decode_mode": [i32],
-    "scry_hip_decode_mode_active": [vp, P(i32)],
     "scry_hip_llama_bench_decode": [vp, vp, i32, i32, i32, vp, P(f64)],
     "scry_hip_llama_bench_decode_sampled": [vp, vp, i32, i32, i32, P(SamplingConfigC), u64, vp, P(f64)],
     "scry_hip_llama_time_projection": [vp, i32, i32, i32, P(f64), P(f64)],

@@ -310,6 +310,122 @@ class HipBackend:
         rng.state = int(st.value)
         return int(out.value)
 
+    # ---- the rest of the trait surface (mod.rs; CPU semantics cpu.rs)
+    @staticmethod
+    def ones(n: int) -> Storage:
+        o = _out()
+        call("scry_hip_ones", n, C.byref(o))
+        return _st(o, n)
+
+    @staticmethod
+    def add_shapes(a, a_shape, b, b_shape, out_shape) -> Storage:
+        """MathBackend::add with broadcasting (shapes as tuples)."""
+        dims = [(C.c_size_t * len(d))(*d) for d in (a_shape, b_shape, out_shape)]
+        o = _out()
+        call("scry_hip_add_broadcast", a.h, dims[0], len(a_shape), b.h, dims[1], len(b_shape),
+             dims[2], len(out_shape), C.byref(o))
+        return _st(o, int(np.prod(out_shape)))
+
+    @staticmethod
+    def add_inplace(dst, src) -> None:
+        call("scry_hip_add_inplace", dst.h, src.h)
+
+    @staticmethod
+    def scaled_softmax(x, scale, rows, cols) -> Storage:
+        o = _out()
+        call("scry_hip_scaled_softmax", x.h, scale, rows, cols, C.byref(o))
+        return _st(o, x.n)
+
+    @staticmethod
+    def layernorm(x, gamma, beta, rows, d, eps=1e-5):
+        """Returns (output, mean [rows], rstd [rows])."""
+        o, mu, rs = _out(), _out(), _out()
+        call("scry_hip_layernorm", x.h, gamma.h, beta.h, rows, d, eps, C.byref(o), C.byref(mu),
+             C.byref(rs))
+        return _st(o, x.n), _st(mu, rows), _st(rs, rows)
+
+    @staticmethod
+    def layernorm_inference(x, gamma, beta, rows, d, eps=1e-5) -> Storage:
+        o = _out()
+        call("scry_hip_layernorm_inference", x.h, gamma.h, beta.h, rows, d, eps, C.byref(o))
+        return _st(o, x.n)
+
+    @staticmethod
+    def gelu(x) -> Storage:
+        o = _out()
+        call("scry_hip_gelu", x.h, C.byref(o))
+        return _st(o, x.n)
+
+    @staticmethod
+    def sum(x) -> float:
+        out = C.c_float()
+        call("scry_hip_sum", x.h, C.byref(out))
+        return float(np.float32(out.value))
+
+    @staticmethod
+    def mul_elementwise(a, b) -> Storage:
+        o = _out()
+        call("scry_hip_mul_elementwise", a.h, b.h, C.byref(o))
+        return _st(o, min(a.n, b.n))
+
+    @staticmethod
+    def concat_rows(a, b, a_rows, b_rows, cols) -> Storage:
+        o = _out()
+        call("scry_hip_concat_rows", a.h, b.h, a_rows, b_rows, cols, C.byref(o))
+        return _st(o, a.n + b.n)
+
+    @staticmethod
+    def rope(x, rows, last_dim, pos, head_dim, theta) -> Storage:
+        """MathBackend::rope on rows of last_dim values (the shape's last axis)."""
+        o = _out()
+        call("scry_hip_rope", x.h, rows, last_dim, pos, head_dim, theta, C.byref(o))
+        return _st(o, x.n)
+
+    @staticmethod
+    def gather_columns(x, rows, total_cols, col_start, col_count) -> Storage:
+        o = _out()
+        call("scry_hip_gather_columns", x.h, rows, total_cols, col_start, col_count, C.byref(o))
+        return _st(o, rows * col_count)
+
+    @staticmethod
+    def scatter_columns(dst, src, rows, total_cols, col_start, col_count) -> None:
+        call("scry_hip_scatter_columns", dst.h, src.h, rows, total_cols, col_start, col_count)
+
+    @staticmethod
+    def gather_rows(x, total_rows, cols, row_start, row_count) -> Storage:
+        o = _out()
+        call("scry_hip_gather_rows", x.h, total_rows, cols, row_start, row_count, C.byref(o))
+        return _st(o, row_count * cols)
+
+    @staticmethod
+    def apply_causal_mask_and_scale(scores, seq, scale, mask_value) -> None:
+        call("scry_hip_apply_causal_mask_and_scale", scores.h, seq, scale, mask_value)
+
+    @staticmethod
+    def apply_batched_causal_mask_and_scale(scores, num_matrices, seq, scale, mask_value) -> None:
+        call("scry_hip_apply_batched_causal_mask_and_scale", scores.h, num_matrices, seq, scale,
+             mask_value)
+
+    @staticmethod
+    def split_qkv_reshape_heads(qkv, seq, n_heads, d_head):
+        q, k, v = _out(), _out(), _out()
+        call("scry_hip_split_qkv_reshape_heads", qkv.h, seq, n_heads, d_head, C.byref(q),
+             C.byref(k), C.byref(v))
+        n = seq * n_heads * d_head
+        return _st(q, n), _st(k, n), _st(v, n)
+
+    @staticmethod
+    def reshape_for_heads(x, batch, seq, n_heads, d_head) -> Storage:
+        o = _out()
+        call("scry_hip_reshape_for_heads", x.h, batch, seq, n_heads, d_head, C.byref(o))
+        return _st(o, batch * seq * n_heads * d_head)
+
+    @staticmethod
+    def reshape_from_heads(x, batch, seq, n_heads, d_head) -> Storage:
+        o = _out()
+        call("scry_hip_reshape_from_heads", x.h, batch, seq, n_heads, d_head, C.byref(o))
+        return _st(o, batch * seq * n_heads * d_head)
+
 
 def init(device: int = 0) -> None:
     HipBackend.init_gpu(device)

@@ -2,6 +2,7 @@
 // storage and the MathBackend methods on the int8 Llama path.  The reference
 // trait methods are static and panic on failure (backend/mod.rs:12-622); here
 // every entry point returns a status code instead.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -902,6 +903,303 @@ int scry_hip_sample_token(scry_buf logits, const scry_sampling_config *cfg, uint
     *out = h.toks[1];
     *rng_state = h.rng;
     return SCRY_OK;
+}
+
+// ------------------------------------------- the rest of the trait surface
+int scry_hip_ones(size_t n, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    SCRY_TRY(new_buf(n, out));
+    return launch_fill_f32((*out)->d, n, 1.f, ctx().stream);
+}
+
+int scry_hip_add_broadcast(scry_buf a, const size_t *a_dims, int a_ndim, scry_buf b, const size_t *b_dims,
+                           int b_ndim, const size_t *out_dims, int out_ndim, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(a, "add");
+    CHECK_BUF(b, "add");
+    if (a_ndim < 1 || b_ndim < 1 || out_ndim < 1 || a_ndim > 6 || b_ndim > 6 || out_ndim > 6 || !a_dims ||
+        !b_dims || !out_dims)
+        return set_error(SCRY_ERR_INVALID, "add: 1 to 6 dimensions per shape (Shape MAX_DIMS)");
+    // Shape::broadcast (tensor/shape.rs): the output shape must be the broadcast of a and b
+    const int nd = a_ndim > b_ndim ? a_ndim : b_ndim;
+    if (out_ndim != nd) return set_error(SCRY_ERR_INVALID, "add: output shape is not the broadcast shape");
+    size_t na = 1, nb = 1;
+    for (int i = 0; i < a_ndim; i++) na *= a_dims[i];
+    for (int i = 0; i < b_ndim; i++) nb *= b_dims[i];
+    for (int i = 0; i < nd; i++) {
+        const size_t da = i < a_ndim ? a_dims[a_ndim - 1 - i] : 1, db = i < b_ndim ? b_dims[b_ndim - 1 - i] : 1;
+        const size_t want = da == db ? da : (da == 1 ? db : (db == 1 ? da : (size_t)-1));
+        if (want == (size_t)-1) return set_error(SCRY_ERR_INVALID, "add: broadcast failed (incompatible shapes)");
+        if (out_dims[nd - 1 - i] != want)
+            return set_error(SCRY_ERR_INVALID, "add: output shape is not the broadcast shape");
+    }
+    if (a->n < na || b->n < nb) return set_error(SCRY_ERR_INVALID, "add: storage shorter than its shape");
+    size_t no = 1;
+    for (int i = 0; i < nd; i++) no *= out_dims[i];
+    SCRY_TRY(new_buf(no, out));
+    return launch_add_bcast(a->d, a_dims, a_ndim, b->d, b_dims, b_ndim, out_dims, out_ndim, (*out)->d,
+                            ctx().stream);
+}
+
+int scry_hip_add_inplace(scry_buf dst, scry_buf src) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(dst, "add_inplace");
+    CHECK_BUF(src, "add_inplace");
+    SCRY_TRY(launch_add_inplace(dst->d, src->d, dst->n < src->n ? dst->n : src->n, ctx().stream));  // zip
+    bf16_stale(dst);
+    return SCRY_OK;
+}
+
+int scry_hip_scaled_softmax(scry_buf x, float scale, int rows, int cols, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "scaled_softmax");
+    if (rows <= 0 || cols <= 0 || x->n != (size_t)rows * cols)
+        return set_error(SCRY_ERR_INVALID, "scaled_softmax: shape mismatch");
+    SCRY_TRY(new_buf(x->n, out));
+    return launch_scaled_softmax(x->d, rows, cols, scale, (*out)->d, ctx().stream);
+}
+
+static int layernorm_common(scry_buf x, scry_buf gamma, scry_buf beta, int rows, int d, float eps, scry_buf *out,
+                            scry_buf *mean, scry_buf *rstd) {
+    CHECK_BUF(x, "layernorm");
+    CHECK_BUF(gamma, "layernorm");
+    CHECK_BUF(beta, "layernorm");
+    if (rows <= 0 || d <= 0 || x->n != (size_t)rows * d || gamma->n < (size_t)d || beta->n < (size_t)d)
+        return set_error(SCRY_ERR_INVALID, "layernorm: shape mismatch");
+    scry_buf o = nullptr, mu = nullptr, rs = nullptr;
+    int rc = new_buf(x->n, &o);
+    if (!rc && mean) rc = new_buf((size_t)rows, &mu);
+    if (!rc && mean) rc = new_buf((size_t)rows, &rs);
+    if (!rc)
+        rc = launch_layernorm(x->d, gamma->d, beta->d, rows, d, eps, o->d, mu ? mu->d : nullptr,
+                              rs ? rs->d : nullptr, ctx().stream);
+    if (rc) {
+        del_buf(o);
+        del_buf(mu);
+        del_buf(rs);
+        return rc;
+    }
+    *out = o;
+    if (mean) {
+        *mean = mu;
+        *rstd = rs;
+    }
+    return SCRY_OK;
+}
+
+int scry_hip_layernorm(scry_buf x, scry_buf gamma, scry_buf beta, int rows, int d, float eps, scry_buf *out,
+                       scry_buf *mean, scry_buf *rstd) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!out || !mean || !rstd) return set_error(SCRY_ERR_INVALID, "layernorm: null output handle");
+    return layernorm_common(x, gamma, beta, rows, d, eps, out, mean, rstd);
+}
+
+int scry_hip_layernorm_inference(scry_buf x, scry_buf gamma, scry_buf beta, int rows, int d, float eps,
+                                 scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!out) return set_error(SCRY_ERR_INVALID, "layernorm_inference: null output handle");
+    return layernorm_common(x, gamma, beta, rows, d, eps, out, nullptr, nullptr);
+}
+
+int scry_hip_gelu(scry_buf x, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "gelu");
+    SCRY_TRY(new_buf(x->n, out));
+    return launch_gelu(x->d, x->n, (*out)->d, ctx().stream);
+}
+
+int scry_hip_sum(scry_buf x, float *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "sum");
+    if (!out) return set_error(SCRY_ERR_INVALID, "sum: null output");
+    char *blk = nullptr;
+    SCRY_TRY(dev_alloc((void **)&blk, 16 + sizeof(double) * (size_t)sum_partials(x->n)));
+    float *d_out = (float *)blk;
+    int rc = launch_sum(x->d, x->n, (double *)(blk + 16), d_out, ctx().stream);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(out, d_out, sizeof(float), hipMemcpyDeviceToHost, ctx().stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx().stream);
+        if (e != hipSuccess) rc = hip_fail(e, "sum readback", __FILE__, __LINE__);
+    }
+    dev_free(blk);
+    return rc;
+}
+
+int scry_hip_mul_elementwise(scry_buf a, scry_buf b, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(a, "mul_elementwise");
+    CHECK_BUF(b, "mul_elementwise");
+    const size_t n = a->n < b->n ? a->n : b->n;  // zip
+    SCRY_TRY(new_buf(n, out));
+    return launch_mul(a->d, b->d, n, (*out)->d, ctx().stream);
+}
+
+int scry_hip_concat_rows(scry_buf a, scry_buf b, int a_rows, int b_rows, int cols, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(a, "concat_rows");
+    CHECK_BUF(b, "concat_rows");
+    if (a_rows < 0 || b_rows < 0 || cols < 0) return set_error(SCRY_ERR_INVALID, "concat_rows: negative shape");
+    // cpu.rs:526-539: the whole of a, then the whole of b
+    SCRY_TRY(new_buf(a->n + b->n, out));
+    if (a->n)
+        SCRY_HIP(hipMemcpyAsync((*out)->d, a->d, sizeof(float) * a->n, hipMemcpyDeviceToDevice, ctx().stream));
+    if (b->n)
+        SCRY_HIP(hipMemcpyAsync((*out)->d + a->n, b->d, sizeof(float) * b->n, hipMemcpyDeviceToDevice,
+                                ctx().stream));
+    return SCRY_OK;
+}
+
+int scry_hip_rope(scry_buf x, size_t rows, int last_dim, int pos, int head_dim, float theta, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "rope");
+    if (last_dim <= 0 || head_dim <= 0 || pos < 0 || x->n != rows * (size_t)last_dim)
+        return set_error(SCRY_ERR_INVALID, "rope: shape mismatch");
+    // cpu.rs:612-624: freq = 1 / theta^(2i / head_dim), angle = pos * freq,
+    // cos / sin in f64 (glibc, as the reference) rounded to f32
+    const int np = head_dim / 2;
+    std::vector<float2> cs((size_t)(np > 0 ? np : 1));
+    const double th = (double)theta;
+    for (int i = 0; i < np; i++) {
+        const double freq = 1.0 / std::pow(th, 2.0 * (double)i / (double)head_dim);
+        const double ang = (double)pos * freq;
+        cs[i] = make_float2((float)std::cos(ang), (float)std::sin(ang));
+    }
+    float2 *d_cs = nullptr;
+    SCRY_TRY(dev_alloc((void **)&d_cs, sizeof(float2) * cs.size()));
+    int rc = new_buf(x->n, out);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(d_cs, cs.data(), sizeof(float2) * cs.size(), hipMemcpyHostToDevice,
+                                      ctx().stream);
+        rc = e == hipSuccess ? SCRY_OK : hip_fail(e, "rope table upload", __FILE__, __LINE__);
+        if (!rc) rc = launch_rope_row(x->d, rows, last_dim, head_dim, d_cs, (*out)->d, ctx().stream);
+        if (!rc) rc = sync();  // the table is freed below
+    }
+    dev_free(d_cs);
+    return rc;
+}
+
+int scry_hip_gather_columns(scry_buf x, int rows, int total_cols, int col_start, int col_count, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "gather_columns");
+    if (rows < 0 || col_start < 0 || col_count < 0 || col_start + col_count > total_cols ||
+        x->n < (size_t)rows * total_cols)
+        return set_error(SCRY_ERR_RANGE, "gather_columns: columns [%d, %d) outside %d", col_start,
+                         col_start + col_count, total_cols);
+    SCRY_TRY(new_buf((size_t)rows * col_count, out));
+    return launch_gather_cols(x->d, (size_t)rows, total_cols, col_start, col_count, (*out)->d, ctx().stream);
+}
+
+int scry_hip_scatter_columns(scry_buf dst, scry_buf src, int rows, int total_cols, int col_start, int col_count) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(dst, "scatter_columns");
+    CHECK_BUF(src, "scatter_columns");
+    if (rows < 0 || col_start < 0 || col_count < 0 || col_start + col_count > total_cols ||
+        dst->n < (size_t)rows * total_cols || src->n < (size_t)rows * col_count)
+        return set_error(SCRY_ERR_RANGE, "scatter_columns: columns [%d, %d) outside %d", col_start,
+                         col_start + col_count, total_cols);
+    SCRY_TRY(launch_scatter_cols_add(dst->d, src->d, (size_t)rows, total_cols, col_start, col_count, ctx().stream));
+    bf16_stale(dst);
+    return SCRY_OK;
+}
+
+int scry_hip_gather_rows(scry_buf x, int total_rows, int cols, int row_start, int row_count, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(x, "gather_rows");
+    if (cols < 0 || row_start < 0 || row_count < 0 || x->n < (size_t)(row_start + row_count) * cols)
+        return set_error(SCRY_ERR_RANGE, "gather_rows: rows [%d, %d) outside the storage", row_start,
+                         row_start + row_count);
+    (void)total_rows;  // mod.rs:360 ignores it as well
+    const size_t n = (size_t)row_count * cols;
+    SCRY_TRY(new_buf(n, out));
+    if (n)
+        SCRY_HIP(hipMemcpyAsync((*out)->d, x->d + (size_t)row_start * cols, sizeof(float) * n,
+                                hipMemcpyDeviceToDevice, ctx().stream));
+    return SCRY_OK;
+}
+
+int scry_hip_apply_causal_mask_and_scale(scry_buf scores, int seq, float scale, float mask_value) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(scores, "apply_causal_mask_and_scale");
+    if (seq < 0 || scores->n < (size_t)seq * seq)
+        return set_error(SCRY_ERR_INVALID, "apply_causal_mask_and_scale: shape mismatch");
+    SCRY_TRY(launch_causal_mask(scores->d, seq ? 1 : 0, seq, scale, mask_value, ctx().stream));
+    bf16_stale(scores);
+    return SCRY_OK;
+}
+
+int scry_hip_apply_batched_causal_mask_and_scale(scry_buf scores, int num_matrices, int seq, float scale,
+                                                 float mask_value) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(scores, "apply_batched_causal_mask_and_scale");
+    if (seq <= 0 || num_matrices < 0) return set_error(SCRY_ERR_INVALID, "apply_batched_causal_mask_and_scale: shape");
+    // mod.rs:602-606: every whole [seq, seq] matrix of the storage (num_matrices unused)
+    SCRY_TRY(launch_causal_mask(scores->d, scores->n / ((size_t)seq * seq), seq, scale, mask_value, ctx().stream));
+    bf16_stale(scores);
+    return SCRY_OK;
+}
+
+int scry_hip_split_qkv_reshape_heads(scry_buf qkv, int seq, int n_heads, int d_head, scry_buf *q, scry_buf *k,
+                                     scry_buf *v) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    CHECK_BUF(qkv, "split_qkv_reshape_heads");
+    if (!q || !k || !v) return set_error(SCRY_ERR_INVALID, "split_qkv_reshape_heads: null output handle");
+    const size_t hl = (size_t)seq * n_heads * d_head;
+    if (seq < 0 || n_heads < 0 || d_head < 0 || qkv->n < 3 * hl)
+        return set_error(SCRY_ERR_INVALID, "split_qkv_reshape_heads: shape mismatch");
+    scry_buf bq = nullptr, bk = nullptr, bv = nullptr;
+    int rc = new_buf(hl, &bq);
+    if (!rc) rc = new_buf(hl, &bk);
+    if (!rc) rc = new_buf(hl, &bv);
+    if (!rc) rc = launch_split_qkv(qkv->d, seq, n_heads, d_head, bq->d, bk->d, bv->d, ctx().stream);
+    if (rc) {
+        del_buf(bq);
+        del_buf(bk);
+        del_buf(bv);
+        return rc;
+    }
+    *q = bq;
+    *k = bk;
+    *v = bv;
+    return SCRY_OK;
+}
+
+static int reshape_heads(scry_buf x, int batch, int seq, int n_heads, int d_head, int dir, scry_buf *out) {
+    CHECK_BUF(x, "reshape_heads");
+    const size_t n = (size_t)batch * seq * n_heads * d_head;
+    if (batch < 0 || seq < 0 || n_heads < 0 || d_head < 0 || x->n < n)
+        return set_error(SCRY_ERR_INVALID, "reshape_heads: shape mismatch");
+    if (batch == 1 && seq == 1) return scry_hip_clone_storage(x, out);  // mod.rs:449-451, 492-494
+    SCRY_TRY(new_buf(n, out));
+    return launch_reshape_heads(x->d, batch, seq, n_heads, d_head, dir, (*out)->d, ctx().stream);
+}
+
+int scry_hip_reshape_for_heads(scry_buf x, int batch, int seq, int n_heads, int d_head, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    return reshape_heads(x, batch, seq, n_heads, d_head, 0, out);
+}
+
+int scry_hip_reshape_from_heads(scry_buf x, int batch, int seq, int n_heads, int d_head, scry_buf *out) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    return reshape_heads(x, batch, seq, n_heads, d_head, 1, out);
 }
 
 }  // extern "C"

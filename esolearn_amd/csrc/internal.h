@@ -215,58 +215,27 @@ int launch_argmax(const float *x, int64_t n, int64_t *out, hipStream_t s);
 int launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
 int launch_fill_u32(unsigned int *p, size_t n, unsigned int v, hipStream_t s);
 
-// decode.hip -- persistent decode step (one launch per token, every layer)
-struct DecLayer {
-    const uint8_t *w[4];        // packed qkv, o, fused gate/up, down
-    float scale[5];             // qkv, o, gate, up, down
-    const float *norm_in, *norm_post;
-    float *k_cache, *v_cache;   // [max_seq][kv_dim]
-};
-
-struct DecArgs {
-    const DecLayer *layers;
-    int L, h, qd, kvd, qkv_rows, ffn, V;
-    int n_heads, n_kv, hd, ns;  // ns: attention splits per query head
-    int kp_h, kp_q, kp_f;       // packed row strides for k = h, q_dim, ffn
-    int nch_max, part_cap;      // LDS activation chunks / partial slots per workgroup
-    int qkv_pairs;              // LDS RoPE slots: qkv row pairs per workgroup (multiple of 8)
-    const uint8_t *w_lm;
-    float s_lm;
-    const float *norm_final;
-    const float *embed;
-    int64_t *tokens;
-    DevState *state;
-    int64_t *argmax_out;
-    int advance;
-    const float2 *rope_cs;
-    float q_scale, eps;
-    // Activations exchanged between workgroups (floats): per layer ws_stride
-    // floats at these offsets.
-    float *ws;
-    size_t ws_stride;
-    int o_xq, o_xk, o_xv, o_xa, o_xo, o_xg, o_xd, o_apo, o_apm;
-    // Attention split partials: O at o_apo + head*apo_hs + split*hd, (M, L) at
-    // o_apm + head*64 + 2*split.  Each head's block starts on its own 256-byte
-    // boundary: a head's merge reads its block once its splits are published,
-    // and an L2 line read early must not hold another head's later writes.
-    int apo_hs;
-    unsigned *lm_part;          // [n_wg][8] LM-head argmax partials
-    float *logits;
-    // Completion counters: [5L+1][8] per (stage, XCD), then [L][n_heads] per
-    // head; after launch number `tag` they hold tag x (workgroups counted).
-    unsigned *ctr;
-    int *abort_flag;
-    unsigned tag;               // this launch's number (1, 2, ...)
-    unsigned spin_limit;
-};
-
-constexpr int DEC_THREADS = 512;
-// Dynamic LDS bytes for a configuration (before the one-workgroup-per-CU floor).
-size_t decode_lds_bytes(int nch_max, int part_cap, int h, int qkv_pairs);
-// Checks that the kernel for this head_dim can run n_wg co-resident workgroups
-// with `lds` bytes each; sets the LDS attribute.
-int decode_prepare(int hd, size_t lds, int n_wg);
-int launch_decode(const DecArgs &a, int n_wg, size_t lds, hipStream_t s);
+// ops.hip -- the rest of the trait surface
+int launch_layernorm(const float *x, const float *g, const float *b, int rows, int d, float eps, float *out,
+                     float *mean, float *rstd, hipStream_t s);
+int launch_gelu(const float *x, size_t n, float *out, hipStream_t s);
+int sum_partials(size_t n);  // f64 partials launch_sum needs
+int launch_sum(const float *x, size_t n, double *part, float *out, hipStream_t s);
+int launch_mul(const float *a, const float *b, size_t n, float *out, hipStream_t s);
+int launch_rope_row(const float *x, size_t rows, int last_dim, int head_dim, const float2 *cs, float *out,
+                    hipStream_t s);
+int launch_gather_cols(const float *x, size_t rows, int total, int start, int count, float *out, hipStream_t s);
+int launch_scatter_cols_add(float *dst, const float *src, size_t rows, int total, int start, int count,
+                            hipStream_t s);
+int launch_add_bcast(const float *a, const size_t *a_dims, int a_ndim, const float *b, const size_t *b_dims,
+                     int b_ndim, const size_t *o_dims, int o_ndim, float *out, hipStream_t s);
+int launch_add_inplace(float *d, const float *src, size_t n, hipStream_t s);
+int launch_scaled_softmax(const float *x, int rows, int cols, float scale, float *out, hipStream_t s);
+int launch_causal_mask(float *sc, size_t n_mat, int seq, float scale, float mask_value, hipStream_t s);
+int launch_split_qkv(const float *qkv, int seq, int n_heads, int d_head, float *q, float *k, float *v,
+                     hipStream_t s);
+int launch_reshape_heads(const float *x, int batch, int seq, int n_heads, int d_head, int dir, float *out,
+                         hipStream_t s);
 
 // prefill.hip -- batched prefill (GEMMs on the matrix cores)
 constexpr int PF_MAX_SEQS = 16;

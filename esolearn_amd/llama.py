@@ -18,16 +18,6 @@ from ._lib import LlamaConfigC, SamplingConfigC, call, load
 QUANT_PER_TENSOR = 0
 QUANT_BLOCK32 = 1
 T_EMBED, T_QKV, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(7)
-DECODE_KERNELS = 0     # captured per-kernel graph (default)
-DECODE_PERSISTENT = 1  # persistent decode kernel where the configuration allows it
-
-
-def set_decode_mode(mode: int) -> None:
-    """Process-wide choice of the decode-step implementation (both give the
-    same tokens; a backend choice with no counterpart in the reference)."""
-    call("scry_hip_set_decode_mode", mode)
-
-
 @dataclass
 class LlamaConfig:
     """LlamaConfig (llama.rs:20-34)."""
@@ -243,12 +233,6 @@ class LlamaModel:
         call("scry_hip_llama_bench_prefill", self.h, p.ctypes.data, n_seq, n_prompt, decode_steps,
              toks.ctypes.data, C.byref(pm), C.byref(dm))
         return pm.value, dm.value, toks
-
-    def decode_persistent(self) -> bool:
-        """True when this model's decode steps run on the persistent kernel."""
-        v = C.c_int()
-        call("scry_hip_decode_mode_active", self.h, C.byref(v))
-        return bool(v.value)
 
     def bench_decode(self, prompt, warmup: int, steps: int):
         p = np.ascontiguousarray(prompt, dtype=np.int64)

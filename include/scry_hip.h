@@ -175,6 +175,64 @@ int scry_hip_normal_vec(uint64_t *rng_state, size_t n, float mean, float std_dev
 int scry_hip_sample_token(scry_buf logits, const scry_sampling_config *cfg, uint64_t *rng_state,
                           int64_t *out);
 
+/* ------------------------------------ the rest of the trait surface
+ * Every other required method of DeviceBackend / MathBackend, and the
+ * defaulted ones whose default body is a host round trip (to_vec, loop,
+ * from_vec), run on the device.  Arithmetic as the CPU backend's (cpu.rs). */
+/* DeviceBackend::ones (mod.rs:24; cpu.rs:37-39) */
+int scry_hip_ones(size_t n, scry_buf *out);
+/* MathBackend::add with broadcasting (mod.rs:89-95; cpu.rs:94-188): shapes as
+ * dims arrays (1 to 6 dims, Shape MAX_DIMS); out_dims must be
+ * Shape::broadcast(a, b) (ops::add, ops.rs:38-42), else SCRY_ERR_INVALID (the
+ * reference panics "broadcast failed"). */
+int scry_hip_add_broadcast(scry_buf a, const size_t *a_dims, int a_ndim, scry_buf b, const size_t *b_dims,
+                           int b_ndim, const size_t *out_dims, int out_ndim, scry_buf *out);
+/* MathBackend::add_inplace (mod.rs:99-107; cpu.rs:88-92): dst[i] += src[i] over
+ * the shorter of the two */
+int scry_hip_add_inplace(scry_buf dst, scry_buf src);
+/* MathBackend::scaled_softmax (mod.rs:114-117; cpu.rs:300-334): rows x cols */
+int scry_hip_scaled_softmax(scry_buf x, float scale, int rows, int cols, scry_buf *out);
+/* MathBackend::layernorm (mod.rs:121-127; cpu.rs:416-475): rows x d; also the
+ * per-row mean and rstd [rows] */
+int scry_hip_layernorm(scry_buf x, scry_buf gamma, scry_buf beta, int rows, int d, float eps, scry_buf *out,
+                       scry_buf *mean, scry_buf *rstd);
+/* MathBackend::layernorm_inference (mod.rs:130-139; cpu.rs:368-414) */
+int scry_hip_layernorm_inference(scry_buf x, scry_buf gamma, scry_buf beta, int rows, int d, float eps,
+                                 scry_buf *out);
+/* MathBackend::gelu, tanh approximation (mod.rs:142; cpu.rs:477-483, 1110-1116) */
+int scry_hip_gelu(scry_buf x, scry_buf *out);
+/* MathBackend::sum (mod.rs:153; cpu.rs:500-503): f64 sum rounded to f32 */
+int scry_hip_sum(scry_buf x, float *out);
+/* MathBackend::mul_elementwise (mod.rs:156; cpu.rs:505-507) */
+int scry_hip_mul_elementwise(scry_buf a, scry_buf b, scry_buf *out);
+/* MathBackend::concat_rows (mod.rs:162-168; cpu.rs:526-539): a then b */
+int scry_hip_concat_rows(scry_buf a, scry_buf b, int a_rows, int b_rows, int cols, scry_buf *out);
+/* MathBackend::rope (mod.rs:194-200; cpu.rs:601-633): rows of last_dim values
+ * (the shape's last axis), heads of head_dim inside each row, position pos,
+ * frequencies 1/theta^(2i/head_dim) */
+int scry_hip_rope(scry_buf x, size_t rows, int last_dim, int pos, int head_dim, float theta, scry_buf *out);
+/* MathBackend::gather_columns (mod.rs:316-331): [rows, total_cols] ->
+ * [rows, col_count] from col_start; llama.rs:389-391 calls it every layer */
+int scry_hip_gather_columns(scry_buf x, int rows, int total_cols, int col_start, int col_count, scry_buf *out);
+/* MathBackend::scatter_columns (mod.rs:334-350): additive, in place */
+int scry_hip_scatter_columns(scry_buf dst, scry_buf src, int rows, int total_cols, int col_start, int col_count);
+/* MathBackend::gather_rows (mod.rs:353-365) */
+int scry_hip_gather_rows(scry_buf x, int total_rows, int cols, int row_start, int row_count, scry_buf *out);
+/* MathBackend::apply_causal_mask_and_scale (mod.rs:384-401): in place */
+int scry_hip_apply_causal_mask_and_scale(scry_buf scores, int seq, float scale, float mask_value);
+/* MathBackend::apply_batched_causal_mask_and_scale (mod.rs:595-621): every
+ * whole [seq, seq] matrix of the storage, in place */
+int scry_hip_apply_batched_causal_mask_and_scale(scry_buf scores, int num_matrices, int seq, float scale,
+                                                 float mask_value);
+/* MathBackend::split_qkv_reshape_heads (mod.rs:408-438): [seq, 3*d_model] ->
+ * three [n_heads, seq, d_head] */
+int scry_hip_split_qkv_reshape_heads(scry_buf qkv, int seq, int n_heads, int d_head, scry_buf *q, scry_buf *k,
+                                     scry_buf *v);
+/* MathBackend::reshape_for_heads (mod.rs:441-467): [B*S, H*d] -> [B*H, S, d] */
+int scry_hip_reshape_for_heads(scry_buf x, int batch, int seq, int n_heads, int d_head, scry_buf *out);
+/* MathBackend::reshape_from_heads (mod.rs:484-510): the inverse */
+int scry_hip_reshape_from_heads(scry_buf x, int batch, int seq, int n_heads, int d_head, scry_buf *out);
+
 /* ------------------------------------------------------ Llama (llama.rs) */
 typedef struct {
     int32_t vocab_size, hidden_size, intermediate_size, n_layers, n_heads, n_kv_heads,
@@ -250,9 +308,9 @@ int scry_hip_llama_forward_with_cache(scry_llama m, scry_kv_cache c, int64_t tok
 
 /* generate() with temperature 0 (generate.rs:51-89, 92-98): the prompt is fed
  * token by token through the cache path, then greedy tokens follow.  The whole
- * loop runs on the device (one persistent-kernel launch, or one replay of the
- * captured per-kernel graph, per token); only the token ids come back.  Writes max(1, max_tokens) ids to out_tokens and
- * the count to *n_out.  step_logits (optional) receives [n_out, V] logits. */
+ * loop runs on the device (one replay of the captured per-kernel step graph
+ * per token); only the token ids come back.  Writes max(1, max_tokens) ids to
+ * out_tokens and the count to *n_out.  step_logits (optional) receives [n_out, V] logits. */
 int scry_hip_llama_generate_greedy(scry_llama m, const int64_t *prompt, int n_prompt,
                                    int max_tokens, int64_t *out_tokens, int *n_out,
                                    float *step_logits);
@@ -295,20 +353,6 @@ int scry_hip_llama_forward(scry_llama m, const int64_t *tokens, int seq, float *
  * distinct caches, head_dim <= 128. */
 int scry_hip_llama_prefill(scry_llama m, scry_kv_cache *caches, int n_seq, const int64_t *tokens,
                            int seq, float *last_logits);
-
-/* Decode-step implementation (no counterpart in the reference: a backend
- * choice).  SCRY_DECODE_KERNELS (the default) runs each token as one replay of
- * the captured per-kernel graph.  SCRY_DECODE_PERSISTENT runs each token as
- * one launch of the persistent decode kernel where the configuration allows it
- * (per-tensor int8 scales, head_dim <= 256, n_heads <= CU count) and as the
- * per-kernel graph otherwise.  Both give the same tokens; logits agree to
- * float rounding.  Process-wide; the environment variable
- * SCRY_HIP_DECODE=persistent selects the persistent kernel at start. */
-enum { SCRY_DECODE_KERNELS = 0, SCRY_DECODE_PERSISTENT = 1 };
-int scry_hip_set_decode_mode(int mode);
-/* *persistent = 1 when decode steps of this model run on the persistent kernel
- * under the current mode. */
-int scry_hip_decode_mode_active(scry_llama m, int *persistent);
 
 /* ------------------------------------------------ measurement helpers */
 /* Decode-step session for benchmarks: binds a model and cache, feeds the

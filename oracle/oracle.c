@@ -1247,3 +1247,375 @@ done:
     orc_cache_free(c);
     return rc;
 }
+
+/* ------------------------------------------------------------------------
+ * Layer-major evaluation of the cache path, for parity runs at the
+ * Llama-2-7B shape.  n tokens go through orc_llama_forward_with_cache one
+ * after another (llama.rs:744-763) -- but computed layer by layer over all n
+ * rows, so each int8 weight is read once per call instead of once per token.
+ * Every element sees the same operations in the same order as in the
+ * token-by-token function, so results are bit-identical (tested against it):
+ *   - matmul_i8_f32 rows are independent; c[i][j] accumulates
+ *     f32(f64(a) * (f64(q) * f64(scale))) in increasing p.  It is evaluated as
+ *     f32((f64(a) * f64(scale)) * f64(q)): q*scale (8 x 24 bits) and a*scale
+ *     (24 x 24 bits) are both exact in f64, so the single rounded f64 product
+ *     is the same number;
+ *   - row r's attention reads the cache rows 0 .. len+r, exactly those the
+ *     token-by-token call sees, with gemv_trans_b / softmax / gemv_into
+ *     arithmetic (cpu.rs:825-871, 336-366) on the cache rows in place;
+ *   - rmsnorm, RoPE, scale, swiglu and add are per row.
+ * Per-tensor int8 (forward mode 1) only.
+ * ---------------------------------------------------------------------- */
+#define MM_RB 8
+#define MM_JW 256
+#define MM_PD 24
+
+__attribute__((target_clones("avx512f", "avx2", "default")))
+static void mm_tile(const float *a, int k, int rows, const int8_t *q, int n, int j0, int jw,
+                    double sd, float *c) {
+    float acc[MM_RB][MM_JW];
+    double qd[MM_JW];
+    for (int i = 0; i < rows; i++)
+        for (int j = 0; j < jw; j++) acc[i][j] = 0.0f;
+    for (int p = 0; p < k; p++) {
+        const int8_t *qr = q + (size_t)p * n + j0;
+        if (p + MM_PD < k)  /* rows are n bytes apart: no hardware prefetch */
+            for (int j = 0; j < jw; j += 64) __builtin_prefetch(qr + (size_t)MM_PD * n + j);
+        for (int j = 0; j < jw; j++) qd[j] = (double)qr[j];
+        for (int i = 0; i < rows; i++) {
+            const double asd = (double)a[(size_t)i * k + p] * sd;
+            float *ar = acc[i];
+            for (int j = 0; j < jw; j++) ar[j] += (float)(asd * qd[j]);
+        }
+    }
+    for (int i = 0; i < rows; i++) memcpy(c + (size_t)i * n + j0, acc[i], sizeof(float) * (size_t)jw);
+}
+
+/* matmul_i8_f32 (cpu.rs:1128-1160 per-element order) of a [m,k] by q [k,n] */
+static void mm_i8(const float *a, int m, int k, const int8_t *q, int n, float scale, float *c) {
+    const double sd = (double)scale;
+    const int nj = (n + MM_JW - 1) / MM_JW, ni = (m + MM_RB - 1) / MM_RB;
+#pragma omp parallel for schedule(dynamic, 1) collapse(2) num_threads(NT) if (PAR_IF)
+    for (int jc = 0; jc < nj; jc++)
+        for (int ib = 0; ib < ni; ib++) {
+            const int j0 = jc * MM_JW, jw = n - j0 < MM_JW ? n - j0 : MM_JW;
+            const int i0 = ib * MM_RB, rows = m - i0 < MM_RB ? m - i0 : MM_RB;
+            mm_tile(a + (size_t)i0 * k, k, rows, q, n, j0, jw, sd, c + (size_t)i0 * n);
+        }
+}
+
+/* One query head against cache rows 0..L-1 (row stride kvd, head offset off):
+ * gather_reshape_repeat_kv + gemv_trans_b (scores) + softmax + gemv_into,
+ * with the cache read in place. */
+static void attn_head(const float *qh, const float *K, const float *Vc, int kvd, int off, int L,
+                      int hd, float *sc, float *pr, float *out) {
+    const int k4 = hd & ~3;
+    for (int j = 0; j < L; j++) {
+        const float *row = K + (size_t)j * kvd + off;
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        for (int p = 0; p < k4; p += 4) {
+            a0 += qh[p] * row[p];
+            a1 += qh[p + 1] * row[p + 1];
+            a2 += qh[p + 2] * row[p + 2];
+            a3 += qh[p + 3] * row[p + 3];
+        }
+        float acc = a0 + a1 + a2 + a3;
+        for (int p = k4; p < hd; p++) acc += qh[p] * row[p];
+        sc[j] = acc;
+    }
+    orc_softmax(sc, 1, L, pr);
+    for (int j = 0; j < hd; j++) out[j] = 0.0f;
+    const int L4 = L & ~3;
+    for (int p = 0; p < L4; p += 4) {
+        const float v0 = pr[p], v1 = pr[p + 1], v2 = pr[p + 2], v3 = pr[p + 3];
+        const float *r0 = Vc + (size_t)p * kvd + off, *r1 = r0 + kvd, *r2 = r1 + kvd, *r3 = r2 + kvd;
+        for (int j = 0; j < hd; j++) out[j] += v0 * r0[j] + v1 * r1[j] + v2 * r2[j] + v3 * r3[j];
+    }
+    for (int p = L4; p < L; p++) {
+        const float v = pr[p];
+        const float *r = Vc + (size_t)p * kvd + off;
+        for (int j = 0; j < hd; j++) out[j] += v * r[j];
+    }
+}
+
+/* the LM head [V,h] as q [h,V] (same values; the kernel above reads [k,n]) */
+static int8_t *lm_transposed(const orc_llama *m) {
+    const int h = m->cfg.hidden_size, V = m->cfg.vocab_size;
+    int8_t *t = (int8_t *)malloc((size_t)h * V);
+    if (!t) return NULL;
+#pragma omp parallel for schedule(static) num_threads(NT) if (PAR_IF)
+    for (int p = 0; p < h; p++)
+        for (int j = 0; j < V; j++) t[(size_t)p * V + j] = m->lm.q[(size_t)j * h + p];
+    return t;
+}
+
+static int fwd_seq(const orc_llama *m, orc_cache *c, const int8_t *lm_kn, const int64_t *tokens, int n,
+                   int pos0, int n_logits, float *logits) {
+    const orc_llama_config *cf = &m->cfg;
+    const int h = cf->hidden_size, V = cf->vocab_size, ffn = cf->intermediate_size;
+    const int nh = cf->n_heads, nkv = cf->n_kv_heads, hd = m->hd, nrep = nh / nkv;
+    const int qd = m->q_dim, kvd = m->kv_dim, qkvd = m->qkv_dim;
+    if (n <= 0 || n_logits < 0 || n_logits > n) return -4;
+    for (int l = 0; l < cf->n_layers; l++) {
+        for (int t = 0; t < 5; t++)
+            if (!m->proj[(size_t)l * 5 + t].q) return -3;
+        if (c->len[l] + n > c->max_seq) return -2;
+    }
+    if (n_logits && !m->lm.q) return -3;
+    if (n_logits && m->lm.tb && !lm_kn) return -3;
+    const size_t N = (size_t)n;
+    float *x = ALLOC(N * h), *xn = ALLOC(N * h), *qkv = ALLOC(N * qkvd), *qs = ALLOC(N * qd),
+          *att = ALLOC(N * qd), *proj = ALLOC(N * h), *g = ALLOC(N * ffn), *u = ALLOC(N * ffn),
+          *act = ALLOC(N * ffn);
+    const float qscale = (float)(1.0 / sqrt((double)hd));
+    int rc = orc_embedding(m->embed, tokens, n, V, h, x);
+    if (rc != 0) goto done;
+    for (int l = 0; l < cf->n_layers; l++) {
+        const orc_proj *P = m->proj + (size_t)l * 5;
+        orc_rmsnorm(x, norm_w(m, 0, l), n, h, m->norm_eps, xn);
+        mm_i8(xn, n, h, P[0].q, qkvd, P[0].s, qkv);
+        const int base = c->len[l];
+        float *Kc = c->k[l], *Vc = c->v[l];
+#pragma omp parallel num_threads(NT) if (PAR_IF && n > 1)
+        {
+            float *qr = ALLOC(qd), *kr = ALLOC(kvd);
+#pragma omp for schedule(static)
+            for (int r = 0; r < n; r++) {
+                const float *row = qkv + (size_t)r * qkvd;
+                orc_rope_with_freqs_preloaded(row, 1, nh, hd, pos0 + r, m->freqs, qr);
+                orc_scale(qr, (size_t)qd, qscale, qs + (size_t)r * qd);
+                orc_rope_with_freqs_preloaded(row + qd, 1, nkv, hd, pos0 + r, m->freqs, kr);
+                memcpy(Kc + (size_t)(base + r) * kvd, kr, sizeof(float) * kvd);
+                memcpy(Vc + (size_t)(base + r) * kvd, row + qd + kvd, sizeof(float) * kvd);
+            }
+            free(qr);
+            free(kr);
+        }
+        c->len[l] = base + n;
+#pragma omp parallel num_threads(NT) if (PAR_IF)
+        {
+            float *sc = ALLOC(base + n), *pr = ALLOC(base + n);
+#pragma omp for schedule(dynamic, 4) collapse(2)
+            for (int r = 0; r < n; r++)
+                for (int hh = 0; hh < nh; hh++)
+                    attn_head(qs + (size_t)r * qd + (size_t)hh * hd, Kc, Vc, kvd, (hh / nrep) * hd,
+                              base + r + 1, hd, sc, pr, att + (size_t)r * qd + (size_t)hh * hd);
+            free(sc);
+            free(pr);
+        }
+        mm_i8(att, n, qd, P[1].q, h, P[1].s, proj);
+        orc_add(x, proj, N * h, x);
+        orc_rmsnorm(x, norm_w(m, 1, l), n, h, m->norm_eps, xn);
+        mm_i8(xn, n, h, P[2].q, ffn, P[2].s, g);
+        mm_i8(xn, n, h, P[3].q, ffn, P[3].s, u);
+        orc_swiglu(g, u, N * ffn, act);
+        mm_i8(act, n, ffn, P[4].q, h, P[4].s, proj);
+        orc_add(x, proj, N * h, x);
+    }
+    if (n_logits) {
+        const int r0 = n - n_logits;
+        orc_rmsnorm(x + (size_t)r0 * h, norm_w(m, 2, 0), n_logits, h, m->norm_eps, xn);
+        mm_i8(xn, n_logits, h, m->lm.tb ? lm_kn : m->lm.q, V, m->lm.s, logits);
+    }
+done:
+    free(x); free(xn); free(qkv); free(qs); free(att); free(proj); free(g); free(u); free(act);
+    return rc;
+}
+
+int orc_llama_forward_cache_seq(const orc_llama *m, orc_cache *c, const int64_t *tokens, int n,
+                                int pos0, int n_logits, float *logits) {
+    int8_t *lm_kn = (n_logits > 0 && m->lm.tb && m->lm.q) ? lm_transposed(m) : NULL;
+    int rc = fwd_seq(m, c, lm_kn, tokens, n, pos0, n_logits, logits);
+    free(lm_kn);
+    return rc;
+}
+
+/* orc_generate_greedy in mode 1, with the prompt run layer-major (one call)
+ * and each generated token through the same layer-major code: the same
+ * tokens and bit-identical step logits. */
+int orc_generate_greedy_fast(const orc_llama *m, const int64_t *prompt, int n_prompt, int max_tokens,
+                             int64_t *out_tokens, float *step_logits) {
+    if (n_prompt <= 0) return -1;
+    const int V = m->cfg.vocab_size;
+    orc_cache *c = orc_cache_new(m, n_prompt + max_tokens);
+    int8_t *lm_kn = (m->lm.tb && m->lm.q) ? lm_transposed(m) : NULL;
+    float *lg = ALLOC(V);
+    int ng = 0;
+    int rc = fwd_seq(m, c, lm_kn, prompt, n_prompt, 0, 1, lg);
+    if (rc != 0) goto done;
+    if (step_logits) memcpy(step_logits, lg, sizeof(float) * V);
+    out_tokens[ng++] = orc_argmax(lg, V);
+    for (int i = 1; i < max_tokens; i++) {
+        if ((rc = fwd_seq(m, c, lm_kn, &out_tokens[ng - 1], 1, n_prompt + i - 1, 1, lg)) != 0) goto done;
+        if (step_logits) memcpy(step_logits + (size_t)ng * V, lg, sizeof(float) * V);
+        out_tokens[ng++] = orc_argmax(lg, V);
+    }
+    rc = ng;
+done:
+    free(lg);
+    free(lm_kn);
+    orc_cache_free(c);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------
+ * The rest of the trait surface (cpu.rs), for the device exports of the same
+ * names.
+ * ---------------------------------------------------------------------- */
+/* cpu.rs:416-475 layernorm (layernorm_inference, 368-414, is the same output):
+ * per row f64 mean (sequential sum / d), f64 variance of (x - mean),
+ * rstd = 1 / sqrt(var + eps); out = f32((x - mean) * rstd * gamma + beta). */
+void orc_layernorm(const float *x, const float *gamma, const float *beta, int rows, int d, float eps,
+                   float *out, float *mean_out, float *rstd_out) {
+    for (int i = 0; i < rows; i++) {
+        const float *r = x + (size_t)i * d;
+        double s = 0.0;
+        for (int j = 0; j < d; j++) s += (double)r[j];
+        const double mean = s / (double)d;
+        double v = 0.0;
+        for (int j = 0; j < d; j++) {
+            const double df = (double)r[j] - mean;
+            v += df * df;
+        }
+        const double var = v / (double)d;
+        const double rstd = 1.0 / sqrt(var + (double)eps);
+        if (mean_out) mean_out[i] = (float)mean;
+        if (rstd_out) rstd_out[i] = (float)rstd;
+        for (int j = 0; j < d; j++) {
+            const double nrm = ((double)r[j] - mean) * rstd;
+            out[(size_t)i * d + j] = (float)(nrm * (double)gamma[j] + (double)beta[j]);
+        }
+    }
+}
+
+/* cpu.rs:1110-1116 gelu_scalar (f64, tanh approximation) */
+float orc_gelu(float x) {
+    const double x64 = (double)x;
+    const double c = sqrt(2.0 / M_PI);
+    const double inner = c * (x64 + 0.044715 * x64 * x64 * x64);
+    return (float)(0.5 * x64 * (1.0 + tanh(inner)));
+}
+
+void orc_gelu_vec(const float *x, size_t n, float *out) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_gelu(x[i]);
+}
+
+/* cpu.rs:500-503 sum: sequential f64, rounded once */
+float orc_sum(const float *x, size_t n) {
+    double s = 0.0;
+    for (size_t i = 0; i < n; i++) s += (double)x[i];
+    return (float)s;
+}
+
+/* cpu.rs:505-507 mul_elementwise */
+void orc_mul(const float *a, const float *b, size_t n, float *out) {
+    for (size_t i = 0; i < n; i++) out[i] = a[i] * b[i];
+}
+
+/* cpu.rs:601-633 rope: rows of last_dim, heads of head_dim, position pos;
+ * freq_i = 1 / theta^(2i/head_dim) in f64, angle = pos * freq, cos / sin
+ * rounded to f32, pairs (2i, 2i+1) rotated in f32; the rest copied. */
+void orc_rope_rows(const float *x, size_t rows, int last_dim, int pos, int head_dim, float theta, float *out) {
+    memcpy(out, x, sizeof(float) * rows * (size_t)last_dim);
+    const double th = (double)theta;
+    const int nh = last_dim / head_dim;
+    for (size_t r = 0; r < rows; r++)
+        for (int h = 0; h < nh; h++) {
+            const size_t hs = r * (size_t)last_dim + (size_t)h * head_dim;
+            for (int i = 0; i < head_dim / 2; i++) {
+                const double freq = 1.0 / pow(th, 2.0 * (double)i / (double)head_dim);
+                const double ang = (double)pos * freq;
+                const float cv = (float)cos(ang), sv = (float)sin(ang);
+                const float x0 = x[hs + 2 * i], x1 = x[hs + 2 * i + 1];
+                out[hs + 2 * i] = x0 * cv - x1 * sv;
+                out[hs + 2 * i + 1] = x0 * sv + x1 * cv;
+            }
+        }
+}
+
+/* mod.rs:316-331 gather_columns */
+void orc_gather_columns(const float *x, int rows, int total, int start, int count, float *out) {
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < count; c++) out[(size_t)r * count + c] = x[(size_t)r * total + start + c];
+}
+
+/* mod.rs:334-350 scatter_columns (additive, in place) */
+void orc_scatter_columns(float *dst, const float *src, int rows, int total, int start, int count) {
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < count; c++) dst[(size_t)r * total + start + c] += src[(size_t)r * count + c];
+}
+
+/* cpu.rs:94-188 add, generic broadcast form (tensor/shape.rs broadcast_strides):
+ * every fast path of the CPU add computes the same a + b per output element. */
+void orc_add_broadcast(const float *a, const size_t *ad, int an, const float *b, const size_t *bd, int bn,
+                       const size_t *od, int on, float *out) {
+    size_t os[6], as[6], bs[6], ast[6], bst[6], n = 1;
+    for (int i = on - 1, acc = 1; i >= 0; i--) { os[i] = (size_t)acc; acc *= (int)od[i]; }
+    { size_t acc = 1; for (int i = an - 1; i >= 0; i--) { as[i] = acc; acc *= ad[i]; } }
+    { size_t acc = 1; for (int i = bn - 1; i >= 0; i--) { bs[i] = acc; acc *= bd[i]; } }
+    for (int i = 0; i < on; i++) {
+        const int ia = i - (on - an), ib = i - (on - bn);
+        ast[i] = (ia < 0 || (ad[ia] == 1 && od[i] != 1)) ? 0 : as[ia];
+        bst[i] = (ib < 0 || (bd[ib] == 1 && od[i] != 1)) ? 0 : bs[ib];
+        n *= od[i];
+    }
+    for (size_t idx = 0; idx < n; idx++) {
+        size_t rem = idx, ao = 0, bo = 0;
+        for (int d = 0; d < on; d++) {
+            const size_t c = rem / os[d];
+            rem %= os[d];
+            ao += c * ast[d];
+            bo += c * bst[d];
+        }
+        out[idx] = a[ao] + b[bo];
+    }
+}
+
+/* cpu.rs:300-334 scaled_softmax: f32 max of x*scale, e = expf(x*scale - max)
+ * kept as f32, f64 sum, out = f32(f64(e) / sum) */
+void orc_scaled_softmax(const float *x, int rows, int cols, float scale, float *out) {
+    for (int r = 0; r < rows; r++) {
+        const float *in = x + (size_t)r * cols;
+        float *o = out + (size_t)r * cols;
+        float mx = -INFINITY;
+        for (int i = 0; i < cols; i++) mx = fmaxf(mx, in[i] * scale);
+        double sum = 0.0;
+        for (int i = 0; i < cols; i++) {
+            const double e = (double)expf(in[i] * scale - mx);
+            o[i] = (float)e;
+            sum += e;
+        }
+        for (int i = 0; i < cols; i++) o[i] = (float)((double)o[i] / sum);
+    }
+}
+
+/* mod.rs:408-438 split_qkv_reshape_heads */
+void orc_split_qkv_reshape_heads(const float *qkv, int seq, int n_heads, int d_head, float *q, float *k,
+                                 float *v) {
+    const int dm = n_heads * d_head;
+    for (int s = 0; s < seq; s++)
+        for (int h = 0; h < n_heads; h++)
+            for (int d = 0; d < d_head; d++) {
+                const size_t dst = ((size_t)h * seq + s) * d_head + d;
+                const size_t src = (size_t)s * 3 * dm + (size_t)h * d_head + d;
+                q[dst] = qkv[src];
+                k[dst] = qkv[src + dm];
+                v[dst] = qkv[src + 2 * dm];
+            }
+}
+
+/* mod.rs:441-467 reshape_for_heads (dir 0) and 484-510 reshape_from_heads (dir 1) */
+void orc_reshape_heads(const float *x, int batch, int seq, int n_heads, int d_head, int dir, float *out) {
+    const int dm = n_heads * d_head;
+    for (int b = 0; b < batch; b++)
+        for (int h = 0; h < n_heads; h++)
+            for (int s = 0; s < seq; s++)
+                for (int d = 0; d < d_head; d++) {
+                    const size_t heads = ((size_t)(b * n_heads + h) * seq + s) * d_head + d;
+                    const size_t flat = (size_t)(b * seq + s) * dm + (size_t)h * d_head + d;
+                    if (dir == 0)
+                        out[heads] = x[flat];
+                    else
+                        out[flat] = x[heads];
+                }
+}

@@ -101,6 +101,23 @@ void orc_compute_rope_freqs(int head_dim, float theta, int has_scaling, double f
                             double low_freq_factor, double high_freq_factor,
                             int64_t original_max_pos, double *out);
 
+/* ---- the rest of the trait surface (cpu.rs, mod.rs default bodies) ---- */
+void orc_layernorm(const float *x, const float *gamma, const float *beta, int rows, int d, float eps,
+                   float *out, float *mean_out, float *rstd_out);
+float orc_gelu(float x);
+void orc_gelu_vec(const float *x, size_t n, float *out);
+float orc_sum(const float *x, size_t n);
+void orc_mul(const float *a, const float *b, size_t n, float *out);
+void orc_rope_rows(const float *x, size_t rows, int last_dim, int pos, int head_dim, float theta, float *out);
+void orc_gather_columns(const float *x, int rows, int total, int start, int count, float *out);
+void orc_scatter_columns(float *dst, const float *src, int rows, int total, int start, int count);
+void orc_add_broadcast(const float *a, const size_t *ad, int an, const float *b, const size_t *bd, int bn,
+                       const size_t *od, int on, float *out);
+void orc_scaled_softmax(const float *x, int rows, int cols, float scale, float *out);
+void orc_split_qkv_reshape_heads(const float *qkv, int seq, int n_heads, int d_head, float *q, float *k,
+                                 float *v);
+void orc_reshape_heads(const float *x, int batch, int seq, int n_heads, int d_head, int dir, float *out);
+
 /* ---- llama.rs model ---- */
 typedef struct {
     int32_t vocab_size, hidden_size, intermediate_size, n_layers, n_heads, n_kv_heads,
@@ -165,6 +182,18 @@ int orc_generate(const orc_llama *m, const int64_t *prompt, int n_prompt, int ma
                  int64_t top_k, float top_p, uint64_t seed, int mode, int64_t *out_tokens, float *step_logits);
 int orc_generate_greedy(const orc_llama *m, const int64_t *prompt, int n_prompt, int max_tokens,
                         int mode, int64_t *out_tokens, float *step_logits);
+
+/* The cache path evaluated layer by layer (per-tensor int8, mode 1 only):
+ * n tokens at positions pos0.. are appended to c, bit-identical to n calls of
+ * orc_llama_forward_with_cache; logits (if n_logits > 0) receives the last
+ * n_logits rows' logits [n_logits, V].  Returns 0, -1 (token out of range),
+ * -2 (cache full), -3 (a projection has no per-tensor int8 weights) or -4. */
+int orc_llama_forward_cache_seq(const orc_llama *m, orc_cache *c, const int64_t *tokens, int n,
+                                int pos0, int n_logits, float *logits);
+/* orc_generate_greedy(mode 1) on the layer-major path: same tokens,
+ * bit-identical step logits. */
+int orc_generate_greedy_fast(const orc_llama *m, const int64_t *prompt, int n_prompt, int max_tokens,
+                             int64_t *out_tokens, float *step_logits);
 
 /* threading: 0 = reference-faithful single-threaded loops; n>0 = bit-identical
  * parallel variants on n threads */

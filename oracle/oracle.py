@@ -22,6 +22,7 @@ f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
 i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
 u64p = np.ctypeslib.ndpointer(dtype=np.uint64, flags="C_CONTIGUOUS")
+szp = np.ctypeslib.ndpointer(dtype=np.uintp, flags="C_CONTIGUOUS")
 
 
 def build() -> str:
@@ -91,8 +92,22 @@ def lib():
         "orc_llama_forward_with_cache": (i32, [vp, vp, C.c_int64, i32, i32, f32p]),
         "orc_llama_forward": (i32, [vp, i64p, i32, i32, f32p]),
         "orc_generate_greedy": (i32, [vp, i64p, i32, i32, i32, i64p, vp]),
+        "orc_generate_greedy_fast": (i32, [vp, i64p, i32, i32, i64p, vp]),
+        "orc_llama_forward_cache_seq": (i32, [vp, vp, i64p, i32, i32, i32, vp]),
         "orc_generate": (i32, [vp, i64p, i32, i32, f32, C.c_int64, f32, u64, i32, i64p, vp]),
         "orc_sample_token": (C.c_int64, [f32p, C.c_int64, f32, C.c_int64, f32, C.POINTER(u64)]),
+        "orc_layernorm": (None, [f32p, f32p, f32p, i32, i32, f32, f32p, vp, vp]),
+        "orc_gelu": (f32, [f32]),
+        "orc_gelu_vec": (None, [f32p, sz, f32p]),
+        "orc_sum": (f32, [f32p, sz]),
+        "orc_mul": (None, [f32p, f32p, sz, f32p]),
+        "orc_rope_rows": (None, [f32p, sz, i32, i32, i32, f32, f32p]),
+        "orc_gather_columns": (None, [f32p, i32, i32, i32, i32, f32p]),
+        "orc_scatter_columns": (None, [f32p, f32p, i32, i32, i32, i32]),
+        "orc_add_broadcast": (None, [f32p, szp, i32, f32p, szp, i32, szp, i32, f32p]),
+        "orc_scaled_softmax": (None, [f32p, i32, i32, f32, f32p]),
+        "orc_split_qkv_reshape_heads": (None, [f32p, i32, i32, i32, f32p, f32p, f32p]),
+        "orc_reshape_heads": (None, [f32p, i32, i32, i32, i32, i32, f32p]),
         "orc_set_threads": (None, [i32]),
         "orc_get_threads": (i32, []),
     }
@@ -333,6 +348,87 @@ def compute_rope_freqs(head_dim, theta, scaling=None):
     return out
 
 
+# ---- the rest of the trait surface ----
+def layernorm(x, gamma, beta, rows, d, eps=1e-5):
+    """cpu.rs:416-475: (out [rows*d], mean [rows], rstd [rows])"""
+    out = np.empty(rows * d, np.float32)
+    mu = np.empty(rows, np.float32)
+    rs = np.empty(rows, np.float32)
+    lib().orc_layernorm(_f32(x).ravel(), _f32(gamma).ravel(), _f32(beta).ravel(), rows, d, eps, out,
+                        mu.ctypes.data, rs.ctypes.data)
+    return out, mu, rs
+
+
+def gelu(x):
+    x = _f32(x).ravel()
+    out = np.empty_like(x)
+    lib().orc_gelu_vec(x, x.size, out)
+    return out
+
+
+def sum_(x) -> float:
+    x = _f32(x).ravel()
+    return float(np.float32(lib().orc_sum(x, x.size)))
+
+
+def mul_elementwise(a, b):
+    a, b = _f32(a).ravel(), _f32(b).ravel()
+    n = min(a.size, b.size)
+    out = np.empty(n, np.float32)
+    lib().orc_mul(a, b, n, out)
+    return out
+
+
+def rope(x, rows, last_dim, pos, head_dim, theta):
+    out = np.empty(rows * last_dim, np.float32)
+    lib().orc_rope_rows(_f32(x).ravel(), rows, last_dim, pos, head_dim, theta, out)
+    return out
+
+
+def gather_columns(x, rows, total, start, count):
+    out = np.empty(rows * count, np.float32)
+    lib().orc_gather_columns(_f32(x).ravel(), rows, total, start, count, out)
+    return out
+
+
+def scatter_columns(dst, src, rows, total, start, count):
+    d = _f32(dst).ravel().copy()
+    lib().orc_scatter_columns(d, _f32(src).ravel(), rows, total, start, count)
+    return d
+
+
+def add_broadcast(a, a_dims, b, b_dims, out_dims):
+    ad, bd, od = (np.asarray(v, np.uintp) for v in (a_dims, b_dims, out_dims))
+    out = np.empty(int(np.prod(od)), np.float32)
+    lib().orc_add_broadcast(_f32(a).ravel(), ad, ad.size, _f32(b).ravel(), bd, bd.size, od, od.size, out)
+    return out
+
+
+def scaled_softmax(x, rows, cols, scale_):
+    out = np.empty(rows * cols, np.float32)
+    lib().orc_scaled_softmax(_f32(x).ravel(), rows, cols, scale_, out)
+    return out
+
+
+def split_qkv_reshape_heads(qkv, seq, n_heads, d_head):
+    n = seq * n_heads * d_head
+    q, k, v = (np.empty(n, np.float32) for _ in range(3))
+    lib().orc_split_qkv_reshape_heads(_f32(qkv).ravel(), seq, n_heads, d_head, q, k, v)
+    return q, k, v
+
+
+def reshape_for_heads(x, batch, seq, n_heads, d_head):
+    out = np.empty(batch * seq * n_heads * d_head, np.float32)
+    lib().orc_reshape_heads(_f32(x).ravel(), batch, seq, n_heads, d_head, 0, out)
+    return out
+
+
+def reshape_from_heads(x, batch, seq, n_heads, d_head):
+    out = np.empty(batch * seq * n_heads * d_head, np.float32)
+    lib().orc_reshape_heads(_f32(x).ravel(), batch, seq, n_heads, d_head, 1, out)
+    return out
+
+
 # ---- model ----
 class _Cfg(C.Structure):
     _fields_ = [
@@ -495,6 +591,35 @@ class Llama:
         if want_logits:
             return toks[:rc], lg.reshape(nout, -1)[:rc]
         return toks[:rc]
+
+
+    def generate_greedy_fast(self, prompt, max_tokens, want_logits=False):
+        """generate_greedy(mode=1) evaluated layer-major (orc_generate_greedy_fast):
+        the same tokens and bit-identical step logits, with each int8 weight read
+        once for the whole prompt."""
+        p = np.ascontiguousarray(prompt, np.int64)
+        nout = max(1, max_tokens)
+        toks = np.empty(nout, np.int64)
+        lg = np.empty(nout * self.cfg.vocab_size, np.float32) if want_logits else None
+        rc = lib().orc_generate_greedy_fast(self.h, p, p.size, max_tokens, toks,
+                                            lg.ctypes.data if lg is not None else None)
+        if rc < 0:
+            raise RuntimeError(f"oracle generate_greedy_fast failed: {rc}")
+        if want_logits:
+            return toks[:rc], lg.reshape(nout, -1)[:rc]
+        return toks[:rc]
+
+    def forward_cache_seq(self, cache, tokens, pos0, n_logits=1):
+        """n tokens through the cache path at positions pos0.. (layer-major,
+        bit-identical to forward_with_cache per token); logits of the last
+        n_logits rows."""
+        t = np.ascontiguousarray(tokens, np.int64)
+        lg = np.empty(max(1, n_logits) * self.cfg.vocab_size, np.float32)
+        rc = lib().orc_llama_forward_cache_seq(self.h, cache.h, t, t.size, int(pos0), int(n_logits),
+                                               lg.ctypes.data)
+        if rc != 0:
+            raise RuntimeError(f"oracle forward_cache_seq failed: {rc}")
+        return lg.reshape(max(1, n_logits), -1)[:n_logits]
 
 
 class _Cache:

@@ -40,4 +40,5 @@ def test_calls_before_init_fail_cleanly():
     with pytest.raises(E.ScryHipError) as ei:
         E.HipBackend.zeros(8)
     assert ei.value.code == 4
-    assert b"not called" in _lib.load().scry_hip_last_error() or True
+    assert "scry_hip_init not called" in str(ei.value)
+    assert b"not called" in _lib.load().scry_hip_last_error()

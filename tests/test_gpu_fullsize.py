@@ -1,0 +1,230 @@
+"""Parity at the full size of the headline configurations.
+
+Config 4 (Llama-2-7B shape, 32 layers, 512-token prompt + 256 greedy tokens)
+runs on the GPU exactly as bench.py runs it (device init of the same seeded
+weights) and is checked against the CPU oracle on the GPU model's own int8
+weights:
+  - every step's logits within 1e-3 relative;
+  - the oracle's greedy choice (argmax, generate.rs:167-173) equals the GPU's
+    token at every step.
+The oracle evaluates the cache path layer-major over the prompt plus the
+GPU's tokens (orc_llama_forward_cache_seq, bit-identical to the token-by-token
+path; tests/test_oracle.py).  Its logits at step t are what its own greedy run
+computes at step t whenever the tokens before t agree.  Since every earlier
+step's argmax also agrees, its own greedy run produces the same 256 tokens
+(induction on t).
+
+Config 5 (Llama-3-8B shape) is checked twice:
+  - at its dimensions with 2 layers against the oracle (batched prefill of 4
+    sequences, then greedy steps);
+  - at full size against the GPU's own token-by-token path.  The oracle would
+    need ~6e13 multiply-adds for 4 x 2048 prompts.
+"""
+import numpy as np
+import pytest
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+LOGIT_TOL = 1e-3
+
+LLAMA2_7B = dict(vocab_size=32000, hidden_size=4096, intermediate_size=11008, n_layers=32,
+                 n_heads=32, n_kv_heads=32, max_seq_len=2048, rope_theta=10000.0,
+                 tie_word_embeddings=False)
+LLAMA3_8B = dict(vocab_size=128256, hidden_size=4096, intermediate_size=14336, n_layers=32,
+                 n_heads=32, n_kv_heads=8, max_seq_len=2048, rope_theta=500000.0,
+                 tie_word_embeddings=False)
+PROJ = ("T_QKV", "T_O", "T_GATE", "T_UP", "T_DOWN")
+
+
+def rel_err(g, c):
+    g = np.asarray(g, np.float64)
+    c = np.asarray(c, np.float64)
+    return np.abs(g - c).max() / max(np.abs(c).max(), 1e-6)
+
+
+def top2_margin(lg):
+    t = np.partition(np.asarray(lg, np.float64), -2)[-2:]
+    return float(t[1] - t[0])
+
+
+def oracle_from_gpu(orc, hm, cfg, layers=None):
+    """An oracle model holding exactly the GPU model's int8 weights, scales and
+    f32 embedding table."""
+    om = orc.Llama(orc.LlamaConfig(**cfg), None)
+    for layer in range(cfg["n_layers"] if layers is None else layers):
+        if layer % 8 == 0:
+            print(f"[case] copying layer {layer} to the oracle", flush=True)
+        for name in PROJ:
+            tid = getattr(orc, name)
+            q, s = hm.qtensor(tid, layer)
+            om.set_qtensor(tid, layer, q, s)
+    q, s = hm.qtensor(orc.T_LM_HEAD)
+    om.set_qtensor(orc.T_LM_HEAD, 0, q, s)
+    del q
+    om.set_embed(hm.embed())
+    return om
+
+
+@pytest.fixture(scope="module")
+def model7b(hip):
+    print("[case] config 4 model: Llama-2-7B shape, seed 0, device init (as bench.py)", flush=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**LLAMA2_7B), seed=0, init_on_device=True)
+    yield hm
+    hm.free()
+
+
+def test_config4_device_init_equals_host_init(hip, orc, model7b):
+    """The bench's device init (k_normal_init) against the host init, which is
+    bit-exact with the oracle's normal_vec (test_gpu_llama.py): every int8
+    tensor, scale and the f32 embedding of the 7B model."""
+    print("[case] config 4 host init (glibc, all host cores)", flush=True)
+    hh = hip.LlamaModel.new_random(hip.LlamaConfig(**LLAMA2_7B), seed=0, init_on_device=False)
+    diff = total = 0
+    try:
+        for layer in range(LLAMA2_7B["n_layers"]):
+            for name in PROJ:
+                tid = getattr(orc, name)
+                qd, sd = model7b.qtensor(tid, layer)
+                qh, sh = hh.qtensor(tid, layer)
+                assert sd == sh, (layer, name, sd, sh)
+                d = int(np.count_nonzero(qd != qh))
+                if d:
+                    assert np.abs(qd.astype(np.int16) - qh.astype(np.int16)).max() <= 1
+                diff += d
+                total += qd.size
+        qd, sd = model7b.qtensor(orc.T_LM_HEAD)
+        qh, sh = hh.qtensor(orc.T_LM_HEAD)
+        assert sd == sh
+        diff += int(np.count_nonzero(qd != qh))
+        total += qd.size
+        ed, eh = model7b.embed(), hh.embed()
+        emb_diff = int(np.count_nonzero(ed != eh))
+        emb_ulp = int(np.abs(ed.view(np.int32).astype(np.int64) - eh.view(np.int32)).max())
+    finally:
+        hh.free()
+    print(f"[err] device vs host init: {diff} of {total} int8 weights differ (by 1); "
+          f"{emb_diff} embedding values differ, by at most {emb_ulp} ulp", flush=True)
+    # the two libms (device vs glibc log/cos) may differ in the last bit of a
+    # sample, which moves a quantized value only when it sits on a rounding
+    # boundary
+    assert diff <= total * 1e-6
+    assert emb_ulp <= 1
+
+
+def test_config4_full_depth_vs_oracle(hip, orc, model7b):
+    """32 layers, 512-token seeded prompt (seed 1), 256
+    greedy tokens, token-by-token and with the batched prompt prefill."""
+    cfg = LLAMA2_7B
+    prompt = orc.prompt_ids(1, 512, cfg["vocab_size"])
+    print("[case] config 4 GPU generate: 512 prompt + 256 greedy, token by token", flush=True)
+    toks, lg = model7b.generate_greedy(prompt, 256, want_logits=True)
+    print("[case] config 4 GPU generate with batched prefill", flush=True)
+    toks_p, lg_p = model7b.generate_greedy(prompt, 256, want_logits=True, prefill=True)
+    assert len(toks) == 256 and len(toks_p) == 256
+    orc.set_threads(16)
+    print("[case] config 4 oracle: GPU int8 weights, layer-major cache path over 767 rows",
+          flush=True)
+    om = oracle_from_gpu(orc, model7b, cfg)
+    try:
+        seq = np.concatenate([prompt, toks[:-1]])  # row i >= 511 gives step i - 511
+        cache = om.new_cache(len(seq))
+        ref = []
+        for s0 in range(0, len(seq), 128):  # chunks: the same rows, bit-identical
+            chunk = seq[s0:s0 + 128]
+            nl = max(0, s0 + len(chunk) - 511) - max(0, s0 - 511)
+            ref.append(om.forward_cache_seq(cache, chunk, s0, n_logits=nl))
+            print(f"[case] oracle rows {s0}..{s0 + len(chunk) - 1} done", flush=True)
+        ref = np.concatenate(ref)
+        assert ref.shape == (256, cfg["vocab_size"])
+        del cache
+    finally:
+        om.close()
+        orc.set_threads(0)
+    errs = np.array([rel_err(lg[i], ref[i]) for i in range(256)])
+    errs_p = np.array([rel_err(lg_p[i], ref[i]) for i in range(256)])
+    ref_toks = np.array([orc.argmax(ref[i]) for i in range(256)])
+    margins = np.array([top2_margin(ref[i]) for i in range(256)])
+    print(f"[err] config 4: max step rel err {errs.max():.3e} (prefill path {errs_p.max():.3e}); "
+          f"{len(np.unique(toks))} distinct tokens; smallest top-1/top-2 margin "
+          f"{margins.min():.4g}", flush=True)
+    assert errs.max() < LOGIT_TOL
+    assert (ref_toks == toks).all()
+    assert (toks_p == toks).all()
+    assert errs_p.max() < LOGIT_TOL
+
+
+def test_config5_dims_two_layers_vs_oracle(hip, orc):
+    """Config-5 tensor shapes (h4096, 32:8 GQA, ffn 14336, V 128256, theta 5e5)
+    with 2 layers: the batched prefill of 4 x 255 tokens (seeds 1-4) and 16
+    greedy steps per sequence against the oracle."""
+    cfg = dict(LLAMA3_8B, n_layers=2)
+    print("[case] config-5 dims, 2 layers: batched prefill 4 x 255 + 16 greedy", flush=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), seed=0, init_on_device=True)
+    V = cfg["vocab_size"]
+    prompts = np.stack([orc.prompt_ids(s + 1, 256, V) for s in range(4)])
+    try:
+        caches = [hm.new_llama_kv_cache(256 + 16) for _ in range(4)]
+        last = hm.prefill(caches, prompts[:, :255])
+        gpu_lg, gpu_tok = [], []
+        for s in range(4):
+            tok, pos, lgs, ts = int(prompts[s, 255]), 255, [], []
+            for _ in range(16):
+                lg, am = hm.forward_with_llama_cache(tok, pos, caches[s])
+                lgs.append(lg)
+                ts.append(am)
+                tok, pos = am, pos + 1
+            gpu_lg.append(np.stack(lgs))
+            gpu_tok.append(np.array(ts))
+        orc.set_threads(16)
+        om = oracle_from_gpu(orc, hm, cfg)
+    finally:
+        hm.free()
+    try:
+        for s in range(4):
+            seq = np.concatenate([prompts[s], gpu_tok[s][:-1]])  # 271 rows
+            cache = om.new_cache(len(seq))
+            ref = om.forward_cache_seq(cache, seq, 0, n_logits=17)
+            del cache
+            e_pre = rel_err(last[s], ref[0])
+            errs = [rel_err(gpu_lg[s][i], ref[i + 1]) for i in range(16)]
+            ref_toks = np.array([orc.argmax(ref[i + 1]) for i in range(16)])
+            print(f"[err] config-5 dims seq {s}: prefill last logits {e_pre:.3e}, "
+                  f"decode max {max(errs):.3e}", flush=True)
+            assert e_pre < LOGIT_TOL
+            assert max(errs) < LOGIT_TOL
+            assert (ref_toks == gpu_tok[s]).all()
+    finally:
+        om.close()
+        orc.set_threads(0)
+
+
+def test_config5_full_batched_prefill_vs_token_by_token(hip, orc):
+    """BASELINE config 5 at full size: 4 x 2048-token prompts (seeds 1-4), the
+    first 2047 tokens of each through one batched prefill, then 64 greedy
+    steps per sequence -- against the GPU's token-by-token cache path of each
+    sequence (generate.rs:51-89): identical tokens, logits within 1e-3."""
+    cfg = LLAMA3_8B
+    print("[case] config 5 full: batched prefill 4 x 2047 + 64 greedy vs token by token",
+          flush=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), seed=0, init_on_device=True)
+    V = cfg["vocab_size"]
+    prompts = np.stack([orc.prompt_ids(s + 1, 2048, V) for s in range(4)])
+    try:
+        caches = [hm.new_llama_kv_cache(2048 + 64) for _ in range(4)]
+        hm.prefill(caches, prompts[:, :2047], want_logits=False)
+        for s in range(4):
+            tok, pos, lgs, ts = int(prompts[s, 2047]), 2047, [], []
+            for _ in range(64):
+                lg, am = hm.forward_with_llama_cache(tok, pos, caches[s])
+                lgs.append(lg)
+                ts.append(am)
+                tok, pos = am, pos + 1
+            caches[s].free()
+            print(f"[case] config 5 seq {s}: token-by-token generate", flush=True)
+            ref_tok, ref_lg = hm.generate_greedy(prompts[s], 64, want_logits=True)
+            err = max(rel_err(lgs[i], ref_lg[i]) for i in range(64))
+            print(f"[err] config 5 seq {s}: max step rel err {err:.3e}; tokens "
+                  f"{np.array(ts[:4]).tolist()}", flush=True)
+            assert err < LOGIT_TOL
+            assert (np.array(ts) == ref_tok).all()
+    finally:
+        hm.free()

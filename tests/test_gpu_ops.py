@@ -63,6 +63,8 @@ SHAPES = [
     (4, 4096, 11008),
     (4, 11008, 4096),
     (16, 4096, 4096),
+    (16, 4096, 11008),  # config 3 at batch 16
+    (16, 11008, 4096),
     (1, 288, 864),      # tiny qkv
     (3, 100, 65),       # ragged
     (2, 16, 5),
@@ -103,6 +105,25 @@ def test_matmul_i8_f32_bias_and_block32(hip, orc):
     ref = orc.matmul_i8_f32_b32(a, q32, s32, m, k, n)
     out = B.matmul_i8_f32_block32(B.from_vec(a), B.i8_from_vec(q32), B.from_vec(s32), m, k, n)
     assert rel_err(out.to_vec().reshape(m, n), ref) < 2e-5
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 4096), (4, 4096, 11008), (16, 11008, 4096),
+                                   (16, 4096, 11008), (1, 11008, 4096)])
+def test_matmul_i8_f32_block32_shapes(hip, orc, m, k, n):
+    """Block-32 scales at the config 2 / 3 shapes and batches."""
+    B = hip.HipBackend
+    rng = np.random.default_rng(m * 5 + k + 3 * n)
+    print(f"[case] matmul_i8_f32_block32 m={m} k={k} n={n}", flush=True)
+    a = rng.normal(0, 1, (m, k)).astype(F)
+    w = rng.normal(0, 0.02, (k, n)).astype(F)
+    q32, s32 = orc.quantize_block32(w, k, n)
+    orc.set_threads(8)
+    ref = orc.matmul_i8_f32_b32(a, q32, s32, m, k, n)
+    orc.set_threads(0)
+    out = B.matmul_i8_f32_block32(B.from_vec(a), B.i8_from_vec(q32), B.from_vec(s32), m, k, n)
+    err = rel_err(out.to_vec().reshape(m, n), ref)
+    print(f"[err] rel {err:.3e}", flush=True)
+    assert err < 2e-5
 
 
 def test_matmul_i8_exact_integer(hip):

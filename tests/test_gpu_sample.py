@@ -204,19 +204,3 @@ def test_generate_edge_cases(small, orc, hip):
         hm.generate(prompt, hip.SamplingConfig(temperature=float("nan"), max_tokens=4), rng)
     with pytest.raises(ValueError):
         hip.generate(hm, prompt, hip.SamplingConfig(temperature=1.0, max_tokens=4))
-
-
-def test_sampling_ignores_the_persistent_decode_mode(small, orc, hip):
-    """The persistent decode kernel finishes with the argmax; a sampled
-    generate keeps the captured per-kernel step (same tokens in both modes)."""
-    om, hm = small
-    print("[case] sampled generate under SCRY_DECODE_PERSISTENT", flush=True)
-    prompt = orc.prompt_ids(8, 6, SMALL["vocab_size"])
-    sc = hip.SamplingConfig(temperature=0.9, top_k=20, top_p=0.9, max_tokens=12)
-    a = hm.generate(prompt, sc, hip.Rng.with_seed(3))
-    hip.set_decode_mode(hip.DECODE_PERSISTENT)
-    try:
-        b = hm.generate(prompt, sc, hip.Rng.with_seed(3))
-    finally:
-        hip.set_decode_mode(hip.DECODE_KERNELS)
-    assert (a == b).all()

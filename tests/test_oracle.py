@@ -571,3 +571,215 @@ def test_matmul_bf16_oracle(orc, ta, tb):
     got = orc.matmul_bf16(a.T.copy() if ta else a, b.T.copy() if tb else b, m, k, n, ta, tb)
     assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
     assert not np.array_equal(got, a @ b)  # the rounding of the operands is there
+
+
+# ------------------------------------------------- distribution of sample_token
+def _closed_form_probs(logits, t, k, p):
+    """generate.rs:92-165 written from its definition: keep the k largest of
+    logits / t, softmax over the kept ones, then keep the smallest
+    most-probable prefix whose mass reaches p and renormalise."""
+    z = np.asarray(logits, np.float64) / np.float64(np.float32(t))
+    order = np.argsort(-z, kind="stable")
+    keep = np.zeros(z.size, bool)
+    keep[order[: (k if 0 < k < z.size else z.size)]] = True
+    e = np.where(keep, np.exp(z - z[keep].max()), 0.0)
+    pr = e / e.sum()
+    pf = float(np.float32(p))
+    if 0.0 < pf < 1.0:
+        o2 = np.argsort(-pr, kind="stable")
+        cut = int(np.searchsorted(np.cumsum(pr[o2]), pf)) + 1
+        pr2 = np.zeros_like(pr)
+        pr2[o2[:cut]] = pr[o2[:cut]]
+        pr = pr2 / pr2.sum()
+    return pr
+
+
+@pytest.mark.parametrize("t,k,p", [(0.8, 4, 1.0), (1.3, 0, 0.7), (0.9, 5, 0.85), (1.0, 0, 1.0)])
+def test_sample_token_distribution_chi_square(orc, t, k, p):
+    """Token frequencies over 100000 rng states against the closed-form
+    kept-and-renormalised probabilities (Pearson chi-square).  A wrong
+    temperature direction, an off-by-one in the top-k or top-p cut, or a
+    missing renormalisation moves the frequencies far outside the test."""
+    stats = pytest.importorskip("scipy.stats")
+    logits = np.array([1.7, -0.3, 0.9, 2.4, 0.1, -1.2, 1.1, 0.5], np.float32)
+    want = _closed_form_probs(logits, t, k, p)
+    n = 100_000
+    counts = np.zeros(logits.size, np.int64)
+    for s in range(n):
+        counts[orc.sample_token(logits, t, k, p, s * 7919 + 13)[0]] += 1
+    kept = want > 0
+    assert (counts[~kept] == 0).all(), (counts, want)
+    chi2, pval = stats.chisquare(counts[kept], want[kept] * n)
+    assert pval > 1e-4, (chi2, pval, counts, want)
+
+
+# ------------------------------------------ f64 accumulation of the m > 1 path
+def test_matmul_fallback_accumulates_in_f64(orc):
+    """cpu.rs:964-999 matmul_tiled_fallback accumulates in f64 and rounds once:
+    a row [2^24, 1, -2^24] against ones sums to 1 (in f32 the 1 is lost).  At
+    m == 1 the dispatch (cpu.rs:924-945) takes the f32 GEMV instead: 0."""
+    a = np.array([[2.0**24, 1.0, -(2.0**24)], [1.0, 2.0**24, -(2.0**24)]], np.float32)
+    b = np.ones((3, 2), np.float32)
+    assert orc.matmul_f32(a, b, 2, 3, 2).tolist() == [[1.0, 1.0], [1.0, 1.0]]
+    assert orc.matmul_f32(a[:1], b, 1, 3, 2).tolist() == [[0.0, 0.0]]
+    assert orc.matmul_f32(a.T.copy(), b, 2, 3, 2, trans_a=True).tolist() == [[1.0, 1.0], [1.0, 1.0]]
+
+
+# ------------------------------------------------ layer-major cache path
+FAST_CFGS = [
+    dict(vocab_size=32000, hidden_size=288, intermediate_size=768, n_layers=6, n_heads=6,
+         n_kv_heads=6, max_seq_len=256, rope_theta=10000.0, tie_word_embeddings=True),
+    dict(vocab_size=500, hidden_size=512, intermediate_size=300, n_layers=2, n_heads=4,
+         n_kv_heads=1, max_seq_len=300, rope_theta=500000.0, tie_word_embeddings=False),
+    dict(vocab_size=77, hidden_size=40, intermediate_size=52, n_layers=3, n_heads=5,
+         n_kv_heads=5, max_seq_len=80, rope_theta=10000.0, tie_word_embeddings=False),
+    dict(vocab_size=300, hidden_size=96, intermediate_size=70, n_layers=2, n_heads=8,
+         n_kv_heads=2, max_seq_len=80, rope_theta=10000.0, tie_word_embeddings=True),
+]
+
+
+@pytest.mark.parametrize("ci", range(len(FAST_CFGS)))
+def test_layer_major_cache_path_bit_identical(orc, ci):
+    """orc_generate_greedy_fast / orc_llama_forward_cache_seq (the oracle's
+    full-size parity mode) against the token-by-token cache path: the same
+    tokens, bit-identical logits and KV cache rows, single- and multi-threaded
+    (head dims 48, 128, 8 and 12; GQA 1:1, 4:1 and 4:1 with odd vocab)."""
+    cfg = orc.LlamaConfig(**FAST_CFGS[ci])
+    om = orc.Llama(cfg, ci, quantize=True, keep_f32=False)
+    prompt = orc.prompt_ids(ci + 1, 37, cfg.vocab_size)
+    ref_t, ref_l = om.generate_greedy(prompt, 20, mode=1, want_logits=True)
+    for th in (0, 8):
+        orc.set_threads(th)
+        t, lg = om.generate_greedy_fast(prompt, 20, want_logits=True)
+        assert (t == ref_t).all()
+        assert np.array_equal(lg, ref_l)
+    # a split over several calls, logits of several rows, cache contents
+    c_ref = om.new_cache(60)
+    ref_rows = [om.forward_with_cache(c_ref, int(tok), pos, mode=1)
+                for pos, tok in enumerate(prompt[:30])]
+    c = om.new_cache(60)
+    got_a = om.forward_cache_seq(c, prompt[:11], 0, n_logits=3)
+    got_b = om.forward_cache_seq(c, prompt[11:30], 11, n_logits=19)
+    orc.set_threads(0)
+    assert np.array_equal(got_a, np.stack(ref_rows[8:11]))
+    assert np.array_equal(got_b, np.stack(ref_rows[11:30]))
+    for layer in range(cfg.n_layers):
+        assert c.seq_len(layer) == 30
+        ka, va = c.layer(layer)
+        kb, vb = c_ref.layer(layer)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    with pytest.raises(RuntimeError):
+        om.forward_cache_seq(c, prompt[:31], 30)  # cache full
+    om.close()
+
+
+# ------------------------------------------------ the rest of the trait surface
+def test_gelu_kat_and_erf_bound(orc):
+    """cpu.rs:1494-1497 gelu_zero, published values of the tanh form, and the
+    approximation bound against the exact erf GELU (a wrong constant in the
+    tanh form breaks the bound)."""
+    import math
+    assert abs(orc.gelu([0.0])[0]) < 1e-7
+    g = orc.gelu(np.array([1.0, -1.0, 2.0, -3.0], np.float32))
+    assert np.allclose(g, [0.8411920, -0.1588080, 1.9545977, -0.0036373], atol=2e-7)
+    xs = np.linspace(-6, 6, 2001).astype(np.float32)
+    exact = np.array([0.5 * x * (1 + math.erf(x / math.sqrt(2))) for x in xs.astype(np.float64)])
+    assert np.abs(orc.gelu(xs) - exact).max() < 6e-4
+    assert (orc.gelu(np.array([20.0, -20.0], np.float32)) == np.array([20.0, -0.0], np.float32)).all()
+
+
+def test_layernorm_kat_and_closed_form(orc):
+    """cpu.rs:1585-1599 layernorm_inference_matches, and the closed form
+    (x - mean) / sqrt(var + eps) * gamma + beta against numpy's mean / var."""
+    x = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    out, mu, rs = orc.layernorm(x, np.ones(3, np.float32), np.zeros(3, np.float32), 2, 3, 1e-5)
+    want = np.array([-1.2247357, 0.0, 1.2247357] * 2, np.float32)
+    assert np.abs(out - want).max() < 1e-6
+    assert mu.tolist() == [2.0, 5.0]
+    rng = np.random.default_rng(21)
+    x = rng.normal(3, 2, (5, 77)).astype(np.float32)
+    g = rng.normal(1, 0.3, 77).astype(np.float32)
+    b = rng.normal(0, 0.3, 77).astype(np.float32)
+    out, mu, rs = orc.layernorm(x, g, b, 5, 77, 1e-5)
+    x64 = x.astype(np.float64)
+    m = x64.mean(1, keepdims=True)
+    r = 1 / np.sqrt(x64.var(1, keepdims=True) + np.float64(np.float32(1e-5)))
+    assert np.abs(out.reshape(5, 77) - ((x64 - m) * r * g + b)).max() < 1e-5
+    assert np.allclose(mu, m.ravel(), rtol=1e-7) and np.allclose(rs, r.ravel(), rtol=1e-7)
+
+
+def test_sum_accumulates_in_f64(orc):
+    """cpu.rs:500-503: an f64 sum rounded once (in f32 the 1 would be lost)."""
+    assert orc.sum_(np.array([2.0**24, 1.0, -(2.0**24)], np.float32)) == 1.0
+    assert orc.sum_(np.zeros(0, np.float32)) == 0.0
+    x = np.random.default_rng(22).normal(0, 1, 10001).astype(np.float32)
+    assert orc.sum_(x) == np.float32(x.astype(np.float64).sum())
+
+
+def test_rope_trait_kat_and_rotation(orc):
+    """cpu.rs:1538-1549 rope_basic (pos 1, head_dim 4: cos 1, sin 1), position
+    0 is the identity, and each pair is the textbook rotation by
+    pos / theta^(2i/hd); a trailing partial head and an odd last value are
+    copied."""
+    out = orc.rope(np.array([1, 0, 1, 0], np.float32), 1, 4, 1, 4, 10000.0)
+    assert abs(out[0] - 0.5403) < 1e-3 and abs(out[1] - 0.8415) < 1e-3
+    rng = np.random.default_rng(23)
+    x = rng.normal(0, 1, 3 * 70).astype(np.float32)
+    assert np.array_equal(orc.rope(x, 3, 70, 0, 16, 10000.0), x)
+    pos, hd, th = 37, 16, 10000.0
+    out = orc.rope(x, 3, 70, pos, hd, th).reshape(3, 70)
+    xr = x.reshape(3, 70).astype(np.float64)
+    for h in range(70 // hd):
+        for i in range(hd // 2):
+            ang = pos / th ** (2 * i / hd)
+            z = (xr[:, h * hd + 2 * i] + 1j * xr[:, h * hd + 2 * i + 1]) * np.exp(1j * ang)
+            assert np.abs(out[:, h * hd + 2 * i] - z.real).max() < 1e-5
+            assert np.abs(out[:, h * hd + 2 * i + 1] - z.imag).max() < 1e-5
+    assert np.array_equal(out[:, 64:], x.reshape(3, 70)[:, 64:])
+
+
+def test_column_row_and_head_moves_match_numpy(orc):
+    """gather_columns / scatter_columns (mod.rs:316-350), reshape_for_heads /
+    reshape_from_heads (441-510) and split_qkv_reshape_heads (408-438, with
+    cpu.rs:1601-1630 split_qkv_reshape_heads_matches_manual) against numpy
+    slicing and transposes."""
+    rng = np.random.default_rng(24)
+    x = rng.normal(0, 1, (7, 13)).astype(np.float32)
+    assert np.array_equal(orc.gather_columns(x, 7, 13, 4, 6), x[:, 4:10].ravel())
+    src = rng.normal(0, 1, (7, 6)).astype(np.float32)
+    want = x.copy()
+    want[:, 4:10] += src
+    assert np.array_equal(orc.scatter_columns(x, src, 7, 13, 4, 6), want.ravel())
+    B, S, H, D = 2, 5, 3, 4
+    flat = rng.normal(0, 1, (B * S, H * D)).astype(np.float32)
+    heads = flat.reshape(B, S, H, D).transpose(0, 2, 1, 3).reshape(B * H, S, D)
+    assert np.array_equal(orc.reshape_for_heads(flat, B, S, H, D), heads.ravel())
+    assert np.array_equal(orc.reshape_from_heads(heads, B, S, H, D), flat.ravel())
+    seq, nh, dh = 2, 2, 3
+    qkv = np.arange(seq * 3 * nh * dh, dtype=np.float32)
+    q, k, v = orc.split_qkv_reshape_heads(qkv, seq, nh, dh)
+    rows = qkv.reshape(seq, 3, nh * dh)
+    for got, part in ((q, 0), (k, 1), (v, 2)):
+        assert np.array_equal(got, orc.reshape_for_heads(rows[:, part].copy(), 1, seq, nh, dh))
+
+
+@pytest.mark.parametrize("ad,bd", [((4, 5), (4, 5)), ((4, 5), (1, 5)), ((4, 5), (5,)), ((1, 5), (4, 5)),
+                                   ((4, 5), (4, 1)), ((4, 1), (4, 5)), ((2, 3, 4), (3, 1)),
+                                   ((2, 1, 4), (1, 3, 1)), ((6,), (1,)), ((2, 1, 3, 1, 2, 1), (3, 4, 1, 5))])
+def test_add_broadcast_matches_numpy(orc, ad, bd):
+    """cpu.rs:94-188 add (every fast path and the generic broadcast) against
+    numpy's broadcasting, bit-exact."""
+    rng = np.random.default_rng(len(ad) * 10 + len(bd))
+    a = rng.normal(0, 1, ad).astype(np.float32)
+    b = rng.normal(0, 1, bd).astype(np.float32)
+    want = a + b
+    assert np.array_equal(orc.add_broadcast(a, ad, b, bd, want.shape), want.ravel())
+
+
+def test_scaled_softmax_kat(orc):
+    """cpu.rs:1569-1583 scaled_softmax_matches_separate: softmax of scale(x);
+    with the same f32 products the two are bit-identical."""
+    x = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    assert np.array_equal(orc.scaled_softmax(x, 2, 3, 0.5), orc.softmax(orc.scale(x, 0.5), 2, 3))
+    y = np.random.default_rng(25).normal(0, 4, (3, 50)).astype(np.float32)
+    assert np.array_equal(orc.scaled_softmax(y, 3, 50, 0.125), orc.softmax(orc.scale(y, 0.125), 3, 50))
