@@ -26,9 +26,14 @@ Also reported:
                 batched prefill of the first 2047 tokens of each prompt on the
                 matrix cores, then 64 greedy decode steps per sequence
 
+  gemv_micro    BASELINE configs 2 and 3: matmul_i8_f32 at 1, 4 and 16 rows,
+                block-32 and per-tensor scales, 1000 launches over 32 weight
+                copies: median / p10 / p90 per-launch device time
+
 Profiling modes (no JSON line): --pmc-probe runs a 256 MiB device copy (the
 counter calibration) and each decode projection kernel over all layers;
---prefill-only runs the config-5 measurement alone.
+--prefill-only runs the config-5 measurement alone; --gemv-only the
+configs 2 / 3 micro-benchmark alone.
 """
 from __future__ import annotations
 
@@ -182,6 +187,53 @@ def bf16_sweep(E) -> list:
     return out
 
 
+GEMV_CASES = [("config 2: attention projection", 4096, 4096, (1,)),
+              ("config 3: gate/up", 4096, 11008, (1, 4, 16)),
+              ("config 3: down", 11008, 4096, (1, 4, 16))]
+FP32_VALU_PEAK_TFLOPS = 157.3
+
+
+def gemv_micro(EL, iters: int = 1000, n_bufs: int = 32) -> list:
+    """BASELINE configs 2 and 3: matmul_i8_f32 at batch 1, 4 and 16 with the
+    reference's block (32-wide) scales and with per-tensor scales; iters timed
+    launches over n_bufs distinct weight copies (more than the 256 MB Infinity
+    Cache), per-launch device times (an event between launches) -> median and
+    p10 / p90, plus the back-to-back average.  At 16 rows both the GEMV and the
+    MFMA GEMM are timed (matmul_i8_f32 routes 16 rows to the GEMV)."""
+    import numpy as np
+    out = []
+    for name, k, n, ms in GEMV_CASES:
+        for qm, qname in ((EL.QUANT_BLOCK32, "block-32"), (EL.QUANT_PER_TENSOR, "per-tensor")):
+            for m in ms:
+                for path in ((1, 2) if m == 16 else (0,)):
+                    per, avg, b = EL.bench_qgemv_dist(m, k, n, qm, path, n_bufs, 50, iters)
+                    p10, med, p90 = (float(v) for v in np.percentile(per, [10, 50, 90]))
+                    fl = 2.0 * m * k * n
+                    e = {"case": name, "k": k, "n": n, "m": m, "scales": qname,
+                         "kernel": "mfma gemm" if path == 2 else "gemv",
+                         "iters": iters, "weight_buffers": n_bufs,
+                         "median_us": round(med, 3), "p10_us": round(p10, 3), "p90_us": round(p90, 3),
+                         "avg_us": round(avg, 3), "bytes": int(b),
+                         "gbs_median": round(b / med / 1e3, 1), "hbm_frac_median": round(b / med / 1e3 / HBM_PEAK_GBS, 4),
+                         "tflops_median": round(fl / med / 1e6, 2)}
+                    out.append(e)
+                    print(f"[bench] gemv {name:32s} m={m:2d} {qname:10s} {e['kernel']:9s} median {med:7.2f} us "
+                          f"(p10 {p10:6.2f} p90 {p90:6.2f}) {e['gbs_median']:7.1f} GB/s {e['tflops_median']:6.2f} TFLOP/s",
+                          file=sys.stderr, flush=True)
+    return out
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def weight_bytes(cfg) -> int:
     """int8 weight bytes + per-tensor scales read per decode token."""
     h, ffn, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.n_layers
@@ -192,7 +244,8 @@ def weight_bytes(cfg) -> int:
 
 
 def cpu_baseline(model, cfg, prompt, n_tok: int) -> dict:
-    """Oracle decode on the GPU model's own int8 weights, single-threaded."""
+    """Oracle decode on the GPU model's own int8 weights: reference-faithful
+    single-threaded, and the bit-identical all-core mode beside it."""
     from oracle import oracle as O
     import esolearn_amd.llama as EL
 
@@ -208,6 +261,16 @@ def cpu_baseline(model, cfg, prompt, n_tok: int) -> dict:
     om.set_qtensor(EL.T_LM_HEAD, 0, q, s)
     del q
     om.set_embed(model.embed())
+    # the bit-identical all-core mode: the same decode steps, one token at a
+    # time through the layer-major cache path on every host core
+    cores = min(16, os.cpu_count() or 1)
+    O.set_threads(cores)
+    cache = om.new_cache(n_tok + 1)
+    t0 = time.perf_counter()
+    for i in range(n_tok):
+        om.forward_cache_seq(cache, [int(prompt[i])], i, n_logits=1)
+    dt_all = time.perf_counter() - t0
+    del cache
     O.set_threads(0)  # matmul_i8_f32_tiled exactly as written: one thread
     cache = om.new_cache(n_tok + 1)
     t0 = time.perf_counter()
@@ -215,16 +278,21 @@ def cpu_baseline(model, cfg, prompt, n_tok: int) -> dict:
         om.forward_with_cache(cache, int(prompt[i]), i, mode=1)
     dt = time.perf_counter() - t0
     om.close()
+    model_name = cpu_model()
     return {
         "value": round(n_tok / dt, 5),
         "unit": "tok/s",
         "cores": 1,
         "kind": "port",
+        "cpu_model": model_name,
         "sample": (f"{n_tok} decode steps (positions 0..{n_tok - 1}) of the same "
                    "Llama-2-7B-shape int8 model on the host, oracle in reference-faithful "
                    "mode (single-threaded matmul_i8_f32_tiled, f64 products); "
-                   f"{dt:.1f} s; host {platform.processor() or platform.machine()}, "
-                   f"nproc {os.cpu_count()}"),
+                   f"{dt:.1f} s; host {model_name}, nproc {os.cpu_count()}"),
+        "all_cores": {"value": round(n_tok / dt_all, 4), "unit": "tok/s", "cores": cores,
+                      "mode": "bit-identical parallel oracle (layer-major cache path, SIMD across "
+                              "output columns, the same per-element operation order)",
+                      "seconds": round(dt_all, 2)},
     }
 
 
@@ -248,6 +316,9 @@ def main() -> int:
                     help="quantized Linear (bias GEMV) at GPT-2 / Whisper shapes only")
     ap.add_argument("--sampling-only", action="store_true",
                     help="greedy vs device-sampled decode over a few sampling configs only")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="the config 2 / 3 isolated GEMV micro-benchmark only")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the config 2 / 3 micro-benchmark")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -272,6 +343,9 @@ def main() -> int:
         return 0
     if args.prefill_only:
         print(json.dumps(prefill_config5(E)), flush=True)
+        return 0
+    if args.gemv_only:
+        print(json.dumps({"gemv_micro": gemv_micro(EL)}), flush=True)
         return 0
     info = E.HipBackend.device_info()
     cfg = E.LlamaConfig.llama2_7b()
@@ -337,6 +411,7 @@ def main() -> int:
         print(f"[bench] cpu baseline: {args.cpu_tokens} tokens", file=sys.stderr, flush=True)
         cpu = cpu_baseline(model, cfg, prompt, args.cpu_tokens)
     model.free()
+    gemv = None if args.no_gemv else gemv_micro(EL)
     pre = None if args.no_prefill else prefill_config5(E)
 
     line = {
@@ -367,6 +442,7 @@ def main() -> int:
         "projections": proj,
         "greedy_tokens_head": [int(t) for t in toks[:8]],
         "sampled_decode": sampled,
+        "gemv_micro": gemv,
         "prefill": pre,
     }
     print(json.dumps(line), flush=True)

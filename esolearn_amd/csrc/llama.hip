@@ -1466,6 +1466,113 @@ int bench_qgemv_impl(int m_rows, int k, int n, int quant_mode, int n_bufs, int w
     return rc;
 }
 
+// Per-launch device times of matmul_i8_f32 at (m, k, n) over n_bufs weight
+// copies.  path 0: the route matmul_i8_f32 takes (the GEMV up to GEMV_MAX_M
+// activation rows, the MFMA GEMM above); 1: the GEMV; 2: the GEMM (its bf16
+// activation split included, as matmul_i8_f32 runs it).
+int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_bufs, int warmup, int iters,
+                          double *per_launch_us, double *avg_us, double *bytes_per_launch) {
+    SCRY_REQUIRE_INIT();
+    if (m <= 0 || k <= 0 || n <= 0 || n_bufs <= 0 || iters <= 0 || !avg_us || path < 0 || path > 2 ||
+        (quant_mode != SCRY_QUANT_PER_TENSOR && quant_mode != SCRY_QUANT_BLOCK32))
+        return set_error(SCRY_ERR_INVALID, "bench_qgemv_dist: bad arguments");
+    const bool gemm = path == 2 || (path == 0 && m > GEMV_MAX_M);
+    if (!gemm && m > GEMV_MAX_M) return set_error(SCRY_ERR_INVALID, "bench_qgemv_dist: the GEMV takes <= %d rows", GEMV_MAX_M);
+    hipStream_t s = ctx().stream;
+    std::vector<Packed> W(n_bufs);
+    float *x = nullptr, *y = nullptr;
+    unsigned short *pl = nullptr;
+    const int mp = prefill_rows_pad(m), ld = prefill_k_pad(k);
+    int rc = dev_alloc((void **)&x, sizeof(float) * (size_t)m * k);
+    if (!rc) rc = dev_alloc((void **)&y, sizeof(float) * (size_t)m * n);
+    if (!rc) rc = launch_fill_f32(x, (size_t)m * k, 0.5f, s);
+    if (!rc && gemm) rc = dev_alloc((void **)&pl, sizeof(unsigned short) * 2 * (size_t)mp * ld);
+    if (!rc && gemm) rc = launch_fill_u32((unsigned *)pl, (size_t)mp * ld, 0u, s);
+    for (int b = 0; b < n_bufs && !rc; b++) {
+        Packed &P = W[b];
+        P.k = k;
+        P.n = n;
+        P.kp = round_up(k, 16);
+        P.rows = n;
+        P.scale = 1.0f / 127.0f;
+        rc = dev_alloc((void **)&P.d, P.bytes());
+        if (!rc) rc = launch_fill_u32((unsigned *)P.d, P.bytes() / 4, 0x8a7f9180u + b, s);
+        if (!rc && quant_mode == SCRY_QUANT_BLOCK32) {
+            P.nb = (k + 31) / 32;
+            rc = dev_alloc((void **)&P.s32, sizeof(float) * (size_t)n * P.nb);
+            if (!rc) rc = launch_fill_f32(P.s32, (size_t)n * P.nb, 1.0f / 127.0f, s);
+        }
+    }
+    auto launch = [&](int i) {
+        if (!gemm) {
+            GemvArgs g;
+            g.w = &W[i % n_bufs];
+            g.x = x;
+            g.ldx = k;
+            g.m = m;
+            g.y = y;
+            g.ldy = n;
+            return launch_qgemv(EPI_STORE, g, s);
+        }
+        SCRY_TRY(launch_split(x, k, m, k, pl, pl + (size_t)mp * ld, ld, s));
+        PrefillGemm g;
+        g.w = &W[i % n_bufs];
+        g.ahi = pl;
+        g.alo = pl + (size_t)mp * ld;
+        g.lda = ld;
+        g.M = m;
+        g.c = y;
+        g.ldc = n;
+        return launch_gemm(PF_STORE, g, s);
+    };
+    for (int i = 0; i < warmup && !rc; i++) rc = launch(i);
+    std::vector<hipEvent_t> ev;
+    const int nev = per_launch_us ? iters + 1 : 0;
+    for (int i = 0; i < nev + 2 && !rc; i++) {
+        hipEvent_t e = nullptr;
+        hipError_t he = hipEventCreate(&e);
+        if (he != hipSuccess) rc = hip_fail(he, "event create", __FILE__, __LINE__);
+        else ev.push_back(e);
+    }
+    // the average: back-to-back launches between two events
+    if (!rc) {
+        hipError_t e = hipEventRecord(ev[0], s);
+        for (int i = 0; i < iters && !rc && e == hipSuccess; i++) rc = launch(i);
+        if (!rc && e == hipSuccess) e = hipEventRecord(ev[1], s);
+        if (!rc && e == hipSuccess) e = hipEventSynchronize(ev[1]);
+        float f = 0.f;
+        if (!rc && e == hipSuccess) e = hipEventElapsedTime(&f, ev[0], ev[1]);
+        if (!rc && e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
+        if (!rc) *avg_us = 1000.0 * f / iters;
+    }
+    // the distribution: an event between every two launches
+    if (!rc && per_launch_us) {
+        hipError_t e = hipEventRecord(ev[2], s);
+        for (int i = 0; i < iters && !rc && e == hipSuccess; i++) {
+            rc = launch(i);
+            if (!rc) e = hipEventRecord(ev[3 + i], s);
+        }
+        if (!rc && e == hipSuccess) e = hipEventSynchronize(ev[2 + iters]);
+        for (int i = 0; i < iters && !rc && e == hipSuccess; i++) {
+            float f = 0.f;
+            e = hipEventElapsedTime(&f, ev[2 + i], ev[3 + i]);
+            per_launch_us[i] = 1000.0 * f;
+        }
+        if (!rc && e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
+    }
+    if (bytes_per_launch) {
+        const double scales = quant_mode == SCRY_QUANT_BLOCK32 ? 4.0 * n * ((k + 31) / 32) : 4.0;
+        *bytes_per_launch = (double)k * n + scales + 4.0 * m * k + 4.0 * m * n;
+    }
+    for (auto e : ev) (void)hipEventDestroy(e);
+    (void)hipStreamSynchronize(s);
+    for (auto &P : W) packed_free(P);
+    dev_free(x);
+    dev_free(y);
+    dev_free(pl);
+    return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1474,6 +1581,13 @@ int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, i
                          int iters, double *avg_us, double *bytes_per_launch) {
     API_LOCK;
     return bench_qgemv_impl(m_rows, k, n, quant_mode, n_bufs, warmup, iters, false, avg_us, bytes_per_launch);
+}
+
+int scry_hip_bench_qgemv_dist(int m, int k, int n, int quant_mode, int path, int n_bufs, int warmup, int iters,
+                              double *per_launch_us, double *avg_us, double *bytes_per_launch) {
+    API_LOCK;
+    return bench_qgemv_dist_impl(m, k, n, quant_mode, path, n_bufs, warmup, iters, per_launch_us, avg_us,
+                                 bytes_per_launch);
 }
 
 int scry_hip_bench_gemv_bf16(int m_rows, int k, int n, int n_bufs, int warmup, int iters, double *avg_us,

@@ -316,3 +316,15 @@ def bench_qgemv(m: int, k: int, n: int, quant_mode: int = QUANT_PER_TENSOR, n_bu
     call("scry_hip_bench_qgemv", m, k, n, quant_mode, n_bufs, warmup, iters, C.byref(us),
          C.byref(b))
     return us.value, b.value
+
+
+def bench_qgemv_dist(m: int, k: int, n: int, quant_mode: int = QUANT_PER_TENSOR, path: int = 0,
+                     n_bufs: int = 32, warmup: int = 50, iters: int = 1000):
+    """(per-launch device times [iters] in us, back-to-back average us, algorithmic
+    bytes per launch) of matmul_i8_f32 at (m, k, n); path 0 = the automatic
+    route, 1 = the GEMV, 2 = the MFMA GEMM."""
+    per = np.empty(iters, np.float64)
+    us, b = C.c_double(), C.c_double()
+    call("scry_hip_bench_qgemv_dist", m, k, n, quant_mode, path, n_bufs, warmup, iters, per.ctypes.data,
+         C.byref(us), C.byref(b))
+    return per, us.value, b.value
