@@ -197,8 +197,9 @@ def gemv_micro(EL, iters: int = 1000, n_bufs: int = 32) -> list:
     """BASELINE configs 2 and 3: matmul_i8_f32 at batch 1, 4 and 16 with the
     reference's block (32-wide) scales and with per-tensor scales; iters timed
     launches over n_bufs distinct weight copies (more than the 256 MB Infinity
-    Cache), per-launch device times (an event between launches) -> median and
-    p10 / p90, plus the back-to-back average.  At 16 rows both the GEMV and the
+    Cache): the back-to-back average, and median and p10 / p90 of the
+    per-launch device time of each group of 8 consecutive launches (an event
+    between single launches would add its own gap to every sample).  At 16 rows both the GEMV and the
     MFMA GEMM are timed (matmul_i8_f32 routes 16 rows to the GEMV)."""
     import numpy as np
     out = []
@@ -206,14 +207,15 @@ def gemv_micro(EL, iters: int = 1000, n_bufs: int = 32) -> list:
         for qm, qname in ((EL.QUANT_BLOCK32, "block-32"), (EL.QUANT_PER_TENSOR, "per-tensor")):
             for m in ms:
                 for path in ((1, 2) if m == 16 else (0,)):
-                    per, avg, b = EL.bench_qgemv_dist(m, k, n, qm, path, n_bufs, 50, iters)
+                    per, avg, b = EL.bench_qgemv_dist(m, k, n, qm, path, n_bufs, 50, iters, 8)
                     p10, med, p90 = (float(v) for v in np.percentile(per, [10, 50, 90]))
                     fl = 2.0 * m * k * n
                     e = {"case": name, "k": k, "n": n, "m": m, "scales": qname,
                          "kernel": "mfma gemm" if path == 2 else "gemv",
-                         "iters": iters, "weight_buffers": n_bufs,
+                         "iters": iters, "weight_buffers": n_bufs, "group": 8,
                          "median_us": round(med, 3), "p10_us": round(p10, 3), "p90_us": round(p90, 3),
                          "avg_us": round(avg, 3), "bytes": int(b),
+                         "gbs_avg": round(b / avg / 1e3, 1), "hbm_frac_avg": round(b / avg / 1e3 / HBM_PEAK_GBS, 4),
                          "gbs_median": round(b / med / 1e3, 1), "hbm_frac_median": round(b / med / 1e3 / HBM_PEAK_GBS, 4),
                          "tflops_median": round(fl / med / 1e6, 2)}
                     out.append(e)

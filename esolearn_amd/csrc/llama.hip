@@ -1471,9 +1471,10 @@ int bench_qgemv_impl(int m_rows, int k, int n, int quant_mode, int n_bufs, int w
 // activation rows, the MFMA GEMM above); 1: the GEMV; 2: the GEMM (its bf16
 // activation split included, as matmul_i8_f32 runs it).
 int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_bufs, int warmup, int iters,
-                          double *per_launch_us, double *avg_us, double *bytes_per_launch) {
+                          int group, double *per_launch_us, double *avg_us, double *bytes_per_launch) {
     SCRY_REQUIRE_INIT();
     if (m <= 0 || k <= 0 || n <= 0 || n_bufs <= 0 || iters <= 0 || !avg_us || path < 0 || path > 2 ||
+        group < 1 || iters % group ||
         (quant_mode != SCRY_QUANT_PER_TENSOR && quant_mode != SCRY_QUANT_BLOCK32))
         return set_error(SCRY_ERR_INVALID, "bench_qgemv_dist: bad arguments");
     const bool gemm = path == 2 || (path == 0 && m > GEMV_MAX_M);
@@ -1527,7 +1528,8 @@ int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_b
     };
     for (int i = 0; i < warmup && !rc; i++) rc = launch(i);
     std::vector<hipEvent_t> ev;
-    const int nev = per_launch_us ? iters + 1 : 0;
+    const int ng = iters / group;
+    const int nev = per_launch_us ? ng + 1 : 0;
     for (int i = 0; i < nev + 2 && !rc; i++) {
         hipEvent_t e = nullptr;
         hipError_t he = hipEventCreate(&e);
@@ -1545,18 +1547,20 @@ int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_b
         if (!rc && e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
         if (!rc) *avg_us = 1000.0 * f / iters;
     }
-    // the distribution: an event between every two launches
+    // the distribution: an event after every `group` launches (per-launch
+    // average of each group; an event between single launches adds its own
+    // gap to every sample)
     if (!rc && per_launch_us) {
         hipError_t e = hipEventRecord(ev[2], s);
         for (int i = 0; i < iters && !rc && e == hipSuccess; i++) {
             rc = launch(i);
-            if (!rc) e = hipEventRecord(ev[3 + i], s);
+            if (!rc && (i + 1) % group == 0) e = hipEventRecord(ev[3 + i / group], s);
         }
-        if (!rc && e == hipSuccess) e = hipEventSynchronize(ev[2 + iters]);
-        for (int i = 0; i < iters && !rc && e == hipSuccess; i++) {
+        if (!rc && e == hipSuccess) e = hipEventSynchronize(ev[2 + ng]);
+        for (int i = 0; i < ng && !rc && e == hipSuccess; i++) {
             float f = 0.f;
             e = hipEventElapsedTime(&f, ev[2 + i], ev[3 + i]);
-            per_launch_us[i] = 1000.0 * f;
+            per_launch_us[i] = 1000.0 * f / group;
         }
         if (!rc && e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
     }
@@ -1584,9 +1588,9 @@ int scry_hip_bench_qgemv(int m_rows, int k, int n, int quant_mode, int n_bufs, i
 }
 
 int scry_hip_bench_qgemv_dist(int m, int k, int n, int quant_mode, int path, int n_bufs, int warmup, int iters,
-                              double *per_launch_us, double *avg_us, double *bytes_per_launch) {
+                              int group, double *per_group_us, double *avg_us, double *bytes_per_launch) {
     API_LOCK;
-    return bench_qgemv_dist_impl(m, k, n, quant_mode, path, n_bufs, warmup, iters, per_launch_us, avg_us,
+    return bench_qgemv_dist_impl(m, k, n, quant_mode, path, n_bufs, warmup, iters, group, per_group_us, avg_us,
                                  bytes_per_launch);
 }
 

@@ -319,12 +319,13 @@ def bench_qgemv(m: int, k: int, n: int, quant_mode: int = QUANT_PER_TENSOR, n_bu
 
 
 def bench_qgemv_dist(m: int, k: int, n: int, quant_mode: int = QUANT_PER_TENSOR, path: int = 0,
-                     n_bufs: int = 32, warmup: int = 50, iters: int = 1000):
-    """(per-launch device times [iters] in us, back-to-back average us, algorithmic
-    bytes per launch) of matmul_i8_f32 at (m, k, n); path 0 = the automatic
-    route, 1 = the GEMV, 2 = the MFMA GEMM."""
-    per = np.empty(iters, np.float64)
+                     n_bufs: int = 32, warmup: int = 50, iters: int = 1000, group: int = 8):
+    """(per-launch device times of each group of `group` launches [iters/group]
+    in us, back-to-back average us, algorithmic bytes per launch) of
+    matmul_i8_f32 at (m, k, n); path 0 = the automatic route, 1 = the GEMV,
+    2 = the MFMA GEMM."""
+    per = np.empty(iters // group, np.float64)
     us, b = C.c_double(), C.c_double()
-    call("scry_hip_bench_qgemv_dist", m, k, n, quant_mode, path, n_bufs, warmup, iters, per.ctypes.data,
-         C.byref(us), C.byref(b))
+    call("scry_hip_bench_qgemv_dist", m, k, n, quant_mode, path, n_bufs, warmup, iters, group,
+         per.ctypes.data, C.byref(us), C.byref(b))
     return per, us.value, b.value

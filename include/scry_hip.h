@@ -384,13 +384,14 @@ int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq
 int scry_hip_bench_qgemv(int m, int k, int n, int quant_mode, int n_bufs, int warmup, int iters,
                          double *avg_us, double *bytes_per_launch);
 /* matmul_i8_f32 (m, k, n) launched `iters` times over n_bufs weight copies:
- * *avg_us from back-to-back launches, and (if per_launch_us is not NULL) the
- * device time of each launch with an event between launches, for the
- * distribution.  path 0: the route matmul_i8_f32 takes (GEMV up to 16
- * activation rows, MFMA GEMM above); 1: the GEMV; 2: the MFMA GEMM (with its
- * bf16 activation split).  quant_mode: per-tensor or block-32 scales. */
+ * *avg_us from back-to-back launches, and (if per_group_us is not NULL) the
+ * per-launch device time of each group of `group` consecutive launches
+ * (iters / group entries; iters a multiple of group), for the distribution.
+ * path 0: the route matmul_i8_f32 takes (GEMV up to 16 activation rows, MFMA
+ * GEMM above); 1: the GEMV; 2: the MFMA GEMM (with its bf16 activation
+ * split).  quant_mode: per-tensor or block-32 scales. */
 int scry_hip_bench_qgemv_dist(int m, int k, int n, int quant_mode, int path, int n_bufs, int warmup, int iters,
-                              double *per_launch_us, double *avg_us, double *bytes_per_launch);
+                              int group, double *per_group_us, double *avg_us, double *bytes_per_launch);
 /* The same with a bias row (matmul_i8_f32_bias, cpu.rs:553-570; the quantized
  * Linear::forward, linear.rs:67-94): per-tensor int8, bias added in the
  * GEMV's store epilogue. */
