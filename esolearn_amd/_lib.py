@@ -84,6 +84,7 @@ SIGNATURES = {
     "scry_hip_scatter_rows": [vp, vp, i32, i32, i32, i32],
     "scry_hip_argmax": [vp, P(i64)],
     "scry_hip_sample_token": [vp, P(SamplingConfigC), P(u64), P(i64)],
+    "scry_hip_sample_token_noalloc": [vp, P(SamplingConfigC), P(u64), P(i64)],
     "scry_hip_normal_vec": [P(u64), sz, f32, f32, P(vp)],
     "scry_hip_init_bf16": [i32],
     "scry_hip_set_bf16_mode": [i32],

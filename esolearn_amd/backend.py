@@ -310,6 +310,18 @@ class HipBackend:
         rng.state = int(st.value)
         return int(out.value)
 
+    @staticmethod
+    def sample_token_noalloc(logits: Storage, config, rng) -> int:
+        """sample_token with no device allocation (a static scratch array per
+        GPU, vocabularies up to 262144): same result and rng advance."""
+        sc = _lib.SamplingConfigC(float(config.temperature), int(config.top_k),
+                                  float(config.top_p), int(config.max_tokens))
+        st = C.c_uint64(rng.state)
+        out = C.c_int64()
+        call("scry_hip_sample_token_noalloc", logits.h, C.byref(sc), C.byref(st), C.byref(out))
+        rng.state = int(st.value)
+        return int(out.value)
+
     # ---- the rest of the trait surface (mod.rs; CPU semantics cpu.rs)
     @staticmethod
     def ones(n: int) -> Storage:

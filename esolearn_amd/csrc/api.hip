@@ -301,6 +301,7 @@ int scry_hip_init(int device) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return set_error(SCRY_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only",
                          device, prop.gcnArchName);
+    SCRY_TRY(noalloc_setup(device));  // the device address of the static sampler scratch
     SCRY_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
     c.bf16 = false;
     c.device = device;

@@ -161,6 +161,10 @@ size_t sample_prep_bytes(int V);
 int launch_sample(const float *logits, int V, const scry_sampling_config &sc, double *ws,
                   unsigned long long *rng, DevState *st, int64_t *tokens, void *prep, hipStream_t s);
 
+// noalloc.hip: with `device` current, look up the device address of the
+// static scratch of scry_hip_sample_token_noalloc (once per device)
+int noalloc_setup(int device);
+
 // safetensors.hip: memory-mapped safetensors shards and the device dtype
 // widening of the checkpoint loader
 enum { ST_OTHER = 0, ST_F32 = 1, ST_BF16 = 2, ST_F16 = 3 };
