@@ -26,6 +26,8 @@ Also reported:
                 batched prefill of the first 2047 tokens of each prompt on the
                 matrix cores, then 64 greedy decode steps per sequence
 
+  bf16_decode   the same decode with the model in bf16 (the reference's bf16
+                feature): tok/s and the per-projection GEMV rates
   gemv_micro    BASELINE configs 2 and 3: matmul_i8_f32 at 1, 4 and 16 rows,
                 block-32 and per-tensor scales, 1000 launches over 32 weight
                 copies: median / p10 / p90 per-launch device time
@@ -245,6 +247,32 @@ def weight_bytes(cfg) -> int:
     return L * per_layer + V * h + 4 * (5 * L + 1)
 
 
+def bf16_decode(E, EL, cfg, prompt, warmup: int, steps: int, proj_iters: int) -> dict:
+    """The same decode with the model in bf16 (the reference's bf16 feature:
+    bf16 weights, activations cast to bf16 at each projection, f32
+    accumulation), device init of the same seeded weights."""
+    model = E.LlamaModel.new_random(cfg, seed=0, quant_mode=EL.QUANT_BF16, init_on_device=True)
+    try:
+        ms, toks = model.bench_decode(prompt, warmup, steps)
+        proj = {}
+        for name, tid in (("qkv", EL.T_QKV), ("o", EL.T_O), ("gate_up", EL.T_GATE),
+                          ("down", EL.T_DOWN), ("lm_head", EL.T_LM_HEAD)):
+            us, b = model.time_projection(tid, proj_iters)
+            proj[name] = {"avg_us": round(us, 3), "bytes": int(b), "gbs": round(b / us / 1e3, 1),
+                          "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    finally:
+        model.free()
+    tok_s = steps / (ms / 1000.0)
+    wb = 2 * (weight_bytes(cfg) - 4 * (5 * cfg.n_layers + 1))
+    print(f"[bench] bf16 decode {tok_s:.1f} tok/s; gate_up {proj['gate_up']['gbs']} GB/s",
+          file=sys.stderr, flush=True)
+    return {"workload": "llama2-7b-shape bf16 batch-1 greedy decode, same prompt and steps",
+            "tok_s": round(tok_s, 2), "ms_per_step": round(ms / steps, 4),
+            "weight_bytes_per_token": wb,
+            "decode_roofline_frac": round(tok_s * wb / (HBM_PEAK_GBS * 1e9), 4),
+            "greedy_tokens_head": [int(t) for t in toks[:8]], "projections": proj}
+
+
 def cpu_baseline(model, cfg, prompt, n_tok: int) -> dict:
     """Oracle decode on the GPU model's own int8 weights: reference-faithful
     single-threaded, and the bit-identical all-core mode beside it."""
@@ -321,6 +349,7 @@ def main() -> int:
     ap.add_argument("--gemv-only", action="store_true",
                     help="the config 2 / 3 isolated GEMV micro-benchmark only")
     ap.add_argument("--no-gemv", action="store_true", help="skip the config 2 / 3 micro-benchmark")
+    ap.add_argument("--no-bf16-decode", action="store_true", help="skip the bf16-model decode line")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -413,6 +442,8 @@ def main() -> int:
         print(f"[bench] cpu baseline: {args.cpu_tokens} tokens", file=sys.stderr, flush=True)
         cpu = cpu_baseline(model, cfg, prompt, args.cpu_tokens)
     model.free()
+    bf16 = None if args.no_bf16_decode else bf16_decode(E, EL, cfg, prompt, args.warmup, args.steps,
+                                                        args.proj_iters)
     gemv = None if args.no_gemv else gemv_micro(EL)
     pre = None if args.no_prefill else prefill_config5(E)
 
@@ -444,6 +475,7 @@ def main() -> int:
         "projections": proj,
         "greedy_tokens_head": [int(t) for t in toks[:8]],
         "sampled_decode": sampled,
+        "bf16_decode": bf16,
         "gemv_micro": gemv,
         "prefill": pre,
     }

@@ -7,7 +7,7 @@ interface: ``HipBackend`` (backend trait methods), ``LlamaModel`` /
 """
 from .backend import HipBackend, I8Storage, Storage, init  # noqa: F401
 from .linear import Linear, QuantState, normal_vec  # noqa: F401
-from .llama import (QUANT_BLOCK32, QUANT_PER_TENSOR, LlamaConfig, LlamaKvCache,  # noqa: F401
+from .llama import (QUANT_BF16, QUANT_BLOCK32, QUANT_PER_TENSOR, LlamaConfig, LlamaKvCache,  # noqa: F401
                     LlamaModel, Rng, SamplingConfig, bench_qgemv, generate)
 from ._lib import ScryHipError  # noqa: F401
 from . import synth  # noqa: F401

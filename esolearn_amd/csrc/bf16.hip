@@ -31,6 +31,35 @@ __device__ __forceinline__ u16 to_bf16(float x) {
 }
 __device__ __forceinline__ float from_bf16(unsigned h) { return __uint_as_float(h << 16); }
 
+// A model's f32 weight W[k, n] (or [n, k] when src_nk) as bf16 rows of the
+// GEMV layout: output j -> packed row (j / grp) * stride + off + j % grp,
+// kpe values per row (k, then zeros), each the reference's cast.  64 x 64
+// tiles transpose through LDS so both the reads and the writes are coalesced.
+__global__ __launch_bounds__(256) void k_pack_model_bf16(const float *__restrict__ w, int k, int n, int src_nk,
+                                                         u16 *__restrict__ dst, int kpe, int grp, int stride,
+                                                         int off) {
+    __shared__ u16 tile[64][66];  // [p][j]
+    const int j0 = blockIdx.x * 64, p0 = blockIdx.y * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        // src_nk: rows j, consecutive p; else rows p, consecutive j
+        const int p = src_nk ? p0 + tx : p0 + i, j = src_nk ? j0 + i : j0 + tx;
+        u16 v = 0;
+        if (p < k && j < n) v = to_bf16(src_nk ? w[(size_t)j * k + p] : w[(size_t)p * n + j]);
+        if (src_nk)
+            tile[tx][i] = v;
+        else
+            tile[i][tx] = v;
+    }
+    __syncthreads();
+    for (int jj = ty; jj < 64; jj += 4) {
+        const int j = j0 + jj, p = p0 + tx;
+        if (j >= n || p >= kpe) continue;
+        const size_t row = (size_t)(j / grp) * stride + off + j % grp;
+        dst[row * kpe + p] = tile[tx][jj];
+    }
+}
+
 __global__ __launch_bounds__(256) void k_cast_bf16(const float *__restrict__ x, u16 *__restrict__ y, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) y[i] = to_bf16(x[i]);
 }
@@ -173,6 +202,14 @@ unsigned grid_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256,
 }  // namespace
 
 int bf16_row_pad(int k) { return (k + 63) / 64 * 64; }
+
+int launch_pack_model_bf16(const float *w, int k, int n, int src_nk, unsigned short *dst, int kpe, int grp,
+                           int stride, int off, hipStream_t s) {
+    dim3 g((n + 63) / 64, (kpe + 63) / 64);
+    hipLaunchKernelGGL(k_pack_model_bf16, g, dim3(256), 0, s, w, k, n, src_nk, dst, kpe, grp, stride, off);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
 
 int launch_cast_bf16(const float *x, size_t n, unsigned short *y, hipStream_t s) {
     if (n == 0) return SCRY_OK;

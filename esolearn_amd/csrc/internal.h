@@ -53,6 +53,9 @@ void dev_free(void *p);
 // q XOR 0x80 (= q + 128 as an unsigned byte), padding bytes 0x80 (q = 0).
 // A fused gate/up pair interleaves rows in groups of four:
 // gate[2t], gate[2t+1], up[2t], up[2t+1].
+// bf16 weights (a bf16-mode model) use the same rows of bf16 values (the
+// reference's cast of the f32 weight), kp = 2 * (k rounded up to 8) bytes,
+// padding 0.
 struct Packed {
     uint8_t *d = nullptr;
     int k = 0;         // logical in-dimension
@@ -64,6 +67,7 @@ struct Packed {
     float scale2 = 0.f;// up scale when fused
     float *s32 = nullptr; // block-32 scales [rows][nb] (packed-row order) or nullptr
     int nb = 0;
+    int bf16 = 0;         // 1: rows of bf16 values (no scales)
     size_t bytes() const { return (size_t)rows * kp; }
 };
 
@@ -281,6 +285,9 @@ int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, i
 // bf16.hip -- bf16 mode: the reference's cast, widening, B-operand rows
 // [n][kp] (kp = bf16_row_pad(k)), the GEMM activation plane, the bf16 GEMV
 int bf16_row_pad(int k);
+// a model's f32 weight as bf16 GEMV rows (row mapping as launch_quant_pack; kpe values per row)
+int launch_pack_model_bf16(const float *w, int k, int n, int src_nk, unsigned short *dst, int kpe, int grp,
+                           int stride, int off, hipStream_t s);
 int launch_cast_bf16(const float *x, size_t n, unsigned short *y, hipStream_t s);
 int launch_round_bf16(const float *x, size_t n, float *y, hipStream_t s);
 int launch_widen_bf16(const unsigned short *x, size_t n, float *y, hipStream_t s);

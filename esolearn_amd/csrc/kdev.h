@@ -12,6 +12,28 @@ constexpr int TPB = 256;  // threads per workgroup (4 waves of 64)
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// 8 bf16 weights (little-endian pairs in w) times 8 activations: the bf16
+// value is the upper half of its f32, so each product is exact in f32
+__device__ __forceinline__ float dot8_bf16(u32x4 w, float4 x0, float4 x1, float acc) {
+    acc = fmaf(x0.x, __uint_as_float(w.x << 16), acc);
+    acc = fmaf(x0.y, __uint_as_float(w.x & 0xffff0000u), acc);
+    acc = fmaf(x0.z, __uint_as_float(w.y << 16), acc);
+    acc = fmaf(x0.w, __uint_as_float(w.y & 0xffff0000u), acc);
+    acc = fmaf(x1.x, __uint_as_float(w.z << 16), acc);
+    acc = fmaf(x1.y, __uint_as_float(w.z & 0xffff0000u), acc);
+    acc = fmaf(x1.z, __uint_as_float(w.w << 16), acc);
+    acc = fmaf(x1.w, __uint_as_float(w.w & 0xffff0000u), acc);
+    return acc;
+}
+
+// The bf16 feature's cast (kernels.rs:629-633) as an f32 value: round to
+// nearest even by adding 0x7fff plus the lowest kept bit to the f32 bits in
+// 32-bit unsigned arithmetic, then drop the low half.
+__device__ __forceinline__ float bf16_cast(float x) {
+    const unsigned b = __float_as_uint(x);
+    return __uint_as_float((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
+}
+
 __device__ __forceinline__ float dot16(u32x4 w, float4 x0, float4 x1, float4 x2, float4 x3,
                                        float acc) {
     acc = fmaf(x0.x, (float)(w.x & 0xffu), acc);

@@ -124,6 +124,11 @@ int sync_stream() {
 int quant_into(scry_llama m, const float *dw, int k, int n, int src_nk, Packed &P, int grp,
                int stride, int off, bool second) {
     hipStream_t s = ctx().stream;
+    if (m->quant_mode == SCRY_QUANT_BF16) {
+        (void)second;
+        SCRY_TRY(launch_pack_model_bf16(dw, k, n, src_nk, (unsigned short *)P.d, P.kp / 2, grp, stride, off, s));
+        return sync_stream();
+    }
     if (m->quant_mode == SCRY_QUANT_PER_TENSOR) {
         SCRY_TRY(launch_absmax(dw, (size_t)k * n, m->bits, s));
         unsigned int bits = 0;
@@ -156,7 +161,9 @@ int quant_into(scry_llama m, const float *dw, int k, int n, int src_nk, Packed &
 int alloc_packed(scry_llama m, Packed &P, int k, int n, int rows, int fused) {
     P.k = k;
     P.n = n;
-    P.kp = round_up(k, 16);
+    P.bf16 = m->quant_mode == SCRY_QUANT_BF16;
+    P.kp = P.bf16 ? 2 * round_up(k, 8) : round_up(k, 16);
+    P.scale = P.scale2 = 1.0f;
     P.rows = rows;
     P.fused = fused;
     SCRY_TRY(dev_alloc((void **)&P.d, P.bytes()));
@@ -236,7 +243,7 @@ void model_free(scry_llama m) {
 
 int model_alloc(const scry_llama_config *cfg, int quant_mode, scry_llama *out) {
     if (!cfg || !out) return set_error(SCRY_ERR_INVALID, "null argument");
-    if (quant_mode != SCRY_QUANT_PER_TENSOR && quant_mode != SCRY_QUANT_BLOCK32)
+    if (quant_mode != SCRY_QUANT_PER_TENSOR && quant_mode != SCRY_QUANT_BLOCK32 && quant_mode != SCRY_QUANT_BF16)
         return set_error(SCRY_ERR_INVALID, "unknown quant mode %d", quant_mode);
     const int h = cfg->hidden_size, nh = cfg->n_heads, nkv = cfg->n_kv_heads;
     if (h <= 0 || nh <= 0 || nkv <= 0 || h % nh || nh % nkv || cfg->vocab_size <= 0 ||
@@ -645,6 +652,8 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
     if (n_seq < 1 || n_seq > PF_MAX_SEQS || seq < 1)
         return set_error(SCRY_ERR_INVALID, "prefill: n_seq must be 1..%d and seq >= 1", PF_MAX_SEQS);
     if (m->hd > 128) return set_error(SCRY_ERR_UNSUPPORTED, "prefill: head_dim %d > 128", m->hd);
+    if (m->quant_mode == SCRY_QUANT_BF16)
+        return set_error(SCRY_ERR_UNSUPPORTED, "prefill: the batched prefill runs on int8 weights (bf16 model: decode)");
     PrefillSeqs t{};
     for (int i = 0; i < n_seq; i++) {
         scry_kv_cache c = cs[i];
@@ -1011,6 +1020,8 @@ int scry_hip_llama_get_qtensor(scry_llama m, int tensor_id, int layer, int8_t *h
     API_LOCK;
     SCRY_REQUIRE_INIT();
     if (!m || !host) return set_error(SCRY_ERR_INVALID, "null argument");
+    if (m->quant_mode == SCRY_QUANT_BF16)
+        return set_error(SCRY_ERR_UNSUPPORTED, "get_qtensor: the model holds bf16 weights, not int8");
     const Packed *P = nullptr;
     int grp = 1, stride = 1, off = 0, nk = 0;
     float sc = 0.f;
@@ -1356,10 +1367,10 @@ int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int i
         default: rc = set_error(SCRY_ERR_INVALID, "time_projection: tensor id %d", tensor_id);
     }
     if (P) {
-        // algorithmic bytes: int8 weights + scales + activation in + result out
+        // algorithmic bytes: weights (int8 + scales, or bf16) + activation in + result out
         const double out_n = tensor_id == SCRY_T_GATE ? P->rows / 2.0 : (double)P->rows;
-        const double scales = P->s32 ? 4.0 * P->rows * P->nb : (P->fused ? 8.0 : 4.0);
-        bytes = (double)P->rows * P->k + scales + 4.0 * P->k + 4.0 * out_n;
+        const double scales = P->bf16 ? 0.0 : P->s32 ? 4.0 * P->rows * P->nb : (P->fused ? 8.0 : 4.0);
+        bytes = (double)P->rows * P->k * (P->bf16 ? 2.0 : 1.0) + scales + 4.0 * P->k + 4.0 * out_n;
     }
     const int nl = tensor_id == SCRY_T_LM_HEAD ? 1 : m->L;
     // the RMSNorm'd GEMVs read the pre-scaled row and partial sums that the

@@ -28,6 +28,13 @@
 //              from that GEMV's per-workgroup sum(x^2) partials.
 // Both sums of squares are reduced after the staging barrier, in a fixed order.
 //
+// bf16 weights (the reference's bf16 feature, cuda.rs:1206-1290) take the
+// same path with a weight type WT = WT_BF16: rows of bf16 values (512 per
+// 1 KiB chunk), and activations normalised (with the RMSNorm prologues) and
+// rounded with the reference's bf16 cast while they are staged, since the
+// reference's bf16 matmul rounds its activation operand.  Each product of two
+// bf16 values is exact in f32; the accumulation is f32.
+//
 // Epilogues fused into the same pass (llama.rs:371-511):
 //   EPI_STORE   y = acc (+ bias)                     -- matmul_i8_f32[_bias]
 //   EPI_RESID   y = resid + acc; optionally x*g_next and sum(y^2) per workgroup
@@ -92,9 +99,17 @@ constexpr Shape shape_for(int nch, int mt) {
            : nch == 4  ? Shape{1, 8, 4}
            : nch == 11 ? Shape{1, 8, 8}
            : nch == 14 ? Shape{1, 8, 7}
+           : nch == 8  ? Shape{1, 8, 8}  // bf16 rows, k = 4096
+           : nch == 22 ? Shape{1, 8, 8}  // bf16 rows, k = 11008
+           : nch == 28 ? Shape{1, 8, 7}  // bf16 rows, k = 14336
            : nch == 0  ? Shape{1, 8, 4}  // any k, one row: 8 rows per workgroup
                        : Shape{4, 4, 4};
 }
+
+// weight types
+enum { WT_I8 = 0, WT_I8B32 = 1, WT_BF16 = 2 };
+// activation values per 1 KiB weight chunk
+constexpr int chunk_vals(int wt) { return wt == WT_BF16 ? 512 : 1024; }
 
 // Activation row source for row mr (nullptr if mr >= m).  Only the
 // self-contained RMSNorm prologue (the first layer) reads the embedding row of
@@ -111,22 +126,37 @@ __device__ __forceinline__ const float *act_row(const KArgs &a, int mr) {
 // Thread t loads the float4s f4 = p*NT + t (p < XP) of a k-vector.  A wave
 // whose float4s all lie past k loads nothing (zeros).
 template <int XP, int NT>
-__device__ __forceinline__ void load_vec(const float *src, int k, int nch, float4 (&v)[XP]) {
+__device__ __forceinline__ void load_vec(const float *src, int k, int tot4, float4 (&v)[XP]) {
     const __amdgpu_buffer_rsrc_t r = make_rsrc(src, src ? (size_t)k * 4 : 0);
     const int tid = threadIdx.x;
 #pragma unroll
     for (int p = 0; p < XP; p++) {
         const int f4 = p * NT + tid;
         v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (src && f4 < nch * 256 && (f4 & ~63) * 4 < k) v[p] = bload16f(r, (unsigned)f4 << 4);
+        if (src && f4 < tot4 && (f4 & ~63) * 4 < k) v[p] = bload16f(r, (unsigned)f4 << 4);
     }
 }
 
 // One 1024-wide k chunk for RWT rows and MT activation rows.
-template <int MT, bool B32, int RWT>
+template <int MT, int WT, int RWT>
 __device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RWT], int c, const float *xs, int kc,
                                           const float *xsum, __amdgpu_buffer_rsrc_t sr, int nb,
-                                          const int (&wrow)[RWT], int lane, float (&acc)[MT][RWT]) {
+                                          const int (&wrow)[RWT], int lane, float (&acc)[MT][RWT],
+                                          int kp) {
+    constexpr bool B32 = WT == WT_I8B32;
+    if constexpr (WT == WT_BF16) {
+        // lane L holds bf16 values 8L .. 8L+7 of chunk c: x at c*512 + 4L (+256)
+        if ((c << 10) + (lane << 4) >= kp) return;  // past the row (the next row's bytes)
+#pragma unroll
+        for (int mi = 0; mi < MT; mi++) {
+            const float *xb = xs + mi * kc + (c << 9) + (lane << 2);
+            const float4 x0 = *(const float4 *)(xb);
+            const float4 x1 = *(const float4 *)(xb + 256);
+#pragma unroll
+            for (int r = 0; r < RWT; r++) acc[mi][r] = dot8_bf16(w[r], x0, x1, acc[mi][r]);
+        }
+        return;
+    }
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         const float *xb = xs + mi * kc + (c << 10) + (lane << 2);
@@ -152,21 +182,25 @@ __device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RWT], int c, const fl
     }
 }
 
-template <int EPI, int PRO, bool B32, int MT, int NCH>
+template <int EPI, int PRO, int WT, int MT, int NCH>
 __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
     constexpr Shape S = shape_for(NCH, MT);
     constexpr int RWT = S.rwt, NW = S.nw, PF = S.pf, RPW = RWT * NW, NT = 64 * NW;
-    constexpr int XP = ((NCH > 0 ? NCH : 16) * 256 + NT - 1) / NT;  // float4 per thread per row
+    constexpr bool B32 = WT == WT_I8B32, WB = WT == WT_BF16;
+    constexpr int CV = chunk_vals(WT);  // activation values per chunk
+    constexpr int XP = ((NCH > 0 ? NCH : (WB ? 32 : 16)) * (CV / 4) + NT - 1) / NT;  // float4 per thread per row
     constexpr bool NORM = PRO != PRO_PLAIN;
+    static_assert(!WB || MT == 1, "bf16 weights take one activation row per pass");
     static_assert(!NORM || MT == 1, "the RMSNorm prologues take one activation row");
     static_assert(EPI == EPI_STORE || MT == 1, "only the store epilogue takes several rows");
     static_assert(EPI == EPI_STORE || EPI == EPI_RESID || RPW % 4 == 0,
                   "the SwiGLU, QKV and logits epilogues combine rows in groups of 4");
     extern __shared__ float4 dyn4[];
     const int nch = NCH > 0 ? NCH : a.nch;
-    const int kc = nch << 10;
+    const int kc = nch * CV;
+    const int tot4 = kc >> 2;  // float4 slots of one staged activation row
     float *xs = reinterpret_cast<float *>(dyn4);  // [MT][kc] permuted activation rows
-    float *xsum = xs + MT * kc;                    // [MT][nch][64] per-lane 16-value sums
+    float *xsum = xs + MT * kc;                    // [MT][nch][64] per-lane 16-value sums (int8)
     __shared__ double s_ss[NW];  // per-wave sums of squares for the RMSNorm
     __shared__ float s_rstd;
     __shared__ float s_val[MT * RPW];
@@ -179,9 +213,9 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
     // chunks of every row: waiting for the activations leaves the weight
     // stream in flight
     float4 xr[XP];
-    load_vec<XP, NT>(act_row<PRO, MT>(a, m0), a.k, nch, xr);
+    load_vec<XP, NT>(act_row<PRO, MT>(a, m0), a.k, tot4, xr);
     float4 gw[PRO == PRO_NORM ? XP : 1];
-    if constexpr (PRO == PRO_NORM) load_vec<XP, NT>(a.norm_w, a.k, nch, gw);
+    if constexpr (PRO == PRO_NORM) load_vec<XP, NT>(a.norm_w, a.k, tot4, gw);
     // PRO_NORMP: this thread's share of the producer's partial sums
     // (unconditional clamped loads: no wait inside a branch)
     float ssv[PRO == PRO_NORMP ? SSW : 1];
@@ -223,9 +257,60 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
 
     // ---- 2. stage the activation rows into LDS with the per-lane sums
     double ssp = 0.0;
+    if constexpr (WB) {
+        // bf16: the RMSNorm scale first (cpu.rs:574-599; f64 sum of squares,
+        // reduced in a fixed order), then each value normalised and rounded
+        // with the reference's cast as it is staged
+        double rstd = 1.0;
+        if constexpr (NORM) {
+            if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+                for (int p = 0; p < XP; p++) {
+                    const float4 v = xr[p];
+                    ssp += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < SSW; j++)
+                    if (tid + NT * j < a.n_ss) ssp += ssv[j];
+            }
+            ssp = wave_sum_d_dpp(ssp);
+            if (lane == 0) s_ss[wave] = ssp;
+            __syncthreads();
+            double t = 0.0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) t += s_ss[w];
+            rstd = 1.0 / sqrt(t / (double)a.k + (double)a.eps);
+        }
+#pragma unroll
+        for (int p = 0; p < XP; p++) {
+            const int f4 = p * NT + tid;
+            if (f4 < tot4) {
+                float4 v = xr[p];
+                if constexpr (PRO == PRO_NORM) {  // f32(f64(x) * rstd * f64(w))
+                    v.x = (float)((double)v.x * rstd * (double)gw[p].x);
+                    v.y = (float)((double)v.y * rstd * (double)gw[p].y);
+                    v.z = (float)((double)v.z * rstd * (double)gw[p].z);
+                    v.w = (float)((double)v.w * rstd * (double)gw[p].w);
+                } else if constexpr (PRO == PRO_NORMP) {  // the producer's x * w, times rstd
+                    v.x = (float)((double)v.x * rstd);
+                    v.y = (float)((double)v.y * rstd);
+                    v.z = (float)((double)v.z * rstd);
+                    v.w = (float)((double)v.w * rstd);
+                }
+                v.x = bf16_cast(v.x);
+                v.y = bf16_cast(v.y);
+                v.z = bf16_cast(v.z);
+                v.w = bf16_cast(v.w);
+                // value 512c + 8L + 4j + e (lane L's j-th float4 of chunk c)
+                const int c = f4 >> 7, w = f4 & 127;
+                *(float4 *)(xs + (c << 9) + ((w & 1) << 8) + ((w >> 1) << 2)) = v;
+            }
+        }
+    } else {
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
-        if (mi > 0) load_vec<XP, NT>(act_row<PRO, MT>(a, m0 + mi), a.k, nch, xr);
+        if (mi > 0) load_vec<XP, NT>(act_row<PRO, MT>(a, m0 + mi), a.k, tot4, xr);
 #pragma unroll
         for (int p = 0; p < XP; p++) {
             const int f4 = p * NT + tid;
@@ -257,8 +342,9 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
         ssp = wave_sum_d_dpp(ssp);
         if (lane == 0) s_ss[wave] = ssp;
     }
+    }  // int8 staging
     __syncthreads();
-    if (NORM && wave == 0) {
+    if (NORM && !WB && wave == 0) {
         // cpu.rs:574-599: rstd = 1/sqrt(mean(x^2) + eps) in f64 (waves in order)
         double t = 0.0;
 #pragma unroll
@@ -279,7 +365,7 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
         // straight-line stream: chunk c computes from wb[c % PF], then refills it
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
-            chunk_fma<MT, B32, RWT>(wb[c % PF], c, xs, kc, xsum, sr, a.nb, wrow, lane, acc);
+            chunk_fma<MT, WT, RWT>(wb[c % PF], c, xs, kc, xsum, sr, a.nb, wrow, lane, acc, a.kp);
             if (c + PF < NCH) {
 #pragma unroll
                 for (int r = 0; r < RWT; r++) wb[c % PF][r] = bload16(wr, woff[r] + ((c + PF) << 10));
@@ -291,7 +377,7 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
             for (int d = 0; d < PF; d++) {
                 const int c = c0 + d;
                 if (c < nch) {
-                    chunk_fma<MT, B32, RWT>(wb[d], c, xs, kc, xsum, sr, a.nb, wrow, lane, acc);
+                    chunk_fma<MT, WT, RWT>(wb[d], c, xs, kc, xsum, sr, a.nb, wrow, lane, acc, a.kp);
                     if (c + PF < nch) {
 #pragma unroll
                         for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + ((c + PF) << 10));
@@ -307,13 +393,13 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         float sxl = 0.f;
-        if (!B32)
+        if (WT == WT_I8)
             for (int c = 0; c < nch; c++) sxl += xsum[mi * (kc >> 4) + (c << 6) + lane];
 #pragma unroll
         for (int r = 0; r < RWT; r++) {
-            const float s = wave_sum(B32 ? acc[mi][r] : fmaf(-128.f, sxl, acc[mi][r]));
+            const float s = wave_sum(WT == WT_I8 ? fmaf(-128.f, sxl, acc[mi][r]) : acc[mi][r]);
             // fused gate/up rows come as gate, gate, up, up
-            const float sc = B32 ? 1.f : (EPI == EPI_SWIGLU && ((row0 + r) & 2)) ? a.scale2 : a.scale;
+            const float sc = WT != WT_I8 ? 1.f : (EPI == EPI_SWIGLU && ((row0 + r) & 2)) ? a.scale2 : a.scale;
             val[mi][r] = sc * s;
         }
     }
@@ -357,7 +443,7 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
             if (lane == r) s_val[wave * RWT + r] = val[0][r];
         __syncthreads();
     }
-    const float rs = NORM ? s_rstd : 1.f;
+    const float rs = (NORM && !WB) ? s_rstd : 1.f;  // bf16: normalised while staged
     if constexpr (EPI == EPI_SWIGLU) {
         // rows 4i..4i+3 = gate[2i], gate[2i+1], up[2i], up[2i+1]
         if (tid < RPW / 2 && rb + 2 * tid < a.rows) {
@@ -424,7 +510,11 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
 struct Sel {
     int nch_t, mt;
 };
-Sel select_cfg(int epi, int nch, int m) {
+Sel select_cfg(int epi, int nch, int m, int wt) {
+    if (wt == WT_BF16) {  // one activation row per pass; the Llama k's compiled
+        const int nt = (nch == 8 || nch == 22 || nch == 28) ? nch : 0;
+        return {nt, 1};
+    }
     int mt = 1;
     if (epi == EPI_STORE && nch <= 4) mt = m >= 4 ? 4 : (m >= 2 ? 2 : 1);
     int nt = 0;
@@ -433,9 +523,10 @@ Sel select_cfg(int epi, int nch, int m) {
     return {nt, mt};
 }
 
-size_t lds_bytes(int epi, int nch, int mt, int pro) {
-    const Shape S = shape_for(select_cfg(epi, nch, mt).nch_t, mt);
-    const size_t dyn = (size_t)mt * nch * 1024 * sizeof(float) * 17 / 16;
+size_t lds_bytes(int epi, int nch, int mt, int pro, int wt) {
+    const Shape S = shape_for(select_cfg(epi, nch, mt, wt).nch_t, mt);
+    const size_t dyn = wt == WT_BF16 ? (size_t)nch * 512 * sizeof(float)
+                                     : (size_t)mt * nch * 1024 * sizeof(float) * 17 / 16;
     (void)pro;
     const size_t stat = S.nw * sizeof(double) +
                         (size_t)mt * S.rwt * S.nw * sizeof(float);
@@ -444,68 +535,88 @@ size_t lds_bytes(int epi, int nch, int mt, int pro) {
 
 constexpr size_t kLdsMax = 160 * 1024;  // gfx950 LDS per workgroup
 
-template <int EPI, int PRO, bool B32, int MT, int NCH>
+template <int EPI, int PRO, int WT, int MT, int NCH>
 int launch_t(const KArgs &ka, hipStream_t s) {
     constexpr Shape S = shape_for(NCH, MT);
-    const size_t lds = (size_t)MT * (ka.nch << 10) * sizeof(float) * 17 / 16;
+    const size_t lds = WT == WT_BF16 ? (size_t)ka.nch * 512 * sizeof(float)
+                                     : (size_t)MT * (ka.nch << 10) * sizeof(float) * 17 / 16;
     if (lds > 64 * 1024) {  // above the default dynamic LDS limit
         static bool attr = false;
         if (!attr) {
-            const size_t stat = lds_bytes(EPI, ka.nch, MT, PRO) - lds;
-            SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_qgemv<EPI, PRO, B32, MT, NCH>),
+            const size_t stat = lds_bytes(EPI, ka.nch, MT, PRO, WT) - lds;
+            SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_qgemv<EPI, PRO, WT, MT, NCH>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kLdsMax - stat)));
             attr = true;
         }
     }
     dim3 grid((ka.rows + S.rwt * S.nw - 1) / (S.rwt * S.nw), (ka.m + MT - 1) / MT);
-    hipLaunchKernelGGL((k_qgemv<EPI, PRO, B32, MT, NCH>), grid, dim3(64 * S.nw), lds, s, ka);
+    hipLaunchKernelGGL((k_qgemv<EPI, PRO, WT, MT, NCH>), grid, dim3(64 * S.nw), lds, s, ka);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }
 
-template <int EPI, int PRO, bool B32, int MT>
+template <int EPI, int PRO, int WT, int MT>
 int launch_nch(const KArgs &ka, int nch_t, hipStream_t s) {
-    switch (nch_t) {
-        case 1: return launch_t<EPI, PRO, B32, MT, 1>(ka, s);
-        case 4: return launch_t<EPI, PRO, B32, MT, 4>(ka, s);
-        default: break;
+    if constexpr (WT == WT_BF16) {
+        switch (nch_t) {
+            case 8: return launch_t<EPI, PRO, WT, MT, 8>(ka, s);
+            case 22: return launch_t<EPI, PRO, WT, MT, 22>(ka, s);
+            case 28: return launch_t<EPI, PRO, WT, MT, 28>(ka, s);
+            default: return launch_t<EPI, PRO, WT, MT, 0>(ka, s);
+        }
+    } else {
+        switch (nch_t) {
+            case 1: return launch_t<EPI, PRO, WT, MT, 1>(ka, s);
+            case 4: return launch_t<EPI, PRO, WT, MT, 4>(ka, s);
+            default: break;
+        }
+        if constexpr (MT == 1 && (EPI == EPI_STORE || EPI == EPI_RESID)) {
+            if (nch_t == 11) return launch_t<EPI, PRO, WT, MT, 11>(ka, s);
+            if (nch_t == 14) return launch_t<EPI, PRO, WT, MT, 14>(ka, s);
+        }
+        return launch_t<EPI, PRO, WT, MT, 0>(ka, s);
     }
-    if constexpr (MT == 1 && (EPI == EPI_STORE || EPI == EPI_RESID)) {
-        if (nch_t == 11) return launch_t<EPI, PRO, B32, MT, 11>(ka, s);
-        if (nch_t == 14) return launch_t<EPI, PRO, B32, MT, 14>(ka, s);
-    }
-    return launch_t<EPI, PRO, B32, MT, 0>(ka, s);
 }
 
-template <int EPI, int PRO, bool B32>
+template <int EPI, int PRO, int WT>
 int launch_mt(const KArgs &ka, Sel sel, hipStream_t s) {
-    if constexpr (EPI == EPI_STORE) {
-        if (sel.mt == 4) return launch_nch<EPI, PRO, B32, 4>(ka, sel.nch_t, s);
-        if (sel.mt == 2) return launch_nch<EPI, PRO, B32, 2>(ka, sel.nch_t, s);
+    if constexpr (EPI == EPI_STORE && WT != WT_BF16) {
+        if (sel.mt == 4) return launch_nch<EPI, PRO, WT, 4>(ka, sel.nch_t, s);
+        if (sel.mt == 2) return launch_nch<EPI, PRO, WT, 2>(ka, sel.nch_t, s);
     }
-    return launch_nch<EPI, PRO, B32, 1>(ka, sel.nch_t, s);
+    return launch_nch<EPI, PRO, WT, 1>(ka, sel.nch_t, s);
+}
+
+template <int EPI, int PRO>
+int launch_wt(const KArgs &ka, int wt, Sel sel, hipStream_t s) {
+    if (wt == WT_BF16) return launch_mt<EPI, PRO, WT_BF16>(ka, sel, s);
+    if (wt == WT_I8B32) return launch_mt<EPI, PRO, WT_I8B32>(ka, sel, s);
+    return launch_mt<EPI, PRO, WT_I8>(ka, sel, s);
 }
 
 template <int EPI>
-int launch_e(const KArgs &ka, int pro, bool b32, Sel sel, hipStream_t s) {
+int launch_e(const KArgs &ka, int pro, int wt, Sel sel, hipStream_t s) {
     // the decode epilogues QKV/SWIGLU/LOGITS always take a fused RMSNorm
     constexpr bool kNorm = (EPI == EPI_QKV || EPI == EPI_SWIGLU || EPI == EPI_LOGITS);
     if ((pro != PRO_PLAIN) != kNorm)
         return set_error(SCRY_ERR_INVALID, "qgemv: epilogue %d %s a fused RMSNorm", EPI,
                          kNorm ? "requires" : "does not take");
     if constexpr (kNorm) {
-        if (pro == PRO_NORMP)
-            return b32 ? launch_mt<EPI, PRO_NORMP, true>(ka, sel, s) : launch_mt<EPI, PRO_NORMP, false>(ka, sel, s);
-        return b32 ? launch_mt<EPI, PRO_NORM, true>(ka, sel, s) : launch_mt<EPI, PRO_NORM, false>(ka, sel, s);
+        if (pro == PRO_NORMP) return launch_wt<EPI, PRO_NORMP>(ka, wt, sel, s);
+        return launch_wt<EPI, PRO_NORM>(ka, wt, sel, s);
     } else {
-        return b32 ? launch_mt<EPI, PRO_PLAIN, true>(ka, sel, s) : launch_mt<EPI, PRO_PLAIN, false>(ka, sel, s);
+        return launch_wt<EPI, PRO_PLAIN>(ka, wt, sel, s);
     }
 }
+
+int weight_type(const Packed &w) { return w.bf16 ? WT_BF16 : (w.s32 ? WT_I8B32 : WT_I8); }
+// 1 KiB weight chunks per row
+int row_chunks(const Packed &w) { return (w.bf16 ? 2 * w.k + 1023 : w.k + 1023) / 1024; }
 
 }  // namespace
 
 int qgemv_blocks(int epi, const Packed &w, int m) {
-    const Sel sel = select_cfg(epi, (w.k + 1023) / 1024, m);
+    const Sel sel = select_cfg(epi, row_chunks(w), m, weight_type(w));
     const Shape S = shape_for(sel.nch_t, sel.mt);
     return (w.rows + S.rwt * S.nw - 1) / (S.rwt * S.nw);
 }
@@ -518,11 +629,14 @@ int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     if (g.m < 1) return set_error(SCRY_ERR_INVALID, "qgemv: m must be >= 1");
     if (!g.x && !(g.norm_w && g.embed && g.tokens && g.state && g.m == 1))
         return set_error(SCRY_ERR_INVALID, "qgemv: no activation (only the fused RMSNorm reads the embedding row)");
-    const int nch = (w.k + 1023) / 1024;
+    const int wt = weight_type(w);
+    const int nch = row_chunks(w);
     const int pro = g.ss_in ? PRO_NORMP : g.norm_w ? PRO_NORM : PRO_PLAIN;
-    const Sel sel = select_cfg(epi, nch, g.m);
-    if (nch > 16 || lds_bytes(epi, nch, sel.mt, pro) > kLdsMax)
+    const Sel sel = select_cfg(epi, nch, g.m, wt);
+    if (nch > (wt == WT_BF16 ? 32 : 16) || lds_bytes(epi, nch, sel.mt, pro, wt) > kLdsMax)
         return set_error(SCRY_ERR_UNSUPPORTED, "qgemv: k=%d exceeds the LDS activation stage", w.k);
+    if (wt == WT_BF16 && (g.m != 1 || w.kp != 2 * round_up(w.k, 8)))
+        return set_error(SCRY_ERR_INVALID, "qgemv: bf16 rows take one activation row and a 16-byte row pad");
     if (epi == EPI_SWIGLU && (w.fused != 1 || w.rows % 4 != 0))
         return set_error(SCRY_ERR_INVALID, "qgemv: swiglu epilogue needs the fused gate/up layout");
     if ((epi == EPI_QKV || epi == EPI_LOGITS || epi == EPI_SWIGLU || epi == EPI_RESID) && g.m != 1)
@@ -573,13 +687,12 @@ int launch_qgemv(int epi, const GemvArgs &g, hipStream_t s) {
     ka.part_val = g.part_val;
     ka.part_idx = g.part_idx;
     ka.part_nan = g.part_nan;
-    const bool b32 = w.s32 != nullptr;
     switch (epi) {
-        case EPI_STORE: return launch_e<EPI_STORE>(ka, pro, b32, sel, s);
-        case EPI_RESID: return launch_e<EPI_RESID>(ka, pro, b32, sel, s);
-        case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(ka, pro, b32, sel, s);
-        case EPI_QKV: return launch_e<EPI_QKV>(ka, pro, b32, sel, s);
-        case EPI_LOGITS: return launch_e<EPI_LOGITS>(ka, pro, b32, sel, s);
+        case EPI_STORE: return launch_e<EPI_STORE>(ka, pro, wt, sel, s);
+        case EPI_RESID: return launch_e<EPI_RESID>(ka, pro, wt, sel, s);
+        case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(ka, pro, wt, sel, s);
+        case EPI_QKV: return launch_e<EPI_QKV>(ka, pro, wt, sel, s);
+        case EPI_LOGITS: return launch_e<EPI_LOGITS>(ka, pro, wt, sel, s);
     }
     return set_error(SCRY_ERR_INVALID, "qgemv: unknown epilogue %d", epi);
 }

@@ -17,6 +17,7 @@ from ._lib import LlamaConfigC, SamplingConfigC, call, load
 
 QUANT_PER_TENSOR = 0
 QUANT_BLOCK32 = 1
+QUANT_BF16 = 2  # bf16 weights, bf16-rounded activations (the reference's bf16 feature)
 T_EMBED, T_QKV, T_O, T_GATE, T_UP, T_DOWN, T_LM_HEAD = range(7)
 @dataclass
 class LlamaConfig:

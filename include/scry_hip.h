@@ -252,7 +252,13 @@ typedef struct {
     int64_t rs_original_max_pos;
 } scry_llama_config; /* LlamaConfig (llama.rs:20-34) */
 
-enum { SCRY_QUANT_PER_TENSOR = 0, SCRY_QUANT_BLOCK32 = 1 };
+/* SCRY_QUANT_BF16: no int8 step -- every projection is kept as bf16 (the
+ * reference's cast of the f32 weight) and each matmul rounds its activation
+ * to bf16 and accumulates in f32, as the reference's bf16 feature does
+ * (cuda.rs:1206-1290); attention, norms and the residual stream stay f32.
+ * Decode (forward_with_cache, generate) runs on it; the batched prefill and
+ * the per-tensor int8 readback refuse it (SCRY_ERR_UNSUPPORTED). */
+enum { SCRY_QUANT_PER_TENSOR = 0, SCRY_QUANT_BLOCK32 = 1, SCRY_QUANT_BF16 = 2 };
 
 enum {
     SCRY_T_EMBED = 0,

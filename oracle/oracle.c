@@ -402,6 +402,43 @@ void orc_matmul_bf16(const float *a, const float *b, int m, int k, int n, int tr
         }
 }
 
+/* orc_matmul_bf16 (trans_a = 0) on all cores, bit-identical: the same f64
+ * sum of exact bf16 products in increasing p, per output element. */
+void orc_matmul_bf16_par(const float *a, const float *b, int m, int k, int n, int trans_b, float *c) {
+    double *ab = (double *)malloc(sizeof(double) * (size_t)m * k);
+    for (size_t i = 0; i < (size_t)m * k; i++) ab[i] = (double)bf16_val(orc_f32_to_bf16(a[i]));
+    if (trans_b) {
+#pragma omp parallel for schedule(static) num_threads(NT) if (PAR_IF)
+        for (int j = 0; j < n; j++) {
+            const float *row = b + (size_t)j * k;
+            for (int i = 0; i < m; i++) {
+                const double *ar = ab + (size_t)i * k;
+                double acc = 0.0;
+                for (int p = 0; p < k; p++) acc += ar[p] * (double)bf16_val(orc_f32_to_bf16(row[p]));
+                c[(size_t)i * n + j] = (float)acc;
+            }
+        }
+    } else {
+        const int CH = 256, nch = (n + CH - 1) / CH;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(NT) if (PAR_IF)
+        for (int ch = 0; ch < nch; ch++) {
+            const int j0 = ch * CH, j1 = j0 + CH < n ? j0 + CH : n;
+            double *acc = (double *)malloc(sizeof(double) * CH);
+            for (int i = 0; i < m; i++) {
+                const double *ar = ab + (size_t)i * k;
+                for (int j = j0; j < j1; j++) acc[j - j0] = 0.0;
+                for (int p = 0; p < k; p++) {
+                    const float *br = b + (size_t)p * n;
+                    for (int j = j0; j < j1; j++) acc[j - j0] += ar[p] * (double)bf16_val(orc_f32_to_bf16(br[j]));
+                }
+                for (int j = j0; j < j1; j++) c[(size_t)i * n + j] = (float)acc[j - j0];
+            }
+            free(acc);
+        }
+    }
+    free(ab);
+}
+
 /* cpu.rs:1321-1350 (+ fallback 1444-1468) matmul_strided_batched_impl */
 void orc_matmul_strided_batched(const float *a, const float *b, int batch, int m, int k, int n,
                                 int trans_a, int trans_b, float *c) {
@@ -901,6 +938,11 @@ static int run_proj(const orc_proj *P, const float *x, int rows, int mode, float
     if (mode == 0) {
         if (!P->w) return -1;
         orc_matmul_f32(x, P->w, rows, P->k, P->n, 0, P->tb, out);
+        return 0;
+    }
+    if (mode == 3) {  /* the bf16 feature: bf16 operands, f32 result (cuda.rs:1226-1290) */
+        if (!P->w) return -1;
+        orc_matmul_bf16_par(x, P->w, rows, P->k, P->n, P->tb, out);
         return 0;
     }
     if (mode == 1) {

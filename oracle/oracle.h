@@ -74,6 +74,8 @@ uint16_t orc_f32_to_bf16(float x);
 void orc_f32_to_bf16_vec(const float *x, size_t n, uint16_t *out);
 void orc_matmul_bf16(const float *a, const float *b, int m, int k, int n, int trans_a, int trans_b,
                      float *c);
+/* the same (trans_a = 0) on all cores, bit-identical */
+void orc_matmul_bf16_par(const float *a, const float *b, int m, int k, int n, int trans_b, float *c);
 
 /* ---- cpu.rs glue ops ---- */
 void orc_rmsnorm(const float *x, const float *w, int rows, int d, float eps, float *out);
@@ -170,7 +172,8 @@ int orc_cache_len(const orc_cache *c, int layer);
 void orc_cache_layer(const orc_cache *c, int layer, float *k_out, float *v_out);
 
 /* LlamaModel::forward_with_llama_cache (llama.rs:744-763);
- * mode 0 = reference f32 weights, 1 = int8 per-tensor, 2 = int8 block-32 */
+ * mode 0 = reference f32 weights, 1 = int8 per-tensor, 2 = int8 block-32,
+ * 3 = the bf16 feature (bf16 weights and activations, f32 result) */
 int orc_llama_forward_with_cache(const orc_llama *m, orc_cache *c, int64_t token, int pos,
                                  int mode, float *logits);
 /* LlamaModel::forward (llama.rs:683-700): logits [seq, V] */

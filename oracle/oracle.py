@@ -59,6 +59,7 @@ def lib():
         "orc_matmul_f32": (None, [f32p, f32p, i32, i32, i32, i32, i32, f32p]),
         "orc_f32_to_bf16_vec": (None, [f32p, sz, C.c_void_p]),
         "orc_matmul_bf16": (None, [f32p, f32p, i32, i32, i32, i32, i32, f32p]),
+        "orc_matmul_bf16_par": (None, [f32p, f32p, i32, i32, i32, i32, f32p]),
         "orc_matmul_strided_batched": (None, [f32p, f32p, i32, i32, i32, i32, i32, i32, f32p]),
         "orc_rmsnorm": (None, [f32p, f32p, i32, i32, f32, f32p]),
         "orc_rope_with_freqs_preloaded": (None, [f32p, i32, i32, i32, i32, f32p, f32p]),
@@ -224,6 +225,13 @@ def matmul_bf16(a, b, m, k, n, trans_a=False, trans_b=False):
     products summed in f64 and rounded once."""
     c = np.empty(m * n, np.float32)
     lib().orc_matmul_bf16(_f32(a).ravel(), _f32(b).ravel(), m, k, n, int(trans_a), int(trans_b), c)
+    return c.reshape(m, n)
+
+
+def matmul_bf16_par(a, b, m, k, n, trans_b=False):
+    """matmul_bf16 (trans_a = 0) on all cores: bit-identical."""
+    c = np.empty(m * n, np.float32)
+    lib().orc_matmul_bf16_par(_f32(a).ravel(), _f32(b).ravel(), m, k, n, int(trans_b), c)
     return c.reshape(m, n)
 
 

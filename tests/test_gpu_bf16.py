@@ -121,3 +121,101 @@ def test_bf16_storage(bf16_mode, hip, orc):
     w[10:12] = 3.0
     y1 = B.matmul(B.from_vec(x), ws, 1, k, n).to_vec()
     assert np.array_equal(y1, w.sum(0))
+
+
+# ------------------------------------------------- the bf16 model's decode step
+# The bf16 model rounds every projection's activations to bf16, so a last-bit
+# difference in an f32 value upstream (accumulation order) moves a rounded
+# activation by one bf16 step whenever it sits at a rounding boundary, and
+# such steps compound with depth and sequence length.  Measured on the oracle
+# itself by switching its matmul from the f64 sum to an f32 sum in the same
+# order: 2e-7..4e-5 relative on the logits at 1-2 layers of width <= 288 and a
+# few positions ("shallow"), 2.3e-3..4.7e-3 at width 512-4096 or 6 layers x 40
+# positions ("deep").  The gap between bf16 and f32 semantics (forward mode 3
+# against mode 0) is 4e-3..1.3e-2 on the same cases, so the shallow bar below
+# separates them by 10x either side; the deep bar catches gross errors (packing,
+# chunking, epilogues at the large shapes) together with identical tokens.
+SHALLOW_TOL = 5e-4
+DEEP_TOL = 1e-2
+TINY = dict(vocab_size=32000, hidden_size=288, intermediate_size=768, n_layers=6, n_heads=6,
+            n_kv_heads=6, max_seq_len=256, rope_theta=10000.0, tie_word_embeddings=True)
+
+
+def _bf16_decode_vs_oracle(hip, orc, cfg, seed, prompt, steps, tol, init_on_device=False):
+    """The GPU model in QUANT_BF16 (bf16 weights packed from the seeded f32
+    init, activations cast to bf16 at each projection, f32 accumulation)
+    against the oracle's forward mode 3 on the same seeded f32 weights
+    (llama.rs:593-680 init, cuda.rs:1226-1290 matmul): logits within `tol`
+    relative, identical greedy tokens, replays bit-identical."""
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), seed, quant_mode=hip.QUANT_BF16,
+                                   init_on_device=init_on_device)
+    try:
+        kt, kl = hm.generate_greedy(prompt, steps, want_logits=True)
+        kt2, kl2 = hm.generate_greedy(prompt, steps, want_logits=True)
+        with pytest.raises(hip.ScryHipError):
+            hm.qtensor(orc.T_QKV, 0)  # the model holds no int8 weights
+    finally:
+        hm.free()
+    orc.set_threads(16)
+    om = orc.Llama(orc.LlamaConfig(**cfg), seed, quantize=False)
+    try:
+        ref_t, ref_l = om.generate_greedy(prompt, steps, mode=3, want_logits=True)
+        f32_l = om.generate_greedy(prompt, steps, mode=0, want_logits=True)[1]
+    finally:
+        om.close()
+        orc.set_threads(0)
+    err = max(rel_err(kl[i], ref_l[i]) for i in range(steps))
+    gap = max(rel_err(f32_l[i], ref_l[i]) for i in range(steps))
+    print(f"[err] bf16 decode {err:.3e} (bar {tol:g}; f32 semantics would be {gap:.3e} away); "
+          f"tokens {kt[:6].tolist()}", flush=True)
+    assert err < tol
+    assert (kt == ref_t).all()
+    assert (kt2 == kt).all() and np.array_equal(kl2, kl)  # replays reproduce bit for bit
+
+
+@pytest.mark.parametrize("layers", [1, 2])
+def test_bf16_model_decode_shallow(hip, orc, layers):
+    print(f"[case] bf16 model: tiny dims (tied head), {layers} layer(s), prompt 4, 4 greedy", flush=True)
+    cfg = dict(TINY, n_layers=layers)
+    _bf16_decode_vs_oracle(hip, orc, cfg, 0, orc.prompt_ids(1, 4, TINY["vocab_size"]), 4, SHALLOW_TOL)
+
+
+def test_bf16_model_decode_shallow_gqa(hip, orc):
+    print("[case] bf16 model: GQA nh=8 nkv=2 hd=4, prompt 100, 20 greedy", flush=True)
+    cfg = dict(vocab_size=64, hidden_size=32, intermediate_size=256, n_layers=2, n_heads=8,
+               n_kv_heads=2, max_seq_len=160, rope_theta=500000.0, tie_word_embeddings=False)
+    _bf16_decode_vs_oracle(hip, orc, cfg, 7, orc.prompt_ids(3, 100, 64), 20, SHALLOW_TOL)
+
+
+def test_bf16_model_decode_tiny_deep(hip, orc):
+    print("[case] bf16 model: tiny, 6 layers, prompt 8, 32 greedy", flush=True)
+    _bf16_decode_vs_oracle(hip, orc, TINY, 0, orc.prompt_ids(1, 8, TINY["vocab_size"]), 32, DEEP_TOL)
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(4, 1, 128), (16, 4, 64)])
+def test_bf16_model_decode_gqa_deep(hip, orc, nh, nkv, hd):
+    print(f"[case] bf16 model: GQA nh={nh} nkv={nkv} hd={hd}, prompt 100, 20 greedy", flush=True)
+    cfg = dict(vocab_size=64, hidden_size=nh * hd, intermediate_size=256, n_layers=2,
+               n_heads=nh, n_kv_heads=nkv, max_seq_len=160, rope_theta=500000.0,
+               tie_word_embeddings=False)
+    _bf16_decode_vs_oracle(hip, orc, cfg, 7, orc.prompt_ids(3, 100, 64), 20, DEEP_TOL)
+
+
+def test_bf16_model_decode_7b_dims(hip, orc):
+    """Config-4 shapes with 2 layers (device init, as bench.py)."""
+    print("[case] bf16 model: 7B dims, 2 layers, prompt 24, 8 greedy", flush=True)
+    cfg = dict(vocab_size=32000, hidden_size=4096, intermediate_size=11008, n_layers=2,
+               n_heads=32, n_kv_heads=32, max_seq_len=2048, rope_theta=10000.0,
+               tie_word_embeddings=False)
+    _bf16_decode_vs_oracle(hip, orc, cfg, 0, orc.prompt_ids(1, 24, 32000), 8, DEEP_TOL,
+                           init_on_device=True)
+
+
+def test_bf16_model_refuses_prefill(hip, orc):
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**TINY), 0, quant_mode=hip.QUANT_BF16)
+    try:
+        with pytest.raises(hip.ScryHipError) as ei:
+            hm.generate_greedy(orc.prompt_ids(1, 8, TINY["vocab_size"]), 4, prefill=True)
+        assert "bf16" in str(ei.value)
+    finally:
+        hm.free()

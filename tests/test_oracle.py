@@ -573,6 +573,42 @@ def test_matmul_bf16_oracle(orc, ta, tb):
     assert not np.array_equal(got, a @ b)  # the rounding of the operands is there
 
 
+@pytest.mark.parametrize("m,k,n,tb", [(1, 300, 700, False), (3, 129, 257, False), (2, 64, 513, True),
+                                      (5, 37, 11, True)])
+def test_matmul_bf16_par_bit_identical(orc, m, k, n, tb):
+    """The all-core bf16 matmul (forward mode 3) sums the same exact products
+    in the same order as the pinned scalar one: equal bit for bit."""
+    rng = np.random.default_rng(m * 1000 + k)
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    b = rng.normal(0, 1, (n, k) if tb else (k, n)).astype(np.float32)
+    orc.set_threads(4)
+    try:
+        got = orc.matmul_bf16_par(a, b, m, k, n, tb)
+    finally:
+        orc.set_threads(0)
+    want = orc.matmul_bf16(a, b, m, k, n, False, tb)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_forward_mode3_is_the_bf16_composition(orc):
+    """Forward mode 3 (the bf16 feature) runs the mode-0 composition with
+    every projection through matmul_bf16_par (pinned above and against
+    torch's bf16 rounding): on a tiny model the two modes differ by the bf16
+    rounding of the operands only."""
+    cfg = orc.LlamaConfig(vocab_size=64, hidden_size=32, intermediate_size=64, n_layers=2, n_heads=4,
+                          n_kv_heads=2, max_seq_len=16, rope_theta=10000.0, tie_word_embeddings=False)
+    m = orc.Llama(cfg, 5, quantize=False)
+    try:
+        toks = np.array([1, 7, 3, 60], np.int64)
+        l0 = m.forward(toks, mode=0)
+        l3 = m.forward(toks, mode=3)
+    finally:
+        m.close()
+    rel = np.abs(l3 - l0).max() / np.abs(l0).max()
+    assert 1e-5 < rel < 3e-2, rel  # bf16 operands: ~2^-8 relative per product
+    assert (np.argmax(l3, -1) == np.argmax(l0, -1)).mean() >= 0.75
+
+
 # ------------------------------------------------- distribution of sample_token
 def _closed_form_probs(logits, t, k, p):
     """generate.rs:92-165 written from its definition: keep the k largest of
