@@ -34,6 +34,7 @@ Also reported:
 
 Profiling modes (no JSON line): --pmc-probe runs a 256 MiB device copy (the
 counter calibration) and each decode projection kernel over all layers;
+--prefill-profile runs the config-5 batched prefill twice without decode;
 --prefill-only runs the config-5 measurement alone; --gemv-only the
 configs 2 / 3 micro-benchmark alone.
 """
@@ -123,6 +124,25 @@ def pmc_probe(E) -> None:
         us, b = m.time_projection(tid, 32)
         print(f"[probe] {name} {us:.2f} us {b:.0f} B", flush=True)
     m.free()
+
+
+def prefill_profile(E) -> None:
+    """The workload of the committed prefill counter summaries: config 5's
+    batched prefill (4 x 2047 tokens), twice, without the decode steps."""
+    import numpy as np
+    cfg = E.LlamaConfig.llama3_8b()
+    print("[profile] config-5 model, device init", flush=True)
+    m = E.LlamaModel.new_random(cfg, seed=0, init_on_device=True)
+    prompts = np.stack([E.synth.prompt_ids(s + 1, 2048, cfg.vocab_size) for s in range(4)])
+    for p in range(2):
+        caches = [m.new_llama_kv_cache(2048) for _ in range(4)]
+        print(f"[profile] prefill pass {p}", flush=True)
+        m.prefill(caches, prompts[:, :2047], want_logits=False)
+        E.HipBackend.synchronize()
+        for c in caches:
+            c.free()
+    m.free()
+    print("[profile] done", flush=True)
 
 
 SAMPLING_SWEEP = [(0.8, 40, 0.95), (0.8, 0, 0.95), (1.0, 0, 1.0), (0.7, 0, 0.5)]
@@ -340,6 +360,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill line")
     ap.add_argument("--pmc-probe", action="store_true", help="profiling workload only (see above)")
     ap.add_argument("--prefill-only", action="store_true", help="config-5 measurement only")
+    ap.add_argument("--prefill-profile", action="store_true",
+                    help="profiling workload only: config-5 prefill twice, no decode")
     ap.add_argument("--bf16-only", action="store_true",
                     help="bf16-mode GEMV (bf16 weights) at Llama-2-7B projection shapes only")
     ap.add_argument("--linear-only", action="store_true",
@@ -374,6 +396,9 @@ def main() -> int:
         return 0
     if args.prefill_only:
         print(json.dumps(prefill_config5(E)), flush=True)
+        return 0
+    if args.prefill_profile:
+        prefill_profile(E)
         return 0
     if args.gemv_only:
         print(json.dumps({"gemv_micro": gemv_micro(EL)}), flush=True)
@@ -423,6 +448,13 @@ def main() -> int:
                       "us_per_token": round(us * per_token[name], 1)}
         print(f"[bench] {name:8s} {us:8.2f} us  {b / 1e6:8.2f} MB  {b / us / 1e3:7.1f} GB/s",
               file=sys.stderr, flush=True)
+    # decode attention at the bench's mid-decode context (HIP events, rotating layers)
+    ctx = args.prompt_len + args.steps // 2
+    a_us, a_b = model.time_attention(ctx, args.proj_iters)
+    attention = {"context": ctx, "avg_us": round(a_us, 3), "bytes": int(a_b),
+                 "gbs": round(a_b / a_us / 1e3, 1), "us_per_token": round(a_us * cfg.n_layers, 1)}
+    print(f"[bench] attention {a_us:8.2f} us  {a_b / 1e6:8.2f} MB  {a_b / a_us / 1e3:7.1f} GB/s "
+          f"(context {ctx})", file=sys.stderr, flush=True)
     dom = max(proj, key=lambda k: proj[k]["us_per_token"])
     wb = weight_bytes(cfg)
     roofline = {
@@ -473,6 +505,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "projections": proj,
+        "attention": attention,
         "greedy_tokens_head": [int(t) for t in toks[:8]],
         "sampled_decode": sampled,
         "bf16_decode": bf16,

@@ -131,6 +131,7 @@ SIGNATURES = {
     "scry_hip_llama_bench_decode": [vp, vp, i32, i32, i32, vp, P(f64)],
     "scry_hip_llama_bench_decode_sampled": [vp, vp, i32, i32, i32, P(SamplingConfigC), u64, vp, P(f64)],
     "scry_hip_llama_time_projection": [vp, i32, i32, i32, P(f64), P(f64)],
+    "scry_hip_llama_time_attention": [vp, i32, i32, P(f64), P(f64)],
     "scry_hip_bench_qgemv": [i32, i32, i32, i32, i32, i32, i32, P(f64), P(f64)],
     "scry_hip_bench_qgemv_dist": [i32, i32, i32, i32, i32, i32, i32, i32, i32, vp, P(f64), P(f64)],
 }

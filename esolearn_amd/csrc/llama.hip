@@ -1403,6 +1403,48 @@ int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int i
     return rc;
 }
 
+int scry_hip_llama_time_attention(scry_llama m, int ctx_len, int iters, double *avg_us, double *bytes_per_launch) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    if (!m || ctx_len <= 0 || ctx_len > m->cfg.max_seq_len || iters <= 0 || !avg_us)
+        return set_error(SCRY_ERR_INVALID, "time_attention: bad arguments");
+    scry_kv_cache c = nullptr;
+    SCRY_TRY(cache_new(m, ctx_len, &c));
+    hipStream_t s = ctx().stream;
+    // every layer's cache holds ctx_len rows (the decode step's shape at that length)
+    int rc = launch_fill_f32(c->kv, (size_t)m->L * 2 * ctx_len * m->kv_dim, 0.03125f, s);
+    if (!rc) rc = launch_fill_f32(c->xq, m->q_dim, 0.0625f, s);
+    auto launch = [&](int l) {
+        AttnArgs a = attn_args(c, l);
+        a.fixed_len = ctx_len;
+        return launch_attn_decode(a, s);
+    };
+    for (int i = 0; i < std::min(iters, 8) && !rc; i++) rc = launch(i % m->L);  // warm-up
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc) {
+        hipError_t e = hipEventCreate(&e0);
+        if (e == hipSuccess) e = hipEventCreate(&e1);
+        if (e == hipSuccess) e = hipEventRecord(e0, s);
+        if (e != hipSuccess) rc = hip_fail(e, "event setup", __FILE__, __LINE__);
+    }
+    for (int i = 0; i < iters && !rc; i++) rc = launch(i % m->L);  // rotating: K/V stream from HBM
+    if (!rc) {
+        hipError_t e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float f = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&f, e0, e1);
+        if (e != hipSuccess) rc = hip_fail(e, "event timing", __FILE__, __LINE__);
+        *avg_us = 1000.0 * f / iters;
+    }
+    // algorithmic bytes: the K and V rows once, q in, the attention row out
+    if (bytes_per_launch) *bytes_per_launch = 8.0 * ctx_len * m->kv_dim + 8.0 * m->q_dim;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(s);
+    cache_free(c);
+    return rc;
+}
+
 }  // extern "C"
 
 namespace {

@@ -261,6 +261,14 @@ class LlamaModel:
              C.byref(b))
         return us.value, b.value
 
+    def time_attention(self, ctx_len: int, iters: int = 64):
+        """Average device time of the decode attention kernel at ctx_len cached
+        positions (rotating over the layers' caches) and its algorithmic bytes."""
+        us, b = C.c_double(), C.c_double()
+        call("scry_hip_llama_time_attention", self.h, int(ctx_len), int(iters), C.byref(us),
+             C.byref(b))
+        return us.value, b.value
+
     def free(self) -> None:
         if self.h:
             for c in self._caches:

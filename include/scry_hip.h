@@ -385,6 +385,13 @@ int scry_hip_llama_bench_decode_sampled(scry_llama m, const int64_t *prompt, int
  * step uses.  tensor_id: SCRY_T_QKV / O / GATE (fused gate+up) / DOWN / LM_HEAD. */
 int scry_hip_llama_time_projection(scry_llama m, int tensor_id, int layer, int iters,
                                    double *avg_us, double *bytes_per_launch);
+/* Average device time of `iters` launches of the decode attention kernel
+ * (one query token against ctx_len cached positions, every layer's cache in
+ * turn) with the decode step's launch shape.  The reference's counterpart is
+ * the per-token attention sequence of llama.rs:411-455; this entry is timing
+ * only. */
+int scry_hip_llama_time_attention(scry_llama m, int ctx_len, int iters, double *avg_us,
+                                  double *bytes_per_launch);
 /* Prefill then decode, timed: prompts [n_seq, n_prompt]; the first
  * n_prompt - 1 tokens of every sequence go through one batched prefill
  * (*prefill_ms, after an untimed pass), then each sequence runs decode_steps
