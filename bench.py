@@ -221,19 +221,21 @@ def gemv_micro(EL, iters: int = 1000, n_bufs: int = 32) -> list:
     launches over n_bufs distinct weight copies (more than the 256 MB Infinity
     Cache): the back-to-back average, and median and p10 / p90 of the
     per-launch device time of each group of 8 consecutive launches (an event
-    between single launches would add its own gap to every sample).  At 16 rows both the GEMV and the
-    MFMA GEMM are timed (matmul_i8_f32 routes 16 rows to the GEMV)."""
+    between single launches would add its own gap to every sample).  Above one
+    row the GEMV (up to 4 rows per weight pass), the skinny MFMA kernel (every
+    weight byte once for up to 16 rows; matmul_i8_f32's route there) and, at 16
+    rows, the prefill MFMA GEMM are timed."""
     import numpy as np
     out = []
     for name, k, n, ms in GEMV_CASES:
         for qm, qname in ((EL.QUANT_BLOCK32, "block-32"), (EL.QUANT_PER_TENSOR, "per-tensor")):
             for m in ms:
-                for path in ((1, 2) if m == 16 else (0,)):
+                for path in ((1, 3, 2) if m == 16 else (1, 3) if m > 1 else (0,)):
                     per, avg, b = EL.bench_qgemv_dist(m, k, n, qm, path, n_bufs, 50, iters, 8)
                     p10, med, p90 = (float(v) for v in np.percentile(per, [10, 50, 90]))
                     fl = 2.0 * m * k * n
                     e = {"case": name, "k": k, "n": n, "m": m, "scales": qname,
-                         "kernel": "mfma gemm" if path == 2 else "gemv",
+                         "kernel": {2: "mfma gemm", 3: "skinny mfma"}.get(path, "gemv"),
                          "iters": iters, "weight_buffers": n_bufs, "group": 8,
                          "median_us": round(med, 3), "p10_us": round(p10, 3), "p90_us": round(p90, 3),
                          "avg_us": round(avg, 3), "bytes": int(b),
@@ -241,7 +243,7 @@ def gemv_micro(EL, iters: int = 1000, n_bufs: int = 32) -> list:
                          "gbs_median": round(b / med / 1e3, 1), "hbm_frac_median": round(b / med / 1e3 / HBM_PEAK_GBS, 4),
                          "tflops_median": round(fl / med / 1e6, 2)}
                     out.append(e)
-                    print(f"[bench] gemv {name:32s} m={m:2d} {qname:10s} {e['kernel']:9s} median {med:7.2f} us "
+                    print(f"[bench] gemv {name:32s} m={m:2d} {qname:10s} {e['kernel']:11s} median {med:7.2f} us "
                           f"(p10 {p10:6.2f} p90 {p90:6.2f}) {e['gbs_median']:7.1f} GB/s {e['tflops_median']:6.2f} TFLOP/s",
                           file=sys.stderr, flush=True)
     return out

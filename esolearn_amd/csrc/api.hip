@@ -53,6 +53,21 @@ int dev_alloc(void **p, size_t bytes) {
     return SCRY_OK;
 }
 
+int ctx_workspace(size_t bytes, void **p) {
+    Ctx &c = ctx();
+    if (c.ws_bytes < bytes) {
+        SCRY_HIP(hipStreamSynchronize(c.stream));
+        dev_free(c.ws);
+        c.ws = nullptr;
+        c.ws_bytes = 0;
+        const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+        SCRY_TRY(dev_alloc(&c.ws, want));
+        c.ws_bytes = want;
+    }
+    *p = c.ws;
+    return SCRY_OK;
+}
+
 void dev_free(void *p) {
     if (p) (void)hipFree(p);
 }
@@ -237,7 +252,19 @@ int qmatmul(scry_buf a, scry_i8buf bq, float scale, const float *scales32, const
     w.s32 = const_cast<float *>(scales32);
     w.nb = (k + 31) / 32;
     int rc;
-    if (m <= GEMV_MAX_M) {
+    if (skinny_route(m, k, n)) {
+        void *ws = nullptr;
+        rc = ctx_workspace(skinny_ws_bytes(m, k, n), &ws);
+        SkinnyMM sm;
+        sm.w = &w;
+        sm.x = a->d;
+        sm.ldx = k;
+        sm.m = m;
+        sm.bias = bias;
+        sm.y = o->d;
+        sm.ldy = n;
+        if (!rc) rc = launch_skinny(sm, (float *)ws, ctx().ws_bytes, ctx().stream);
+    } else if (m <= GEMV_MAX_M) {
         GemvArgs g;
         g.w = &w;
         g.x = a->d;
@@ -317,6 +344,7 @@ int scry_hip_shutdown(void) {
     Ctx &c = ctx();
     if (!c.init) return SCRY_OK;
     (void)hipStreamSynchronize(c.stream);
+    dev_free(c.ws);
     (void)hipStreamDestroy(c.stream);
     c = Ctx{};
     return SCRY_OK;

@@ -20,9 +20,14 @@ struct Ctx {
     hipStream_t stream = nullptr;
     int cu_count = 0;
     std::string name, arch;
+    void *ws = nullptr;  // op workspace on the stream (grown on demand, kept)
+    size_t ws_bytes = 0;
 };
 
 Ctx &ctx();
+// The context's workspace, at least `bytes` large.  Work already queued on
+// the stream may still use the old one, so growing it synchronises first.
+int ctx_workspace(size_t bytes, void **p);
 std::recursive_mutex &api_mutex();
 
 int set_error(int code, const char *fmt, ...);
@@ -154,6 +159,20 @@ int launch_qgemv(int epi, const GemvArgs &a, hipStream_t s);
 int qgemv_blocks(int epi, const Packed &w, int m);
 // matmul_i8_f32 with more activation rows than this runs as the MFMA GEMM
 constexpr int GEMV_MAX_M = 16;
+// skinny.hip: matmul_i8_f32 for SKINNY_MIN_M..16 activation rows on the matrix
+// cores (k splits into a workspace of partial sums, then an ordered reduction)
+constexpr int SKINNY_MIN_M = 3;  // measured: the GEMV (two rows per weight pass) is faster at 2
+struct SkinnyMM {
+    const Packed *w = nullptr;  // plain int8 rows (not fused, not bf16)
+    const float *x = nullptr;
+    int ldx = 0, m = 0;
+    const float *bias = nullptr;
+    float *y = nullptr;
+    int ldy = 0;
+};
+bool skinny_route(int m, int k, int n);
+size_t skinny_ws_bytes(int m, int k, int n);
+int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s);
 int launch_logits_finish(const GemvArgs &a, hipStream_t s);
 // sample_token on the device (sample.hip): logits [V] -> tokens[pos + 1] when
 // the position draws a token, then the position advances.  ws: [V] f64

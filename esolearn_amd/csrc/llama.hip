@@ -1520,18 +1520,25 @@ int bench_qgemv_impl(int m_rows, int k, int n, int quant_mode, int n_bufs, int w
 }
 
 // Per-launch device times of matmul_i8_f32 at (m, k, n) over n_bufs weight
-// copies.  path 0: the route matmul_i8_f32 takes (the GEMV up to GEMV_MAX_M
-// activation rows, the MFMA GEMM above); 1: the GEMV; 2: the GEMM (its bf16
-// activation split included, as matmul_i8_f32 runs it).
+// copies.  path 0: the route matmul_i8_f32 takes (the skinny MFMA kernel where
+// skinny_route admits the shape, else the GEMV up to GEMV_MAX_M activation
+// rows, the MFMA GEMM above); 1: the GEMV; 2: the GEMM (its bf16 activation
+// split included, as matmul_i8_f32 runs it); 3: the skinny MFMA kernel (its
+// ordered split reduction included).
 int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_bufs, int warmup, int iters,
                           int group, double *per_launch_us, double *avg_us, double *bytes_per_launch) {
     SCRY_REQUIRE_INIT();
-    if (m <= 0 || k <= 0 || n <= 0 || n_bufs <= 0 || iters <= 0 || !avg_us || path < 0 || path > 2 ||
+    if (m <= 0 || k <= 0 || n <= 0 || n_bufs <= 0 || iters <= 0 || !avg_us || path < 0 || path > 3 ||
         group < 1 || iters % group ||
         (quant_mode != SCRY_QUANT_PER_TENSOR && quant_mode != SCRY_QUANT_BLOCK32))
         return set_error(SCRY_ERR_INVALID, "bench_qgemv_dist: bad arguments");
-    const bool gemm = path == 2 || (path == 0 && m > GEMV_MAX_M);
-    if (!gemm && m > GEMV_MAX_M) return set_error(SCRY_ERR_INVALID, "bench_qgemv_dist: the GEMV takes <= %d rows", GEMV_MAX_M);
+    const bool skinny = path == 3 || (path == 0 && skinny_route(m, k, n));
+    const bool gemm = !skinny && (path == 2 || (path == 0 && m > GEMV_MAX_M));
+    if (!gemm && !skinny && m > GEMV_MAX_M)
+        return set_error(SCRY_ERR_INVALID, "bench_qgemv_dist: the GEMV takes <= %d rows", GEMV_MAX_M);
+    if (skinny && (m > GEMV_MAX_M || k % 8 != 0))
+        return set_error(SCRY_ERR_INVALID, "bench_qgemv_dist: the skinny kernel takes <= %d rows and k %% 8 == 0",
+                         GEMV_MAX_M);
     hipStream_t s = ctx().stream;
     std::vector<Packed> W(n_bufs);
     float *x = nullptr, *y = nullptr;
@@ -1542,6 +1549,8 @@ int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_b
     if (!rc) rc = launch_fill_f32(x, (size_t)m * k, 0.5f, s);
     if (!rc && gemm) rc = dev_alloc((void **)&pl, sizeof(unsigned short) * 2 * (size_t)mp * ld);
     if (!rc && gemm) rc = launch_fill_u32((unsigned *)pl, (size_t)mp * ld, 0u, s);
+    void *sws = nullptr;
+    if (!rc && skinny) rc = ctx_workspace(skinny_ws_bytes(m, k, n), &sws);
     for (int b = 0; b < n_bufs && !rc; b++) {
         Packed &P = W[b];
         P.k = k;
@@ -1558,6 +1567,16 @@ int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_b
         }
     }
     auto launch = [&](int i) {
+        if (skinny) {
+            SkinnyMM sm;
+            sm.w = &W[i % n_bufs];
+            sm.x = x;
+            sm.ldx = k;
+            sm.m = m;
+            sm.y = y;
+            sm.ldy = n;
+            return launch_skinny(sm, (float *)sws, ctx().ws_bytes, s);
+        }
         if (!gemm) {
             GemvArgs g;
             g.w = &W[i % n_bufs];

@@ -1,0 +1,331 @@
+// matmul_i8_f32 for 3..16 activation rows on the matrix cores
+// (ops::matmul_i8_f32 / _bias, quantize.rs block-32 variant; cpu.rs:1128-1160):
+//   y[i][j] = scale * sum_p x[i][p] * q[j][p]  (+ bias[j])
+// on the packed weight rows (bytes q + 128, the decode GEMV's layout).
+//
+// The GEMV takes at most 4 activation rows per weight pass and spends a VALU
+// multiply-add per weight byte and row, so 16 rows cost four passes of VALU
+// work.  Here one 16-row v_mfma_f32_16x16x32_bf16 tile consumes every weight
+// byte once for all rows:
+//   - activations: three bf16 planes per value, truncated so that
+//     x = h + m + l exactly for finite x (8 + 8 + 8 significand bits); a
+//     non-finite x goes whole into the first plane;
+//   - weights: q = byte - 128 is an integer of at most 8 bits, exact in bf16;
+//   - each product is exact in f32 and the matrix core accumulates in f32, so
+//     the result carries f32 accumulation error only, like the GEMV.
+// Block-32 scales: each MFMA covers exactly one 32-wide k block, its result is
+// multiplied by that block's scale of the lane's output column.
+//
+// Work split: a workgroup (4 waves, 32 output columns each as two 16-column
+// MFMA blocks) covers 128 columns over KS 64-wide k blocks; the k splits of a
+// column tile write partial sums, which k_skinny_reduce adds in split order
+// (deterministic), then applies the scale and the bias.
+#include "internal.h"
+#include "kdev.h"
+
+namespace scry {
+namespace {
+
+using namespace dev;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int SK_COLS = 128;  // output columns per workgroup
+constexpr int SK_NT = 256;    // threads per workgroup
+constexpr int SK_ROWS = 16;   // MFMA rows (activation rows, zero past m)
+
+struct SkArgs {
+    const float *x;
+    int ldx, m, k;
+    const uint8_t *w;
+    int kp, n;
+    const float *s32;  // block-32 scales [n][nb], or null
+    int nb;
+    float *part;  // [n_split][16][n_pad] partial sums
+    int n_pad, n_split, kblocks;
+};
+
+// x = h + m + l in truncated bf16 planes (bits of each plane's bf16)
+__device__ __forceinline__ void split3(float x, unsigned &h, unsigned &mi, unsigned &lo) {
+    const unsigned b = __float_as_uint(x);
+    if ((b & 0x7f800000u) == 0x7f800000u) {
+        h = b >> 16;
+        mi = lo = 0;
+        return;
+    }
+    const float r1 = x - __uint_as_float(b & 0xffff0000u);  // exact
+    const unsigned b1 = __float_as_uint(r1);
+    const float r2 = r1 - __uint_as_float(b1 & 0xffff0000u);  // exact, <= 8 significand bits
+    h = b >> 16;
+    mi = b1 >> 16;
+    lo = __float_as_uint(r2) >> 16;
+}
+
+// bytes 4j..4j+3 of (d0, d1) hold q + 128: the bf16 values of q, in byte order.
+// Flipping bit 7 gives q's two's-complement byte; |q| <= 128 is exact in bf16
+// (v_cvt_f32_i32 on a sign-extended byte, then v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16x8 q8_bf16(unsigned d0, unsigned d1) {
+    const unsigned e0 = d0 ^ 0x80808080u, e1 = d1 ^ 0x80808080u;
+    bf16x8 r;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        r[j] = (__bf16)(float)(int)(signed char)(e0 >> (8 * j));
+        r[4 + j] = (__bf16)(float)(int)(signed char)(e1 >> (8 * j));
+    }
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Lane layouts of v_mfma_f32_16x16x32_bf16 (16 x 32 A, 32 x 16 B, 16 x 16 D):
+// lane l holds A[l % 16][8 (l / 16) + e], B[8 (l / 16) + e][l % 16] (e = 0..7)
+// and D[4 (l / 16) + r][l % 16] (r = 0..3).  The k index inside an MFMA is a
+// summation index only; the 64-wide block kb is laid out as
+//   per-tensor: lane group g, half f -> k = 64 kb + 16 g + 8 f + e (one 16-byte
+//               LDS read per lane and column block feeds both halves);
+//   block-32:   lane group g, half f -> k = 64 kb + 32 f + 8 g + e (each half is
+//               one 32-wide scale block).
+// LDS: A planes as 16-byte fragments [kb][plane][half][lane]; per wave a
+// [32 rows][144 B] weight tile for two 64-wide blocks (rows padded by 16 bytes
+// so the 16-byte fragment reads of 16 rows hit distinct banks) and, for
+// block-32, the wave's scales [32 columns][2 KS blocks].
+//
+// Weights come from HBM in whole 128-byte lines: load instruction j of segment
+// s (128 bytes of k = two blocks) reads rows 8 (j % 4) .. +8 of the wave's 32,
+// lane l taking bytes 16 (l % 8) of row l / 8.  Fragments in the MFMA layout
+// (16 rows x 64 bytes per instruction) would split every line in two.
+constexpr int SK_WROW = 144;                 // bytes per weight row in the LDS tile
+constexpr int SK_WTILE = 32 * SK_WROW;       // bytes per wave
+template <int KS, bool B32>
+__global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
+    static_assert(KS % 2 == 0, "weights come in 128-byte segments of two blocks");
+    __shared__ u32x4 s_a[KS * 3 * 2 * 64];
+    __shared__ __attribute__((aligned(16))) unsigned char s_w[4 * SK_WTILE];
+    __shared__ float s_sc[B32 ? 4 * 32 * 2 * KS : 1];
+    const int split = blockIdx.x % a.n_split, tile = blockIdx.x / a.n_split;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kb0 = split * KS;
+    const int nkb = min(KS, a.kblocks - kb0);
+    const int k0 = kb0 * 64;
+
+    // ---- 1. activation loads: unit u = (kb, row, q8) holds x[row][k0 + 64 kb + 8 q8 + 0..7];
+    // eight consecutive threads read 256 contiguous bytes of one row
+    constexpr int UPT = KS * SK_ROWS * 8 / SK_NT;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, ((size_t)(a.m - 1) * a.ldx + a.k) * 4);
+    float4 xv[UPT][2];
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = tid + SK_NT * i, kb = u >> 7, row = (u >> 3) & 15, q8 = u & 7;
+        const int kk = k0 + kb * 64 + q8 * 8;
+        const unsigned off = (row < a.m && kb < nkb && kk < a.k) ? (unsigned)(row * a.ldx + kk) * 4 : 0x80000000u;
+        xv[i][0] = bload16f(xr, off);
+        xv[i][1] = bload16f(xr, off + 16);
+    }
+
+    // ---- 2. the wave's 32 weight rows over this split, all requested now
+    const int cw = tile * SK_COLS + wave * 32;  // the wave's first column
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, (size_t)a.n * a.kp);
+    constexpr int NSEG = KS / 2;
+    u32x4 wv[NSEG][4];
+#pragma unroll
+    for (int sg = 0; sg < NSEG; sg++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = cw + 8 * j + (lane >> 3);
+            const bool ok = 2 * sg < nkb && row < a.n;
+            wv[sg][j] = bload16(wr, ok ? (unsigned)row * a.kp + k0 + 128 * sg + 16 * (lane & 7) : 0x80000000u);
+        }
+    float scv[B32 ? KS : 1];
+    if constexpr (B32) {  // lane l: column cw + l / 2, blocks 2 kb0 + KS (l % 2) .. + KS
+        const int c = cw + (lane >> 1), blk0 = 2 * kb0 + KS * (lane & 1);
+#pragma unroll
+        for (int i = 0; i < KS; i++)
+            scv[i] = (c < a.n && blk0 + i < a.nb) ? a.s32[(size_t)c * a.nb + blk0 + i] : 0.f;
+    }
+
+    // ---- 3. stage the activation planes (and the scales)
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = tid + SK_NT * i, kb = u >> 7, row = (u >> 3) & 15, q8 = u & 7;
+        const int kk = k0 + kb * 64 + q8 * 8;
+        float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                      xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+        unsigned pl[3][8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if (kk + e >= a.k) v[e] = 0.f;  // past the row: the next row's values
+            split3(v[e], pl[0][e], pl[1][e], pl[2][e]);
+        }
+        const int gg = B32 ? (q8 & 3) : (q8 >> 1), f = B32 ? (q8 >> 2) : (q8 & 1);
+        const int l = row + 16 * gg;
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            u32x4 q;
+            q.x = pl[p][0] | (pl[p][1] << 16);
+            q.y = pl[p][2] | (pl[p][3] << 16);
+            q.z = pl[p][4] | (pl[p][5] << 16);
+            q.w = pl[p][6] | (pl[p][7] << 16);
+            s_a[((kb * 3 + p) * 2 + f) * 64 + l] = q;
+        }
+    }
+    float *scw = s_sc + wave * (32 * 2 * KS);  // [32 columns][2 KS blocks]
+    if constexpr (B32) {
+#pragma unroll
+        for (int i = 0; i < KS; i++) scw[(lane >> 1) * 2 * KS + KS * (lane & 1) + i] = scv[i];
+    }
+    __syncthreads();
+
+    // ---- 4. per 128-byte segment: weights through the wave's LDS tile, then
+    // the matrix-core passes of its two blocks
+    unsigned char *tw = s_w + wave * SK_WTILE;
+    const int nn = lane & 15, g = lane >> 4;
+    f32x4 acc[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sg = 0; sg < NSEG; sg++) {
+        if (2 * sg >= nkb) break;  // uniform
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *(u32x4 *)(tw + (8 * j + (lane >> 3)) * SK_WROW + 16 * (lane & 7)) = wv[sg][j];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int kb = 2 * sg + h;
+            if (kb >= nkb) break;  // uniform
+            bf16x8 av[3][2];
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+#pragma unroll
+                for (int f = 0; f < 2; f++) av[p][f] = as_bf16x8(s_a[((kb * 3 + p) * 2 + f) * 64 + lane]);
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++) {
+                const unsigned char *wrow = tw + (16 * cb + nn) * SK_WROW + 64 * h;
+                if constexpr (!B32) {
+                    const u32x4 w = *(const u32x4 *)(wrow + 16 * g);
+                    const bf16x8 b0 = q8_bf16(w.x, w.y), b1 = q8_bf16(w.z, w.w);
+#pragma unroll
+                    for (int p = 0; p < 3; p++) {
+                        acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[p][0], b0, acc[cb], 0, 0, 0);
+                        acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[p][1], b1, acc[cb], 0, 0, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int f = 0; f < 2; f++) {
+                        const uint2 w = *(const uint2 *)(wrow + 32 * f + 8 * g);
+                        const bf16x8 bq = q8_bf16(w.x, w.y);
+                        f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int p = 0; p < 3; p++) t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[p][f], bq, t, 0, 0, 0);
+                        const float sc = scw[(16 * cb + nn) * 2 * KS + 2 * kb + f];
+                        acc[cb].x = fmaf(t.x, sc, acc[cb].x);
+                        acc[cb].y = fmaf(t.y, sc, acc[cb].y);
+                        acc[cb].z = fmaf(t.z, sc, acc[cb].z);
+                        acc[cb].w = fmaf(t.w, sc, acc[cb].w);
+                    }
+                }
+            }
+        }
+    }
+    int col[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) col[cb] = cw + cb * 16 + nn;
+
+    // ---- 5. this split's partial sums: lane holds rows 4 g + r of column col[cb]
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = 4 * g + r;
+            if (row < a.m) a.part[((size_t)split * SK_ROWS + row) * a.n_pad + col[cb]] = acc[cb][r];
+        }
+}
+
+// y[row][col] = scale * (sum of the splits' partials, in split order) (+ bias[col])
+__global__ __launch_bounds__(256) void k_skinny_reduce(const float *part, int n_split, int n_pad, int n,
+                                                       float scale, const float *bias, float *y, int ldy) {
+    const int col = blockIdx.x * 256 + threadIdx.x, row = blockIdx.y;
+    if (col >= n) return;
+    const float bb = bias ? bias[col] : 0.f;  // requested with the partials
+    const float *p = part + (size_t)row * n_pad + col;
+    const size_t st = (size_t)SK_ROWS * n_pad;
+    float s = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < n_split; i++) s += p[i * st];
+    float v = s * scale;
+    if (bias) v = v + bb;
+    y[(size_t)row * ldy + col] = v;
+}
+
+struct SkPlan {
+    int ks, kblocks, n_split, tiles, n_pad;
+};
+
+SkPlan plan(int k, int n) {
+    SkPlan p;
+    p.kblocks = (k + 63) / 64;
+    p.tiles = (n + SK_COLS - 1) / SK_COLS;
+    p.n_pad = p.tiles * SK_COLS;
+    p.ks = 8;
+    if ((size_t)p.tiles * ((p.kblocks + 7) / 8) < 512) p.ks = 4;  // enough workgroups to stream the weights
+    p.n_split = (p.kblocks + p.ks - 1) / p.ks;
+    return p;
+}
+
+template <int KS, bool B32>
+int launch_ks(const SkArgs &a, int tiles, hipStream_t s) {
+    hipLaunchKernelGGL((k_skinny<KS, B32>), dim3(tiles * a.n_split), dim3(SK_NT), 0, s, a);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
+
+}  // namespace
+
+bool skinny_route(int m, int k, int n) {
+    return m >= SKINNY_MIN_M && m <= SK_ROWS && k % 8 == 0 && k >= 256 && n >= 256;
+}
+
+size_t skinny_ws_bytes(int m, int k, int n) {
+    (void)m;
+    const SkPlan p = plan(k, n);
+    return sizeof(float) * (size_t)p.n_split * SK_ROWS * p.n_pad;
+}
+
+int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s) {
+    const Packed &w = *mm.w;
+    if (w.bf16 || w.fused || w.rows != w.n)
+        return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: plain int8 weight rows only");
+    if (mm.m < 1 || mm.m > SK_ROWS || mm.ldx < w.k || mm.ldy < w.n)
+        return set_error(SCRY_ERR_INVALID, "skinny matmul: %d rows (1..%d), ldx %d, ldy %d", mm.m, SK_ROWS,
+                         mm.ldx, mm.ldy);
+    if (w.k % 8 != 0) return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: k %% 8 != 0");
+    if (w.kp < w.k || (size_t)w.n * w.kp > 0x7fffffffu || (size_t)mm.m * mm.ldx * 4 > 0x7fffffffu)
+        return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: operands above the 2 GiB buffer range");
+    const SkPlan p = plan(w.k, w.n);
+    if (ws_bytes < skinny_ws_bytes(mm.m, w.k, w.n))
+        return set_error(SCRY_ERR_INVALID, "skinny matmul: workspace too small");
+    SkArgs a;
+    a.x = mm.x;
+    a.ldx = mm.ldx;
+    a.m = mm.m;
+    a.k = w.k;
+    a.w = w.d;
+    a.kp = w.kp;
+    a.n = w.n;
+    a.s32 = w.s32;
+    a.nb = w.nb;
+    a.part = ws;
+    a.n_pad = p.n_pad;
+    a.n_split = p.n_split;
+    a.kblocks = p.kblocks;
+    const bool b32 = w.s32 != nullptr;
+    const int rc = p.ks == 8 ? (b32 ? launch_ks<8, true>(a, p.tiles, s) : launch_ks<8, false>(a, p.tiles, s))
+                             : (b32 ? launch_ks<4, true>(a, p.tiles, s) : launch_ks<4, false>(a, p.tiles, s));
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_skinny_reduce, dim3((w.n + 255) / 256, mm.m), dim3(256), 0, s, ws, p.n_split, p.n_pad,
+                       w.n, b32 ? 1.0f : w.scale, mm.bias, mm.y, mm.ldy);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
+
+}  // namespace scry

@@ -332,7 +332,7 @@ def bench_qgemv_dist(m: int, k: int, n: int, quant_mode: int = QUANT_PER_TENSOR,
     """(per-launch device times of each group of `group` launches [iters/group]
     in us, back-to-back average us, algorithmic bytes per launch) of
     matmul_i8_f32 at (m, k, n); path 0 = the automatic route, 1 = the GEMV,
-    2 = the MFMA GEMM."""
+    2 = the MFMA GEMM, 3 = the skinny MFMA kernel (up to 16 rows)."""
     per = np.empty(iters // group, np.float64)
     us, b = C.c_double(), C.c_double()
     call("scry_hip_bench_qgemv_dist", m, k, n, quant_mode, path, n_bufs, warmup, iters, group,

@@ -135,6 +135,94 @@ def test_matmul_i8_exact_integer(hip):
     assert (out == q.astype(np.int64).sum(0)).all()
 
 
+# ------------------------------------------------ skinny MFMA route (2..16 rows)
+# matmul_i8_f32 takes 3..16 activation rows with k % 8 == 0, k >= 256 and
+# n >= 256 to the skinny MFMA kernel (three exact bf16 planes of x, q in bf16,
+# k splits added in order); the shapes of test_matmul_i8_f32 at m = 4 and 16
+# and the block-32 shapes above already run there.
+@pytest.mark.parametrize("m,k,n", [(3, 1000, 300), (7, 4096, 4096), (13, 1032, 513), (16, 14336, 4096),
+                                   (9, 11008, 300)])
+def test_skinny_matmul_vs_oracle(hip, orc, m, k, n):
+    """Ragged k (a partial last 64-wide block), ragged n (a partial column
+    tile), every row count class, per-tensor with bias and block-32."""
+    B = hip.HipBackend
+    rng = np.random.default_rng(m * 11 + k + n)
+    print(f"[case] skinny matmul m={m} k={k} n={n}", flush=True)
+    a = rng.normal(0, 1, (m, k)).astype(F)
+    w = rng.normal(0, 0.02, (k, n)).astype(F)
+    bias = rng.normal(0, 1, n).astype(F)
+    q, s = orc.quantize_symmetric(w)
+    q32, s32 = orc.quantize_block32(w, k, n)
+    orc.set_threads(8)
+    ref = orc.matmul_i8_f32_bias(a, q, s, bias, m, k, n)
+    ref32 = orc.matmul_i8_f32_b32(a, q32, s32, m, k, n)
+    orc.set_threads(0)
+    out = B.matmul_i8_f32_bias(B.from_vec(a), B.i8_from_vec(q), s, B.from_vec(bias), m, k, n)
+    out32 = B.matmul_i8_f32_block32(B.from_vec(a), B.i8_from_vec(q32), B.from_vec(s32), m, k, n)
+    e, e32 = rel_err(out.to_vec().reshape(m, n), ref), rel_err(out32.to_vec().reshape(m, n), ref32)
+    print(f"[err] per-tensor+bias {e:.3e} block-32 {e32:.3e}", flush=True)
+    assert e < 2e-5 and e32 < 2e-5
+
+
+def test_skinny_matmul_exact_integers(hip):
+    """Exact results that pin the three activation planes, the k order inside
+    an MFMA and the column mapping:
+      - 24-bit integer activations (every plane carries bits) and one weight of
+        +-1 per output column at a random k: each output is +-x exactly;
+      - two such weights per column with 22-bit activations: exact sums;
+      - 15-bit activations and full-range weights, two per column: exact;
+      - block-32 with power-of-two scales and one weight per column: exact."""
+    B = hip.HipBackend
+    rng = np.random.default_rng(21)
+    m, k, n = 5, 1024, 384
+
+    def sparse_q(per_col, full_range):
+        q = np.zeros((k, n), np.int8)
+        for j in range(n):
+            rows = rng.choice(k, per_col, replace=False)
+            q[rows, j] = (rng.integers(-127, 128, per_col) if full_range
+                          else rng.choice([-1, 1], per_col))
+        return q
+
+    def ints(bits):
+        return (rng.integers(0, 2 ** bits, (m, k)) * rng.choice([-1, 1], (m, k))).astype(np.int64)
+
+    for bits, per_col, full in ((23, 1, False), (22, 2, False), (15, 2, True)):
+        x, q = ints(bits), sparse_q(per_col, full)
+        want = x @ q.astype(np.int64)
+        assert np.abs(want).max() < 2 ** 24
+        out = B.matmul_i8_f32(B.from_vec(x.astype(F)), B.i8_from_vec(q), 1.0, m, k, n).to_vec()
+        assert np.array_equal(out.reshape(m, n).astype(np.int64), want), (bits, per_col)
+    x, q = ints(23), sparse_q(1, False)
+    s32 = (2.0 ** rng.integers(-2, 3, (n, k // 32))).astype(F)
+    w32 = q.astype(np.float64) * np.repeat(s32.T.astype(np.float64), 32, axis=0)
+    want32 = x.astype(np.float64) @ w32
+    out32 = B.matmul_i8_f32_block32(B.from_vec(x.astype(F)), B.i8_from_vec(q), B.from_vec(s32.ravel()),
+                                    m, k, n).to_vec().reshape(m, n)
+    assert np.array_equal(out32.astype(np.float64), want32)
+
+
+def test_skinny_matmul_nonfinite(hip, orc):
+    """Inf and NaN activations reach the outputs as the reference's f32 sums
+    give them (Inf times a nonzero weight stays infinite, times 0 is NaN)."""
+    B = hip.HipBackend
+    rng = np.random.default_rng(22)
+    m, k, n = 4, 512, 256
+    a = rng.normal(0, 1, (m, k)).astype(F)
+    a[0, 3] = np.inf
+    a[1, 100] = -np.inf
+    a[2, 7] = np.nan
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    q[3, :16] = 0
+    ref = orc.matmul_i8_f32(a, q, 0.01, m, k, n)
+    out = B.matmul_i8_f32(B.from_vec(a), B.i8_from_vec(q), 0.01, m, k, n).to_vec().reshape(m, n)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    assert np.array_equal(np.isinf(out), np.isinf(ref))
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.sign(out[np.isinf(out)]), np.sign(ref[np.isinf(ref)]))
+    assert rel_err(out[fin], ref[fin]) < 2e-5
+
+
 def test_matmul_shape_errors(hip):
     B = hip.HipBackend
     with pytest.raises(hip.ScryHipError) as ei:
