@@ -652,8 +652,6 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
     if (n_seq < 1 || n_seq > PF_MAX_SEQS || seq < 1)
         return set_error(SCRY_ERR_INVALID, "prefill: n_seq must be 1..%d and seq >= 1", PF_MAX_SEQS);
     if (m->hd > 128) return set_error(SCRY_ERR_UNSUPPORTED, "prefill: head_dim %d > 128", m->hd);
-    if (m->quant_mode == SCRY_QUANT_BF16)
-        return set_error(SCRY_ERR_UNSUPPORTED, "prefill: the batched prefill runs on int8 weights (bf16 model: decode)");
     PrefillSeqs t{};
     for (int i = 0; i < n_seq; i++) {
         scry_kv_cache c = cs[i];
@@ -751,7 +749,16 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         g.m = n_seq;
         g.y = last_logits;
         g.ldy = m->V;
-        SCRY_TRY(launch_qgemv(EPI_STORE, g, s));
+        if (m->lm.bf16) {  // the bf16 GEMV takes one activation row per launch
+            g.m = 1;
+            for (int i = 0; i < n_seq; i++) {
+                g.x = P.xl + (size_t)i * m->h;
+                g.y = last_logits + (size_t)i * m->V;
+                SCRY_TRY(launch_qgemv(EPI_STORE, g, s));
+            }
+        } else {
+            SCRY_TRY(launch_qgemv(EPI_STORE, g, s));
+        }
     }
     for (int i = 0; i < n_seq; i++) cs[i]->seq_len += seq;
     return SCRY_OK;

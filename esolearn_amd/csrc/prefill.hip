@@ -639,7 +639,9 @@ int launch_split(const float *x, int ldx, int rows, int k, u16 *hi, u16 *lo, int
 
 int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
     const Packed &w = *g.w;
-    if (w.kp % 16 || w.k > w.kp) return set_error(SCRY_ERR_INVALID, "gemm: bad packed layout");
+    const int kp_el = w.bf16 ? w.kp / 2 : w.kp;  // row stride in weights
+    if (w.kp % 16 || w.k > kp_el) return set_error(SCRY_ERR_INVALID, "gemm: bad packed layout");
+    if (w.bf16 && w.s32) return set_error(SCRY_ERR_INVALID, "gemm: bf16 weights carry no block scales");
     if (w.bytes() >= 0x7fffffffull)  // buffer offsets are 32-bit
         return set_error(SCRY_ERR_UNSUPPORTED, "gemm: %zu weight bytes (limit 2 GiB per tensor)", w.bytes());
     const int kpad = prefill_k_pad(w.k);
@@ -652,7 +654,7 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
     p.alo = g.alo;
     p.lda = g.lda;
     p.w = w.d;
-    p.kp = w.kp;
+    p.kp = kp_el;
     p.N = w.rows;
     p.s32 = w.s32;
     p.nb = w.nb;
@@ -671,6 +673,15 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
     p.ldo = g.ldo;
     p.opad = g.opad;
     const bool b32 = w.s32 != nullptr;
+    if (w.bf16) {  // the bf16 model: weight rows as they are, the hi plane = the reference's bf16 cast
+        p.alo = nullptr;
+        switch (epi) {
+            case GE_STORE: return gemm_t<GE_STORE, false, true>(p, s);
+            case GE_RESID: return gemm_t<GE_RESID, false, true>(p, s);
+            case GE_SWIGLU: return gemm_t<GE_SWIGLU, false, true>(p, s);
+        }
+        return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
+    }
     switch (epi) {
         case GE_STORE: return b32 ? gemm_t<GE_STORE, true>(p, s) : gemm_t<GE_STORE, false>(p, s);
         case GE_RESID: return b32 ? gemm_t<GE_RESID, true>(p, s) : gemm_t<GE_RESID, false>(p, s);

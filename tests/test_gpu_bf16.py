@@ -152,6 +152,8 @@ def _bf16_decode_vs_oracle(hip, orc, cfg, seed, prompt, steps, tol, init_on_devi
     try:
         kt, kl = hm.generate_greedy(prompt, steps, want_logits=True)
         kt2, kl2 = hm.generate_greedy(prompt, steps, want_logits=True)
+        # the prompt through the batched prefill (the MFMA GEMM on the bf16 rows)
+        pt, pl = hm.generate_greedy(prompt, steps, want_logits=True, prefill=True)
         with pytest.raises(hip.ScryHipError):
             hm.qtensor(orc.T_QKV, 0)  # the model holds no int8 weights
     finally:
@@ -165,11 +167,12 @@ def _bf16_decode_vs_oracle(hip, orc, cfg, seed, prompt, steps, tol, init_on_devi
         om.close()
         orc.set_threads(0)
     err = max(rel_err(kl[i], ref_l[i]) for i in range(steps))
+    perr = max(rel_err(pl[i], ref_l[i]) for i in range(steps))
     gap = max(rel_err(f32_l[i], ref_l[i]) for i in range(steps))
-    print(f"[err] bf16 decode {err:.3e} (bar {tol:g}; f32 semantics would be {gap:.3e} away); "
-          f"tokens {kt[:6].tolist()}", flush=True)
-    assert err < tol
-    assert (kt == ref_t).all()
+    print(f"[err] bf16 decode {err:.3e}, with batched prefill {perr:.3e} (bar {tol:g}; f32 semantics "
+          f"would be {gap:.3e} away); tokens {kt[:6].tolist()}", flush=True)
+    assert err < tol and perr < tol
+    assert (kt == ref_t).all() and (pt == ref_t).all()
     assert (kt2 == kt).all() and np.array_equal(kl2, kl)  # replays reproduce bit for bit
 
 
@@ -211,11 +214,23 @@ def test_bf16_model_decode_7b_dims(hip, orc):
                            init_on_device=True)
 
 
-def test_bf16_model_refuses_prefill(hip, orc):
-    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**TINY), 0, quant_mode=hip.QUANT_BF16)
+@pytest.mark.parametrize("layers,tol", [(1, SHALLOW_TOL), (6, DEEP_TOL)])
+def test_bf16_model_forward_all_positions(hip, orc, layers, tol):
+    """LlamaModel::forward (llama.rs:683-700) on the bf16 model: every
+    position's logits through the batched GEMMs, against oracle forward mode 3."""
+    print(f"[case] bf16 model forward, tiny dims, {layers} layer(s), 12 tokens", flush=True)
+    cfg = dict(TINY, n_layers=layers)
+    toks = orc.prompt_ids(5, 12, TINY["vocab_size"])
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), 0, quant_mode=hip.QUANT_BF16)
     try:
-        with pytest.raises(hip.ScryHipError) as ei:
-            hm.generate_greedy(orc.prompt_ids(1, 8, TINY["vocab_size"]), 4, prefill=True)
-        assert "bf16" in str(ei.value)
+        got = hm.forward(toks)
     finally:
         hm.free()
+    om = orc.Llama(orc.LlamaConfig(**cfg), 0, quantize=False)
+    try:
+        ref = om.forward(toks, mode=3)
+    finally:
+        om.close()
+    err = max(rel_err(got[i], ref[i]) for i in range(len(toks)))
+    print(f"[err] bf16 forward {err:.3e} (bar {tol:g})", flush=True)
+    assert err < tol
