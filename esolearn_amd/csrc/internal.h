@@ -272,6 +272,13 @@ struct PrefillSeqs {  // per sequence: its KV cache and first position
     const float2 *rope[PF_MAX_SEQS];         // (cos, sin) [max_seq][hd/2]
     int p0[PF_MAX_SEQS];
 };
+// bf16 hi / lo planes of the K and V rows a prefill attends over, per
+// (sequence, KV head): [n_seq][n_kv][rows][hd] each (hi = bf16(x), lo =
+// bf16(x - hi)); null kh: the attention reads the f32 cache instead.
+struct PrefillKVP {
+    unsigned short *kh = nullptr, *kl = nullptr, *vh = nullptr, *vl = nullptr;
+    int rows = 0;
+};
 struct PrefillGemm {
     const Packed *w = nullptr;
     const unsigned short *ahi = nullptr, *alo = nullptr;  // bf16 planes [Mp][lda], lda >= prefill_k_pad(k)
@@ -297,9 +304,13 @@ int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, co
 int launch_split(const float *x, int ldx, int rows, int k, unsigned short *hi, unsigned short *lo, int ldp,
                  hipStream_t s);
 int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s);
+// RoPE + K/V cache append; with kp.kh also the planes of the new K / V rows
+// (and of the rows [0, p0) already in the caches)
 int launch_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, const PrefillSeqs &t, int l,
-                   hipStream_t s);
-int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hipStream_t s);
+                   const PrefillKVP &kp, int n_seq, hipStream_t s);
+bool attn_prefill_planes(int hd);  // head sizes the bf16 plane attention takes
+int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, const PrefillKVP &kv,
+                        hipStream_t s);
 
 // bf16.hip -- bf16 mode: the reference's cast, widening, B-operand rows
 // [n][kp] (kp = bf16_row_pad(k)), the GEMM activation plane, the bf16 GEMV

@@ -60,6 +60,8 @@ struct scry_llama_s {
         float *x = nullptr, *qkv = nullptr, *last = nullptr, *xl = nullptr;
         int64_t *ids = nullptr;
     } pf;
+    unsigned short *kvp = nullptr;  // the prefill attention's K / V planes (grown on demand)
+    size_t kvp_n = 0;
     const float *norm_in(int l) const { return norms + (size_t)(2 * l) * h; }
     const float *norm_post(int l) const { return norms + (size_t)(2 * l + 1) * h; }
     const float *norm_final() const { return norms + (size_t)(2 * L) * h; }
@@ -238,6 +240,7 @@ void model_free(scry_llama m) {
     dev_free(m->pf.last);
     dev_free(m->pf.xl);
     dev_free(m->pf.ids);
+    dev_free(m->kvp);
     delete m;
 }
 
@@ -670,6 +673,26 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
     const int M = n_seq * seq;
     SCRY_TRY(check_ids(m, tokens, M));
     SCRY_TRY(prefill_ws(m, M, n_seq));
+    // K / V planes for the bf16 matrix-core attention: rows [0, p0 + seq) of every sequence
+    PrefillKVP kvp;
+    if (attn_prefill_planes(m->hd)) {
+        int rows = 0;
+        for (int i = 0; i < n_seq; i++) rows = std::max(rows, t.p0[i] + seq);
+        const size_t per = (size_t)n_seq * m->nkv * rows * m->hd;
+        if (m->kvp_n < 4 * per) {
+            SCRY_TRY(sync_stream());  // queued work may still read the old planes
+            dev_free(m->kvp);
+            m->kvp = nullptr;
+            m->kvp_n = 0;
+            SCRY_TRY(dev_alloc((void **)&m->kvp, sizeof(unsigned short) * 4 * per));
+            m->kvp_n = 4 * per;
+        }
+        kvp.kh = m->kvp;
+        kvp.kl = m->kvp + per;
+        kvp.vh = m->kvp + 2 * per;
+        kvp.vl = m->kvp + 3 * per;
+        kvp.rows = rows;
+    }
     auto &P = m->pf;
     hipStream_t s = ctx().stream;
     unsigned short *h0 = P.p0, *l0 = P.p0 + (size_t)P.Mp * P.ld0;
@@ -689,7 +712,7 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         g.c = P.qkv;
         g.ldc = m->qkv_dim;
         SCRY_TRY(launch_gemm(PF_STORE, g, s));
-        SCRY_TRY(launch_rope_kv(P.qkv, m->qkv_dim, M, seq, m->q_dim, m->kv_dim, m->hd, t, l, s));
+        SCRY_TRY(launch_rope_kv(P.qkv, m->qkv_dim, M, seq, m->q_dim, m->kv_dim, m->hd, t, l, kvp, n_seq, s));
         PrefillAttn at;
         at.qkv = P.qkv;
         at.ldq = m->qkv_dim;
@@ -703,7 +726,7 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         at.olo = l0;
         at.ldo = P.ld0;
         at.opad = prefill_k_pad(m->q_dim);
-        SCRY_TRY(launch_attn_prefill(at, n_seq, t, l, s));
+        SCRY_TRY(launch_attn_prefill(at, n_seq, t, l, kvp, s));
         g.w = &Ly.o;
         g.c = P.x;
         g.ldc = m->h;

@@ -347,8 +347,9 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
 // in place (llama.rs:208-216 without a pre-scale: forward scales the scores),
 // k pairs are rotated into the cache row, v is copied into the cache row
 // (kv_cache.rs:99-118).  cpu.rs:655-658 in f32, no contraction.
-__global__ void k_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, PrefillSeqs t, int l) {
-    const int hh = hd >> 1;
+__global__ void k_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, PrefillSeqs t, int l,
+                          PrefillKVP kp) {
+    const int hh = hd >> 1, nkv = kvd / hd;
     const int per_row = (qd >> 1) + (kvd >> 1) + kvd;
     const size_t total = (size_t)M * per_row;
     for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (size_t)gridDim.x * blockDim.x) {
@@ -372,10 +373,38 @@ __global__ void k_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, 
             } else {
                 kc[j] = r0;
                 kc[j + 1] = r1;
+                if (kp.kh) {  // the attention's planes of this K row
+                    const size_t at = ((size_t)(s * nkv + j / hd) * kp.rows + pos) * hd + j % hd;
+                    u16 h0, l0, h1, l1;
+                    split_bf16(r0, h0, l0);
+                    split_bf16(r1, h1, l1);
+                    *(unsigned *)(kp.kh + at) = (unsigned)h0 | ((unsigned)h1 << 16);
+                    *(unsigned *)(kp.kl + at) = (unsigned)l0 | ((unsigned)l1 << 16);
+                }
             }
         } else {
             const int j = e - (qd >> 1) - (kvd >> 1);
-            vc[j] = row[qd + kvd + j];
+            const float v = row[qd + kvd + j];
+            vc[j] = v;
+            if (kp.kh) {
+                const size_t at = ((size_t)(s * nkv + j / hd) * kp.rows + pos) * hd + j % hd;
+                split_bf16(v, kp.vh[at], kp.vl[at]);
+            }
+        }
+    }
+}
+
+// The planes of the K / V rows [0, p0) that earlier calls left in the caches.
+__global__ void k_kv_planes(PrefillSeqs t, int l, int n_seq, int kvd, int hd, PrefillKVP kp) {
+    const int nkv = kvd / hd;
+    for (int s = 0; s < n_seq; s++) {
+        const size_t total = (size_t)t.p0[s] * kvd;
+        const float *kc = t.k[s] + (size_t)l * t.ls[s], *vc = t.v[s] + (size_t)l * t.ls[s];
+        for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (size_t)gridDim.x * blockDim.x) {
+            const int row = (int)(g / kvd), c = (int)(g % kvd);
+            const size_t at = ((size_t)(s * nkv + c / hd) * kp.rows + row) * hd + c % hd;
+            split_bf16(kc[g], kp.kh[at], kp.kl[at]);
+            split_bf16(vc[g], kp.vh[at], kp.vl[at]);
         }
     }
 }
@@ -585,6 +614,190 @@ __global__ __launch_bounds__(64 * MQW) void k_attn_mfma(PrefillAttn a, PrefillSe
         }
 }
 
+// The same attention on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16),
+// every f32 operand x carried as hi = bf16(x), lo = bf16(x - hi) and each
+// product as hi*hi + hi*lo + lo*hi (the lo*lo term is below 2^-16 of it):
+// error ~2^-16 relative per product, where the fp32 matrix cores give 2^-24
+// at one sixteenth of the rate.  K and V come as planes written once per row
+// (k_rope_kv, k_kv_planes); q is split in registers.
+// Workgroup: 16 query rows per wave, 8 waves, one (head, sequence); K / V
+// tiles of 64 keys in LDS, K key-major [key][hd], V transposed [hd][key].
+// Per wave and 32 keys:
+//   S^T = K Q^T for two 16-key halves (A = K [16 keys][32 hd], B = Q^T):
+//     lane l gets query l % 16 against keys 4 (l / 16) + r of each half;
+//   online softmax per query over the 32 keys (4 lanes l % 16 + 16 g);
+//   O^T += V^T P^T with the 32 keys as the MFMA's k: slot 8 g + e is key
+//     4 g + e (e < 4) of the first half and 16 + 4 g + (e - 4) of the
+//     second, which is exactly the P values lane (l % 16, g) holds.
+constexpr int BQW = 8, BQ = 16 * BQW, BKT = 64;  // waves; query rows; keys per tile
+
+__device__ __forceinline__ unsigned pack_hl(float a, float b, bool lo_plane) {
+    u16 ha, la, hb, lb;
+    split_bf16(a, ha, la);
+    split_bf16(b, hb, lb);
+    return lo_plane ? ((unsigned)la | ((unsigned)lb << 16)) : ((unsigned)ha | ((unsigned)hb << 16));
+}
+
+template <int HD>
+__global__ __launch_bounds__(64 * BQW) void k_attn_bf3(PrefillAttn a, PrefillSeqs t, PrefillKVP kv) {
+    constexpr int NKB = HD / 32, NDT = HD / 16, KLD = HD + 8, VLD = BKT + 8;
+    extern __shared__ float4 ab4[];
+    u16 *sKh = reinterpret_cast<u16 *>(ab4);
+    u16 *sKl = sKh + BKT * KLD, *sVh = sKl + BKT * KLD, *sVl = sVh + HD * VLD;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
+    const int h = blockIdx.y, s = blockIdx.z;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int i = qb * BQ + w * 16 + lr;
+    const bool valid = i < a.seq;
+    const int p0 = t.p0[s], pos = p0 + i;
+    const int kvh = h / (a.nh / a.nkv);
+    const size_t m = (size_t)s * a.seq + i;
+    // Q^T fragments: lane (query lr, group lg) holds head dims 32 kb + 8 lg + e
+    bf16x8 qh[NKB], ql[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+        if (valid) {
+            const float *qr = a.qkv + m * a.ldq + h * HD + 32 * kb + 8 * lg;
+            v0 = *(const float4 *)qr;
+            v1 = *(const float4 *)(qr + 4);
+        }
+        u32x4 hv, lv;
+        hv.x = pack_hl(v0.x, v0.y, false), lv.x = pack_hl(v0.x, v0.y, true);
+        hv.y = pack_hl(v0.z, v0.w, false), lv.y = pack_hl(v0.z, v0.w, true);
+        hv.z = pack_hl(v1.x, v1.y, false), lv.z = pack_hl(v1.x, v1.y, true);
+        hv.w = pack_hl(v1.z, v1.w, false), lv.w = pack_hl(v1.z, v1.w, true);
+        qh[kb] = __builtin_bit_cast(bf16x8, hv);
+        ql[kb] = __builtin_bit_cast(bf16x8, lv);
+    }
+    f32x4 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float mrow = -INFINITY, lrow = 0.f;
+    const int kend = p0 + min(a.seq, (qb + 1) * BQ);               // keys of the workgroup
+    const int wlast = p0 + min(a.seq, qb * BQ + w * 16 + 16) - 1;  // last key of this wave's rows
+    const size_t pb = ((size_t)s * a.nkv + kvh) * kv.rows * HD;     // plane rows of (s, kvh)
+    for (int k0 = 0; k0 < kend; k0 += BKT) {
+        __syncthreads();
+        // K planes: key j, 8 head dims per chunk
+        for (int idx = tid; idx < 2 * BKT * (HD / 8); idx += 64 * BQW) {
+            const int pl = idx / (BKT * (HD / 8)), r = idx - pl * (BKT * (HD / 8));
+            const int j = r / (HD / 8), c = r - j * (HD / 8);
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if (k0 + j < kend) v = *(const u32x4 *)((pl ? kv.kl : kv.kh) + pb + (size_t)(k0 + j) * HD + 8 * c);
+            *(u32x4 *)((pl ? sKl : sKh) + j * KLD + 8 * c) = v;
+        }
+        // V planes transposed: keys 2 jp, 2 jp + 1 of 8 head dims -> 8 words [hd][key pair]
+        for (int idx = tid; idx < 2 * (BKT / 2) * (HD / 8); idx += 64 * BQW) {
+            const int pl = idx / ((BKT / 2) * (HD / 8)), r = idx - pl * ((BKT / 2) * (HD / 8));
+            const int c = r / (BKT / 2), jp = r - c * (BKT / 2), j = 2 * jp;
+            const u16 *src = (pl ? kv.vl : kv.vh) + pb;
+            u32x4 v0 = u32x4{0u, 0u, 0u, 0u}, v1 = v0;
+            if (k0 + j < kend) v0 = *(const u32x4 *)(src + (size_t)(k0 + j) * HD + 8 * c);
+            if (k0 + j + 1 < kend) v1 = *(const u32x4 *)(src + (size_t)(k0 + j + 1) * HD + 8 * c);
+            u16 *dst = (pl ? sVl : sVh) + (8 * c) * VLD + j;
+            const unsigned a0[4] = {v0.x, v0.y, v0.z, v0.w}, a1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                *(unsigned *)(dst + (2 * e) * VLD) = (a0[e] & 0xffffu) | (a1[e] << 16);
+                *(unsigned *)(dst + (2 * e + 1) * VLD) = (a0[e] >> 16) | (a1[e] & 0xffff0000u);
+            }
+        }
+        __syncthreads();
+        for (int c32 = 0; c32 < BKT; c32 += 32) {
+            const int kb0 = k0 + c32;
+            if (kb0 > wlast) break;  // wave-uniform: masked for every row of the wave
+            float p[8];
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int kr = (c32 + 16 * hf + lr) * KLD + 8 * lg;
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) {
+                    const bf16x8 kh = *(const bf16x8 *)(sKh + kr + 32 * kb);
+                    const bf16x8 kl = *(const bf16x8 *)(sKl + kr + 32 * kb);
+                    st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[kb], st, 0, 0, 0);
+                    st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[kb], st, 0, 0, 0);
+                    st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[kb], st, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    p[4 * hf + r] = kb0 + 16 * hf + 4 * lg + r <= pos ? st[r] * a.scale : -INFINITY;  // llama.rs:225-234
+            }
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 8; e++) tmax = fmaxf(tmax, p[e]);
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const float mn = fmaxf(mrow, tmax);  // finite: key 0 is visible to every row
+            const float alpha = expf(mrow - mn);
+            float ps = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                p[e] = expf(p[e] - mn);
+                ps += p[e];
+            }
+            ps += __shfl_xor(ps, 16);
+            ps += __shfl_xor(ps, 32);
+            lrow = lrow * alpha + ps;
+            mrow = mn;
+            u32x4 phv, plv;
+            phv.x = pack_hl(p[0], p[1], false), plv.x = pack_hl(p[0], p[1], true);
+            phv.y = pack_hl(p[2], p[3], false), plv.y = pack_hl(p[2], p[3], true);
+            phv.z = pack_hl(p[4], p[5], false), plv.z = pack_hl(p[4], p[5], true);
+            phv.w = pack_hl(p[6], p[7], false), plv.w = pack_hl(p[6], p[7], true);
+            const bf16x8 ph = __builtin_bit_cast(bf16x8, phv), pl = __builtin_bit_cast(bf16x8, plv);
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                o[dt] *= alpha;
+                const int vr = (16 * dt + lr) * VLD + c32 + 4 * lg;
+                u32x4 vh, vl;
+                const uint2 h0 = *(const uint2 *)(sVh + vr), h1 = *(const uint2 *)(sVh + vr + 16);
+                const uint2 l0 = *(const uint2 *)(sVl + vr), l1 = *(const uint2 *)(sVl + vr + 16);
+                vh.x = h0.x, vh.y = h0.y, vh.z = h1.x, vh.w = h1.y;
+                vl.x = l0.x, vl.y = l0.y, vl.z = l1.x, vl.w = l1.y;
+                const bf16x8 bvh = __builtin_bit_cast(bf16x8, vh), bvl = __builtin_bit_cast(bf16x8, vl);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bvh, ph, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bvh, pl, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bvl, ph, o[dt], 0, 0, 0);
+            }
+        }
+    }
+    if (!valid) return;
+    const float inv = 1.f / lrow;
+    u16 *oh = a.ohi + m * a.ldo + h * HD, *ol = a.olo + m * a.ldo + h * HD;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int d = dt * 16 + 4 * lg + r;
+            u16 x0, x1;
+            split_bf16(o[dt][r] * inv, x0, x1);
+            oh[d] = x0;
+            ol[d] = x1;
+        }
+    if (h == a.nh - 1 && lg == 0)  // zero the k padding of the o_proj input
+        for (int c = a.nh * HD; c < a.opad; c++) {
+            a.ohi[m * a.ldo + c] = 0;
+            a.olo[m * a.ldo + c] = 0;
+        }
+}
+
+template <int HD>
+int attn_bf3_t(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, const PrefillKVP &kv, hipStream_t s) {
+    constexpr size_t lds = (2 * (size_t)BKT * (HD + 8) + 2 * (size_t)HD * (BKT + 8)) * sizeof(u16);
+    static bool attr = false;
+    if (!attr) {
+        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_bf3<HD>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    const dim3 grid((a.seq + BQ - 1) / BQ, a.nh, n_seq);
+    hipLaunchKernelGGL(k_attn_bf3<HD>, grid, dim3(64 * BQW), lds, s, a, t, kv);
+    PF_LAUNCH_CHECK();
+}
+
 template <int HD>
 int attn_mfma_t(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hipStream_t s) {
     constexpr size_t lds = 2 * (size_t)MK * (HD + 4) * sizeof(float);
@@ -718,18 +931,37 @@ int launch_gemm_bf16(const unsigned short *w, int kp, int N, int k, const unsign
 }
 
 int launch_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, const PrefillSeqs &t, int l,
-                   hipStream_t s) {
+                   const PrefillKVP &kp, int n_seq, hipStream_t s) {
     if (hd % 2 || qd % hd || kvd % hd) return set_error(SCRY_ERR_INVALID, "rope_kv: bad head dims");
+    if (kp.kh) {
+        int rmax = 0, any_old = 0;
+        for (int i = 0; i < n_seq; i++) {
+            rmax = std::max(rmax, t.p0[i] + seq);
+            any_old |= t.p0[i] > 0;
+        }
+        if (rmax > kp.rows) return set_error(SCRY_ERR_INVALID, "rope_kv: %d plane rows < %d", kp.rows, rmax);
+        if (any_old) {
+            hipLaunchKernelGGL(k_kv_planes, dim3(1024), dim3(256), 0, s, t, l, n_seq, kvd, hd, kp);
+            SCRY_HIP(hipGetLastError());
+        }
+    }
     const size_t total = (size_t)M * ((qd >> 1) + (kvd >> 1) + kvd);
     if (total == 0) return SCRY_OK;
     const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256, 65536);
-    hipLaunchKernelGGL(k_rope_kv, dim3(grid), dim3(256), 0, s, qkv, ldq, M, seq, qd, kvd, hd, t, l);
+    hipLaunchKernelGGL(k_rope_kv, dim3(grid), dim3(256), 0, s, qkv, ldq, M, seq, qd, kvd, hd, t, l, kp);
     PF_LAUNCH_CHECK();
 }
 
-int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, hipStream_t s) {
+bool attn_prefill_planes(int hd) { return hd == 64 || hd == 128; }
+
+int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, int l, const PrefillKVP &kv,
+                        hipStream_t s) {
     if (a.hd % 2 || a.hd > 128 || a.nkv <= 0 || a.nh % a.nkv)
         return set_error(SCRY_ERR_UNSUPPORTED, "attn_prefill: head_dim %d / heads %d,%d", a.hd, a.nh, a.nkv);
+    if (kv.kh && attn_prefill_planes(a.hd)) {  // bf16 matrix cores on the K / V planes
+        if (a.hd == 128) return attn_bf3_t<128>(a, n_seq, t, kv, s);
+        return attn_bf3_t<64>(a, n_seq, t, kv, s);
+    }
     switch (a.hd) {  // matrix-core kernel for the common head sizes
         case 32: return attn_mfma_t<32>(a, n_seq, t, l, s);
         case 48: return attn_mfma_t<48>(a, n_seq, t, l, s);
