@@ -295,6 +295,7 @@ struct PrefillAttn {
     float scale = 1.f;
     unsigned short *ohi = nullptr, *olo = nullptr;  // o_proj input planes
     int ldo = 0, opad = 0;
+    int nqb = 0, nseq = 0;  // set by the launcher: query blocks per sequence, sequences
 };
 enum { PF_STORE = 0, PF_RESID = 1, PF_SWIGLU = 2 };
 int prefill_rows_pad(int M);  // GEMM input plane rows for M activation rows

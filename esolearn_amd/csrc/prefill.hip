@@ -645,13 +645,18 @@ __global__ __launch_bounds__(64 * BQW) void k_attn_bf3(PrefillAttn a, PrefillSeq
     u16 *sKh = reinterpret_cast<u16 *>(ab4);
     u16 *sKl = sKh + BKT * KLD, *sVh = sKl + BKT * KLD, *sVl = sVh + HD * VLD;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
-    const int h = blockIdx.y, s = blockIdx.z;
+    // 1-D grid, the longest query blocks of every (head, sequence) first; within
+    // a block row, index g -> (sequence, KV head) g % (n_seq nkv), query head of
+    // the group g / (n_seq nkv): the heads sharing K / V rows land on one XCD
+    // (workgroup b runs on XCD b % 8)
+    const int nhs = a.nh * a.nseq, nkvs = a.nkv * a.nseq;
+    const int qb = a.nqb - 1 - (int)blockIdx.x / nhs, g = (int)blockIdx.x % nhs;
+    const int kvg = g % nkvs, rep = g / nkvs;
+    const int s = kvg / a.nkv, kvh = kvg % a.nkv, h = kvh * (a.nh / a.nkv) + rep;
     const int lr = lane & 15, lg = lane >> 4;
     const int i = qb * BQ + w * 16 + lr;
     const bool valid = i < a.seq;
     const int p0 = t.p0[s], pos = p0 + i;
-    const int kvh = h / (a.nh / a.nkv);
     const size_t m = (size_t)s * a.seq + i;
     // Q^T fragments: lane (query lr, group lg) holds head dims 32 kb + 8 lg + e
     bf16x8 qh[NKB], ql[NKB];
@@ -793,8 +798,10 @@ int attn_bf3_t(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, const Pref
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
-    const dim3 grid((a.seq + BQ - 1) / BQ, a.nh, n_seq);
-    hipLaunchKernelGGL(k_attn_bf3<HD>, grid, dim3(64 * BQW), lds, s, a, t, kv);
+    PrefillAttn ag = a;
+    ag.nqb = (a.seq + BQ - 1) / BQ;
+    ag.nseq = n_seq;
+    hipLaunchKernelGGL(k_attn_bf3<HD>, dim3(ag.nqb * a.nh * n_seq), dim3(64 * BQW), lds, s, ag, t, kv);
     PF_LAUNCH_CHECK();
 }
 
