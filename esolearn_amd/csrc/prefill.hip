@@ -141,19 +141,20 @@ __device__ __forceinline__ bool gemm_tile(const GemmP &p, int &mb, int &nb) {
     return mb < p.n_mb && nb < p.n_nb;
 }
 
-// 16 weight bytes (q + 128) -> 16 bf16 of q, as 8 words
+// 16 weight bytes (q + 128) -> 16 bf16 of q, as 8 words.  Flipping bit 7
+// gives q's two's-complement byte; |q| <= 128 is exact in bf16
+// (v_cvt_f32_i32 on the sign-extended byte, then v_cvt_pk_bf16_f32).
 __device__ __forceinline__ void bytes_to_bf16(u32x4 v, u32x4 &o0, u32x4 &o1) {
-    unsigned r[8];
+    bf16x8 r0, r1;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const unsigned wd = v[i];
-        const float f0 = (float)(int)(wd & 0xffu) - 128.f, f1 = (float)(int)((wd >> 8) & 0xffu) - 128.f;
-        const float f2 = (float)(int)((wd >> 16) & 0xffu) - 128.f, f3 = (float)(int)(wd >> 24) - 128.f;
-        r[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-        r[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+    for (int j = 0; j < 4; j++) {
+        r0[j] = (__bf16)(float)(int)(signed char)((v.x ^ 0x80808080u) >> (8 * j));
+        r0[4 + j] = (__bf16)(float)(int)(signed char)((v.y ^ 0x80808080u) >> (8 * j));
+        r1[j] = (__bf16)(float)(int)(signed char)((v.z ^ 0x80808080u) >> (8 * j));
+        r1[4 + j] = (__bf16)(float)(int)(signed char)((v.w ^ 0x80808080u) >> (8 * j));
     }
-    o0 = u32x4{r[0], r[1], r[2], r[3]};
-    o1 = u32x4{r[4], r[5], r[6], r[7]};
+    o0 = __builtin_bit_cast(u32x4, r0);
+    o1 = __builtin_bit_cast(u32x4, r1);
 }
 
 // (block-32: the per-block scaling needs a second accumulator tile, so one
