@@ -74,6 +74,56 @@ __global__ __launch_bounds__(256) void k_norm_split(const float *__restrict__ x,
     }
 }
 
+// The same with 8 consecutive columns per thread and chunk, the row held in
+// registers between the two passes, and 16-byte plane stores (k % 8 == 0,
+// rows of x and w 16-byte aligned, planes only, NC = kpad / 2048 rounded up).
+template <int NC>
+__global__ __launch_bounds__(256) void k_norm_split8(const float *__restrict__ x, int ldx, int rstep, int roff,
+                                                     const float *__restrict__ w, int k, float eps, u16 *hi,
+                                                     u16 *lo, int ldp, int kpad) {
+    __shared__ double red[4];
+    const int r = blockIdx.x, t = threadIdx.x;
+    const float *src = x + ((size_t)r * rstep + roff) * ldx;
+    float4 v[NC][2];
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int j = (c * 256 + t) * 8;
+        v[c][0] = v[c][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j < k) {
+            v[c][0] = *(const float4 *)(src + j);
+            v[c][1] = *(const float4 *)(src + j + 4);
+        }
+        const float e[8] = {v[c][0].x, v[c][0].y, v[c][0].z, v[c][0].w, v[c][1].x, v[c][1].y, v[c][1].z, v[c][1].w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss += (double)e[i] * (double)e[i];
+    }
+    const double rstd = 1.0 / sqrt(block_sum_d(ss, red) / (double)k + (double)eps);
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int j = (c * 256 + t) * 8;
+        if (j >= kpad) break;
+        float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
+        if (j < k) {
+            w0 = *(const float4 *)(w + j);
+            w1 = *(const float4 *)(w + j + 4);
+        }
+        const float e[8] = {v[c][0].x, v[c][0].y, v[c][0].z, v[c][0].w, v[c][1].x, v[c][1].y, v[c][1].z, v[c][1].w};
+        const float g[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        unsigned ph[4], pl[4];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            u16 a0, b0, a1, b1;
+            split_bf16(j + i < k ? (float)((double)e[i] * rstd * (double)g[i]) : 0.f, a0, b0);
+            split_bf16(j + i + 1 < k ? (float)((double)e[i + 1] * rstd * (double)g[i + 1]) : 0.f, a1, b1);
+            ph[i / 2] = (unsigned)a0 | ((unsigned)a1 << 16);
+            pl[i / 2] = (unsigned)b0 | ((unsigned)b1 << 16);
+        }
+        *(u32x4 *)(hi + (size_t)r * ldp + j) = u32x4{ph[0], ph[1], ph[2], ph[3]};
+        *(u32x4 *)(lo + (size_t)r * ldp + j) = u32x4{pl[0], pl[1], pl[2], pl[3]};
+    }
+}
+
 // f32 rows -> bf16 planes (columns [k, kpad) zeroed)
 __global__ void k_split(const float *__restrict__ x, int ldx, int rows, int k, int kpad, u16 *hi, u16 *lo, int ldp) {
     const size_t total = (size_t)rows * kpad;
@@ -391,6 +441,71 @@ __global__ void k_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, 
                 const size_t at = ((size_t)(s * nkv + j / hd) * kp.rows + pos) * hd + j % hd;
                 split_bf16(v, kp.vh[at], kp.vl[at]);
             }
+        }
+    }
+}
+
+// The same with 8 consecutive elements (four rotation pairs, or eight v
+// values) per thread: float4 loads and stores, 16-byte plane stores
+// (qd, kvd, hd multiples of 8; ldq, the caches and the tables 16-byte aligned).
+__global__ void k_rope_kv8(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd, PrefillSeqs t, int l,
+                           PrefillKVP kp) {
+    const int hh = hd >> 1, nkv = kvd / hd;
+    const int per_row = (qd + 2 * kvd) >> 3;
+    const size_t total = (size_t)M * per_row;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(g / per_row), e8 = (int)(g % per_row) * 8;
+        const int s = m / seq, i = m - s * seq;
+        const int pos = t.p0[s] + i;
+        float *row = qkv + (size_t)m * ldq;
+        float *kc = t.k[s] + (size_t)l * t.ls[s] + (size_t)pos * kvd;
+        float *vc = t.v[s] + (size_t)l * t.ls[s] + (size_t)pos * kvd;
+        float o[8];
+        int j;  // element index within q, k or v
+        int part;  // 0 q, 1 k, 2 v
+        if (e8 < qd) {
+            part = 0;
+            j = e8;
+        } else if (e8 < qd + kvd) {
+            part = 1;
+            j = e8 - qd;
+        } else {
+            part = 2;
+            j = e8 - qd - kvd;
+        }
+        const float4 a0 = *(const float4 *)(row + e8), a1 = *(const float4 *)(row + e8 + 4);
+        const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        if (part < 2) {
+            const float4 *cs4 = (const float4 *)(t.rope[s] + (size_t)pos * hh + ((j % hd) >> 1));
+            const float4 c0 = cs4[0], c1 = cs4[1];
+            const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};  // (cos, sin) x 4
+#pragma unroll
+            for (int p = 0; p < 4; p++) {  // cpu.rs:655-658 in f32, no contraction
+                const float x0 = x[2 * p], x1 = x[2 * p + 1], c = cs[2 * p], sn = cs[2 * p + 1];
+                o[2 * p] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
+                o[2 * p + 1] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; q++) o[q] = x[q];
+        }
+        float *dst = part == 0 ? row + j : part == 1 ? kc + j : vc + j;
+        *(float4 *)dst = make_float4(o[0], o[1], o[2], o[3]);
+        *(float4 *)(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        if (part > 0 && kp.kh) {  // the attention's planes of this K / V row
+            const size_t at = ((size_t)(s * nkv + j / hd) * kp.rows + pos) * hd + j % hd;
+            unsigned ph[4], pl[4];
+#pragma unroll
+            for (int q = 0; q < 8; q += 2) {
+                u16 h0, l0, h1, l1;
+                split_bf16(o[q], h0, l0);
+                split_bf16(o[q + 1], h1, l1);
+                ph[q / 2] = (unsigned)h0 | ((unsigned)h1 << 16);
+                pl[q / 2] = (unsigned)l0 | ((unsigned)l1 << 16);
+            }
+            u16 *bh = part == 1 ? kp.kh : kp.vh, *bl = part == 1 ? kp.kl : kp.vl;
+            *(u32x4 *)(bh + at) = u32x4{ph[0], ph[1], ph[2], ph[3]};
+            *(u32x4 *)(bl + at) = u32x4{pl[0], pl[1], pl[2], pl[3]};
         }
     }
 }
@@ -843,6 +958,20 @@ int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, co
     if (rows <= 0) return SCRY_OK;
     const int kpad = hi ? prefill_k_pad(k) : k;
     if (hi && kpad > ldp) return set_error(SCRY_ERR_INVALID, "norm_split: k %d exceeds plane stride %d", k, ldp);
+    const bool al16 = ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0) && ((uintptr_t)hi % 16 == 0) &&
+                      ((uintptr_t)lo % 16 == 0) && ldx % 4 == 0 && ldp % 8 == 0 && (rstep * ldx) % 4 == 0 &&
+                      (roff * ldx) % 4 == 0;
+    const int nc = (kpad + 2047) / 2048;
+    if (hi && !outf && k % 8 == 0 && al16 && nc <= 8) {
+        switch (nc) {
+            case 1: hipLaunchKernelGGL(k_norm_split8<1>, dim3(rows), dim3(256), 0, s, x, ldx, rstep, roff, w, k, eps, hi, lo, ldp, kpad); break;
+            case 2: hipLaunchKernelGGL(k_norm_split8<2>, dim3(rows), dim3(256), 0, s, x, ldx, rstep, roff, w, k, eps, hi, lo, ldp, kpad); break;
+            case 3:
+            case 4: hipLaunchKernelGGL(k_norm_split8<4>, dim3(rows), dim3(256), 0, s, x, ldx, rstep, roff, w, k, eps, hi, lo, ldp, kpad); break;
+            default: hipLaunchKernelGGL(k_norm_split8<8>, dim3(rows), dim3(256), 0, s, x, ldx, rstep, roff, w, k, eps, hi, lo, ldp, kpad); break;
+        }
+        PF_LAUNCH_CHECK();
+    }
     hipLaunchKernelGGL(k_norm_split, dim3(rows), dim3(256), 0, s, x, ldx, rstep, roff, w, k, eps, hi, lo, ldp,
                        kpad, outf, ldf);
     PF_LAUNCH_CHECK();
@@ -952,6 +1081,18 @@ int launch_rope_kv(float *qkv, int ldq, int M, int seq, int qd, int kvd, int hd,
             hipLaunchKernelGGL(k_kv_planes, dim3(1024), dim3(256), 0, s, t, l, n_seq, kvd, hd, kp);
             SCRY_HIP(hipGetLastError());
         }
+    }
+    bool v8 = hd % 8 == 0 && qd % 8 == 0 && kvd % 8 == 0 && ldq % 4 == 0 && (uintptr_t)qkv % 16 == 0 &&
+              (!kp.kh || (uintptr_t)kp.kh % 16 == 0);
+    for (int i = 0; i < n_seq && v8; i++)
+        v8 = (uintptr_t)t.k[i] % 16 == 0 && (uintptr_t)t.v[i] % 16 == 0 && (uintptr_t)t.rope[i] % 16 == 0 &&
+             t.ls[i] % 4 == 0;
+    if (v8) {
+        const size_t total8 = (size_t)M * ((qd + 2 * kvd) >> 3);
+        if (total8 == 0) return SCRY_OK;
+        const unsigned grid = (unsigned)std::min<size_t>((total8 + 255) / 256, 65536);
+        hipLaunchKernelGGL(k_rope_kv8, dim3(grid), dim3(256), 0, s, qkv, ldq, M, seq, qd, kvd, hd, t, l, kp);
+        PF_LAUNCH_CHECK();
     }
     const size_t total = (size_t)M * ((qd >> 1) + (kvd >> 1) + kvd);
     if (total == 0) return SCRY_OK;
