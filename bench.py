@@ -69,7 +69,9 @@ def measured_traffic(kernel: str):
 
 
 def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int = 64) -> dict:
-    """BASELINE config 5 on the GPU: batched prefill, then greedy decode."""
+    """BASELINE config 5 on the GPU: batched prefill, then greedy decode; and
+    the same prefill with the model in bf16 (the reference's bf16 feature)."""
+    import esolearn_amd.llama as EL
     cfg = E.LlamaConfig.llama3_8b()
     t0 = time.perf_counter()
     m = E.LlamaModel.new_random(cfg, seed=0)
@@ -78,6 +80,9 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
     import numpy as np
     pm, dm, toks = m.bench_prefill(np.stack(prompts), decode_steps)
     m.free()
+    mb = E.LlamaModel.new_random(cfg, seed=0, quant_mode=EL.QUANT_BF16, init_on_device=True)
+    pm_bf16, _, toks_bf16 = mb.bench_prefill(np.stack(prompts), 1)
+    mb.free()
     h, ffn, L = cfg.hidden_size, cfg.intermediate_size, cfg.n_layers
     hd = h // cfg.n_heads
     qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
@@ -87,8 +92,8 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
     attn = 4.0 * n_seq * L * cfg.n_heads * (s * (s + 1) / 2) * hd
     tf = proj / (pm / 1e3) / 1e12
     print(f"[bench] prefill {n_seq}x{s}: {pm:.1f} ms ({rows / pm * 1e3:.0f} tok/s, projections "
-          f"{tf:.1f} TFLOP/s); decode {n_seq}x{decode_steps}: {dm:.1f} ms; init {t_init:.1f} s",
-          file=sys.stderr, flush=True)
+          f"{tf:.1f} TFLOP/s); decode {n_seq}x{decode_steps}: {dm:.1f} ms; init {t_init:.1f} s; "
+          f"bf16 model prefill {pm_bf16:.1f} ms", file=sys.stderr, flush=True)
     return {
         "workload": "llama3-8b-shape int8: 4 x 2048-token prompts, batched prefill of the first "
                     "2047 tokens each (GEMMs on MFMA, split-bf16 activations), then 64 greedy "
@@ -104,6 +109,9 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
         "decode_ms": round(dm, 2),
         "decode_tok_s": round(n_seq * decode_steps / (dm / 1e3), 1),
         "greedy_tokens_head": [[int(t) for t in row[:4]] for row in toks],
+        "bf16_model_prefill_ms": round(pm_bf16, 2),
+        "bf16_model_prefill_tok_s": round(rows / (pm_bf16 / 1e3), 1),
+        "bf16_model_first_tokens": [int(t) for t in toks_bf16[:, 0]],
     }
 
 
