@@ -207,6 +207,59 @@ __device__ __forceinline__ void bytes_to_bf16(u32x4 v, u32x4 &o0, u32x4 &o1) {
     o1 = __builtin_bit_cast(u32x4, r1);
 }
 
+// GEMM epilogue for a wave's TM x TN tiles of 16 x 16, D[4 (l / 16) + r][l % 16]
+// of each tile at rows mw + 16 tm, columns nw + 16 tn; s_a / s_b scale the
+// gate / up halves (s_a alone otherwise).
+template <int EPI, int TM, int TN>
+__device__ __forceinline__ void gemm_store(const GemmP &p, const f32x4 (&acc)[TM][TN], int mw, int nw, int lane,
+                                           float s_a, float s_b) {
+    const int fr = lane & 15;
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+        const int n = nw + tn * 16 + fr;
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = mw + tm * 16 + ((lane >> 4) << 2) + r;
+                if (EPI == GE_SWIGLU) {
+                    // fused gate/up rows of a group of 4: gate[2t], gate[2t+1],
+                    // up[2t], up[2t+1] in lanes 4q .. 4q+3; lane 4q stores the
+                    // two outputs 2t, 2t+1 of its group as one 32-bit word per plane
+                    const bool gate = (n & 2) == 0;
+                    const float v = acc[tm][tn][r] * (gate ? s_a : s_b);
+                    const float o = __shfl_xor(v, 2);
+                    u16 a = 0, b = 0;
+                    if (gate) split_bf16(silu_f(v) * o, a, b);  // cpu.rs:666-678
+                    const unsigned hw = (unsigned)a | ((unsigned)__shfl_xor((int)a, 1) << 16);
+                    const unsigned lw = (unsigned)b | ((unsigned)__shfl_xor((int)b, 1) << 16);
+                    if ((n & 3) == 0 && m < p.M && n < p.N) {  // N is a multiple of 4
+                        const size_t at = (size_t)m * p.ldo + (n >> 1);
+                        *(unsigned *)(p.ohi + at) = hw;
+                        *(unsigned *)(p.olo + at) = lw;
+                    }
+                } else if (m < p.M && n < p.N) {
+                    float v = acc[tm][tn][r] * s_a;
+                    float *cp = p.c + (size_t)m * p.ldc + n;
+                    if (EPI == GE_STORE && p.bias) v += p.bias[n];  // cpu.rs:553-570
+                    *cp = EPI == GE_RESID ? *cp + v : v;  // cpu.rs:104-113 add
+                }
+            }
+        }
+    }
+}
+
+// zero the plane columns past the SwiGLU output (k padding of the next GEMM),
+// rows [m0, m0 + BM); one wave of the last column tile
+__device__ __forceinline__ void swiglu_pad(const GemmP &p, int m0, int lane) {
+    const int c0 = p.N >> 1;
+    for (int idx = lane; idx < BM * (p.opad - c0); idx += 64) {
+        const int m = m0 + idx / (p.opad - c0), col = c0 + idx % (p.opad - c0);
+        p.ohi[(size_t)m * p.ldo + col] = 0;
+        p.olo[(size_t)m * p.ldo + col] = 0;
+    }
+}
+
 // (block-32: the per-block scaling needs a second accumulator tile, so one
 // workgroup per CU keeps it in registers)
 // WBF: bf16 weight rows [N][kp] (2 bytes each, copied to LDS as they are) and
@@ -348,49 +401,173 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
     }
 
     // ---- epilogue: D[4 (l / 16) + r][l % 16] of each tile
-    const float s_a = B32 ? 1.f : p.scale, s_b = B32 ? 1.f : p.scale2;
+    gemm_store<EPI, 4, 8>(p, acc, m0 + wm * 64, n0 + wn * 128, lane, B32 ? 1.f : p.scale, B32 ? 1.f : p.scale2);
+    if (EPI == GE_SWIGLU && wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
+}
+
+// ------------------------------------------------------------------ GEMM, direct-to-LDS ring
+// The int8 per-tensor GEMM (every projection of an int8 model).  Same tile
+// (128 x 256), numerics and epilogues as k_gemm; the staging differs:
+//  - activations and weights go from memory straight into LDS (buffer loads
+//    with the LDS destination: M0 = the 1 KB block, lane i writes its 16 bytes
+//    at 16 i), through a ring of 3 k steps, so two steps are in flight while
+//    one is consumed and no register holds staged data;
+//  - the weights stay int8 in LDS (half the bytes of bf16) and each wave
+//    converts the 16 bytes it reads (two MFMA k halves) after the read;
+//  - one barrier per k step: a step's slot is refilled only after every wave
+//    has passed the barrier that follows its last read.
+// 8 waves (2 along M x 4 along N) of 64 x 64 outputs; 144 KB of LDS, one
+// workgroup per CU.  Measured on the config-5 shapes against k_gemm (same box,
+// same run): qkv 811 -> 728 us, gate/up 3129 -> 3045 us, down 1754 -> 1594 us,
+// and a higher clock under the power limit.
+//
+// LDS step layout: hi plane [128 rows][128 B], lo plane likewise, weights
+// [256 columns][64 B].  16-byte chunks are XOR-swizzled so the MFMA operand
+// reads (16 rows of one chunk per 16 lanes) hit distinct banks: activation
+// chunk c of row r sits at c ^ (r & 7), weight chunk c of column n at
+// c ^ ((n >> 1) & 3).  MFMA k order within a step: lane group g of the
+// 16x16x32 MFMA holds k = 16 g + 8 h + e for k half h, e < 8, which makes
+// the weight operand of both halves one 16-byte read per lane.
+namespace ring {
+constexpr int WGM = 2, WGN = 4, TM = 4, TN = 4, NW = WGM * WGN, T = 64 * NW, S = 3;
+static_assert(WGM * TM * 16 == BM && WGN * TN * 16 == BN && BK == 64, "ring tile");
+constexpr int A_PL = BM * BK * 2, B_ST = BN * BK, STAGE = 2 * A_PL + B_ST;
+constexpr int A_UNITS = A_PL / 1024, B_UNITS = B_ST / 1024;  // 1 KB loads
+constexpr int JA = A_UNITS / NW, JB = B_UNITS / NW, L = 2 * JA + JB;  // loads per wave and step
+static_assert(A_UNITS % NW == 0 && B_UNITS % NW == 0, "ring units");
+constexpr size_t LDS = (size_t)S * STAGE;
+static_assert(L * (S - 2) < 64, "vmcnt range");
+}  // namespace ring
+
+// buffer descriptor words (base, stride 0, num_records, raw-buffer flags),
+// wave-uniform
+__device__ __forceinline__ u32x4 ring_desc(const void *base, size_t bytes) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const unsigned n = bytes > 0x7fffffffu ? 0x7fffffffu : (unsigned)bytes;
+    u32x4 d = u32x4{(unsigned)b, (unsigned)(b >> 32) & 0xffffu, n, 0x00020000u};
 #pragma unroll
-    for (int tn = 0; tn < 8; tn++) {
-        const int n = n0 + wn * 128 + tn * 16 + fr;
+    for (int i = 0; i < 4; i++) d[i] = __builtin_amdgcn_readfirstlane(d[i]);
+    return d;
+}
+
+// 64 lanes x 16 bytes of buffer d at voff + soff -> LDS [lds, lds + 1024).
+// The compiler does not see this load: callers wait with ring_wait before
+// reading the LDS it fills (a vmcnt wait it cannot misplace), and M0 is
+// restored.  Every lane's address stays inside the buffer's records or reads
+// zero; no load is out of bounds for every lane (those can complete out of
+// order and break partial vmcnt waits).
+__device__ __forceinline__ void ring_load(u32x4 d, unsigned lds, unsigned voff, unsigned soff) {
+    unsigned saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(d), "s"(soff)
+        : "memory");
+}
+template <int N>
+__device__ __forceinline__ void ring_wait() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+// workgroup barrier without a memory fence (a fence would also wait for the
+// ring's loads); LDS reads and writes of this wave complete first
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int EPI>
+__global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
+    using namespace ring;
+    extern __shared__ float4 rsm[];
+    unsigned char *sm = reinterpret_cast<unsigned char *>(rsm);
+    int mb, nbk;
+    if (!gemm_tile(p, mb, nbk)) return;
+    const int m0 = mb * BM, n0 = nbk * BN;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const size_t a_bytes = (size_t)p.n_mb * BM * p.lda * 2;
+    const u32x4 dh = ring_desc(p.ahi, a_bytes), dl = ring_desc(p.alo, a_bytes);
+    const u32x4 dw = ring_desc(p.w, (size_t)p.N * p.kp);
+    const unsigned sm0 = (unsigned)(uintptr_t)sm;  // LDS address (low half of the flat address)
+    // load j of this wave fills 1 KB block u = j NW + wave: j < JA the hi plane
+    // (8 rows of 128 B), j < 2 JA the lo plane, else the weights (16 columns of 64 B)
+    unsigned voff[L], loff[L];
 #pragma unroll
-        for (int tm = 0; tm < 4; tm++) {
+    for (int j = 0; j < L; j++) {
+        if (j < 2 * JA) {
+            const int pl = j / JA, ua = (j % JA) * NW + wave;
+            const int r = 8 * ua + (lane >> 3), c = (lane & 7) ^ (r & 7);
+            voff[j] = (unsigned)((m0 + r) * p.lda * 2 + c * 16);
+            loff[j] = (unsigned)(pl * A_PL + ua * 1024);
+        } else {
+            const int ub = (j - 2 * JA) * NW + wave;
+            const int n = 16 * ub + (lane >> 2), c = (lane & 3) ^ ((n >> 1) & 3);
+            const int row = min(n0 + n, p.N - 1);  // columns past N re-read row N - 1 (never stored)
+            voff[j] = (unsigned)(row * p.kp + c * 16);
+            loff[j] = (unsigned)(2 * A_PL + ub * 1024);
+        }
+    }
+    // step kt into ring slot; steps past the last re-read the last (in bounds, never used)
+    auto issue = [&](int kt, int slot) {
+        const int ks = min(kt, p.nk - 1);
+        const unsigned base = sm0 + (unsigned)(slot * STAGE);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm * 64 + tm * 16 + ((lane >> 4) << 2) + r;
-                if (EPI == GE_SWIGLU) {
-                    // fused gate/up rows of a group of 4: gate[2t], gate[2t+1],
-                    // up[2t], up[2t+1] in lanes 4q .. 4q+3; lane 4q stores the
-                    // two outputs 2t, 2t+1 of its group as one 32-bit word per plane
-                    const bool gate = (n & 2) == 0;
-                    const float v = acc[tm][tn][r] * (gate ? s_a : s_b);
-                    const float o = __shfl_xor(v, 2);
-                    u16 a = 0, b = 0;
-                    if (gate) split_bf16(silu_f(v) * o, a, b);  // cpu.rs:666-678
-                    const unsigned hw = (unsigned)a | ((unsigned)__shfl_xor((int)a, 1) << 16);
-                    const unsigned lw = (unsigned)b | ((unsigned)__shfl_xor((int)b, 1) << 16);
-                    if ((n & 3) == 0 && m < p.M && n < p.N) {  // N is a multiple of 4
-                        const size_t at = (size_t)m * p.ldo + (n >> 1);
-                        *(unsigned *)(p.ohi + at) = hw;
-                        *(unsigned *)(p.olo + at) = lw;
-                    }
-                } else if (m < p.M && n < p.N) {
-                    float v = acc[tm][tn][r] * s_a;
-                    float *cp = p.c + (size_t)m * p.ldc + n;
-                    if (EPI == GE_STORE && p.bias) v += p.bias[n];  // cpu.rs:553-570
-                    *cp = EPI == GE_RESID ? *cp + v : v;  // cpu.rs:104-113 add
-                }
+        for (int j = 0; j < L; j++) {
+            if (j < JA) ring_load(dh, base + loff[j], voff[j], (unsigned)(ks * BK * 2));
+            else if (j < 2 * JA) ring_load(dl, base + loff[j], voff[j], (unsigned)(ks * BK * 2));
+            else ring_load(dw, base + loff[j], voff[j], (unsigned)(ks * BK));
+        }
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    ring_wait<0>();
+#pragma unroll
+    for (int s = 0; s < S - 1; s++) issue(s, s);
+    const int fr = lane & 15, g = lane >> 4;
+    int cur = 0;  // ring slot of step kt
+    for (int kt = 0; kt < p.nk; kt++) {
+        ring_wait<L * (S - 2)>();  // this wave's loads of step kt have landed
+        ring_barrier();            // every wave's have; slot kt - 1 is free
+        issue(kt + S - 1, cur == 0 ? S - 1 : cur - 1);
+        const unsigned char *st = sm + cur * STAGE;
+        cur = cur == S - 1 ? 0 : cur + 1;
+        bf16x8 b0[TN], b1[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+            const int n = wn * TN * 16 + tn * 16 + fr;
+            const u32x4 v = *(const u32x4 *)(st + 2 * A_PL + n * 64 + ((g ^ ((fr >> 1) & 3)) << 4));
+            u32x4 o0, o1;
+            bytes_to_bf16(v, o0, o1);
+            b0[tn] = __builtin_bit_cast(bf16x8, o0);
+            b1[tn] = __builtin_bit_cast(bf16x8, o1);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            bf16x8 ah[TM], al[TM];
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++) {
+                const int off = (wm * TM * 16 + tm * 16 + fr) * 128 + (((2 * g + h) ^ (fr & 7)) << 4);
+                ah[tm] = *(const bf16x8 *)(st + off);
+                al[tm] = *(const bf16x8 *)(st + A_PL + off);
             }
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+                for (int tm = 0; tm < TM; tm++)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], h ? b1[tn] : b0[tn], acc[tm][tn], 0, 0, 0);
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+                for (int tm = 0; tm < TM; tm++)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], h ? b1[tn] : b0[tn], acc[tm][tn], 0, 0, 0);
         }
     }
-    if (EPI == GE_SWIGLU && wave == 0 && nbk == p.n_nb - 1) {
-        // zero the plane columns past the SwiGLU output (k padding of the next GEMM)
-        const int c0 = p.N >> 1;
-        for (int idx = lane; idx < BM * (p.opad - c0); idx += 64) {
-            const int m = m0 + idx / (p.opad - c0), col = c0 + idx % (p.opad - c0);
-            p.ohi[(size_t)m * p.ldo + col] = 0;
-            p.olo[(size_t)m * p.ldo + col] = 0;
-        }
-    }
+    ring_wait<0>();  // the re-read tail steps land before the workgroup's LDS is released
+    gemm_store<EPI, TM, TN>(p, acc, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, p.scale, p.scale2);
+    if (EPI == GE_SWIGLU && wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
 }
 
 // ------------------------------------------------------------------ RoPE + KV append
@@ -948,6 +1125,19 @@ int gemm_t(const GemmP &p, hipStream_t s) {
     PF_LAUNCH_CHECK();
 }
 
+template <int EPI>
+int gemm_ring_t(const GemmP &p, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_ring<EPI>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)ring::LDS));
+        attr = true;
+    }
+    const int grid = (p.n_super + 7) / 8 * 8 * 32;
+    hipLaunchKernelGGL((k_gemm_ring<EPI>), dim3(grid), dim3(ring::T), ring::LDS, s, p);
+    PF_LAUNCH_CHECK();
+}
+
 }  // namespace
 
 int prefill_rows_pad(int M) { return (M + BM - 1) / BM * BM; }
@@ -1032,10 +1222,28 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
         }
         return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
     }
+    if (b32) {
+        switch (epi) {
+            case GE_STORE: return gemm_t<GE_STORE, true>(p, s);
+            case GE_RESID: return gemm_t<GE_RESID, true>(p, s);
+            case GE_SWIGLU: return gemm_t<GE_SWIGLU, true>(p, s);
+        }
+        return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
+    }
+    // the ring kernel addresses the planes through a buffer descriptor (32-bit
+    // offsets); larger planes take the register-staged kernel
+    if ((size_t)p.n_mb * BM * p.lda * 2 >= 0x7fffffffull) {
+        switch (epi) {
+            case GE_STORE: return gemm_t<GE_STORE, false>(p, s);
+            case GE_RESID: return gemm_t<GE_RESID, false>(p, s);
+            case GE_SWIGLU: return gemm_t<GE_SWIGLU, false>(p, s);
+        }
+        return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
+    }
     switch (epi) {
-        case GE_STORE: return b32 ? gemm_t<GE_STORE, true>(p, s) : gemm_t<GE_STORE, false>(p, s);
-        case GE_RESID: return b32 ? gemm_t<GE_RESID, true>(p, s) : gemm_t<GE_RESID, false>(p, s);
-        case GE_SWIGLU: return b32 ? gemm_t<GE_SWIGLU, true>(p, s) : gemm_t<GE_SWIGLU, false>(p, s);
+        case GE_STORE: return gemm_ring_t<GE_STORE>(p, s);
+        case GE_RESID: return gemm_ring_t<GE_RESID>(p, s);
+        case GE_SWIGLU: return gemm_ring_t<GE_SWIGLU>(p, s);
     }
     return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
 }
