@@ -156,6 +156,7 @@ constexpr int AC = BM * BK / 8 / G_THREADS;   // 16-byte A chunks per thread and
 constexpr int BC = BN * BK / 16 / G_THREADS;  // 16-byte weight chunks per thread
 // dynamic LDS: A hi, A lo, B + [BK/32][BN] block-32 scales
 constexpr size_t GEMM_LDS = (2 * A_TILE + B_TILE) * sizeof(u16) + (BK / 32) * BN * sizeof(float);
+static_assert(GEMM_LDS >= 2 * BM * (BN / 2 + 8) * sizeof(u16), "SwiGLU staging tile");
 
 enum { GE_STORE = PF_STORE, GE_RESID = PF_RESID, GE_SWIGLU = PF_SWIGLU };
 
@@ -210,6 +211,15 @@ __device__ __forceinline__ void bytes_to_bf16(u32x4 v, u32x4 &o0, u32x4 &o1) {
 // GEMM epilogue for a wave's TM x TN tiles of 16 x 16, D[4 (l / 16) + r][l % 16]
 // of each tile at rows mw + 16 tm, columns nw + 16 tn; s_a / s_b scale the
 // gate / up halves (s_a alone otherwise).
+// lane value of the lane l ^ 2 / l ^ 1 (quad permutes, no LDS traffic)
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
+}
+__device__ __forceinline__ int quad_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, false); }
+
+// GEMM epilogue for a wave's TM x TN tiles of 16 x 16, D[4 (l / 16) + r][l % 16]
+// of each tile at rows mw + 16 tm, columns nw + 16 tn; s_a / s_b scale the
+// gate / up halves (s_a alone otherwise).
 template <int EPI, int TM, int TN>
 __device__ __forceinline__ void gemm_store(const GemmP &p, const f32x4 (&acc)[TM][TN], int mw, int nw, int lane,
                                            float s_a, float s_b) {
@@ -219,32 +229,100 @@ __device__ __forceinline__ void gemm_store(const GemmP &p, const f32x4 (&acc)[TM
         const int n = nw + tn * 16 + fr;
 #pragma unroll
         for (int tm = 0; tm < TM; tm++) {
+            if (EPI == GE_SWIGLU) {
+                // fused gate/up rows of a group of 4: gate[2t], gate[2t+1],
+                // up[2t], up[2t+1] in lanes 4q .. 4q+3.  Rows are taken in pairs
+                // (r0, r1) so that every lane evaluates one SiLU: the gate lanes
+                // form output row r0 (their gate, the up lane's r0 value), the up
+                // lanes output row r1 (the gate lane's r1 value, their up); lanes
+                // 4q and 4q+2 then store columns 2t, 2t+1 of their row as one
+                // 32-bit word per plane
+                const bool gate = (n & 2) == 0;
+                const float sc = gate ? s_a : s_b;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = mw + tm * 16 + ((lane >> 4) << 2) + r;
-                if (EPI == GE_SWIGLU) {
-                    // fused gate/up rows of a group of 4: gate[2t], gate[2t+1],
-                    // up[2t], up[2t+1] in lanes 4q .. 4q+3; lane 4q stores the
-                    // two outputs 2t, 2t+1 of its group as one 32-bit word per plane
-                    const bool gate = (n & 2) == 0;
-                    const float v = acc[tm][tn][r] * (gate ? s_a : s_b);
-                    const float o = __shfl_xor(v, 2);
-                    u16 a = 0, b = 0;
-                    if (gate) split_bf16(silu_f(v) * o, a, b);  // cpu.rs:666-678
-                    const unsigned hw = (unsigned)a | ((unsigned)__shfl_xor((int)a, 1) << 16);
-                    const unsigned lw = (unsigned)b | ((unsigned)__shfl_xor((int)b, 1) << 16);
-                    if ((n & 3) == 0 && m < p.M && n < p.N) {  // N is a multiple of 4
-                        const size_t at = (size_t)m * p.ldo + (n >> 1);
+                for (int rp = 0; rp < 2; rp++) {
+                    const float v0 = acc[tm][tn][2 * rp] * sc, v1 = acc[tm][tn][2 * rp + 1] * sc;
+                    const float recv = quad_xor2(gate ? v1 : v0);
+                    const float gv = gate ? v0 : recv, uv = gate ? recv : v1;
+                    u16 a, b;
+                    split_bf16(silu_f(gv) * uv, a, b);  // cpu.rs:666-678
+                    const unsigned hw = (unsigned)a | ((unsigned)quad_xor1((int)a) << 16);
+                    const unsigned lw = (unsigned)b | ((unsigned)quad_xor1((int)b) << 16);
+                    const int m = mw + tm * 16 + ((lane >> 4) << 2) + 2 * rp + (gate ? 0 : 1);
+                    if ((n & 1) == 0 && m < p.M && n < p.N) {  // N is a multiple of 4
+                        const size_t at = (size_t)m * p.ldo + ((n >> 2) << 1);
                         *(unsigned *)(p.ohi + at) = hw;
                         *(unsigned *)(p.olo + at) = lw;
                     }
-                } else if (m < p.M && n < p.N) {
-                    float v = acc[tm][tn][r] * s_a;
-                    float *cp = p.c + (size_t)m * p.ldc + n;
-                    if (EPI == GE_STORE && p.bias) v += p.bias[n];  // cpu.rs:553-570
-                    *cp = EPI == GE_RESID ? *cp + v : v;  // cpu.rs:104-113 add
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = mw + tm * 16 + ((lane >> 4) << 2) + r;
+                    if (m < p.M && n < p.N) {
+                        float v = acc[tm][tn][r] * s_a;
+                        float *cp = p.c + (size_t)m * p.ldc + n;
+                        if (EPI == GE_STORE && p.bias) v += p.bias[n];  // cpu.rs:553-570
+                        *cp = EPI == GE_RESID ? *cp + v : v;  // cpu.rs:104-113 add
+                    }
                 }
             }
+        }
+    }
+}
+
+// SwiGLU epilogue through LDS.  The MFMA layout leaves each lane one column
+// of 4 rows, so direct plane stores are 4-byte pieces of 8 rows per
+// instruction; instead each wave puts its outputs (one SiLU per lane and row
+// pair, as in gemm_store) into an LDS tile [BM][BN / 2] per plane, and the
+// workgroup then writes whole 256-byte plane rows with 16-byte stores.  The
+// caller's LDS is free (no loads in flight, every wave past its last read);
+// so (>= 2 BM (BN / 2 + 8) u16) holds the tile.  Rows past M are not written
+// (they stay zero); columns past N / 2 neither.
+template <int TM, int TN, int NT>
+__device__ __forceinline__ void swiglu_store(const GemmP &p, const f32x4 (&acc)[TM][TN], u16 *so, int ml, int nl, int m0,
+                                             int n0, int lane) {
+    constexpr int OW = BN / 2, LDO = OW + 8;  // output columns per tile; LDS row stride (u16)
+    u16 *sh = so, *sl = so + BM * LDO;
+    const int fr = lane & 15;
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+        const int n = nl + tn * 16 + fr;  // tile column (n0 is a multiple of 4)
+        const bool gate = (n & 2) == 0;
+        const float sc = gate ? p.scale : p.scale2;
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++) {
+#pragma unroll
+            for (int rp = 0; rp < 2; rp++) {
+                const float v0 = acc[tm][tn][2 * rp] * sc, v1 = acc[tm][tn][2 * rp + 1] * sc;
+                const float recv = quad_xor2(gate ? v1 : v0);
+                const float gv = gate ? v0 : recv, uv = gate ? recv : v1;
+                u16 a, b;
+                split_bf16(silu_f(gv) * uv, a, b);  // cpu.rs:666-678
+                const unsigned hw = (unsigned)a | ((unsigned)quad_xor1((int)a) << 16);
+                const unsigned lw = (unsigned)b | ((unsigned)quad_xor1((int)b) << 16);
+                const int r = ml + tm * 16 + ((lane >> 4) << 2) + 2 * rp + (gate ? 0 : 1);
+                if ((n & 1) == 0) {
+                    const int at = r * LDO + ((n >> 2) << 1);
+                    *(unsigned *)(sh + at) = hw;
+                    *(unsigned *)(sl + at) = lw;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int CPR = OW / 8;  // 16-byte chunks per row
+    const int oc0 = n0 >> 1, ocn = p.N >> 1;
+    for (int idx = threadIdx.x; idx < 2 * BM * CPR; idx += NT) {
+        const int pl = idx / (BM * CPR), rem = idx - pl * (BM * CPR), r = rem / CPR, c = rem - r * CPR;
+        const int m = m0 + r, col = oc0 + c * 8;
+        if (m >= p.M || col >= ocn) continue;
+        const u16 *src = (pl ? sl : sh) + r * LDO + c * 8;
+        u16 *dst = (pl ? p.olo : p.ohi) + (size_t)m * p.ldo + col;
+        if (col + 8 <= ocn) {
+            *(u32x4 *)dst = *(const u32x4 *)src;
+        } else {
+            for (int e = 0; e < ocn - col; e++) dst[e] = src[e];
         }
     }
 }
@@ -401,8 +479,13 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
     }
 
     // ---- epilogue: D[4 (l / 16) + r][l % 16] of each tile
-    gemm_store<EPI, 4, 8>(p, acc, m0 + wm * 64, n0 + wn * 128, lane, B32 ? 1.f : p.scale, B32 ? 1.f : p.scale2);
-    if (EPI == GE_SWIGLU && wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
+    if (EPI == GE_SWIGLU && !B32) {  // (the last k step ended with a barrier: LDS is free)
+        swiglu_store<4, 8, G_THREADS>(p, acc, sa, wm * 64, wn * 128, m0, n0, lane);
+        if (wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
+    } else {
+        gemm_store<EPI, 4, 8>(p, acc, m0 + wm * 64, n0 + wn * 128, lane, B32 ? 1.f : p.scale, B32 ? 1.f : p.scale2);
+        if (EPI == GE_SWIGLU && wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
+    }
 }
 
 // ------------------------------------------------------------------ GEMM, direct-to-LDS ring
@@ -437,6 +520,7 @@ constexpr int JA = A_UNITS / NW, JB = B_UNITS / NW, L = 2 * JA + JB;  // loads p
 static_assert(A_UNITS % NW == 0 && B_UNITS % NW == 0, "ring units");
 constexpr size_t LDS = (size_t)S * STAGE;
 static_assert(L * (S - 2) < 64, "vmcnt range");
+static_assert(LDS >= 2 * BM * (BN / 2 + 8) * sizeof(u16), "SwiGLU staging tile");
 }  // namespace ring
 
 // buffer descriptor words (base, stride 0, num_records, raw-buffer flags),
@@ -565,9 +649,14 @@ __global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
                     acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], h ? b1[tn] : b0[tn], acc[tm][tn], 0, 0, 0);
         }
     }
-    ring_wait<0>();  // the re-read tail steps land before the workgroup's LDS is released
-    gemm_store<EPI, TM, TN>(p, acc, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, p.scale, p.scale2);
-    if (EPI == GE_SWIGLU && wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
+    ring_wait<0>();  // the re-read tail steps land before the workgroup's LDS is reused or released
+    if (EPI == GE_SWIGLU) {
+        __syncthreads();  // every wave's tail loads have landed
+        swiglu_store<TM, TN, T>(p, acc, reinterpret_cast<u16 *>(sm), wm * TM * 16, wn * TN * 16, m0, n0, lane);
+        if (wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
+    } else {
+        gemm_store<EPI, TM, TN>(p, acc, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, p.scale, p.scale2);
+    }
 }
 
 // ------------------------------------------------------------------ RoPE + KV append
@@ -1186,7 +1275,8 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
         return set_error(SCRY_ERR_UNSUPPORTED, "gemm: %zu weight bytes (limit 2 GiB per tensor)", w.bytes());
     const int kpad = prefill_k_pad(w.k);
     if (kpad > g.lda || g.lda % 8) return set_error(SCRY_ERR_INVALID, "gemm: plane stride %d < k %d", g.lda, w.k);
-    if (epi == GE_SWIGLU && (w.fused != 1 || w.rows % 4 || (w.rows >> 1) > g.ldo || g.opad > g.ldo || g.ldo % 2))
+    if (epi == GE_SWIGLU && (w.fused != 1 || w.rows % 4 || (w.rows >> 1) > g.ldo || g.opad > g.ldo || g.ldo % 8 ||
+                             ((uintptr_t)g.ohi | (uintptr_t)g.olo) % 16))
         return set_error(SCRY_ERR_INVALID, "gemm: swiglu needs the fused gate/up layout");
     if (w.s32 && w.nb * 32 < w.k) return set_error(SCRY_ERR_INVALID, "gemm: block-32 scales too short");
     GemmP p{};
