@@ -255,18 +255,33 @@ __device__ __forceinline__ void gemm_store(const GemmP &p, const f32x4 (&acc)[TM
                         *(unsigned *)(p.olo + at) = lw;
                     }
                 }
-            } else {
+            }
+        }
+        if (EPI != GE_SWIGLU) {
+            // this column's residual values (or bias) are all requested before the
+            // first store: the compiler cannot tell the stores from later loads of
+            // c apart, and would otherwise wait out one round trip per element
+            const bool nok = n < p.N;
+            const float bn = EPI == GE_STORE && p.bias && nok ? p.bias[n] : 0.f;  // cpu.rs:553-570
+            float res[TM][4];
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int m = mw + tm * 16 + ((lane >> 4) << 2) + r;
-                    if (m < p.M && n < p.N) {
-                        float v = acc[tm][tn][r] * s_a;
-                        float *cp = p.c + (size_t)m * p.ldc + n;
-                        if (EPI == GE_STORE && p.bias) v += p.bias[n];  // cpu.rs:553-570
-                        *cp = EPI == GE_RESID ? *cp + v : v;  // cpu.rs:104-113 add
+                    res[tm][r] = EPI == GE_RESID && nok && m < p.M ? p.c[(size_t)m * p.ldc + n] : 0.f;
+                }
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = mw + tm * 16 + ((lane >> 4) << 2) + r;
+                    if (nok && m < p.M) {
+                        const float v = acc[tm][tn][r] * s_a;
+                        // cpu.rs:104-113 add
+                        p.c[(size_t)m * p.ldc + n] = EPI == GE_RESID ? res[tm][r] + v : (EPI == GE_STORE && p.bias ? v + bn : v);
                     }
                 }
-            }
         }
     }
 }
