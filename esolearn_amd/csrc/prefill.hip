@@ -294,7 +294,16 @@ __device__ __forceinline__ void gemm_store(const GemmP &p, const f32x4 (&acc)[TM
 // caller's LDS is free (no loads in flight, every wave past its last read);
 // so (>= 2 BM (BN / 2 + 8) u16) holds the tile.  Rows past M are not written
 // (they stay zero); columns past N / 2 neither.
-template <int TM, int TN, int NT>
+// SiLU in f32 for outputs that become split-bf16 planes (hi + lo hold x to
+// 2^-17): the f32 evaluation is within a few 2^-24 of the reference's f64
+// one (cpu.rs:1119-1122), so the planes agree with the f64 path's to the
+// split's own bound, at a quarter of the cost.  Where the next GEMM reads
+// one bf16 plane (the bf16 model: the reference's bf16 cast of the f32
+// value), the f64 evaluation is kept, since one ulp of f32 can move a bf16
+// rounding.
+__device__ __forceinline__ float silu_split(float g) { return g / (1.f + expf(-g)); }
+
+template <int TM, int TN, int NT, bool EXACT>
 __device__ __forceinline__ void swiglu_store(const GemmP &p, const f32x4 (&acc)[TM][TN], u16 *so, int ml, int nl, int m0,
                                              int n0, int lane) {
     constexpr int OW = BN / 2, LDO = OW + 8;  // output columns per tile; LDS row stride (u16)
@@ -313,7 +322,7 @@ __device__ __forceinline__ void swiglu_store(const GemmP &p, const f32x4 (&acc)[
                 const float recv = quad_xor2(gate ? v1 : v0);
                 const float gv = gate ? v0 : recv, uv = gate ? recv : v1;
                 u16 a, b;
-                split_bf16(silu_f(gv) * uv, a, b);  // cpu.rs:666-678
+                split_bf16((EXACT ? silu_f(gv) : silu_split(gv)) * uv, a, b);  // cpu.rs:666-678
                 const unsigned hw = (unsigned)a | ((unsigned)quad_xor1((int)a) << 16);
                 const unsigned lw = (unsigned)b | ((unsigned)quad_xor1((int)b) << 16);
                 const int r = ml + tm * 16 + ((lane >> 4) << 2) + 2 * rp + (gate ? 0 : 1);
@@ -495,7 +504,7 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
 
     // ---- epilogue: D[4 (l / 16) + r][l % 16] of each tile
     if (EPI == GE_SWIGLU && !B32) {  // (the last k step ended with a barrier: LDS is free)
-        swiglu_store<4, 8, G_THREADS>(p, acc, sa, wm * 64, wn * 128, m0, n0, lane);
+        swiglu_store<4, 8, G_THREADS, WBF>(p, acc, sa, wm * 64, wn * 128, m0, n0, lane);
         if (wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
     } else {
         gemm_store<EPI, 4, 8>(p, acc, m0 + wm * 64, n0 + wn * 128, lane, B32 ? 1.f : p.scale, B32 ? 1.f : p.scale2);
@@ -667,7 +676,7 @@ __global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
     ring_wait<0>();  // the re-read tail steps land before the workgroup's LDS is reused or released
     if (EPI == GE_SWIGLU) {
         __syncthreads();  // every wave's tail loads have landed
-        swiglu_store<TM, TN, T>(p, acc, reinterpret_cast<u16 *>(sm), wm * TM * 16, wn * TN * 16, m0, n0, lane);
+        swiglu_store<TM, TN, T, false>(p, acc, reinterpret_cast<u16 *>(sm), wm * TM * 16, wn * TN * 16, m0, n0, lane);
         if (wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
     } else {
         gemm_store<EPI, TM, TN>(p, acc, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, p.scale, p.scale2);
