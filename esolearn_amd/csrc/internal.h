@@ -288,6 +288,12 @@ struct PrefillGemm {
     const float *bias = nullptr;  // PF_STORE: + bias[n]
     unsigned short *ohi = nullptr, *olo = nullptr;  // GE_SWIGLU output planes
     int ldo = 0, opad = 0;
+    // instead of ahi / alo (int8 per-tensor weights only): the activations as
+    // 24-bit integers X 2^-E per row, in three balanced int8 digit planes
+    // [3][Mp][lda] (plane stride dstride bytes) and the row exponents E [Mp]
+    const signed char *ad = nullptr;
+    const int *ae = nullptr;
+    size_t dstride = 0;
 };
 struct PrefillAttn {
     const float *qkv = nullptr;  // rows [M][ldq], q part RoPE'd
@@ -302,6 +308,13 @@ int prefill_rows_pad(int M);  // GEMM input plane rows for M activation rows
 int prefill_k_pad(int k);     // GEMM input plane columns (and zero padding) for k
 int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, const float *w, int k, float eps,
                       unsigned short *hi, unsigned short *lo, int ldp, float *outf, int ldf, hipStream_t s);
+// RMSNorm into the digit planes of a PrefillGemm (rows r of [3][.][ldp] at
+// plane stride dstride bytes; columns [k, prefill_k_pad(k)) zero) and the row
+// exponents e[r]
+int launch_norm_digits(const float *x, int ldx, int rows, const float *w, int k, float eps, signed char *dg,
+                       size_t dstride, int *e, int ldp, hipStream_t s);
+// true when a GEMM over w takes digit planes (int8 per-tensor weights)
+bool gemm_takes_digits(const Packed &w);
 int launch_split(const float *x, int ldx, int rows, int k, unsigned short *hi, unsigned short *lo, int ldp,
                  hipStream_t s);
 int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s);

@@ -59,6 +59,8 @@ struct scry_llama_s {
         unsigned short *p0 = nullptr, *p1 = nullptr;
         float *x = nullptr, *qkv = nullptr, *last = nullptr, *xl = nullptr;
         int64_t *ids = nullptr;
+        signed char *dg = nullptr;  // digit planes [3][Mp][ld0] of the RMSNorm outputs (int8 GEMMs)
+        int *de = nullptr;          // their row exponents [Mp]
     } pf;
     unsigned short *kvp = nullptr;  // the prefill attention's K / V planes (grown on demand)
     size_t kvp_n = 0;
@@ -240,6 +242,8 @@ void model_free(scry_llama m) {
     dev_free(m->pf.last);
     dev_free(m->pf.xl);
     dev_free(m->pf.ids);
+    dev_free(m->pf.dg);
+    dev_free(m->pf.de);
     dev_free(m->kvp);
     delete m;
 }
@@ -625,6 +629,8 @@ int prefill_ws(scry_llama m, int M, int n_seq) {
     dev_free(P.last);
     dev_free(P.xl);
     dev_free(P.ids);
+    dev_free(P.dg);
+    dev_free(P.de);
     P = scry_llama_s::Prefill{};
     const size_t n0 = 2 * (size_t)Mp * ld0, n1 = 2 * (size_t)Mp * ld1;
     SCRY_TRY(dev_alloc((void **)&P.p0, n0 * sizeof(unsigned short)));
@@ -634,9 +640,13 @@ int prefill_ws(scry_llama m, int M, int n_seq) {
     SCRY_TRY(dev_alloc((void **)&P.last, (size_t)PF_MAX_SEQS * m->V * sizeof(float)));
     SCRY_TRY(dev_alloc((void **)&P.xl, (size_t)PF_MAX_SEQS * m->h * sizeof(float)));
     SCRY_TRY(dev_alloc((void **)&P.ids, (size_t)Mp * sizeof(int64_t)));
+    SCRY_TRY(dev_alloc((void **)&P.dg, 3 * (size_t)Mp * ld0));
+    SCRY_TRY(dev_alloc((void **)&P.de, (size_t)Mp * sizeof(int)));
     hipStream_t s = ctx().stream;
     SCRY_HIP(hipMemsetAsync(P.p0, 0, n0 * sizeof(unsigned short), s));
     SCRY_HIP(hipMemsetAsync(P.p1, 0, n1 * sizeof(unsigned short), s));
+    SCRY_HIP(hipMemsetAsync(P.dg, 0, 3 * (size_t)Mp * ld0, s));
+    SCRY_HIP(hipMemsetAsync(P.de, 0, (size_t)Mp * sizeof(int), s));
     P.Mp = Mp;
     P.ld0 = ld0;
     P.ld1 = ld1;
@@ -700,15 +710,29 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
     SCRY_HIP(hipMemcpyAsync(P.ids, tokens, sizeof(int64_t) * M, hipMemcpyHostToDevice, s));
     SCRY_TRY(launch_embedding(m->embed, P.ids, M, m->h, P.x, s));  // cpu.rs:485-498
     const float eps = m->eps;
-    for (int l = 0; l < m->L; l++) {
-        const auto &Ly = m->layers[l];
-        SCRY_TRY(launch_norm_split(P.x, m->h, M, 1, 0, m->norm_in(l), m->h, eps, h0, l0, P.ld0, nullptr, 0, s));
-        PrefillGemm g;
-        g.ahi = h0;
-        g.alo = l0;
+    const size_t dstride = (size_t)P.Mp * P.ld0;
+    // RMSNorm of the residual rows into the input of a GEMM over w: digit
+    // planes for int8 per-tensor weights (the int8 matrix cores), bf16 planes
+    // otherwise
+    auto norm_for = [&](const float *nw, const Packed &w, PrefillGemm &g) -> int {
         g.lda = P.ld0;
         g.M = M;
-        g.w = &Ly.qkv;
+        g.w = &w;
+        if (gemm_takes_digits(w)) {
+            g.ad = P.dg;
+            g.ae = P.de;
+            g.dstride = dstride;
+            g.ahi = g.alo = nullptr;
+            return launch_norm_digits(P.x, m->h, M, nw, m->h, eps, P.dg, dstride, P.de, P.ld0, s);
+        }
+        g.ahi = h0;
+        g.alo = l0;
+        return launch_norm_split(P.x, m->h, M, 1, 0, nw, m->h, eps, h0, l0, P.ld0, nullptr, 0, s);
+    };
+    for (int l = 0; l < m->L; l++) {
+        const auto &Ly = m->layers[l];
+        PrefillGemm g;
+        SCRY_TRY(norm_for(m->norm_in(l), Ly.qkv, g));
         g.c = P.qkv;
         g.ldc = m->qkv_dim;
         SCRY_TRY(launch_gemm(PF_STORE, g, s));
@@ -727,18 +751,22 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         at.ldo = P.ld0;
         at.opad = prefill_k_pad(m->q_dim);
         SCRY_TRY(launch_attn_prefill(at, n_seq, t, l, kvp, s));
-        g.w = &Ly.o;
-        g.c = P.x;
-        g.ldc = m->h;
-        SCRY_TRY(launch_gemm(PF_RESID, g, s));
-        SCRY_TRY(launch_norm_split(P.x, m->h, M, 1, 0, m->norm_post(l), m->h, eps, h0, l0, P.ld0, nullptr, 0, s));
-        g.w = &Ly.gu;
-        g.c = nullptr;
-        g.ohi = h1;
-        g.olo = l1;
-        g.ldo = P.ld1;
-        g.opad = prefill_k_pad(m->ffn);
-        SCRY_TRY(launch_gemm(PF_SWIGLU, g, s));
+        PrefillGemm o;
+        o.ahi = h0;
+        o.alo = l0;
+        o.lda = P.ld0;
+        o.M = M;
+        o.w = &Ly.o;
+        o.c = P.x;
+        o.ldc = m->h;
+        SCRY_TRY(launch_gemm(PF_RESID, o, s));
+        PrefillGemm u;
+        SCRY_TRY(norm_for(m->norm_post(l), Ly.gu, u));
+        u.ohi = h1;
+        u.olo = l1;
+        u.ldo = P.ld1;
+        u.opad = prefill_k_pad(m->ffn);
+        SCRY_TRY(launch_gemm(PF_SWIGLU, u, s));
         PrefillGemm d;
         d.ahi = h1;
         d.alo = l1;
@@ -750,13 +778,8 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         SCRY_TRY(launch_gemm(PF_RESID, d, s));
     }
     if (all_logits) {
-        SCRY_TRY(launch_norm_split(P.x, m->h, M, 1, 0, m->norm_final(), m->h, eps, h0, l0, P.ld0, nullptr, 0, s));
         PrefillGemm g;
-        g.ahi = h0;
-        g.alo = l0;
-        g.lda = P.ld0;
-        g.M = M;
-        g.w = &m->lm;
+        SCRY_TRY(norm_for(m->norm_final(), m->lm, g));
         g.c = all_logits;
         g.ldc = m->V;
         SCRY_TRY(launch_gemm(PF_STORE, g, s));

@@ -124,6 +124,102 @@ __global__ __launch_bounds__(256) void k_norm_split8(const float *__restrict__ x
     }
 }
 
+// RMSNorm into digit planes (the input of the int8 GEMM, k_gemm_digits):
+// the same normalised row y as k_norm_split, then per row an exponent E with
+// max|y| 2^E <= 2^23 - 2^16 - 1, X = rint(y 2^E) (exact scaling in f64, one
+// rounding: |y - X 2^-E| <= 2^-E-1 <= 2^-23 max|y|), and X = d0 + 2^8 d1 +
+// 2^16 d2 in balanced digits (d0, d1 in [-128, 127]; the bound keeps d2 in
+// [-127, 127]).  A row holding a NaN or an infinity gets E = DG_NONFINITE
+// and the GEMM writes NaN for it, as the split planes do (lo = bf16(inf - inf)).
+// Thread t holds columns 8 (c 256 + t) .. +7 of chunk c; VEC: 16-byte loads
+// (k % 8 == 0, rows 16-byte aligned).
+constexpr int DG_NONFINITE = 0x7fffffff;
+constexpr double DG_XMAX = 8323071.0;  // 2^23 - 2^16 - 1
+
+template <int NC, bool VEC>
+__global__ __launch_bounds__(256) void k_norm_digits(const float *__restrict__ x, int ldx, const float *__restrict__ w,
+                                                     int k, float eps, signed char *dg, size_t dstride, int *de,
+                                                     int ldp, int kpad) {
+    __shared__ double red[4];
+    __shared__ float s_max[4];
+    __shared__ int s_bad[4];
+    const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const float *src = x + (size_t)r * ldx;
+    float y[NC][8];
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int j = (c * 256 + t) * 8;
+        if (VEC) {
+            float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+            if (j < k) {
+                v0 = *(const float4 *)(src + j);
+                v1 = *(const float4 *)(src + j + 4);
+            }
+            y[c][0] = v0.x, y[c][1] = v0.y, y[c][2] = v0.z, y[c][3] = v0.w;
+            y[c][4] = v1.x, y[c][5] = v1.y, y[c][6] = v1.z, y[c][7] = v1.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) y[c][i] = j + i < k ? src[j + i] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss += (double)y[c][i] * (double)y[c][i];
+    }
+    const double rstd = 1.0 / sqrt(block_sum_d(ss, red) / (double)k + (double)eps);
+    float amax = 0.f;
+    int bad = 0;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int j = (c * 256 + t) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float v = j + i < k ? (float)((double)y[c][i] * rstd * (double)w[j + i]) : 0.f;  // cpu.rs:574-599
+            y[c][i] = v;
+            amax = fmaxf(amax, fabsf(v));
+            bad |= !isfinite(v);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off));
+        bad |= __shfl_xor(bad, off);
+    }
+    if (lane == 0) s_max[wv] = amax, s_bad[wv] = bad;
+    __syncthreads();
+    amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    bad = s_bad[0] | s_bad[1] | s_bad[2] | s_bad[3];
+    int E = 0;
+    if (bad) {
+        E = DG_NONFINITE;
+    } else if (amax > 0.f) {
+        int ex;
+        frexpf(amax, &ex);  // amax = m 2^ex, m in [0.5, 1)
+        E = 23 - ex;
+        if (ldexp((double)amax, E) > DG_XMAX) E--;
+    }
+    const double sc = bad ? 0.0 : ldexp(1.0, E);
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int j = (c * 256 + t) * 8;
+        if (j >= kpad) break;
+        unsigned b[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int X = (int)rint((double)y[c][i] * sc);
+            const int d0 = ((X + 128) & 255) - 128, X1 = (X - d0) >> 8;
+            const int d1 = ((X1 + 128) & 255) - 128, d2 = (X1 - d1) >> 8;
+            const int sh = 8 * (i & 3);
+            b[0][i >> 2] |= (unsigned)(d0 & 255) << sh;
+            b[1][i >> 2] |= (unsigned)(d1 & 255) << sh;
+            b[2][i >> 2] |= (unsigned)(d2 & 255) << sh;
+        }
+#pragma unroll
+        for (int pl = 0; pl < 3; pl++)
+            *(uint2 *)(dg + pl * dstride + (size_t)r * ldp + j) = make_uint2(b[pl][0], b[pl][1]);
+    }
+    if (t == 0) de[r] = E;
+}
+
 // f32 rows -> bf16 planes (columns [k, kpad) zeroed)
 __global__ void k_split(const float *__restrict__ x, int ldx, int rows, int k, int kpad, u16 *hi, u16 *lo, int ldp) {
     const size_t total = (size_t)rows * kpad;
@@ -153,7 +249,6 @@ constexpr int LDT = BK + 8;  // LDS row stride in bf16 (144 B): 16-byte row read
 constexpr int G_THREADS = 256;
 constexpr size_t A_TILE = (size_t)BM * LDT, B_TILE = (size_t)BN * LDT;  // u16 elements
 constexpr int AC = BM * BK / 8 / G_THREADS;   // 16-byte A chunks per thread and plane
-constexpr int BC = BN * BK / 16 / G_THREADS;  // 16-byte weight chunks per thread
 // dynamic LDS: A hi, A lo, B + [BK/32][BN] block-32 scales
 constexpr size_t GEMM_LDS = (2 * A_TILE + B_TILE) * sizeof(u16) + (BK / 32) * BN * sizeof(float);
 static_assert(GEMM_LDS >= 2 * BM * (BN / 2 + 8) * sizeof(u16), "SwiGLU staging tile");
@@ -176,6 +271,9 @@ struct GemmP {
     int ldc;
     u16 *ohi, *olo;
     int ldo, opad;     // SwiGLU planes: row stride, columns written (with zero pad)
+    const signed char *ad;  // digit planes [3][.][lda] (k_gemm_digits), plane stride dstride bytes
+    const int *ae;          // row exponents
+    size_t dstride;
 };
 
 // Workgroup -> tile: workgroup b runs on XCD b % 8.  Tiles are grouped in
@@ -680,6 +778,149 @@ __global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
         if (wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
     } else {
         gemm_store<EPI, TM, TN>(p, acc, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, p.scale, p.scale2);
+    }
+}
+
+// ------------------------------------------------------------------ GEMM on the int8 matrix cores
+// Activations as digit planes (k_norm_digits): x = (d0 + 2^8 d1 + 2^16 d2)
+// 2^-E per row, weights q (byte XOR 0x80).  Three v_mfma_i32_16x16x64_i8
+// per 64-wide k step and tile (one per digit plane) accumulate exact integer
+// sums in i32 (|d q| <= 2^14, k <= 131008); the epilogue forms
+// S = A2 2^16 + A1 2^8 + A0 exactly in f64 and writes f32(S 2^-E scale)
+// (one rounding) through the same store / SwiGLU epilogues.  Against the
+// split-bf16 kernel: 3 int8 MFMAs at twice the bf16 rate instead of 4 bf16
+// ones per 64 k, no weight conversion, 192 activation bytes per row and step
+// instead of 256 (measured on the config-5 shapes in a stand-alone harness:
+// qkv 715-820 -> 512 us, gate/up 3118-3189 -> 2288 us).
+// Staging as k_gemm_ring: a 3-step direct-to-LDS ring; a step holds the three
+// digit planes [128 rows][64 B] and the weights [256 columns][64 B], 16-byte
+// chunk c of row r at c ^ ((r >> 1) & 3).  Lane group g of a 16x16x64 MFMA
+// reads chunk g of its row / column for both operands, so every k pairs with
+// itself.  8 waves of 64 x 64 outputs, 120 KB of LDS, one workgroup per CU.
+namespace dring {
+constexpr int WGM = 2, WGN = 4, TM = 4, TN = 4, NW = WGM * WGN, T = 64 * NW, S = 3;
+static_assert(WGM * TM * 16 == BM && WGN * TN * 16 == BN && BK == 64, "digit ring tile");
+constexpr int A_PL = BM * BK, B_ST = BN * BK, STAGE = 3 * A_PL + B_ST;
+constexpr int A_UNITS = A_PL / 1024, B_UNITS = B_ST / 1024;  // 1 KB loads (16 rows of 64 B)
+constexpr int JA = A_UNITS / NW, JB = B_UNITS / NW, L = 3 * JA + JB;
+static_assert(A_UNITS % NW == 0 && B_UNITS % NW == 0, "digit ring units");
+constexpr size_t LDS = (size_t)S * STAGE;
+static_assert(L * (S - 2) < 64, "vmcnt range");
+static_assert(LDS >= 2 * BM * (BN / 2 + 8) * sizeof(u16), "SwiGLU staging tile");
+}  // namespace dring
+
+template <int EPI>
+__global__ __launch_bounds__(dring::T, 1) void k_gemm_digits(GemmP p) {
+    using namespace dring;
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    extern __shared__ float4 dsm[];
+    unsigned char *sm = reinterpret_cast<unsigned char *>(dsm);
+    int mb, nbk;
+    if (!gemm_tile(p, mb, nbk)) return;
+    const int m0 = mb * BM, n0 = nbk * BN;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const u32x4 da = ring_desc(p.ad, 3 * p.dstride), dw = ring_desc(p.w, (size_t)p.N * p.kp);
+    const unsigned sm0 = (unsigned)(uintptr_t)sm;  // LDS address (low half of the flat address)
+    // load j of this wave fills 1 KB block u = j NW + wave: j < 3 JA digit
+    // plane j / JA (16 rows of 64 B), else the weights (16 columns of 64 B)
+    unsigned voff[L], loff[L];
+#pragma unroll
+    for (int j = 0; j < L; j++) {
+        if (j < 3 * JA) {
+            const int pl = j / JA, ua = (j % JA) * NW + wave;
+            const int r = 16 * ua + (lane >> 2), c = (lane & 3) ^ ((r >> 1) & 3);
+            voff[j] = (unsigned)(pl * p.dstride + (size_t)(m0 + r) * p.lda + c * 16);
+            loff[j] = (unsigned)(pl * A_PL + ua * 1024);
+        } else {
+            const int ub = (j - 3 * JA) * NW + wave;
+            const int n = 16 * ub + (lane >> 2), c = (lane & 3) ^ ((n >> 1) & 3);
+            const int row = min(n0 + n, p.N - 1);  // columns past N re-read row N - 1 (never stored)
+            voff[j] = (unsigned)(row * p.kp + c * 16);
+            loff[j] = (unsigned)(3 * A_PL + ub * 1024);
+        }
+    }
+    // step kt into ring slot; steps past the last re-read the last (in bounds, never used)
+    auto issue = [&](int kt, int slot) {
+        const unsigned ko = (unsigned)(min(kt, p.nk - 1) * BK);
+        const unsigned base = sm0 + (unsigned)(slot * STAGE);
+#pragma unroll
+        for (int j = 0; j < L; j++) ring_load(j < 3 * JA ? da : dw, base + loff[j], voff[j], ko);
+    };
+
+    i32x4 acc[3][TM][TN];
+#pragma unroll
+    for (int d = 0; d < 3; d++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[d][i][j] = i32x4{0, 0, 0, 0};
+    ring_wait<0>();
+#pragma unroll
+    for (int s = 0; s < S - 1; s++) issue(s, s);
+    const int fr = lane & 15, g = lane >> 4;
+    int cur = 0;  // ring slot of step kt
+    for (int kt = 0; kt < p.nk; kt++) {
+        ring_wait<L * (S - 2)>();  // this wave's loads of step kt have landed
+        ring_barrier();            // every wave's have; slot kt - 1 is free
+        issue(kt + S - 1, cur == 0 ? S - 1 : cur - 1);
+        const unsigned char *st = sm + cur * STAGE;
+        cur = cur == S - 1 ? 0 : cur + 1;
+        i32x4 bq[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+            const int n = wn * TN * 16 + tn * 16 + fr;
+            const u32x4 v = *(const u32x4 *)(st + 3 * A_PL + n * 64 + ((g ^ ((fr >> 1) & 3)) << 4)) ^ 0x80808080u;
+            bq[tn] = __builtin_bit_cast(i32x4, v);
+        }
+#pragma unroll
+        for (int d = 0; d < 3; d++) {
+            i32x4 a[TM];
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++) {
+                const int r = wm * TM * 16 + tm * 16 + fr;
+                a[tm] = *(const i32x4 *)(st + d * A_PL + r * 64 + ((g ^ ((fr >> 1) & 3)) << 4));
+            }
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+                for (int tm = 0; tm < TM; tm++)
+                    acc[d][tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[tm], bq[tn], acc[d][tm][tn], 0, 0, 0);
+        }
+    }
+    ring_wait<0>();  // the re-read tail steps land before the workgroup's LDS is reused or released
+    // S 2^-E scale, one rounding to f32; the store epilogues then run at unit scale
+    int er[TM][4];
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = m0 + wm * TM * 16 + tm * 16 + (g << 2) + r;
+            er[tm][r] = m < p.M ? p.ae[m] : 0;
+        }
+    f32x4 v[TM][TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+        const int n = n0 + wn * TN * 16 + tn * 16 + fr;
+        const double sc = EPI == GE_SWIGLU && (n & 2) ? (double)p.scale2 : (double)p.scale;  // gate / up rows
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const double S = (double)acc[2][tm][tn][r] * 65536.0 + (double)acc[1][tm][tn][r] * 256.0 +
+                                 (double)acc[0][tm][tn][r];
+                const int E = er[tm][r];
+                v[tm][tn][r] = E == DG_NONFINITE ? __builtin_nanf("") : (float)(S * ldexp(1.0, -E) * sc);
+            }
+    }
+    GemmP q = p;
+    q.scale = q.scale2 = 1.f;
+    if (EPI == GE_SWIGLU) {
+        __syncthreads();  // every wave's tail loads have landed
+        swiglu_store<TM, TN, T, false>(q, v, reinterpret_cast<u16 *>(sm), wm * TM * 16, wn * TN * 16, m0, n0, lane);
+        if (wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
+    } else {
+        gemm_store<EPI, TM, TN>(q, v, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, 1.f, 1.f);
     }
 }
 
@@ -1239,6 +1480,19 @@ int gemm_t(const GemmP &p, hipStream_t s) {
 }
 
 template <int EPI>
+int gemm_digits_t(const GemmP &p, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_digits<EPI>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)dring::LDS));
+        attr = true;
+    }
+    const int grid = (p.n_super + 7) / 8 * 8 * 32;
+    hipLaunchKernelGGL((k_gemm_digits<EPI>), dim3(grid), dim3(dring::T), dring::LDS, s, p);
+    PF_LAUNCH_CHECK();
+}
+
+template <int EPI>
 int gemm_ring_t(const GemmP &p, hipStream_t s) {
     static bool attr = false;
     if (!attr) {
@@ -1280,6 +1534,38 @@ int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, co
     PF_LAUNCH_CHECK();
 }
 
+bool gemm_takes_digits(const Packed &w) {
+    // int8 per-tensor weights; k bound: |sum of d q| <= 2^14 kpad stays in i32
+    return !w.bf16 && !w.s32 && prefill_k_pad(w.k) <= 131008;
+}
+
+int launch_norm_digits(const float *x, int ldx, int rows, const float *w, int k, float eps, signed char *dg,
+                       size_t dstride, int *e, int ldp, hipStream_t s) {
+    if (rows <= 0) return SCRY_OK;
+    const int kpad = prefill_k_pad(k);
+    if (kpad > ldp || ldp % 16 || dstride % 16 || dstride < (size_t)rows * ldp || (uintptr_t)dg % 16)
+        return set_error(SCRY_ERR_INVALID, "norm_digits: k %d, plane stride %d / %zu", k, ldp, dstride);
+    const int nc = (kpad + 2047) / 2048;
+    if (nc > 8) return set_error(SCRY_ERR_UNSUPPORTED, "norm_digits: k %d > 16384", k);
+    const bool vec = k % 8 == 0 && (uintptr_t)x % 16 == 0 && ldx % 4 == 0;
+#define ND_LAUNCH(NC)                                                                                        \
+    if (vec)                                                                                                 \
+        hipLaunchKernelGGL((k_norm_digits<NC, true>), dim3(rows), dim3(256), 0, s, x, ldx, w, k, eps, dg,   \
+                           dstride, e, ldp, kpad);                                                          \
+    else                                                                                                     \
+        hipLaunchKernelGGL((k_norm_digits<NC, false>), dim3(rows), dim3(256), 0, s, x, ldx, w, k, eps, dg,  \
+                           dstride, e, ldp, kpad)
+    switch (nc) {
+        case 1: ND_LAUNCH(1); break;
+        case 2: ND_LAUNCH(2); break;
+        case 3:
+        case 4: ND_LAUNCH(4); break;
+        default: ND_LAUNCH(8); break;
+    }
+#undef ND_LAUNCH
+    PF_LAUNCH_CHECK();
+}
+
 int launch_split(const float *x, int ldx, int rows, int k, u16 *hi, u16 *lo, int ldp, hipStream_t s) {
     const int kpad = prefill_k_pad(k);
     if (kpad > ldp) return set_error(SCRY_ERR_INVALID, "split: k %d exceeds plane stride %d", k, ldp);
@@ -1303,9 +1589,18 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
                              ((uintptr_t)g.ohi | (uintptr_t)g.olo) % 16))
         return set_error(SCRY_ERR_INVALID, "gemm: swiglu needs the fused gate/up layout");
     if (w.s32 && w.nb * 32 < w.k) return set_error(SCRY_ERR_INVALID, "gemm: block-32 scales too short");
+    if (g.ad) {  // digit planes: the int8 matrix cores
+        if (!gemm_takes_digits(w) || !g.ae || g.lda % 16 || (uintptr_t)g.ad % 16 ||
+            g.dstride < (size_t)prefill_rows_pad(g.M) * g.lda || 3 * g.dstride >= 0x7fffffffull)
+            return set_error(SCRY_ERR_INVALID, "gemm: digit planes need int8 per-tensor weights and a %d-row stride",
+                             prefill_rows_pad(g.M));
+    }
     GemmP p{};
     p.ahi = g.ahi;
     p.alo = g.alo;
+    p.ad = g.ad;
+    p.ae = g.ae;
+    p.dstride = g.dstride;
     p.lda = g.lda;
     p.w = w.d;
     p.kp = kp_el;
@@ -1333,6 +1628,14 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
             case GE_STORE: return gemm_t<GE_STORE, false, true>(p, s);
             case GE_RESID: return gemm_t<GE_RESID, false, true>(p, s);
             case GE_SWIGLU: return gemm_t<GE_SWIGLU, false, true>(p, s);
+        }
+        return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
+    }
+    if (p.ad) {
+        switch (epi) {
+            case GE_STORE: return gemm_digits_t<GE_STORE>(p, s);
+            case GE_RESID: return gemm_digits_t<GE_RESID>(p, s);
+            case GE_SWIGLU: return gemm_digits_t<GE_SWIGLU>(p, s);
         }
         return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
     }
