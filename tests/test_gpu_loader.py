@@ -222,3 +222,62 @@ def test_loader_errors(tmp_path, hip):
     expect([str(tmp_path / "junk.safetensors")], "header length")
     # the complete checkpoint still loads from the original shards
     hip.LlamaModel.from_safetensors(lcfg, paths).free()
+
+
+def _with_norm_weights(tmp_path, cfg, tensors, edits):
+    """The checkpoint with RMSNorm weight entries replaced: {(name, index): value}."""
+    t = {n: v.clone() for n, v in tensors.items()}
+    for (name, idx), val in edits.items():
+        a = t[name].to(torch.float32)
+        a[idx] = val
+        t[name] = a.contiguous()
+    path = tmp_path / "edited.safetensors"
+    st_torch.save_file(t, str(path), metadata={"format": "pt"})
+    return [str(path)], t
+
+
+def test_forward_outlier_channels_vs_oracle(tmp_path, orc, hip):
+    """Norm weights with outlier channels (x300, x-500), so one value of every
+    normalised row dwarfs the rest.  The int8 prefill GEMMs hold each row as
+    24-bit fixed point scaled to its largest value (absolute error 2^-24 of
+    it), so this is their widest per-row range; the logits stay within the bar."""
+    cfg = dict(BASE)
+    _, tensors = make_checkpoint(tmp_path, cfg, 17, False, [torch.float32])
+    edits = {}
+    for i in range(cfg["n_layers"]):
+        edits[(f"model.layers.{i}.input_layernorm.weight", 3 + i)] = 300.0
+        edits[(f"model.layers.{i}.post_attention_layernorm.weight", 40 + i)] = -500.0
+    edits[("model.norm.weight", 7)] = 400.0
+    paths, t2 = _with_norm_weights(tmp_path, cfg, tensors, edits)
+    print("[case] forward with outlier norm channels", flush=True)
+    hm = hip.LlamaModel.from_safetensors(hip.LlamaConfig(**dict(cfg, tie_word_embeddings=False)), paths)
+    om = oracle_model(orc, cfg, t2, False)
+    toks = orc.prompt_ids(5, 40, cfg["vocab_size"])
+    fr = om.forward(toks, mode=1)
+    fg = hm.forward(toks)
+    ef = max(rel_err(fg[i], fr[i]) for i in range(len(toks)))
+    print(f"[err] forward logits {ef:.3e}", flush=True)
+    assert ef < LOGIT_TOL
+    hm.free()
+    om.close()
+
+
+def test_forward_nonfinite_norm_output(tmp_path, orc, hip):
+    """An infinite RMSNorm weight makes one value of every normalised row
+    infinite: the prefill GEMMs' digit rows carry a non-finite marker and
+    give NaN, as the reference's sums of inf * q do; every logit is NaN on
+    both sides."""
+    cfg = dict(BASE, n_layers=1)
+    _, tensors = make_checkpoint(tmp_path, cfg, 19, False, [torch.float32])
+    paths, t2 = _with_norm_weights(tmp_path, cfg, tensors,
+                                   {("model.layers.0.input_layernorm.weight", 5): float("inf")})
+    print("[case] forward with an infinite norm weight", flush=True)
+    hm = hip.LlamaModel.from_safetensors(hip.LlamaConfig(**dict(cfg, tie_word_embeddings=False)), paths)
+    om = oracle_model(orc, cfg, t2, False)
+    toks = orc.prompt_ids(6, 10, cfg["vocab_size"])
+    fr = np.asarray(om.forward(toks, mode=1))
+    fg = np.asarray(hm.forward(toks))
+    print(f"[nan] oracle {np.isnan(fr).mean():.3f} gpu {np.isnan(fg).mean():.3f}", flush=True)
+    assert np.isnan(fr).all() and np.isnan(fg).all()
+    hm.free()
+    om.close()
