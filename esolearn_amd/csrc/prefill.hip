@@ -197,7 +197,7 @@ __global__ __launch_bounds__(256) void k_norm_digits(const float *__restrict__ x
         E = 23 - ex;
         if (ldexp((double)amax, E) > DG_XMAX) E--;
     }
-    const double sc = bad ? 0.0 : ldexp(1.0, E);
+    const int Es = bad ? 0 : E;
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         const int j = (c * 256 + t) * 8;
@@ -205,13 +205,15 @@ __global__ __launch_bounds__(256) void k_norm_digits(const float *__restrict__ x
         unsigned b[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int X = (int)rint((double)y[c][i] * sc);
-            const int d0 = ((X + 128) & 255) - 128, X1 = (X - d0) >> 8;
-            const int d1 = ((X1 + 128) & 255) - 128, d2 = (X1 - d1) >> 8;
+            // y 2^E is exact in f32 (a power-of-two scaling to at most 2^23), rint then exact
+            const int X = bad ? 0 : (int)rintf(ldexpf(y[c][i], Es));
+            // balanced digits: d0 = sext8(X), d1 = sext8(X1), d2 = X2 with X1 = (X - d0) / 2^8, X2 = (X1 - d1) / 2^8
+            const int X1 = (X - (int)(signed char)X) >> 8;
+            const int X2 = (X1 - (int)(signed char)X1) >> 8;
             const int sh = 8 * (i & 3);
-            b[0][i >> 2] |= (unsigned)(d0 & 255) << sh;
-            b[1][i >> 2] |= (unsigned)(d1 & 255) << sh;
-            b[2][i >> 2] |= (unsigned)(d2 & 255) << sh;
+            b[0][i >> 2] |= (unsigned)(X & 255) << sh;
+            b[1][i >> 2] |= (unsigned)(X1 & 255) << sh;
+            b[2][i >> 2] |= (unsigned)(X2 & 255) << sh;
         }
 #pragma unroll
         for (int pl = 0; pl < 3; pl++)
