@@ -294,6 +294,7 @@ struct PrefillGemm {
     const signed char *ad = nullptr;
     const int *ae = nullptr;
     size_t dstride = 0;
+    float *of = nullptr;  // GE_SWIGLU with digit planes: f32 output rows [M][ldo] instead of ohi / olo
 };
 struct PrefillAttn {
     const float *qkv = nullptr;  // rows [M][ldq], q part RoPE'd
@@ -308,9 +309,9 @@ int prefill_rows_pad(int M);  // GEMM input plane rows for M activation rows
 int prefill_k_pad(int k);     // GEMM input plane columns (and zero padding) for k
 int launch_norm_split(const float *x, int ldx, int rows, int rstep, int roff, const float *w, int k, float eps,
                       unsigned short *hi, unsigned short *lo, int ldp, float *outf, int ldf, hipStream_t s);
-// RMSNorm into the digit planes of a PrefillGemm (rows r of [3][.][ldp] at
-// plane stride dstride bytes; columns [k, prefill_k_pad(k)) zero) and the row
-// exponents e[r]
+// RMSNorm (w non-null; the rows as they are for w null) into the digit
+// planes of a PrefillGemm (rows r of [3][.][ldp] at plane stride dstride
+// bytes; columns [k, prefill_k_pad(k)) zero) and the row exponents e[r]
 int launch_norm_digits(const float *x, int ldx, int rows, const float *w, int k, float eps, signed char *dg,
                        size_t dstride, int *e, int ldp, hipStream_t s);
 // true when a GEMM over w takes digit planes (int8 per-tensor weights)

@@ -59,7 +59,7 @@ struct scry_llama_s {
         unsigned short *p0 = nullptr, *p1 = nullptr;
         float *x = nullptr, *qkv = nullptr, *last = nullptr, *xl = nullptr;
         int64_t *ids = nullptr;
-        signed char *dg = nullptr;  // digit planes [3][Mp][ld0] of the RMSNorm outputs (int8 GEMMs)
+        signed char *dg = nullptr;  // digit planes [3][Mp][ld] of the int8 GEMMs' inputs (ld = ld0 or ld1)
         int *de = nullptr;          // their row exponents [Mp]
     } pf;
     unsigned short *kvp = nullptr;  // the prefill attention's K / V planes (grown on demand)
@@ -640,12 +640,13 @@ int prefill_ws(scry_llama m, int M, int n_seq) {
     SCRY_TRY(dev_alloc((void **)&P.last, (size_t)PF_MAX_SEQS * m->V * sizeof(float)));
     SCRY_TRY(dev_alloc((void **)&P.xl, (size_t)PF_MAX_SEQS * m->h * sizeof(float)));
     SCRY_TRY(dev_alloc((void **)&P.ids, (size_t)Mp * sizeof(int64_t)));
-    SCRY_TRY(dev_alloc((void **)&P.dg, 3 * (size_t)Mp * ld0));
+    const size_t ldd = std::max(ld0, ld1);  // digit planes of the RMSNorm outputs (ld0) or the SwiGLU rows (ld1)
+    SCRY_TRY(dev_alloc((void **)&P.dg, 3 * (size_t)Mp * ldd));
     SCRY_TRY(dev_alloc((void **)&P.de, (size_t)Mp * sizeof(int)));
     hipStream_t s = ctx().stream;
     SCRY_HIP(hipMemsetAsync(P.p0, 0, n0 * sizeof(unsigned short), s));
     SCRY_HIP(hipMemsetAsync(P.p1, 0, n1 * sizeof(unsigned short), s));
-    SCRY_HIP(hipMemsetAsync(P.dg, 0, 3 * (size_t)Mp * ld0, s));
+    SCRY_HIP(hipMemsetAsync(P.dg, 0, 3 * (size_t)Mp * ldd, s));
     SCRY_HIP(hipMemsetAsync(P.de, 0, (size_t)Mp * sizeof(int), s));
     P.Mp = Mp;
     P.ld0 = ld0;
@@ -762,19 +763,32 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         SCRY_TRY(launch_gemm(PF_RESID, o, s));
         PrefillGemm u;
         SCRY_TRY(norm_for(m->norm_post(l), Ly.gu, u));
-        u.ohi = h1;
-        u.olo = l1;
-        u.ldo = P.ld1;
-        u.opad = prefill_k_pad(m->ffn);
-        SCRY_TRY(launch_gemm(PF_SWIGLU, u, s));
         PrefillGemm d;
-        d.ahi = h1;
-        d.alo = l1;
         d.lda = P.ld1;
         d.M = M;
         d.w = &Ly.down;
         d.c = P.x;
         d.ldc = m->h;
+        if (u.ad && gemm_takes_digits(Ly.down)) {
+            // SwiGLU rows in f32 (in the planes' buffer), then their digit planes
+            float *f1 = reinterpret_cast<float *>(P.p1);
+            const size_t dstride1 = (size_t)P.Mp * P.ld1;
+            u.of = f1;
+            u.ldo = P.ld1;
+            SCRY_TRY(launch_gemm(PF_SWIGLU, u, s));
+            SCRY_TRY(launch_norm_digits(f1, P.ld1, M, nullptr, m->ffn, 0.f, P.dg, dstride1, P.de, P.ld1, s));
+            d.ad = P.dg;
+            d.ae = P.de;
+            d.dstride = dstride1;
+        } else {
+            u.ohi = h1;
+            u.olo = l1;
+            u.ldo = P.ld1;
+            u.opad = prefill_k_pad(m->ffn);
+            SCRY_TRY(launch_gemm(PF_SWIGLU, u, s));
+            d.ahi = h1;
+            d.alo = l1;
+        }
         SCRY_TRY(launch_gemm(PF_RESID, d, s));
     }
     if (all_logits) {

@@ -132,11 +132,12 @@ __global__ __launch_bounds__(256) void k_norm_split8(const float *__restrict__ x
 // [-127, 127]).  A row holding a NaN or an infinity gets E = DG_NONFINITE
 // and the GEMM writes NaN for it, as the split planes do (lo = bf16(inf - inf)).
 // Thread t holds columns 8 (c 256 + t) .. +7 of chunk c; VEC: 16-byte loads
-// (k % 8 == 0, rows 16-byte aligned).
+// (k % 8 == 0, rows 16-byte aligned).  NORM false: the rows as they are (y = x;
+// w and eps unused), for GEMM inputs that no single kernel holds whole rows of.
 constexpr int DG_NONFINITE = 0x7fffffff;
 constexpr double DG_XMAX = 8323071.0;  // 2^23 - 2^16 - 1
 
-template <int NC, bool VEC>
+template <int NC, bool VEC, bool NORM>
 __global__ __launch_bounds__(256) void k_norm_digits(const float *__restrict__ x, int ldx, const float *__restrict__ w,
                                                      int k, float eps, signed char *dg, size_t dstride, int *de,
                                                      int ldp, int kpad) {
@@ -162,10 +163,12 @@ __global__ __launch_bounds__(256) void k_norm_digits(const float *__restrict__ x
 #pragma unroll
             for (int i = 0; i < 8; i++) y[c][i] = j + i < k ? src[j + i] : 0.f;
         }
+        if (NORM) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) ss += (double)y[c][i] * (double)y[c][i];
+            for (int i = 0; i < 8; i++) ss += (double)y[c][i] * (double)y[c][i];
+        }
     }
-    const double rstd = 1.0 / sqrt(block_sum_d(ss, red) / (double)k + (double)eps);
+    const double rstd = NORM ? 1.0 / sqrt(block_sum_d(ss, red) / (double)k + (double)eps) : 1.0;
     float amax = 0.f;
     int bad = 0;
 #pragma unroll
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(256) void k_norm_digits(const float *__restrict__ x
         const int j = (c * 256 + t) * 8;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float v = j + i < k ? (float)((double)y[c][i] * rstd * (double)w[j + i]) : 0.f;  // cpu.rs:574-599
+            const float v = j + i >= k ? 0.f : NORM ? (float)((double)y[c][i] * rstd * (double)w[j + i]) : y[c][i];  // cpu.rs:574-599
             y[c][i] = v;
             amax = fmaxf(amax, fabsf(v));
             bad |= !isfinite(v);
@@ -276,6 +279,7 @@ struct GemmP {
     const signed char *ad;  // digit planes [3][.][lda] (k_gemm_digits), plane stride dstride bytes
     const int *ae;          // row exponents
     size_t dstride;
+    float *of;              // SwiGLU output as f32 rows [M][ldo] instead of the planes (k_gemm_digits)
 };
 
 // Workgroup -> tile: workgroup b runs on XCD b % 8.  Tiles are grouped in
@@ -407,7 +411,9 @@ template <int TM, int TN, int NT, bool EXACT>
 __device__ __forceinline__ void swiglu_store(const GemmP &p, const f32x4 (&acc)[TM][TN], u16 *so, int ml, int nl, int m0,
                                              int n0, int lane) {
     constexpr int OW = BN / 2, LDO = OW + 8;  // output columns per tile; LDS row stride (u16)
+    constexpr int LDF = OW + 4;               // the same in f32 (p.of: f32 rows instead of planes)
     u16 *sh = so, *sl = so + BM * LDO;
+    float *sf = reinterpret_cast<float *>(so);
     const int fr = lane & 15;
 #pragma unroll
     for (int tn = 0; tn < TN; tn++) {
@@ -421,22 +427,44 @@ __device__ __forceinline__ void swiglu_store(const GemmP &p, const f32x4 (&acc)[
                 const float v0 = acc[tm][tn][2 * rp] * sc, v1 = acc[tm][tn][2 * rp + 1] * sc;
                 const float recv = quad_xor2(gate ? v1 : v0);
                 const float gv = gate ? v0 : recv, uv = gate ? recv : v1;
-                u16 a, b;
-                split_bf16((EXACT ? silu_f(gv) : silu_split(gv)) * uv, a, b);  // cpu.rs:666-678
-                const unsigned hw = (unsigned)a | ((unsigned)quad_xor1((int)a) << 16);
-                const unsigned lw = (unsigned)b | ((unsigned)quad_xor1((int)b) << 16);
+                const float o = (EXACT ? silu_f(gv) : silu_split(gv)) * uv;  // cpu.rs:666-678
                 const int r = ml + tm * 16 + ((lane >> 4) << 2) + 2 * rp + (gate ? 0 : 1);
-                if ((n & 1) == 0) {
-                    const int at = r * LDO + ((n >> 2) << 1);
-                    *(unsigned *)(sh + at) = hw;
-                    *(unsigned *)(sl + at) = lw;
+                if (p.of) {
+                    const float po = __int_as_float(quad_xor1(__float_as_int(o)));
+                    if ((n & 1) == 0) *(float2 *)(sf + r * LDF + ((n >> 2) << 1)) = make_float2(o, po);
+                } else {
+                    u16 a, b;
+                    split_bf16(o, a, b);
+                    const unsigned hw = (unsigned)a | ((unsigned)quad_xor1((int)a) << 16);
+                    const unsigned lw = (unsigned)b | ((unsigned)quad_xor1((int)b) << 16);
+                    if ((n & 1) == 0) {
+                        const int at = r * LDO + ((n >> 2) << 1);
+                        *(unsigned *)(sh + at) = hw;
+                        *(unsigned *)(sl + at) = lw;
+                    }
                 }
             }
         }
     }
     __syncthreads();
-    constexpr int CPR = OW / 8;  // 16-byte chunks per row
     const int oc0 = n0 >> 1, ocn = p.N >> 1;
+    if (p.of) {  // f32 rows: 4 columns per 16-byte store
+        constexpr int CPF = OW / 4;
+        for (int idx = threadIdx.x; idx < BM * CPF; idx += NT) {
+            const int r = idx / CPF, c = idx - r * CPF;
+            const int m = m0 + r, col = oc0 + c * 4;
+            if (m >= p.M || col >= ocn) continue;
+            const float *src = sf + r * LDF + c * 4;
+            float *dst = p.of + (size_t)m * p.ldo + col;
+            if (col + 4 <= ocn) {
+                *(float4 *)dst = *(const float4 *)src;
+            } else {
+                for (int e = 0; e < ocn - col; e++) dst[e] = src[e];
+            }
+        }
+        return;
+    }
+    constexpr int CPR = OW / 8;  // 16-byte chunks per row
     for (int idx = threadIdx.x; idx < 2 * BM * CPR; idx += NT) {
         const int pl = idx / (BM * CPR), rem = idx - pl * (BM * CPR), r = rem / CPR, c = rem - r * CPR;
         const int m = m0 + r, col = oc0 + c * 8;
@@ -808,7 +836,8 @@ constexpr int JA = A_UNITS / NW, JB = B_UNITS / NW, L = 3 * JA + JB;
 static_assert(A_UNITS % NW == 0 && B_UNITS % NW == 0, "digit ring units");
 constexpr size_t LDS = (size_t)S * STAGE;
 static_assert(L * (S - 2) < 64, "vmcnt range");
-static_assert(LDS >= 2 * BM * (BN / 2 + 8) * sizeof(u16), "SwiGLU staging tile");
+static_assert(LDS >= 2 * BM * (BN / 2 + 8) * sizeof(u16) && LDS >= BM * (BN / 2 + 4) * sizeof(float),
+              "SwiGLU staging tile");
 }  // namespace dring
 
 template <int EPI>
@@ -920,7 +949,7 @@ __global__ __launch_bounds__(dring::T, 1) void k_gemm_digits(GemmP p) {
     if (EPI == GE_SWIGLU) {
         __syncthreads();  // every wave's tail loads have landed
         swiglu_store<TM, TN, T, false>(q, v, reinterpret_cast<u16 *>(sm), wm * TM * 16, wn * TN * 16, m0, n0, lane);
-        if (wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
+        if (!p.of && wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
     } else {
         gemm_store<EPI, TM, TN>(q, v, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, 1.f, 1.f);
     }
@@ -1550,20 +1579,22 @@ int launch_norm_digits(const float *x, int ldx, int rows, const float *w, int k,
     const int nc = (kpad + 2047) / 2048;
     if (nc > 8) return set_error(SCRY_ERR_UNSUPPORTED, "norm_digits: k %d > 16384", k);
     const bool vec = k % 8 == 0 && (uintptr_t)x % 16 == 0 && ldx % 4 == 0;
-#define ND_LAUNCH(NC)                                                                                        \
-    if (vec)                                                                                                 \
-        hipLaunchKernelGGL((k_norm_digits<NC, true>), dim3(rows), dim3(256), 0, s, x, ldx, w, k, eps, dg,   \
-                           dstride, e, ldp, kpad);                                                          \
-    else                                                                                                     \
-        hipLaunchKernelGGL((k_norm_digits<NC, false>), dim3(rows), dim3(256), 0, s, x, ldx, w, k, eps, dg,  \
-                           dstride, e, ldp, kpad)
+    const bool norm = w != nullptr;
+#define ND_LAUNCH(NC, V, N) \
+    hipLaunchKernelGGL((k_norm_digits<NC, V, N>), dim3(rows), dim3(256), 0, s, x, ldx, w, k, eps, dg, dstride, e, ldp, kpad)
+#define ND_NC(NC)                         \
+    if (vec && norm) ND_LAUNCH(NC, true, true);   \
+    else if (norm) ND_LAUNCH(NC, false, true);    \
+    else if (vec) ND_LAUNCH(NC, true, false);     \
+    else ND_LAUNCH(NC, false, false)
     switch (nc) {
-        case 1: ND_LAUNCH(1); break;
-        case 2: ND_LAUNCH(2); break;
+        case 1: ND_NC(1); break;
+        case 2: ND_NC(2); break;
         case 3:
-        case 4: ND_LAUNCH(4); break;
-        default: ND_LAUNCH(8); break;
+        case 4: ND_NC(4); break;
+        default: ND_NC(8); break;
     }
+#undef ND_NC
 #undef ND_LAUNCH
     PF_LAUNCH_CHECK();
 }
@@ -1591,6 +1622,8 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
                              ((uintptr_t)g.ohi | (uintptr_t)g.olo) % 16))
         return set_error(SCRY_ERR_INVALID, "gemm: swiglu needs the fused gate/up layout");
     if (w.s32 && w.nb * 32 < w.k) return set_error(SCRY_ERR_INVALID, "gemm: block-32 scales too short");
+    if (g.of && (!g.ad || epi != GE_SWIGLU || (uintptr_t)g.of % 16 || g.ldo % 4))
+        return set_error(SCRY_ERR_INVALID, "gemm: f32 SwiGLU rows need digit planes and 16-byte rows");
     if (g.ad) {  // digit planes: the int8 matrix cores
         if (!gemm_takes_digits(w) || !g.ae || g.lda % 16 || (uintptr_t)g.ad % 16 ||
             g.dstride < (size_t)prefill_rows_pad(g.M) * g.lda || 3 * g.dstride >= 0x7fffffffull)
@@ -1603,6 +1636,7 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
     p.ad = g.ad;
     p.ae = g.ae;
     p.dstride = g.dstride;
+    p.of = g.of;
     p.lda = g.lda;
     p.w = w.d;
     p.kp = kp_el;
