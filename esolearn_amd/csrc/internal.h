@@ -303,6 +303,7 @@ struct PrefillAttn {
     unsigned short *ohi = nullptr, *olo = nullptr;  // o_proj input planes
     int ldo = 0, opad = 0;
     int nqb = 0, nseq = 0;  // set by the launcher: query blocks per sequence, sequences
+    float *of = nullptr;    // instead of the planes: f32 rows [M][ldo] (the bf16 matrix-core kernel only)
 };
 enum { PF_STORE = 0, PF_RESID = 1, PF_SWIGLU = 2 };
 int prefill_rows_pad(int M);  // GEMM input plane rows for M activation rows

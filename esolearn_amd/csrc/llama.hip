@@ -747,19 +747,30 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         at.nkv = m->nkv;
         at.kvd = m->kv_dim;
         at.scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:225-234
-        at.ohi = h0;
-        at.olo = l0;
         at.ldo = P.ld0;
         at.opad = prefill_k_pad(m->q_dim);
-        SCRY_TRY(launch_attn_prefill(at, n_seq, t, l, kvp, s));
         PrefillGemm o;
-        o.ahi = h0;
-        o.alo = l0;
         o.lda = P.ld0;
         o.M = M;
         o.w = &Ly.o;
         o.c = P.x;
         o.ldc = m->h;
+        if (kvp.kh && gemm_takes_digits(Ly.o)) {
+            // attention rows in f32 (in the planes' buffer), then their digit planes
+            float *f0 = reinterpret_cast<float *>(P.p0);
+            at.of = f0;
+            SCRY_TRY(launch_attn_prefill(at, n_seq, t, l, kvp, s));
+            SCRY_TRY(launch_norm_digits(f0, P.ld0, M, nullptr, m->q_dim, 0.f, P.dg, dstride, P.de, P.ld0, s));
+            o.ad = P.dg;
+            o.ae = P.de;
+            o.dstride = dstride;
+        } else {
+            at.ohi = h0;
+            at.olo = l0;
+            SCRY_TRY(launch_attn_prefill(at, n_seq, t, l, kvp, s));
+            o.ahi = h0;
+            o.alo = l0;
+        }
         SCRY_TRY(launch_gemm(PF_RESID, o, s));
         PrefillGemm u;
         SCRY_TRY(norm_for(m->norm_post(l), Ly.gu, u));

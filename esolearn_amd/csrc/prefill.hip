@@ -1449,6 +1449,14 @@ __global__ __launch_bounds__(64 * BQW) void k_attn_bf3(PrefillAttn a, PrefillSeq
     }
     if (!valid) return;
     const float inv = 1.f / lrow;
+    if (a.of) {  // f32 rows (quantized for the o_proj GEMM afterwards)
+        float *orow = a.of + m * a.ldo + h * HD;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+            *(float4 *)(orow + dt * 16 + 4 * lg) =
+                make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+        return;
+    }
     u16 *oh = a.ohi + m * a.ldo + h * HD, *ol = a.olo + m * a.ldo + h * HD;
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++)
@@ -1768,6 +1776,8 @@ int launch_attn_prefill(const PrefillAttn &a, int n_seq, const PrefillSeqs &t, i
                         hipStream_t s) {
     if (a.hd % 2 || a.hd > 128 || a.nkv <= 0 || a.nh % a.nkv)
         return set_error(SCRY_ERR_UNSUPPORTED, "attn_prefill: head_dim %d / heads %d,%d", a.hd, a.nh, a.nkv);
+    if (a.of && (!kv.kh || !attn_prefill_planes(a.hd) || (uintptr_t)a.of % 16 || a.ldo % 4))
+        return set_error(SCRY_ERR_INVALID, "attn_prefill: f32 output rows need the bf16 matrix-core kernel");
     if (kv.kh && attn_prefill_planes(a.hd)) {  // bf16 matrix cores on the K / V planes
         if (a.hd == 128) return attn_bf3_t<128>(a, n_seq, t, kv, s);
         return attn_bf3_t<64>(a, n_seq, t, kv, s);
