@@ -174,9 +174,21 @@ __global__ __launch_bounds__(256) void k_norm_digits(const float *__restrict__ x
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         const int j = (c * 256 + t) * 8;
+        float g[8];
+        if (NORM && VEC) {
+            float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
+            if (j < k) {
+                w0 = *(const float4 *)(w + j);
+                w1 = *(const float4 *)(w + j + 4);
+            }
+            g[0] = w0.x, g[1] = w0.y, g[2] = w0.z, g[3] = w0.w, g[4] = w1.x, g[5] = w1.y, g[6] = w1.z, g[7] = w1.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) g[i] = NORM && j + i < k ? w[j + i] : 0.f;
+        }
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float v = j + i >= k ? 0.f : NORM ? (float)((double)y[c][i] * rstd * (double)w[j + i]) : y[c][i];  // cpu.rs:574-599
+            const float v = j + i >= k ? 0.f : NORM ? (float)((double)y[c][i] * rstd * (double)g[i]) : y[c][i];  // cpu.rs:574-599
             y[c][i] = v;
             amax = fmaxf(amax, fabsf(v));
             bad |= !isfinite(v);
@@ -1586,8 +1598,8 @@ int launch_norm_digits(const float *x, int ldx, int rows, const float *w, int k,
         return set_error(SCRY_ERR_INVALID, "norm_digits: k %d, plane stride %d / %zu", k, ldp, dstride);
     const int nc = (kpad + 2047) / 2048;
     if (nc > 8) return set_error(SCRY_ERR_UNSUPPORTED, "norm_digits: k %d > 16384", k);
-    const bool vec = k % 8 == 0 && (uintptr_t)x % 16 == 0 && ldx % 4 == 0;
     const bool norm = w != nullptr;
+    const bool vec = k % 8 == 0 && (uintptr_t)x % 16 == 0 && ldx % 4 == 0 && (uintptr_t)w % 16 == 0;
 #define ND_LAUNCH(NC, V, N) \
     hipLaunchKernelGGL((k_norm_digits<NC, V, N>), dim3(rows), dim3(256), 0, s, x, ldx, w, k, eps, dg, dstride, e, ldp, kpad)
 #define ND_NC(NC)                         \
