@@ -4,22 +4,29 @@
 // processed positions are appended to each sequence's KV cache, so decode can
 // continue from them.
 //
-// GEMM numerics.  The int8 weights are exact in bf16.  Each f32 activation x
-// is held as two bf16 values hi = bf16(x) and lo = bf16(x - hi), so
-// |x - hi - lo| <= 2^-17 |x|, and two bf16 MFMAs (hi x W, then lo x W)
-// accumulate in f32.  The products are exact, so the result is the
-// f32-accumulated dot product of x (to 2^-17) with the int8 weights, scaled
-// once per output (per-tensor) or once per 32-wide k block (block-32).  The
-// reference accumulates f64(a) * f64(q * scale) into f32 in k order
-// (cpu.rs:1128-1160): the differences are summation order and the 2^-17 split,
-// far inside the 1e-3 logit bar.
+// GEMM numerics.  The reference accumulates f64(a) * f64(q * scale) into f32
+// in k order (cpu.rs:1128-1160).  Two forms of the activations here:
+//  - int8 per-tensor weights (every projection of an int8 model): each row of
+//    activations as 24-bit fixed point, x = X 2^-E with E per row and
+//    |x - X 2^-E| <= 2^-23 max|row|, X in three balanced int8 digits; the int8
+//    matrix cores sum d q exactly in i32, and the epilogue forms the exact
+//    integer dot product and rounds X.q 2^-E scale to f32 once
+//    (k_norm_digits, k_gemm_digits);
+//  - block-32 weights and bf16 weights: each f32 activation as two bf16
+//    values hi = bf16(x), lo = bf16(x - hi) (|x - hi - lo| <= 2^-17 |x|), two
+//    bf16 MFMAs per product accumulated in f32 (one for bf16 weights: the
+//    reference's bf16 cast), scaled per output or per 32-wide k block.
+// The differences from the reference are the activation rounding and the
+// summation order, far inside the 1e-3 logit bar.
 //
-// Data layout.  GEMM inputs are two bf16 planes [Mp][ld] (hi, lo): Mp = rows
-// rounded up to the M tile, ld = k rounded up to the k step (64); the columns past k and
-// the rows past M are zero.  The kernel that produces an activation writes
-// its planes directly (RMSNorm, attention, SwiGLU), so no f32 copy of a GEMM
-// input exists.  Weights are the GEMV stream layout (one row of kp bytes per
-// output, byte = q + 128); the GEMM converts them to bf16 while staging.
+// Data layout.  GEMM inputs are [Mp][ld] planes (three int8 digit planes, or
+// the bf16 hi and lo planes): Mp = rows rounded up to the M tile, ld = k
+// rounded up to the k step (64); the columns past k are zero.  RMSNorm writes
+// its planes directly; the attention and SwiGLU outputs, whose rows no single
+// workgroup holds whole, go through f32 rows and a per-row pass into digit
+// planes (bf16 planes directly for the other weight types).  Weights are the
+// GEMV stream layout (one row of kp bytes per output, byte = q + 128), read
+// as they are by the int8 matrix cores, converted to bf16 for the bf16 ones.
 #include <cmath>
 
 #include "internal.h"
