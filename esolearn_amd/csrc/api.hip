@@ -274,6 +274,29 @@ int qmatmul(scry_buf a, scry_i8buf bq, float scale, const float *scales32, const
         g.ldy = n;
         g.bias = bias;
         rc = launch_qgemv(EPI_STORE, g, ctx().stream);
+    } else if (gemm_takes_digits(w) && k <= 16384) {
+        // prefill shapes, int8 per-tensor: the rows as digit planes (per-row
+        // 24-bit fixed point), then the GEMM on the int8 matrix cores
+        const int mp = prefill_rows_pad(m), ld = prefill_k_pad(k);
+        const size_t dstride = (size_t)mp * ld;
+        signed char *dg = nullptr;
+        rc = dev_alloc((void **)&dg, 3 * dstride + sizeof(int) * (size_t)mp);
+        int *de = reinterpret_cast<int *>(dg + 3 * dstride);
+        if (!rc) rc = launch_fill_u32((unsigned *)dg, (3 * dstride) / 4 + mp, 0u, ctx().stream);
+        if (!rc) rc = launch_norm_digits(a->d, k, m, nullptr, k, 0.f, dg, dstride, de, ld, ctx().stream);
+        PrefillGemm g;
+        g.w = &w;
+        g.ad = dg;
+        g.ae = de;
+        g.dstride = dstride;
+        g.lda = ld;
+        g.M = m;
+        g.c = o->d;
+        g.ldc = n;
+        g.bias = bias;
+        if (!rc) rc = launch_gemm(PF_STORE, g, ctx().stream);
+        if (!rc) rc = sync();  // the planes are freed below
+        dev_free(dg);
     } else {
         // prefill shapes: the activations as bf16 planes, then the MFMA GEMM
         const int mp = prefill_rows_pad(m), ld = prefill_k_pad(k);
