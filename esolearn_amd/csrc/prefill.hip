@@ -685,13 +685,19 @@ __global__ __launch_bounds__(G_THREADS, B32 ? 1 : 2) void k_gemm(GemmP p) {
 namespace ring {
 constexpr int WGM = 2, WGN = 4, TM = 4, TN = 4, NW = WGM * WGN, T = 64 * NW, S = 3;
 static_assert(WGM * TM * 16 == BM && WGN * TN * 16 == BN && BK == 64, "ring tile");
-constexpr int A_PL = BM * BK * 2, B_ST = BN * BK, STAGE = 2 * A_PL + B_ST;
-constexpr int A_UNITS = A_PL / 1024, B_UNITS = B_ST / 1024;  // 1 KB loads
-constexpr int JA = A_UNITS / NW, JB = B_UNITS / NW, L = 2 * JA + JB;  // loads per wave and step
-static_assert(A_UNITS % NW == 0 && B_UNITS % NW == 0, "ring units");
-constexpr size_t LDS = (size_t)S * STAGE;
-static_assert(L * (S - 2) < 64, "vmcnt range");
-static_assert(LDS >= 2 * BM * (BN / 2 + 8) * sizeof(u16), "SwiGLU staging tile");
+// WBF: bf16 weight rows (128 B per column and step, read as they are) and
+// one activation plane (the bf16 model); else int8 weights and hi, lo planes
+template <bool WBF>
+struct Lay {
+    static constexpr int NPL = WBF ? 1 : 2, WB = WBF ? 2 : 1;  // activation planes; bytes per weight
+    static constexpr int A_PL = BM * BK * 2, B_ST = BN * BK * WB, STAGE = NPL * A_PL + B_ST;
+    static constexpr int JA = A_PL / 1024 / NW, JB = B_ST / 1024 / NW;  // 1 KB loads per wave and step
+    static constexpr int L = NPL * JA + JB;
+    static_assert((A_PL / 1024) % NW == 0 && (B_ST / 1024) % NW == 0, "ring units");
+    static constexpr size_t LDS = (size_t)S * STAGE;
+    static_assert(L * (S - 2) < 64, "vmcnt range");
+    static_assert(LDS >= 2 * BM * (BN / 2 + 8) * sizeof(u16), "SwiGLU staging tile");
+};
 }  // namespace ring
 
 // buffer descriptor words (base, stride 0, num_records, raw-buffer flags),
@@ -729,9 +735,11 @@ __device__ __forceinline__ void ring_wait() { asm volatile("s_waitcnt vmcnt(%0)"
 // ring's loads); LDS reads and writes of this wave complete first
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <int EPI>
+template <int EPI, bool WBF>
 __global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
     using namespace ring;
+    using C = Lay<WBF>;
+    constexpr int A_PL = C::A_PL, STAGE = C::STAGE, JA = C::JA, L = C::L, NPL = C::NPL, WB = C::WB;
     extern __shared__ float4 rsm[];
     unsigned char *sm = reinterpret_cast<unsigned char *>(rsm);
     int mb, nbk;
@@ -740,25 +748,32 @@ __global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     const size_t a_bytes = (size_t)p.n_mb * BM * p.lda * 2;
-    const u32x4 dh = ring_desc(p.ahi, a_bytes), dl = ring_desc(p.alo, a_bytes);
-    const u32x4 dw = ring_desc(p.w, (size_t)p.N * p.kp);
+    const u32x4 dh = ring_desc(p.ahi, a_bytes), dl = ring_desc(WBF ? p.ahi : p.alo, a_bytes);
+    const u32x4 dw = ring_desc(p.w, (size_t)p.N * p.kp * WB);
     const unsigned sm0 = (unsigned)(uintptr_t)sm;  // LDS address (low half of the flat address)
     // load j of this wave fills 1 KB block u = j NW + wave: j < JA the hi plane
-    // (8 rows of 128 B), j < 2 JA the lo plane, else the weights (16 columns of 64 B)
+    // (8 rows of 128 B), j < 2 JA the lo plane, else the weights (int8: 16
+    // columns of 64 B; bf16: 8 columns of 128 B)
     unsigned voff[L], loff[L];
 #pragma unroll
     for (int j = 0; j < L; j++) {
-        if (j < 2 * JA) {
+        if (j < NPL * JA) {
             const int pl = j / JA, ua = (j % JA) * NW + wave;
             const int r = 8 * ua + (lane >> 3), c = (lane & 7) ^ (r & 7);
             voff[j] = (unsigned)((m0 + r) * p.lda * 2 + c * 16);
             loff[j] = (unsigned)(pl * A_PL + ua * 1024);
+        } else if (WBF) {
+            const int ub = (j - NPL * JA) * NW + wave;
+            const int n = 8 * ub + (lane >> 3), c = (lane & 7) ^ (n & 7);
+            const int row = min(n0 + n, p.N - 1);  // columns past N re-read row N - 1 (never stored)
+            voff[j] = (unsigned)(row * p.kp * 2 + c * 16);
+            loff[j] = (unsigned)(NPL * A_PL + ub * 1024);
         } else {
-            const int ub = (j - 2 * JA) * NW + wave;
+            const int ub = (j - NPL * JA) * NW + wave;
             const int n = 16 * ub + (lane >> 2), c = (lane & 3) ^ ((n >> 1) & 3);
             const int row = min(n0 + n, p.N - 1);  // columns past N re-read row N - 1 (never stored)
             voff[j] = (unsigned)(row * p.kp + c * 16);
-            loff[j] = (unsigned)(2 * A_PL + ub * 1024);
+            loff[j] = (unsigned)(NPL * A_PL + ub * 1024);
         }
     }
     // step kt into ring slot; steps past the last re-read the last (in bounds, never used)
@@ -768,8 +783,8 @@ __global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
 #pragma unroll
         for (int j = 0; j < L; j++) {
             if (j < JA) ring_load(dh, base + loff[j], voff[j], (unsigned)(ks * BK * 2));
-            else if (j < 2 * JA) ring_load(dl, base + loff[j], voff[j], (unsigned)(ks * BK * 2));
-            else ring_load(dw, base + loff[j], voff[j], (unsigned)(ks * BK));
+            else if (j < NPL * JA) ring_load(dl, base + loff[j], voff[j], (unsigned)(ks * BK * 2));
+            else ring_load(dw, base + loff[j], voff[j], (unsigned)(ks * BK * WB));
         }
     };
 
@@ -793,11 +808,16 @@ __global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
 #pragma unroll
         for (int tn = 0; tn < TN; tn++) {
             const int n = wn * TN * 16 + tn * 16 + fr;
-            const u32x4 v = *(const u32x4 *)(st + 2 * A_PL + n * 64 + ((g ^ ((fr >> 1) & 3)) << 4));
-            u32x4 o0, o1;
-            bytes_to_bf16(v, o0, o1);
-            b0[tn] = __builtin_bit_cast(bf16x8, o0);
-            b1[tn] = __builtin_bit_cast(bf16x8, o1);
+            if constexpr (WBF) {  // bf16 rows: chunk 2 g + h of the column's 128 bytes
+                b0[tn] = *(const bf16x8 *)(st + A_PL + n * 128 + (((2 * g) ^ (fr & 7)) << 4));
+                b1[tn] = *(const bf16x8 *)(st + A_PL + n * 128 + (((2 * g + 1) ^ (fr & 7)) << 4));
+            } else {
+                const u32x4 v = *(const u32x4 *)(st + 2 * A_PL + n * 64 + ((g ^ ((fr >> 1) & 3)) << 4));
+                u32x4 o0, o1;
+                bytes_to_bf16(v, o0, o1);
+                b0[tn] = __builtin_bit_cast(bf16x8, o0);
+                b1[tn] = __builtin_bit_cast(bf16x8, o1);
+            }
         }
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -806,24 +826,26 @@ __global__ __launch_bounds__(ring::T, 1) void k_gemm_ring(GemmP p) {
             for (int tm = 0; tm < TM; tm++) {
                 const int off = (wm * TM * 16 + tm * 16 + fr) * 128 + (((2 * g + h) ^ (fr & 7)) << 4);
                 ah[tm] = *(const bf16x8 *)(st + off);
-                al[tm] = *(const bf16x8 *)(st + A_PL + off);
+                if (!WBF) al[tm] = *(const bf16x8 *)(st + A_PL + off);
             }
 #pragma unroll
             for (int tn = 0; tn < TN; tn++)
 #pragma unroll
                 for (int tm = 0; tm < TM; tm++)
                     acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], h ? b1[tn] : b0[tn], acc[tm][tn], 0, 0, 0);
+            if (!WBF) {
 #pragma unroll
-            for (int tn = 0; tn < TN; tn++)
+                for (int tn = 0; tn < TN; tn++)
 #pragma unroll
-                for (int tm = 0; tm < TM; tm++)
-                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], h ? b1[tn] : b0[tn], acc[tm][tn], 0, 0, 0);
+                    for (int tm = 0; tm < TM; tm++)
+                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], h ? b1[tn] : b0[tn], acc[tm][tn], 0, 0, 0);
+            }
         }
     }
     ring_wait<0>();  // the re-read tail steps land before the workgroup's LDS is reused or released
     if (EPI == GE_SWIGLU) {
         __syncthreads();  // every wave's tail loads have landed
-        swiglu_store<TM, TN, T, false>(p, acc, reinterpret_cast<u16 *>(sm), wm * TM * 16, wn * TN * 16, m0, n0, lane);
+        swiglu_store<TM, TN, T, WBF>(p, acc, reinterpret_cast<u16 *>(sm), wm * TM * 16, wn * TN * 16, m0, n0, lane);
         if (wave == 0 && nbk == p.n_nb - 1) swiglu_pad(p, m0, lane);
     } else {
         gemm_store<EPI, TM, TN>(p, acc, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, p.scale, p.scale2);
@@ -1550,16 +1572,17 @@ int gemm_digits_t(const GemmP &p, hipStream_t s) {
     PF_LAUNCH_CHECK();
 }
 
-template <int EPI>
+template <int EPI, bool WBF>
 int gemm_ring_t(const GemmP &p, hipStream_t s) {
+    constexpr size_t lds = ring::Lay<WBF>::LDS;
     static bool attr = false;
     if (!attr) {
-        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_ring<EPI>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)ring::LDS));
+        SCRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_ring<EPI, WBF>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
     const int grid = (p.n_super + 7) / 8 * 8 * 32;
-    hipLaunchKernelGGL((k_gemm_ring<EPI>), dim3(grid), dim3(ring::T), ring::LDS, s, p);
+    hipLaunchKernelGGL((k_gemm_ring<EPI, WBF>), dim3(grid), dim3(ring::T), lds, s, p);
     PF_LAUNCH_CHECK();
 }
 
@@ -1685,12 +1708,15 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
     p.ldo = g.ldo;
     p.opad = g.opad;
     const bool b32 = w.s32 != nullptr;
+    // the ring kernels address the planes through a buffer descriptor (32-bit
+    // offsets); larger planes take the register-staged kernel
+    const bool ring_ok = (size_t)p.n_mb * BM * p.lda * 2 < 0x7fffffffull;
     if (w.bf16) {  // the bf16 model: weight rows as they are, the hi plane = the reference's bf16 cast
         p.alo = nullptr;
         switch (epi) {
-            case GE_STORE: return gemm_t<GE_STORE, false, true>(p, s);
-            case GE_RESID: return gemm_t<GE_RESID, false, true>(p, s);
-            case GE_SWIGLU: return gemm_t<GE_SWIGLU, false, true>(p, s);
+            case GE_STORE: return ring_ok ? gemm_ring_t<GE_STORE, true>(p, s) : gemm_t<GE_STORE, false, true>(p, s);
+            case GE_RESID: return ring_ok ? gemm_ring_t<GE_RESID, true>(p, s) : gemm_t<GE_RESID, false, true>(p, s);
+            case GE_SWIGLU: return ring_ok ? gemm_ring_t<GE_SWIGLU, true>(p, s) : gemm_t<GE_SWIGLU, false, true>(p, s);
         }
         return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
     }
@@ -1710,9 +1736,7 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
         }
         return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
     }
-    // the ring kernel addresses the planes through a buffer descriptor (32-bit
-    // offsets); larger planes take the register-staged kernel
-    if ((size_t)p.n_mb * BM * p.lda * 2 >= 0x7fffffffull) {
+    if (!ring_ok) {
         switch (epi) {
             case GE_STORE: return gemm_t<GE_STORE, false>(p, s);
             case GE_RESID: return gemm_t<GE_RESID, false>(p, s);
@@ -1721,9 +1745,9 @@ int launch_gemm(int epi, const PrefillGemm &g, hipStream_t s) {
         return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
     }
     switch (epi) {
-        case GE_STORE: return gemm_ring_t<GE_STORE>(p, s);
-        case GE_RESID: return gemm_ring_t<GE_RESID>(p, s);
-        case GE_SWIGLU: return gemm_ring_t<GE_SWIGLU>(p, s);
+        case GE_STORE: return gemm_ring_t<GE_STORE, false>(p, s);
+        case GE_RESID: return gemm_ring_t<GE_RESID, false>(p, s);
+        case GE_SWIGLU: return gemm_ring_t<GE_SWIGLU, false>(p, s);
     }
     return set_error(SCRY_ERR_INVALID, "gemm: unknown epilogue %d", epi);
 }
