@@ -1776,6 +1776,7 @@ int launch_gemm_bf16(const unsigned short *w, int kp, int N, int k, const unsign
     p.bias = bias;
     p.c = c;
     p.ldc = ldc;
+    if ((size_t)p.n_mb * BM * p.lda * 2 < 0x7fffffffull) return gemm_ring_t<GE_STORE, true>(p, s);
     return gemm_t<GE_STORE, false, true>(p, s);
 }
 
