@@ -52,6 +52,14 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # dense
+INT8_MFMA_PEAK_TOPS = 5000.0  # dense
+# Matrix-core busy fraction of the config-5 prefill's projection GEMMs and
+# attention, from the rocprofv3 counter run in
+# profiles/prefill_llama3_8b_mfma_counters.md (SQ_VALU_MFMA_BUSY_CYCLES over
+# GRBM_GUI_ACTIVE / 8 x 1024 SIMDs); counters cannot be read inside this
+# process, so the line carries the profile's figures with their source.
+PREFILL_MFMA_BUSY_PROFILE = {"qkv": 0.551, "o": 0.502, "gate_up": 0.586, "down": 0.584, "attention": 0.238,
+                             "prefill": 0.480, "source": "profiles/prefill_llama3_8b_mfma_counters.md"}
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_projections_pmc_traffic.md")
 
 
@@ -96,16 +104,20 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
           f"bf16 model prefill {pm_bf16:.1f} ms", file=sys.stderr, flush=True)
     return {
         "workload": "llama3-8b-shape int8: 4 x 2048-token prompts, batched prefill of the first "
-                    "2047 tokens each (GEMMs on MFMA, split-bf16 activations), then 64 greedy "
-                    "decode steps per sequence (BASELINE config 5)",
+                    "2047 tokens each (GEMMs on the int8 matrix cores: activations as per-row 24-bit "
+                    "fixed point in three int8 digits, exact integer sums), then 64 greedy decode "
+                    "steps per sequence (BASELINE config 5)",
         "prefill_ms": round(pm, 2),
         "prefill_tok_s": round(rows / (pm / 1e3), 1),
         "projection_tflop": round(proj / 1e12, 2),
         "attention_tflop_causal": round(attn / 1e12, 2),
         "projection_tflops": round(tf, 1),
         "mfma_peak_tflops_bf16": BF16_MFMA_PEAK_TFLOPS,
+        "mfma_peak_tops_int8": INT8_MFMA_PEAK_TOPS,
         "mfma_frac_useful": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
-        "mfma_frac_issued": round(2 * tf / BF16_MFMA_PEAK_TFLOPS, 4),
+        # three int8 MFMA operations per product (one per activation digit)
+        "mfma_frac_issued_int8": round(3 * tf / INT8_MFMA_PEAK_TOPS, 4),
+        "mfma_busy_counters": PREFILL_MFMA_BUSY_PROFILE,
         "decode_ms": round(dm, 2),
         "decode_tok_s": round(n_seq * decode_steps / (dm / 1e3), 1),
         "greedy_tokens_head": [[int(t) for t in row[:4]] for row in toks],
