@@ -43,17 +43,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define PF_LAUNCH_CHECK() SCRY_HIP(hipGetLastError()); return SCRY_OK
 
-// bf16 with round-to-nearest-even (NaN stays NaN)
-__device__ __forceinline__ u16 bf16_rn(float f) {
-    unsigned b = __float_as_uint(f);
-    if ((b & 0x7f800000u) == 0x7f800000u) return (u16)((b >> 16) | ((b & 0xffffu) ? 0x40u : 0u));
-    b += 0x7fffu + ((b >> 16) & 1u);
-    return (u16)(b >> 16);
-}
-__device__ __forceinline__ float bf16_f(u16 h) { return __uint_as_float((unsigned)h << 16); }
+// hi = bf16(x), lo = bf16(x - hi) with the hardware round-to-nearest-even
+// conversion: the bits of bf16_rn for every finite x (NaN stays NaN)
 __device__ __forceinline__ void split_bf16(float x, u16 &hi, u16 &lo) {
-    hi = bf16_rn(x);
-    lo = bf16_rn(x - bf16_f(hi));
+    const __bf16 h = (__bf16)x;
+    hi = __builtin_bit_cast(u16, h);
+    lo = __builtin_bit_cast(u16, (__bf16)(x - (float)h));
 }
 
 // ------------------------------------------------------------------ RMSNorm
@@ -1350,11 +1345,13 @@ __global__ __launch_bounds__(64 * MQW) void k_attn_mfma(PrefillAttn a, PrefillSe
 //     second, which is exactly the P values lane (l % 16, g) holds.
 constexpr int BQW = 8, BQ = 16 * BQW, BKT = 64;  // waves; query rows; keys per tile
 
+// bf16 hi / lo words of two values with the hardware round-to-nearest-even
+// conversion (the same bits as split_bf16 for finite inputs; NaN stays NaN)
 __device__ __forceinline__ unsigned pack_hl(float a, float b, bool lo_plane) {
-    u16 ha, la, hb, lb;
-    split_bf16(a, ha, la);
-    split_bf16(b, hb, lb);
-    return lo_plane ? ((unsigned)la | ((unsigned)lb << 16)) : ((unsigned)ha | ((unsigned)hb << 16));
+    const __bf16 ha = (__bf16)a, hb = (__bf16)b;
+    if (!lo_plane) return (unsigned)__builtin_bit_cast(u16, ha) | ((unsigned)__builtin_bit_cast(u16, hb) << 16);
+    const __bf16 la = (__bf16)(a - (float)ha), lb = (__bf16)(b - (float)hb);
+    return (unsigned)__builtin_bit_cast(u16, la) | ((unsigned)__builtin_bit_cast(u16, lb) << 16);
 }
 
 template <int HD>
@@ -1455,11 +1452,14 @@ __global__ __launch_bounds__(64 * BQW) void k_attn_bf3(PrefillAttn a, PrefillSeq
             tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
             const float mn = fmaxf(mrow, tmax);  // finite: key 0 is visible to every row
-            const float alpha = expf(mrow - mn);
+            // e^x as 2^(x log2 e) on the hardware exp: within ~1e-6 relative where
+            // it matters, below the 2^-17 of the P planes it feeds; the row sum
+            // is formed from the same values, so O / l stays consistent
+            const float alpha = __builtin_amdgcn_exp2f((mrow - mn) * 1.44269504f);
             float ps = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                p[e] = expf(p[e] - mn);
+                p[e] = __builtin_amdgcn_exp2f((p[e] - mn) * 1.44269504f);
                 ps += p[e];
             }
             ps += __shfl_xor(ps, 16);
