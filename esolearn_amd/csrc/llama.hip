@@ -1625,8 +1625,13 @@ int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_b
     int rc = dev_alloc((void **)&x, sizeof(float) * (size_t)m * k);
     if (!rc) rc = dev_alloc((void **)&y, sizeof(float) * (size_t)m * n);
     if (!rc) rc = launch_fill_f32(x, (size_t)m * k, 0.5f, s);
-    if (!rc && gemm) rc = dev_alloc((void **)&pl, sizeof(unsigned short) * 2 * (size_t)mp * ld);
-    if (!rc && gemm) rc = launch_fill_u32((unsigned *)pl, (size_t)mp * ld, 0u, s);
+    // the GEMM's input as matmul_i8_f32 forms it: digit planes (per-tensor,
+    // k <= 16384; the int8 matrix cores) or the bf16 hi / lo planes
+    const bool digits = gemm && quant_mode == SCRY_QUANT_PER_TENSOR && k <= 16384;
+    const size_t dstride = (size_t)mp * ld;
+    if (!rc && gemm) rc = dev_alloc((void **)&pl, digits ? 3 * dstride + sizeof(int) * (size_t)mp
+                                                         : sizeof(unsigned short) * 2 * dstride);
+    if (!rc && gemm) rc = launch_fill_u32((unsigned *)pl, digits ? (3 * dstride) / 4 + mp : dstride, 0u, s);
     void *sws = nullptr;
     if (!rc && skinny) rc = ctx_workspace(skinny_ws_bytes(m, k, n), &sws);
     for (int b = 0; b < n_bufs && !rc; b++) {
@@ -1665,15 +1670,24 @@ int bench_qgemv_dist_impl(int m, int k, int n, int quant_mode, int path, int n_b
             g.ldy = n;
             return launch_qgemv(EPI_STORE, g, s);
         }
-        SCRY_TRY(launch_split(x, k, m, k, pl, pl + (size_t)mp * ld, ld, s));
         PrefillGemm g;
         g.w = &W[i % n_bufs];
-        g.ahi = pl;
-        g.alo = pl + (size_t)mp * ld;
         g.lda = ld;
         g.M = m;
         g.c = y;
         g.ldc = n;
+        if (digits) {
+            signed char *dg = reinterpret_cast<signed char *>(pl);
+            int *de = reinterpret_cast<int *>(dg + 3 * dstride);
+            SCRY_TRY(launch_norm_digits(x, k, m, nullptr, k, 0.f, dg, dstride, de, ld, s));
+            g.ad = dg;
+            g.ae = de;
+            g.dstride = dstride;
+        } else {
+            SCRY_TRY(launch_split(x, k, m, k, pl, pl + dstride, ld, s));
+            g.ahi = pl;
+            g.alo = pl + dstride;
+        }
         return launch_gemm(PF_STORE, g, s);
     };
     for (int i = 0; i < warmup && !rc; i++) rc = launch(i);

@@ -410,8 +410,9 @@ int scry_hip_bench_qgemv(int m, int k, int n, int quant_mode, int n_bufs, int wa
  * (iters / group entries; iters a multiple of group), for the distribution.
  * path 0: the route matmul_i8_f32 takes (the skinny MFMA kernel for 3..16
  * activation rows when k % 8 == 0, k >= 256 and n >= 256, else the GEMV up to
- * 16 rows, the MFMA GEMM above); 1: the GEMV; 2: the MFMA GEMM (with its bf16
- * activation split); 3: the skinny MFMA kernel (with its split reduction).
+ * 16 rows, the MFMA GEMM above); 1: the GEMV; 2: the MFMA GEMM (with its
+ * input pass: int8 digit planes for per-tensor scales and k <= 16384, else the
+ * bf16 activation split); 3: the skinny MFMA kernel (with its split reduction).
  * quant_mode: per-tensor or block-32 scales. */
 int scry_hip_bench_qgemv_dist(int m, int k, int n, int quant_mode, int path, int n_bufs, int warmup, int iters,
                               int group, double *per_group_us, double *avg_us, double *bytes_per_launch);

@@ -58,3 +58,19 @@ def test_time_attention_bytes_and_errors(hip, tiny):
         tiny.time_attention(TINY["max_seq_len"] + 1, 4)
     with pytest.raises(hip.ScryHipError):
         tiny.time_attention(0, 4)
+
+
+@pytest.mark.parametrize("quant", ["per_tensor", "block32"])
+def test_bench_qgemv_dist_gemm_path(hip, quant):
+    """The micro-benchmark's GEMM path (2) and the automatic route above 16
+    rows form the GEMM input as matmul_i8_f32 does (digit planes for per-tensor
+    scales, bf16 planes for block-32) and return positive times and the
+    algorithmic weight bytes."""
+    import esolearn_amd.llama as EL
+    q = EL.QUANT_PER_TENSOR if quant == "per_tensor" else EL.QUANT_BLOCK32
+    print(f"[case] bench_qgemv_dist gemm path, {quant}", flush=True)
+    for path in (2, 0):
+        per, us, b = EL.bench_qgemv_dist(40, 1024, 768, q, path, n_bufs=2, warmup=2, iters=8, group=4)
+        print(f"[time] path {path}: {us:.2f} us, {b:.0f} B", flush=True)
+        assert us > 0 and (per > 0).all()
+        assert b >= 1024 * 768
