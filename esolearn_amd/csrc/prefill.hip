@@ -412,10 +412,11 @@ __device__ __forceinline__ void gemm_store(const GemmP &p, const f32x4 (&acc)[TM
 // caller's LDS is free (no loads in flight, every wave past its last read);
 // so (>= 2 BM (BN / 2 + 8) u16) holds the tile.  Rows past M are not written
 // (they stay zero); columns past N / 2 neither.
-// SiLU in f32 for outputs that become split-bf16 planes (hi + lo hold x to
-// 2^-17): the f32 evaluation is within a few 2^-24 of the reference's f64
-// one (cpu.rs:1119-1122), so the planes agree with the f64 path's to the
-// split's own bound, at a quarter of the cost.  Where the next GEMM reads
+// SiLU in f32 for outputs that become digit planes (each row to 2^-23 of
+// its largest value) or split-bf16 planes (hi + lo hold x to 2^-17): the f32
+// evaluation is within a few 2^-24 of the reference's f64 one
+// (cpu.rs:1119-1122), so the planes agree with the f64 path's to their own
+// bound, at a quarter of the cost.  Where the next GEMM reads
 // one bf16 plane (the bf16 model: the reference's bf16 cast of the f32
 // value), the f64 evaluation is kept, since one ulp of f32 can move a bf16
 // rounding.
