@@ -20,7 +20,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libscry_hip.so")
 ARCH = "gfx950"
 
-SOURCES = ["api.hip", "quant.hip", "qgemv.hip", "skinny.hip", "glue.hip", "ops.hip", "attn.hip", "prefill.hip", "safetensors.hip", "sample.hip", "noalloc.hip", "bf16.hip", "llama.hip", "init.cpp"]
+SOURCES = ["api.hip", "quant.hip", "qgemv.hip", "skinny.hip", "glue.hip", "ops.hip", "attn.hip", "batch.hip", "prefill.hip", "safetensors.hip", "sample.hip", "noalloc.hip", "bf16.hip", "llama.hip", "init.cpp"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 CFLAGS = [

@@ -53,7 +53,7 @@ __device__ __forceinline__ float group_sum(float v) {
 // LDS into one partial per (query head, split); with a single split that is
 // the attention row itself.
 template <int G, int NR, int NW>
-__global__ __launch_bounds__(64 * NW) void k_attn_decode(AttnArgs a) {
+__device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
     constexpr int NT = 64 * NW;
     constexpr int P = 64 / G;  // positions per load instruction
     constexpr int U = 12;      // load instructions per step
@@ -63,8 +63,8 @@ __global__ __launch_bounds__(64 * NW) void k_attn_decode(AttnArgs a) {
     float *s_o = sm;                    // [SLOTS][NR][hd]
     __shared__ float s_m[SLOTS][NR], s_l[SLOTS][NR];
     // block b: group (b % 8) + 8 * ((b / 8) / n_splits), split (b / 8) % n_splits
-    const int bi = blockIdx.x >> 3;
-    const int g = (blockIdx.x & 7) + 8 * (bi / a.n_splits), split = bi % a.n_splits;
+    const int bi = blk >> 3;
+    const int g = (blk & 7) + 8 * (bi / a.n_splits), split = bi % a.n_splits;
     if (g >= a.n_kv) return;  // padding of the last row of 8 groups
     const int nrep = a.n_heads / a.n_kv, hd = a.head_dim, kv_dim = a.n_kv * hd;
     const int L = a.fixed_len >= 0 ? a.fixed_len : a.state->cache_len + 1;
@@ -208,20 +208,54 @@ __global__ __launch_bounds__(64 * NW) void k_attn_decode(AttnArgs a) {
     if (tid == 0) a.merge_ctr[g] = 0;  // ready for the next launch on the stream
 }
 
+template <int G, int NR, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_decode(AttnArgs a) {
+    attn_body<G, NR, NW>(a, blockIdx.x);
+}
+
+// Several sequences, one per blockIdx.y, each with its own cache, length and
+// partial buffers (the rows of a batched decode step).  The linear block id is
+// blockIdx.x + gridDim.x * blockIdx.y with gridDim.x a multiple of 8, so the
+// XCD of a workgroup is still blockIdx.x % 8 and the exchange stays in one L2.
+template <int G, int NR, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_decode_seqs(AttnArgs a, AttnSeqs b) {
+    const int y = blockIdx.y;
+    const int qd = a.n_heads * a.head_dim;
+    AttnArgs s = a;
+    s.q = a.q + (size_t)y * qd;
+    s.k_cache = b.k[y] + (size_t)b.layer * b.ls[y];
+    s.v_cache = b.v[y] + (size_t)b.layer * b.ls[y];
+    s.part_o = a.part_o + (size_t)y * a.n_heads * a.n_splits * a.head_dim;
+    s.part_ml = a.part_ml + (size_t)y * a.n_heads * a.n_splits * 2;
+    s.merge_ctr = a.merge_ctr + (size_t)y * a.n_kv;
+    s.xa = a.xa + (size_t)y * qd;
+    s.fixed_len = b.pos[y] + 1;
+    attn_body<G, NR, NW>(s, blockIdx.x);
+}
+
+template <int G, int NR, int NW>
+void launch_k(const AttnArgs &a, const AttnSeqs *b, dim3 grid, size_t lds, hipStream_t s) {
+    if (b) {
+        grid.y = b->n;
+        hipLaunchKernelGGL((k_attn_decode_seqs<G, NR, NW>), grid, dim3(64 * NW), lds, s, a, *b);
+    } else {
+        hipLaunchKernelGGL((k_attn_decode<G, NR, NW>), grid, dim3(64 * NW), lds, s, a);
+    }
+}
+
 template <int G, int NW>
-int launch_gw(const AttnArgs &a, int nrep, hipStream_t s) {
+int launch_gw(const AttnArgs &a, const AttnSeqs *b, int nrep, hipStream_t s) {
     const int P = 64 / G;
     auto lds = [&](int nr) { return (size_t)NW * P * nr * a.head_dim * 4; };
     dim3 grid(8 * ((a.n_kv + 7) / 8) * a.n_splits);
-    dim3 block(64 * NW);
     if (nrep <= 1) {
-        hipLaunchKernelGGL((k_attn_decode<G, 1, NW>), grid, block, lds(1), s, a);
+        launch_k<G, 1, NW>(a, b, grid, lds(1), s);
     } else if (nrep <= 2) {
-        hipLaunchKernelGGL((k_attn_decode<G, 2, NW>), grid, block, lds(2), s, a);
+        launch_k<G, 2, NW>(a, b, grid, lds(2), s);
     } else if (nrep <= 4) {
-        hipLaunchKernelGGL((k_attn_decode<G, 4, NW>), grid, block, lds(4), s, a);
+        launch_k<G, 4, NW>(a, b, grid, lds(4), s);
     } else if (nrep <= 8) {
-        hipLaunchKernelGGL((k_attn_decode<G, 8, NW>), grid, block, lds(8), s, a);
+        launch_k<G, 8, NW>(a, b, grid, lds(8), s);
     } else {
         return set_error(SCRY_ERR_UNSUPPORTED, "attention: n_heads/n_kv = %d > 8", nrep);
     }
@@ -232,8 +266,8 @@ int launch_gw(const AttnArgs &a, int nrep, hipStream_t s) {
 // 16 waves when one workgroup covers a whole KV group's sequence (more loads
 // in flight per CU), 4 when the sequence is split over workgroups.
 template <int G>
-int launch_g(const AttnArgs &a, int nrep, hipStream_t s) {
-    return a.n_splits == 1 ? launch_gw<G, 16>(a, nrep, s) : launch_gw<G, 4>(a, nrep, s);
+int launch_g(const AttnArgs &a, const AttnSeqs *b, int nrep, hipStream_t s) {
+    return a.n_splits == 1 ? launch_gw<G, 16>(a, b, nrep, s) : launch_gw<G, 4>(a, b, nrep, s);
 }
 
 }  // namespace
@@ -251,7 +285,8 @@ int attn_pick_splits(int n_kv, int max_seq, int *n_splits, int *max_chunk) {
     return SCRY_OK;
 }
 
-int launch_attn_decode(const AttnArgs &a, hipStream_t s) {
+namespace {
+int launch_attn(const AttnArgs &a, const AttnSeqs *b, hipStream_t s) {
     if (!a.xa || (a.n_splits > 1 && (!a.merge_ctr || !a.part_o || !a.part_ml)))
         return set_error(SCRY_ERR_INVALID, "attention: missing output / partial / merge buffers");
     if (a.n_splits < 1 || a.n_splits > MAX_SPLITS)
@@ -263,13 +298,23 @@ int launch_attn_decode(const AttnArgs &a, hipStream_t s) {
                          a.head_dim);
     const int nrep = a.n_heads / a.n_kv;
     const int lanes = a.head_dim / 4;
-    if (lanes <= 1) return launch_g<1>(a, nrep, s);
-    if (lanes <= 2) return launch_g<2>(a, nrep, s);
-    if (lanes <= 4) return launch_g<4>(a, nrep, s);
-    if (lanes <= 8) return launch_g<8>(a, nrep, s);
-    if (lanes <= 16) return launch_g<16>(a, nrep, s);
-    if (lanes <= 32) return launch_g<32>(a, nrep, s);
-    return launch_g<64>(a, nrep, s);
+    if (lanes <= 1) return launch_g<1>(a, b, nrep, s);
+    if (lanes <= 2) return launch_g<2>(a, b, nrep, s);
+    if (lanes <= 4) return launch_g<4>(a, b, nrep, s);
+    if (lanes <= 8) return launch_g<8>(a, b, nrep, s);
+    if (lanes <= 16) return launch_g<16>(a, b, nrep, s);
+    if (lanes <= 32) return launch_g<32>(a, b, nrep, s);
+    return launch_g<64>(a, b, nrep, s);
+}
+}  // namespace
+
+int launch_attn_decode(const AttnArgs &a, hipStream_t s) { return launch_attn(a, nullptr, s); }
+
+int launch_attn_decode_seqs(const AttnArgs &a, const AttnSeqs &b, hipStream_t s) {
+    if (b.n < 1 || b.n > PF_MAX_SEQS || !b.pos || !a.q)
+        return set_error(SCRY_ERR_INVALID, "attention: %d sequences (1..%d) with positions and queries", b.n,
+                         PF_MAX_SEQS);
+    return launch_attn(a, &b, s);
 }
 
 }  // namespace scry

@@ -1,0 +1,105 @@
+// Glue of the batched decode step: n sequences, one token each, through the
+// same layer as the single-sequence step (llama.rs:744-763, 556-569), with
+// each projection as one skinny matmul over the n rows (skinny.hip) and the
+// attention of every sequence against its own cache in one launch (attn.hip).
+// The reference runs each sequence's decode separately; the per-sequence
+// arithmetic here is that step's:
+//   embedding row of the current token            (cpu.rs:485-498)
+//   RoPE of q and k from the cache's cos/sin table, q times 1/sqrt(hd) in a
+//   separate rounding, K / V rows appended at the position (llama.rs:371-410,
+//   cpu.rs:655-658, kv_cache.rs:99-118)
+//   next token = ordered argmax of the logits     (generate.rs:167-173)
+// Positions and tokens live in device memory, so a captured step replays.
+#include "internal.h"
+#include "kdev.h"
+
+namespace scry {
+namespace {
+
+using namespace dev;
+
+// x[y][i] = embed[tokens_y[pos_y]][i]
+__global__ __launch_bounds__(256) void k_bd_embed(const float *__restrict__ embed, int h, DecodeSeqs d,
+                                                  float *__restrict__ x) {
+    const int y = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= h) return;
+    const int64_t tok = d.tokens[y][d.pos[y]];
+    x[(size_t)y * h + i] = embed[(size_t)tok * h + i];
+}
+
+// Thread e of row y: q pair e (e < qd/2), k pair e - qd/2 (< kvd/2), or the v
+// pair after them.  Rotation in f32 without contraction, as the step's QKV
+// epilogue.
+__global__ __launch_bounds__(256) void k_bd_rope_kv(const float *__restrict__ qkv, int ldq, int qd, int kvd,
+                                                    int hd, float q_scale, DecodeSeqs d, AttnSeqs c,
+                                                    float *__restrict__ q_out) {
+    const int y = blockIdx.y, e = blockIdx.x * 256 + threadIdx.x;
+    const int nq = qd >> 1, nk = kvd >> 1;
+    if (e >= nq + 2 * nk) return;
+    const int pos = d.pos[y];
+    const float *row = qkv + (size_t)y * ldq;
+    const size_t at = (size_t)c.layer * c.ls[y] + (size_t)pos * kvd;
+    if (e >= nq + nk) {
+        const int j = 2 * (e - nq - nk);
+        *(float2 *)(c.v[y] + at + j) = *(const float2 *)(row + qd + kvd + j);
+        return;
+    }
+    const bool isq = e < nq;
+    const int j = isq ? 2 * e : 2 * (e - nq);
+    const float2 cs = d.rope[y][(size_t)pos * (hd >> 1) + ((j % hd) >> 1)];
+    const float2 xv = *(const float2 *)(row + (isq ? 0 : qd) + j);
+    const float r0 = __fsub_rn(__fmul_rn(xv.x, cs.x), __fmul_rn(xv.y, cs.y));
+    const float r1 = __fadd_rn(__fmul_rn(xv.x, cs.y), __fmul_rn(xv.y, cs.x));
+    if (isq) {
+        *(float2 *)(q_out + (size_t)y * qd + j) = make_float2(__fmul_rn(r0, q_scale), __fmul_rn(r1, q_scale));
+    } else {
+        *(float2 *)(c.k[y] + at + j) = make_float2(r0, r1);
+    }
+}
+
+// One workgroup per sequence: the ordered argmax of its logits row becomes
+// the token at pos + 1, and the position advances.
+__global__ __launch_bounds__(TPB) void k_bd_argmax(const float *__restrict__ logits, int V, DecodeSeqs d) {
+    __shared__ ArgAcc sh[TPB];
+    const int y = blockIdx.x;
+    const float *x = logits + (size_t)y * V;
+    const ArgAcc r = block_argmax_range(x, 0, V, sh);
+    const int tok = argmax_finish(r, x, V, sh);
+    if (threadIdx.x == 0) {
+        const int p = d.pos[y];
+        d.tokens[y][p + 1] = tok;
+        d.pos[y] = p + 1;
+    }
+}
+
+}  // namespace
+
+int launch_bd_embed(const float *embed, int h, const DecodeSeqs &d, float *x, hipStream_t s) {
+    if (d.n < 1 || d.n > PF_MAX_SEQS) return set_error(SCRY_ERR_INVALID, "batched decode: %d sequences", d.n);
+    hipLaunchKernelGGL(k_bd_embed, dim3((h + 255) / 256, d.n), dim3(256), 0, s, embed, h, d, x);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
+
+int launch_bd_rope_kv(const float *qkv, int ldq, int qd, int kvd, int hd, float q_scale, const DecodeSeqs &d,
+                      const AttnSeqs &c, float *q_out, hipStream_t s) {
+    if (d.n < 1 || d.n > PF_MAX_SEQS || c.n != d.n)
+        return set_error(SCRY_ERR_INVALID, "batched decode: %d sequences", d.n);
+    if (hd % 2 || qd % hd || kvd % hd || ldq % 2 || (uintptr_t)qkv % 8 || (uintptr_t)q_out % 8)
+        return set_error(SCRY_ERR_INVALID, "batched decode: bad head dims or alignment for rope_kv");
+    const int n = (qd >> 1) + kvd;
+    hipLaunchKernelGGL(k_bd_rope_kv, dim3((n + 255) / 256, d.n), dim3(256), 0, s, qkv, ldq, qd, kvd, hd, q_scale,
+                       d, c, q_out);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
+
+int launch_bd_argmax(const float *logits, int V, const DecodeSeqs &d, hipStream_t s) {
+    if (d.n < 1 || d.n > PF_MAX_SEQS || V < 1)
+        return set_error(SCRY_ERR_INVALID, "batched decode: %d sequences, vocab %d", d.n, V);
+    hipLaunchKernelGGL(k_bd_argmax, dim3(d.n), dim3(TPB), 0, s, logits, V, d);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
+
+}  // namespace scry

@@ -163,15 +163,17 @@ constexpr int GEMV_MAX_M = 16;
 // cores (k splits into a workspace of partial sums, then an ordered reduction)
 constexpr int SKINNY_MIN_M = 3;  // measured: the GEMV (two rows per weight pass) is faster at 2
 struct SkinnyMM {
-    const Packed *w = nullptr;  // plain int8 rows (not fused, not bf16)
+    const Packed *w = nullptr;  // int8 rows (not bf16): plain, or the fused gate/up pair with swiglu
     const float *x = nullptr;
     int ldx = 0, m = 0;
     const float *bias = nullptr;
+    const float *resid = nullptr;  // y = resid + x W, resid rows at stride ldy (may alias y)
+    int swiglu = 0;                // fused gate/up rows: y[r][j] = silu(gate_j) * up_j, j < w.n
     float *y = nullptr;
     int ldy = 0;
 };
 bool skinny_route(int m, int k, int n);
-size_t skinny_ws_bytes(int m, int k, int n);
+size_t skinny_ws_bytes(int m, int k, int n);  // n: packed weight rows (2 n for a fused pair)
 int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s);
 int launch_logits_finish(const GemvArgs &a, hipStream_t s);
 // sample_token on the device (sample.hip): logits [V] -> tokens[pos + 1] when
@@ -272,6 +274,34 @@ struct PrefillSeqs {  // per sequence: its KV cache and first position
     const float2 *rope[PF_MAX_SEQS];         // (cos, sin) [max_seq][hd/2]
     int p0[PF_MAX_SEQS];
 };
+// Batched decode attention: one query row per sequence, each against its own
+// cache (rows [0, pos[y]] of layer `layer`).  With it, the AttnArgs q, xa,
+// part_o, part_ml and merge_ctr hold n consecutive per-sequence blocks
+// ([q_dim], [q_dim], [n_heads][n_splits][hd], [n_heads][n_splits][2], [n_kv]);
+// k_cache, v_cache, state and fixed_len are unused.
+struct AttnSeqs {
+    float *k[PF_MAX_SEQS], *v[PF_MAX_SEQS];        // layer-0 K / V rows of each cache
+    size_t ls[PF_MAX_SEQS];                        // floats from one layer's K (V) to the next
+    const int *pos;                                // device [n]: rows cached before this token
+    int layer, n;
+};
+int launch_attn_decode_seqs(const AttnArgs &a, const AttnSeqs &b, hipStream_t s);
+
+// batch.hip -- glue of the batched decode step (n sequences, one token each)
+struct DecodeSeqs {
+    int64_t *tokens[PF_MAX_SEQS];     // each sequence's tokens: position p holds tokens[p]
+    const float2 *rope[PF_MAX_SEQS];  // each cache's (cos, sin) [max_seq][hd/2]
+    int *pos;                         // device [n]: the position being processed (= rows cached)
+    int n;
+};
+int launch_bd_embed(const float *embed, int h, const DecodeSeqs &d, float *x, hipStream_t s);
+// RoPE of q (then times q_scale, into q_out [n][qd]) and k; the K / V rows are
+// written at pos into layer c.layer of each cache
+int launch_bd_rope_kv(const float *qkv, int ldq, int qd, int kvd, int hd, float q_scale, const DecodeSeqs &d,
+                      const AttnSeqs &c, float *q_out, hipStream_t s);
+// ordered argmax of logits [n][V] per sequence -> tokens[pos + 1]; pos += 1
+int launch_bd_argmax(const float *logits, int V, const DecodeSeqs &d, hipStream_t s);
+
 // bf16 hi / lo planes of the K and V rows a prefill attends over, per
 // (sequence, KV head): [n_seq][n_kv][rows][hd] each (hi = bf16(x), lo =
 // bf16(x - hi)); null kh: the attention reads the f32 cache instead.

@@ -64,6 +64,20 @@ struct scry_llama_s {
     } pf;
     unsigned short *kvp = nullptr;  // the prefill attention's K / V planes (grown on demand)
     size_t kvp_n = 0;
+    // batched-decode workspace (allocated on first use, PF_MAX_SEQS rows):
+    // residual rows x, RMSNorm'd rows xn, qkv rows, RoPE'd and scaled q, the
+    // attention rows xa, SwiGLU rows act, logits; the skinny matmuls' split
+    // partials; per-sequence attention partials and arrival counters; the
+    // device positions
+    struct Batch {
+        float *x = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *xa = nullptr, *act = nullptr,
+              *logits = nullptr;
+        float *ws = nullptr;
+        size_t ws_bytes = 0;
+        float *ap_o = nullptr, *ap_ml = nullptr;
+        unsigned *ctr = nullptr;
+        int *pos = nullptr;
+    } bd;
     const float *norm_in(int l) const { return norms + (size_t)(2 * l) * h; }
     const float *norm_post(int l) const { return norms + (size_t)(2 * l + 1) * h; }
     const float *norm_final() const { return norms + (size_t)(2 * L) * h; }
@@ -245,6 +259,11 @@ void model_free(scry_llama m) {
     dev_free(m->pf.dg);
     dev_free(m->pf.de);
     dev_free(m->kvp);
+    for (float *p : {m->bd.x, m->bd.xn, m->bd.qkv, m->bd.q, m->bd.xa, m->bd.act, m->bd.logits, m->bd.ws,
+                     m->bd.ap_o, m->bd.ap_ml})
+        dev_free(p);
+    dev_free(m->bd.ctr);
+    dev_free(m->bd.pos);
     delete m;
 }
 
@@ -835,6 +854,186 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
     return SCRY_OK;
 }
 
+// Batched decode workspace, PF_MAX_SEQS rows (allocated on first use).
+int batch_ws(scry_llama m) {
+    auto &B = m->bd;
+    if (B.pos) return SCRY_OK;
+    const size_t R = PF_MAX_SEQS;
+    const auto &L0 = m->layers[0];
+    size_t ws = skinny_ws_bytes((int)R, m->h, m->lm.rows);
+    for (const Packed *w : {&L0.qkv, &L0.o, &L0.gu, &L0.down}) ws = std::max(ws, skinny_ws_bytes((int)R, w->k, w->rows));
+    const size_t nsp = 16;  // attention splits: attn_pick_splits picks at most 16
+    int rc = dev_alloc((void **)&B.x, sizeof(float) * R * m->h);
+    if (!rc) rc = dev_alloc((void **)&B.xn, sizeof(float) * R * m->h);
+    if (!rc) rc = dev_alloc((void **)&B.qkv, sizeof(float) * R * m->qkv_dim);
+    if (!rc) rc = dev_alloc((void **)&B.q, sizeof(float) * R * m->q_dim);
+    if (!rc) rc = dev_alloc((void **)&B.xa, sizeof(float) * R * m->q_dim);
+    if (!rc) rc = dev_alloc((void **)&B.act, sizeof(float) * R * m->ffn);
+    if (!rc) rc = dev_alloc((void **)&B.logits, sizeof(float) * R * m->V);
+    if (!rc) rc = dev_alloc((void **)&B.ws, ws);
+    if (!rc) rc = dev_alloc((void **)&B.ap_o, sizeof(float) * R * m->nh * nsp * m->hd);
+    if (!rc) rc = dev_alloc((void **)&B.ap_ml, sizeof(float) * R * m->nh * nsp * 2);
+    if (!rc) rc = dev_alloc((void **)&B.ctr, sizeof(unsigned) * R * m->nkv);
+    if (!rc) rc = launch_fill_u32(B.ctr, R * m->nkv, 0u, ctx().stream);  // the last split of a group resets it
+    if (!rc) rc = dev_alloc((void **)&B.pos, sizeof(int) * R);
+    if (rc) {
+        for (float *p : {B.x, B.xn, B.qkv, B.q, B.xa, B.act, B.logits, B.ws, B.ap_o, B.ap_ml}) dev_free(p);
+        dev_free(B.ctr);
+        dev_free(B.pos);
+        B = scry_llama_s::Batch{};
+        return rc;
+    }
+    B.ws_bytes = ws;
+    return SCRY_OK;
+}
+
+// One batched decode step (the layer of record_step for n sequences): each
+// projection is one skinny matmul over the n rows, RMSNorm writes f32 rows
+// (cpu.rs:574-599), attention covers every sequence's cache in one launch,
+// and the step ends with each sequence's next token and position advance.
+int record_batch_step(scry_llama m, const DecodeSeqs &d, AttnSeqs c, int n_splits, int max_chunk, hipStream_t s) {
+    auto &B = m->bd;
+    const int n = d.n;
+    auto norm = [&](const float *w) {
+        return launch_norm_split(B.x, m->h, n, 1, 0, w, m->h, m->eps, nullptr, nullptr, 0, B.xn, m->h, s);
+    };
+    auto mm = [&](const Packed &w, const float *x, int ldx, float *y, int ldy, const float *resid, int swiglu) {
+        SkinnyMM a;
+        a.w = &w;
+        a.x = x;
+        a.ldx = ldx;
+        a.m = n;
+        a.resid = resid;
+        a.swiglu = swiglu;
+        a.y = y;
+        a.ldy = ldy;
+        return launch_skinny(a, B.ws, B.ws_bytes, s);
+    };
+    AttnArgs at;
+    at.q = B.q;
+    at.part_o = B.ap_o;
+    at.part_ml = B.ap_ml;
+    at.merge_ctr = B.ctr;
+    at.xa = B.xa;
+    at.n_heads = m->nh;
+    at.n_kv = m->nkv;
+    at.head_dim = m->hd;
+    at.n_splits = n_splits;
+    at.max_chunk = max_chunk;
+    const float q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
+    SCRY_TRY(launch_bd_embed(m->embed, m->h, d, B.x, s));
+    for (int l = 0; l < m->L; l++) {
+        const auto &Ly = m->layers[l];
+        c.layer = l;
+        SCRY_TRY(norm(m->norm_in(l)));
+        SCRY_TRY(mm(Ly.qkv, B.xn, m->h, B.qkv, m->qkv_dim, nullptr, 0));
+        SCRY_TRY(launch_bd_rope_kv(B.qkv, m->qkv_dim, m->q_dim, m->kv_dim, m->hd, q_scale, d, c, B.q, s));
+        SCRY_TRY(launch_attn_decode_seqs(at, c, s));
+        SCRY_TRY(mm(Ly.o, B.xa, m->q_dim, B.x, m->h, B.x, 0));
+        SCRY_TRY(norm(m->norm_post(l)));
+        SCRY_TRY(mm(Ly.gu, B.xn, m->h, B.act, m->ffn, nullptr, 1));
+        SCRY_TRY(mm(Ly.down, B.act, m->ffn, B.x, m->h, B.x, 0));
+    }
+    SCRY_TRY(norm(m->norm_final()));
+    SCRY_TRY(mm(m->lm, B.xn, m->h, B.logits, m->V, nullptr, 0));
+    return launch_bd_argmax(B.logits, m->V, d, s);
+}
+
+// `steps` greedy decode steps of n sequences at once: tokens[i] is the token
+// at position cs[i]->seq_len (the last one fed), out_tokens [n][steps] the
+// tokens that follow; logits (host, may be null) receives [steps][n][V].  The
+// step is captured once per call and replayed (direct launches under
+// SCRY_HIP_NO_GRAPH).  ev (may be null): events recorded around the replays.
+int decode_batch_core(scry_llama m, scry_kv_cache *cs, int n, const int64_t *tokens, int steps,
+                      int64_t *out_tokens, float *logits, hipEvent_t *ev) {
+    if (n < 1 || n > PF_MAX_SEQS || steps < 1)
+        return set_error(SCRY_ERR_INVALID, "decode_batch: n_seq must be 1..%d and steps >= 1", PF_MAX_SEQS);
+    if (m->lm.bf16)
+        return set_error(SCRY_ERR_UNSUPPORTED, "decode_batch: int8 models only (bf16 weights decode one sequence)");
+    if (m->h % 8 || m->q_dim % 8 || m->ffn % 8)
+        return set_error(SCRY_ERR_UNSUPPORTED, "decode_batch: hidden, q and ffn sizes must be multiples of 8");
+    DecodeSeqs d{};
+    AttnSeqs c{};
+    int max_seq = 0;
+    std::vector<int> pos0(n);
+    for (int i = 0; i < n; i++) {
+        scry_kv_cache k = cs[i];
+        if (!k || k->m != m) return set_error(SCRY_ERR_INVALID, "decode_batch: cache %d does not belong to the model", i);
+        for (int j = 0; j < i; j++)
+            if (cs[j] == k) return set_error(SCRY_ERR_INVALID, "decode_batch: cache %d given twice", i);
+        if (k->seq_len + steps > k->max_seq)
+            return set_error(SCRY_ERR_RANGE, "decode_batch: %d + %d rows exceed the cache (%d)", k->seq_len, steps,
+                             k->max_seq);
+        d.tokens[i] = k->tokens;
+        d.rope[i] = k->rope_cs;
+        c.k[i] = k->K(0);
+        c.v[i] = k->Vc(0);
+        c.ls[i] = (size_t)2 * k->max_seq * m->kv_dim;
+        pos0[i] = k->seq_len;
+        max_seq = std::max(max_seq, k->max_seq);
+    }
+    SCRY_TRY(check_ids(m, tokens, n));
+    SCRY_TRY(batch_ws(m));
+    auto &B = m->bd;
+    d.pos = B.pos;
+    d.n = n;
+    c.pos = B.pos;
+    c.n = n;
+    int ns = 1, max_chunk = 16;
+    attn_pick_splits(m->nkv, max_seq, &ns, &max_chunk);
+    hipStream_t s = ctx().stream;
+    for (int i = 0; i < n; i++)
+        SCRY_HIP(hipMemcpyAsync(cs[i]->tokens + pos0[i], tokens + i, sizeof(int64_t), hipMemcpyHostToDevice, s));
+    SCRY_HIP(hipMemcpyAsync(B.pos, pos0.data(), sizeof(int) * n, hipMemcpyHostToDevice, s));
+    SCRY_TRY(sync_stream());
+    static const bool no_graph = std::getenv("SCRY_HIP_NO_GRAPH") != nullptr;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t gx = nullptr;
+    if (!no_graph) {
+        SCRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        const int rc = record_batch_step(m, d, c, ns, max_chunk, s);
+        const hipError_t e = hipStreamEndCapture(s, &g);
+        if (rc || e != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            if (rc) return rc;
+            return hip_fail(e, "decode_batch capture", __FILE__, __LINE__);
+        }
+        const hipError_t ei = hipGraphInstantiate(&gx, g, nullptr, nullptr, 0);
+        if (ei != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            return hip_fail(ei, "decode_batch instantiate", __FILE__, __LINE__);
+        }
+    }
+    int rc = SCRY_OK;
+    hipError_t e = hipSuccess;
+    if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) rc = hip_fail(e, "event", __FILE__, __LINE__);
+    for (int t = 0; t < steps && !rc; t++) {
+        if (gx) {
+            if ((e = hipGraphLaunch(gx, s)) != hipSuccess) rc = hip_fail(e, "decode_batch replay", __FILE__, __LINE__);
+        } else {
+            rc = record_batch_step(m, d, c, ns, max_chunk, s);
+        }
+        if (!rc && logits) {
+            e = hipMemcpyAsync(logits + (size_t)t * n * m->V, B.logits, sizeof(float) * (size_t)n * m->V,
+                               hipMemcpyDeviceToHost, s);
+            if (e != hipSuccess) rc = hip_fail(e, "logits readback", __FILE__, __LINE__);
+            if (!rc) rc = sync_stream();
+        }
+    }
+    if (!rc && ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) rc = hip_fail(e, "event", __FILE__, __LINE__);
+    if (!rc) rc = sync_stream();
+    for (int i = 0; i < n && !rc; i++) {
+        e = hipMemcpy(out_tokens + (size_t)i * steps, cs[i]->tokens + pos0[i] + 1, sizeof(int64_t) * steps,
+                      hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = hip_fail(e, "token readback", __FILE__, __LINE__);
+    }
+    if (gx) (void)hipGraphExecDestroy(gx);
+    if (g) (void)hipGraphDestroy(g);
+    if (rc) return rc;
+    for (int i = 0; i < n; i++) cs[i]->seq_len += steps;
+    return SCRY_OK;
+}
+
 // generate() (generate.rs:51-89): the prompt is fed token by token through
 // the decode step (or, with prefill, all but its last token through one
 // batched prefill), then tokens follow, greedy (samp == nullptr) or drawn by
@@ -1261,10 +1460,24 @@ int scry_hip_llama_prefill(scry_llama m, scry_kv_cache *caches, int n_seq, const
     return sync_stream();
 }
 
-int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq, int n_prompt, int decode_steps,
-                                 int64_t *out_tokens, double *prefill_ms, double *decode_ms) {
+int scry_hip_llama_decode_batch(scry_llama m, scry_kv_cache *caches, int n_seq, const int64_t *tokens, int steps,
+                                int64_t *out_tokens, float *logits) {
     API_LOCK;
     SCRY_REQUIRE_INIT();
+    if (!m || !caches || !tokens || !out_tokens) return set_error(SCRY_ERR_INVALID, "null argument");
+    return decode_batch_core(m, caches, n_seq, tokens, steps, out_tokens, logits, nullptr);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Prefill then decode, timed (scry_hip_llama_bench_prefill / _batch): the
+// decode steps run sequence after sequence through the single-sequence step,
+// or (batched) all sequences per step through the batched step, whose time
+// covers its graph replays (the capture, once per call, is outside).
+int bench_prefill_impl(scry_llama m, const int64_t *prompts, int n_seq, int n_prompt, int decode_steps,
+                       int batched, int64_t *out_tokens, double *prefill_ms, double *decode_ms) {
     if (!m || !prompts || !prefill_ms || !decode_ms || n_seq < 1 || n_seq > PF_MAX_SEQS || n_prompt < 2 ||
         decode_steps < 1)
         return set_error(SCRY_ERR_INVALID, "bench_prefill: bad arguments");
@@ -1275,13 +1488,14 @@ int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq
     for (int i = 0; i < n_seq; i++)
         std::memcpy(&toks[(size_t)i * pre], prompts + (size_t)i * n_prompt, sizeof(int64_t) * pre);
     hipStream_t s = ctx().stream;
-    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr, e3 = nullptr;
     int rc = SCRY_OK;
     for (int i = 0; i < n_seq && !rc; i++) rc = cache_new(m, n_prompt + decode_steps, &cs[i]);
     hipError_t e = hipSuccess;
     if (!rc) e = hipEventCreate(&e0);
     if (e == hipSuccess) e = hipEventCreate(&e1);
     if (e == hipSuccess) e = hipEventCreate(&e2);
+    if (e == hipSuccess) e = hipEventCreate(&e3);
     if (e != hipSuccess) rc = hip_fail(e, "event create", __FILE__, __LINE__);
     // untimed pass (kernel loading), then the caches restart empty
     if (!rc) rc = prefill_core(m, cs.data(), n_seq, toks.data(), pre, nullptr, nullptr);
@@ -1290,7 +1504,15 @@ int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq
     if (!rc && (e = hipEventRecord(e0, s)) != hipSuccess) rc = hip_fail(e, "event", __FILE__, __LINE__);
     if (!rc) rc = prefill_core(m, cs.data(), n_seq, toks.data(), pre, nullptr, nullptr);
     if (!rc && (e = hipEventRecord(e1, s)) != hipSuccess) rc = hip_fail(e, "event", __FILE__, __LINE__);
-    for (int i = 0; i < n_seq && !rc; i++) {
+    std::vector<int64_t> bt;
+    if (batched && !rc) {
+        std::vector<int64_t> last(n_seq);
+        for (int i = 0; i < n_seq; i++) last[i] = prompts[(size_t)i * n_prompt + pre];
+        bt.resize((size_t)n_seq * decode_steps);
+        hipEvent_t ev[2] = {e3, e2};  // around the replays
+        rc = decode_batch_core(m, cs.data(), n_seq, last.data(), decode_steps, bt.data(), nullptr, ev);
+    }
+    for (int i = 0; i < n_seq && !rc && !batched; i++) {
         scry_kv_cache c = cs[i];
         e = hipMemcpyAsync(c->tokens, prompts + (size_t)i * n_prompt, sizeof(int64_t) * n_prompt,
                            hipMemcpyHostToDevice, s);
@@ -1298,12 +1520,14 @@ int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq
         if (!rc) rc = set_state(c, pre, pre, n_prompt);
         for (int t = 0; t < decode_steps && !rc; t++) rc = run_step(c);
     }
-    if (!rc && (e = hipEventRecord(e2, s)) != hipSuccess) rc = hip_fail(e, "event", __FILE__, __LINE__);
+    if (!rc && !batched && (e = hipEventRecord(e2, s)) != hipSuccess) rc = hip_fail(e, "event", __FILE__, __LINE__);
     if (!rc) rc = sync_stream();
     float f1 = 0.f, f2 = 0.f;
-    if (!rc && (e = hipEventElapsedTime(&f1, e0, e1)) == hipSuccess) e = hipEventElapsedTime(&f2, e1, e2);
+    if (!rc && (e = hipEventElapsedTime(&f1, e0, e1)) == hipSuccess)
+        e = hipEventElapsedTime(&f2, batched ? e3 : e1, e2);
     if (!rc && e != hipSuccess) rc = hip_fail(e, "event time", __FILE__, __LINE__);
-    for (int i = 0; i < n_seq && !rc; i++) {
+    if (!rc && out_tokens && batched) std::memcpy(out_tokens, bt.data(), sizeof(int64_t) * bt.size());
+    for (int i = 0; i < n_seq && !rc && !batched; i++) {
         if (out_tokens) {
             e = hipMemcpy(out_tokens + (size_t)i * decode_steps, cs[i]->tokens + n_prompt,
                           sizeof(int64_t) * decode_steps, hipMemcpyDeviceToHost);
@@ -1313,11 +1537,31 @@ int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     if (e2) (void)hipEventDestroy(e2);
+    if (e3) (void)hipEventDestroy(e3);
     for (auto c : cs) cache_free(c);
     if (rc) return rc;
     *prefill_ms = f1;
     *decode_ms = f2;
     return SCRY_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq, int n_prompt, int decode_steps,
+                                 int64_t *out_tokens, double *prefill_ms, double *decode_ms) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    return bench_prefill_impl(m, prompts, n_seq, n_prompt, decode_steps, 0, out_tokens, prefill_ms, decode_ms);
+}
+
+int scry_hip_llama_bench_prefill_batch(scry_llama m, const int64_t *prompts, int n_seq, int n_prompt,
+                                       int decode_steps, int64_t *out_tokens, double *prefill_ms,
+                                       double *decode_ms) {
+    API_LOCK;
+    SCRY_REQUIRE_INIT();
+    return bench_prefill_impl(m, prompts, n_seq, n_prompt, decode_steps, 1, out_tokens, prefill_ms, decode_ms);
 }
 
 // ------------------------------------------------------------ measurement

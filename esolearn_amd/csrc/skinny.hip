@@ -241,12 +241,16 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
         }
 }
 
-// y[row][col] = scale * (sum of the splits' partials, in split order) (+ bias[col])
+// y[row][col] = scale * (sum of the splits' partials, in split order) (+ bias[col]);
+// RESID: y = resid[row][col] + that (resid rows at stride ldy, may alias y).
+template <bool RESID>
 __global__ __launch_bounds__(256) void k_skinny_reduce(const float *part, int n_split, int n_pad, int n,
-                                                       float scale, const float *bias, float *y, int ldy) {
+                                                       float scale, const float *bias, const float *resid,
+                                                       float *y, int ldy) {
     const int col = blockIdx.x * 256 + threadIdx.x, row = blockIdx.y;
     if (col >= n) return;
     const float bb = bias ? bias[col] : 0.f;  // requested with the partials
+    const float rv = RESID ? resid[(size_t)row * ldy + col] : 0.f;
     const float *p = part + (size_t)row * n_pad + col;
     const size_t st = (size_t)SK_ROWS * n_pad;
     float s = 0.f;
@@ -254,7 +258,26 @@ __global__ __launch_bounds__(256) void k_skinny_reduce(const float *part, int n_
     for (int i = 0; i < n_split; i++) s += p[i * st];
     float v = s * scale;
     if (bias) v = v + bb;
+    if (RESID) v = rv + v;  // llama.rs:556-569: x + o, x + down
     y[(size_t)row * ldy + col] = v;
+}
+
+// Fused gate/up rows (gate[2t], gate[2t+1], up[2t], up[2t+1] in groups of four):
+// y[row][j] = silu(sg * gate_j) * (su * up_j), j < n (cpu.rs:666-678).
+__global__ __launch_bounds__(256) void k_skinny_reduce_swiglu(const float *part, int n_split, int n_pad, int n,
+                                                              float sg, float su, float *y, int ldy) {
+    const int j = blockIdx.x * 256 + threadIdx.x, row = blockIdx.y;
+    if (j >= n) return;
+    const int cg = (j >> 1) * 4 + (j & 1);
+    const float *p = part + (size_t)row * n_pad + cg;
+    const size_t st = (size_t)SK_ROWS * n_pad;
+    float g = 0.f, u = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < n_split; i++) {
+        g += p[i * st];
+        u += p[i * st + 2];
+    }
+    y[(size_t)row * ldy + j] = silu_f(g * sg) * (u * su);
 }
 
 struct SkPlan {
@@ -293,16 +316,19 @@ size_t skinny_ws_bytes(int m, int k, int n) {
 
 int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s) {
     const Packed &w = *mm.w;
-    if (w.bf16 || w.fused || w.rows != w.n)
-        return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: plain int8 weight rows only");
+    if (w.bf16 || (w.fused ? (!mm.swiglu || w.rows != 2 * w.n || w.rows % 4 != 0) : (mm.swiglu || w.rows != w.n)))
+        return set_error(SCRY_ERR_UNSUPPORTED,
+                         "skinny matmul: int8 weight rows only (the fused gate/up pair with the swiglu output)");
+    if (mm.swiglu && (mm.bias || mm.resid))
+        return set_error(SCRY_ERR_INVALID, "skinny matmul: swiglu output takes no bias or residual");
     if (mm.m < 1 || mm.m > SK_ROWS || mm.ldx < w.k || mm.ldy < w.n)
         return set_error(SCRY_ERR_INVALID, "skinny matmul: %d rows (1..%d), ldx %d, ldy %d", mm.m, SK_ROWS,
                          mm.ldx, mm.ldy);
     if (w.k % 8 != 0) return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: k %% 8 != 0");
-    if (w.kp < w.k || (size_t)w.n * w.kp > 0x7fffffffu || (size_t)mm.m * mm.ldx * 4 > 0x7fffffffu)
+    if (w.kp < w.k || (size_t)w.rows * w.kp > 0x7fffffffu || (size_t)mm.m * mm.ldx * 4 > 0x7fffffffu)
         return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: operands above the 2 GiB buffer range");
-    const SkPlan p = plan(w.k, w.n);
-    if (ws_bytes < skinny_ws_bytes(mm.m, w.k, w.n))
+    const SkPlan p = plan(w.k, w.rows);
+    if (ws_bytes < skinny_ws_bytes(mm.m, w.k, w.rows))
         return set_error(SCRY_ERR_INVALID, "skinny matmul: workspace too small");
     SkArgs a;
     a.x = mm.x;
@@ -311,7 +337,7 @@ int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s)
     a.k = w.k;
     a.w = w.d;
     a.kp = w.kp;
-    a.n = w.n;
+    a.n = w.rows;
     a.s32 = w.s32;
     a.nb = w.nb;
     a.part = ws;
@@ -322,8 +348,17 @@ int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s)
     const int rc = p.ks == 8 ? (b32 ? launch_ks<8, true>(a, p.tiles, s) : launch_ks<8, false>(a, p.tiles, s))
                              : (b32 ? launch_ks<4, true>(a, p.tiles, s) : launch_ks<4, false>(a, p.tiles, s));
     if (rc) return rc;
-    hipLaunchKernelGGL(k_skinny_reduce, dim3((w.n + 255) / 256, mm.m), dim3(256), 0, s, ws, p.n_split, p.n_pad,
-                       w.n, b32 ? 1.0f : w.scale, mm.bias, mm.y, mm.ldy);
+    const dim3 grid((w.n + 255) / 256, mm.m);
+    if (mm.swiglu) {  // block-32 scales are applied per block by k_skinny
+        hipLaunchKernelGGL(k_skinny_reduce_swiglu, grid, dim3(256), 0, s, ws, p.n_split, p.n_pad, w.n,
+                           b32 ? 1.0f : w.scale, b32 ? 1.0f : w.scale2, mm.y, mm.ldy);
+    } else if (mm.resid) {
+        hipLaunchKernelGGL(k_skinny_reduce<true>, grid, dim3(256), 0, s, ws, p.n_split, p.n_pad, w.n,
+                           b32 ? 1.0f : w.scale, mm.bias, mm.resid, mm.y, mm.ldy);
+    } else {
+        hipLaunchKernelGGL(k_skinny_reduce<false>, grid, dim3(256), 0, s, ws, p.n_split, p.n_pad, w.n,
+                           b32 ? 1.0f : w.scale, mm.bias, mm.resid, mm.y, mm.ldy);
+    }
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }

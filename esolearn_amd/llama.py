@@ -224,15 +224,32 @@ class LlamaModel:
              lg.ctypes.data if lg is not None else None)
         return lg
 
-    def bench_prefill(self, prompts, decode_steps: int):
+    def decode_batch(self, caches, tokens, steps: int, want_logits: bool = False):
+        """Greedy decode of several sequences at once: tokens[i] is the token at
+        position caches[i].seq_len; returns the next tokens [n_seq, steps] (and
+        the logits [steps, n_seq, V] with want_logits)."""
+        t = np.ascontiguousarray(np.ravel(tokens), dtype=np.int64)
+        n_seq = t.size
+        if len(caches) != n_seq:
+            raise ValueError("one cache per sequence")
+        hs = (C.c_void_p * n_seq)(*[c.h for c in caches])
+        toks = np.empty((n_seq, steps), np.int64)
+        lg = np.empty((steps, n_seq, self.cfg.vocab_size), np.float32) if want_logits else None
+        call("scry_hip_llama_decode_batch", self.h, hs, n_seq, t.ctypes.data, steps, toks.ctypes.data,
+             lg.ctypes.data if lg is not None else None)
+        return (toks, lg) if want_logits else toks
+
+    def bench_prefill(self, prompts, decode_steps: int, batched: bool = False):
         """(prefill ms, decode ms, tokens [n_seq, decode_steps]) for prompts
-        [n_seq, n_prompt]: batched prefill, then greedy decode per sequence."""
+        [n_seq, n_prompt]: batched prefill, then greedy decode per sequence in
+        turn, or (batched) of all sequences per step."""
         p = np.ascontiguousarray(prompts, dtype=np.int64)
         n_seq, n_prompt = p.shape
         toks = np.empty((n_seq, decode_steps), np.int64)
         pm, dm = C.c_double(), C.c_double()
-        call("scry_hip_llama_bench_prefill", self.h, p.ctypes.data, n_seq, n_prompt, decode_steps,
-             toks.ctypes.data, C.byref(pm), C.byref(dm))
+        fn = "scry_hip_llama_bench_prefill_batch" if batched else "scry_hip_llama_bench_prefill"
+        call(fn, self.h, p.ctypes.data, n_seq, n_prompt, decode_steps, toks.ctypes.data, C.byref(pm),
+             C.byref(dm))
         return pm.value, dm.value, toks
 
     def bench_decode(self, prompt, warmup: int, steps: int):

@@ -368,6 +368,21 @@ int scry_hip_llama_forward(scry_llama m, const int64_t *tokens, int seq, float *
 int scry_hip_llama_prefill(scry_llama m, scry_kv_cache *caches, int n_seq, const int64_t *tokens,
                            int seq, float *last_logits);
 
+/* Batched greedy decode.  The reference has no counterpart: it decodes one
+ * sequence at a time (generate.rs:51-89, llama.rs:744-763), and each
+ * sequence's step here computes that step.  n_seq sequences advance `steps`
+ * tokens together; every projection reads its weights once per step for all
+ * of them.  tokens[i] (host) is the token at position caches[i]->seq_len (the
+ * last one fed: after a prefill of all but the last prompt token, that
+ * token).  out_tokens (host, [n_seq][steps]) receives the argmax tokens that
+ * follow (generate.rs:167-173); logits (host, may be NULL) [steps][n_seq][V]
+ * every step's logits.  K/V rows seq_len .. seq_len + steps - 1 are appended
+ * (seq_len advances by steps).  1 <= n_seq <= 16, distinct caches, int8
+ * models (per-tensor or block-32 scales; a bf16 model returns
+ * SCRY_ERR_UNSUPPORTED), hidden, q and ffn sizes multiples of 8. */
+int scry_hip_llama_decode_batch(scry_llama m, scry_kv_cache *caches, int n_seq, const int64_t *tokens,
+                                int steps, int64_t *out_tokens, float *logits);
+
 /* ------------------------------------------------ measurement helpers */
 /* Decode-step session for benchmarks: binds a model and cache, feeds the
  * prompt, then runs `steps` greedy decode steps as graph replays.  The time of
@@ -400,6 +415,12 @@ int scry_hip_llama_time_attention(scry_llama m, int ctx_len, int iters, double *
 int scry_hip_llama_bench_prefill(scry_llama m, const int64_t *prompts, int n_seq, int n_prompt,
                                  int decode_steps, int64_t *out_tokens, double *prefill_ms,
                                  double *decode_ms);
+/* The same with the decode steps of all sequences batched
+ * (scry_hip_llama_decode_batch); *decode_ms covers the step replays (the
+ * step's graph capture, once per call, is outside). */
+int scry_hip_llama_bench_prefill_batch(scry_llama m, const int64_t *prompts, int n_seq, int n_prompt,
+                                       int decode_steps, int64_t *out_tokens, double *prefill_ms,
+                                       double *decode_ms);
 /* Average device time of matmul_i8_f32 at m,k,n rotating over `n_bufs`
  * distinct weight copies (defeats the 256 MB Infinity Cache). */
 int scry_hip_bench_qgemv(int m, int k, int n, int quant_mode, int n_bufs, int warmup, int iters,
