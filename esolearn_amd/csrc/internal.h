@@ -174,6 +174,29 @@ struct SkinnyMM {
 };
 bool skinny_route(int m, int k, int n);
 size_t skinny_ws_bytes(int m, int k, int n);  // n: packed weight rows (2 n for a fused pair)
+// The fused form (the batched decode step's projections): the RMSNorm rides
+// in the activation staging, and one workgroup per 128-column tile adds the
+// k splits' partials in split order and applies the epilogue.
+enum { SKE_STORE = 1, SKE_RESID = 2, SKE_SWIGLU = 3, SKE_LOGITS = 4 };
+struct SkinnyFused {
+    const Packed *w = nullptr;
+    const float *x = nullptr;
+    int ldx = 0, m = 0;
+    // RMSNorm of x (rmsnorm.rs), applied as rstd * (W (x * g)); rstd from the
+    // per-row partial sums of squares of x [m][n_ss_in] (f64, 1..64 of them)
+    const float *norm_w = nullptr;
+    const double *ss_in = nullptr;
+    int n_ss_in = 0;
+    float eps = 1e-5f;
+    int epi = SKE_STORE;  // STORE, RESID (y += x W), SWIGLU (fused gate/up rows), LOGITS
+    float *y = nullptr;
+    int ldy = 0;
+    double *ss_out = nullptr;  // RESID (may be null): [m][skinny_tiles(w)] partial sums of squares of y
+    float *pv = nullptr;       // LOGITS: [m][skinny_tiles(w)] ordered argmax partials
+    int *pi = nullptr, *pn = nullptr;
+};
+int skinny_tiles(const Packed &w);  // 128-row tiles of the packed rows
+int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStream_t s);
 int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s);
 int launch_logits_finish(const GemvArgs &a, hipStream_t s);
 // sample_token on the device (sample.hip): logits [V] -> tokens[pos + 1] when
@@ -294,13 +317,17 @@ struct DecodeSeqs {
     int *pos;                         // device [n]: the position being processed (= rows cached)
     int n;
 };
-int launch_bd_embed(const float *embed, int h, const DecodeSeqs &d, float *x, hipStream_t s);
+// x [n][h] = the embedding rows of the current tokens; ss [n][ceil(h / 128)]
+// their partial sums of squares (f64) for the first RMSNorm
+int launch_bd_embed(const float *embed, int h, const DecodeSeqs &d, float *x, double *ss, hipStream_t s);
 // RoPE of q (then times q_scale, into q_out [n][qd]) and k; the K / V rows are
 // written at pos into layer c.layer of each cache
 int launch_bd_rope_kv(const float *qkv, int ldq, int qd, int kvd, int hd, float q_scale, const DecodeSeqs &d,
                       const AttnSeqs &c, float *q_out, hipStream_t s);
-// ordered argmax of logits [n][V] per sequence -> tokens[pos + 1]; pos += 1
-int launch_bd_argmax(const float *logits, int V, const DecodeSeqs &d, hipStream_t s);
+// ordered argmax of logits [n][V] per sequence (from the np per-row argmax
+// partials of the LM head's fused skinny launch) -> tokens[pos + 1]; pos += 1
+int launch_bd_argmax(const float *logits, int V, const float *pv, const int *pi, const int *pn, int np,
+                     const DecodeSeqs &d, hipStream_t s);
 
 // bf16 hi / lo planes of the K and V rows a prefill attends over, per
 // (sequence, KV head): [n_seq][n_kv][rows][hd] each (hi = bf16(x), lo =

@@ -65,15 +65,18 @@ struct scry_llama_s {
     unsigned short *kvp = nullptr;  // the prefill attention's K / V planes (grown on demand)
     size_t kvp_n = 0;
     // batched-decode workspace (allocated on first use, PF_MAX_SEQS rows):
-    // residual rows x, RMSNorm'd rows xn, qkv rows, RoPE'd and scaled q, the
-    // attention rows xa, SwiGLU rows act, logits; the skinny matmuls' split
-    // partials; per-sequence attention partials and arrival counters; the
-    // device positions
+    // residual rows x, qkv rows, RoPE'd and scaled q, the attention rows xa,
+    // SwiGLU rows act, logits; the residual rows' partial sums of squares ss
+    // [rows][64] (the next RMSNorm's input); the skinny matmuls' split
+    // partials; the LM head's argmax partials; per-sequence
+    // attention partials and arrival counters; the device positions
     struct Batch {
-        float *x = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *xa = nullptr, *act = nullptr,
-              *logits = nullptr;
+        float *x = nullptr, *qkv = nullptr, *q = nullptr, *xa = nullptr, *act = nullptr, *logits = nullptr;
+        double *ss = nullptr;
         float *ws = nullptr;
         size_t ws_bytes = 0;
+        float *pv = nullptr;
+        int *pi = nullptr, *pn = nullptr;
         float *ap_o = nullptr, *ap_ml = nullptr;
         unsigned *ctr = nullptr;
         int *pos = nullptr;
@@ -259,11 +262,10 @@ void model_free(scry_llama m) {
     dev_free(m->pf.dg);
     dev_free(m->pf.de);
     dev_free(m->kvp);
-    for (float *p : {m->bd.x, m->bd.xn, m->bd.qkv, m->bd.q, m->bd.xa, m->bd.act, m->bd.logits, m->bd.ws,
-                     m->bd.ap_o, m->bd.ap_ml})
+    for (void *p : {(void *)m->bd.x, (void *)m->bd.qkv, (void *)m->bd.q, (void *)m->bd.xa, (void *)m->bd.act,
+                    (void *)m->bd.logits, (void *)m->bd.ss, (void *)m->bd.ws, (void *)m->bd.pv, (void *)m->bd.pi, (void *)m->bd.pn, (void *)m->bd.ap_o, (void *)m->bd.ap_ml,
+                    (void *)m->bd.ctr, (void *)m->bd.pos})
         dev_free(p);
-    dev_free(m->bd.ctr);
-    dev_free(m->bd.pos);
     delete m;
 }
 
@@ -862,24 +864,29 @@ int batch_ws(scry_llama m) {
     const auto &L0 = m->layers[0];
     size_t ws = skinny_ws_bytes((int)R, m->h, m->lm.rows);
     for (const Packed *w : {&L0.qkv, &L0.o, &L0.gu, &L0.down}) ws = std::max(ws, skinny_ws_bytes((int)R, w->k, w->rows));
+    const int lt = skinny_tiles(m->lm);
     const size_t nsp = 16;  // attention splits: attn_pick_splits picks at most 16
     int rc = dev_alloc((void **)&B.x, sizeof(float) * R * m->h);
-    if (!rc) rc = dev_alloc((void **)&B.xn, sizeof(float) * R * m->h);
     if (!rc) rc = dev_alloc((void **)&B.qkv, sizeof(float) * R * m->qkv_dim);
     if (!rc) rc = dev_alloc((void **)&B.q, sizeof(float) * R * m->q_dim);
     if (!rc) rc = dev_alloc((void **)&B.xa, sizeof(float) * R * m->q_dim);
     if (!rc) rc = dev_alloc((void **)&B.act, sizeof(float) * R * m->ffn);
     if (!rc) rc = dev_alloc((void **)&B.logits, sizeof(float) * R * m->V);
+    if (!rc) rc = dev_alloc((void **)&B.ss, sizeof(double) * R * 64);
     if (!rc) rc = dev_alloc((void **)&B.ws, ws);
+    if (!rc) rc = dev_alloc((void **)&B.pv, sizeof(float) * R * lt);
+    if (!rc) rc = dev_alloc((void **)&B.pi, sizeof(int) * R * lt);
+    if (!rc) rc = dev_alloc((void **)&B.pn, sizeof(int) * R * lt);
     if (!rc) rc = dev_alloc((void **)&B.ap_o, sizeof(float) * R * m->nh * nsp * m->hd);
     if (!rc) rc = dev_alloc((void **)&B.ap_ml, sizeof(float) * R * m->nh * nsp * 2);
     if (!rc) rc = dev_alloc((void **)&B.ctr, sizeof(unsigned) * R * m->nkv);
     if (!rc) rc = launch_fill_u32(B.ctr, R * m->nkv, 0u, ctx().stream);  // the last split of a group resets it
     if (!rc) rc = dev_alloc((void **)&B.pos, sizeof(int) * R);
     if (rc) {
-        for (float *p : {B.x, B.xn, B.qkv, B.q, B.xa, B.act, B.logits, B.ws, B.ap_o, B.ap_ml}) dev_free(p);
-        dev_free(B.ctr);
-        dev_free(B.pos);
+        for (void *p : {(void *)B.x, (void *)B.qkv, (void *)B.q, (void *)B.xa, (void *)B.act, (void *)B.logits,
+                        (void *)B.ss, (void *)B.ws, (void *)B.pv, (void *)B.pi, (void *)B.pn,
+                        (void *)B.ap_o, (void *)B.ap_ml, (void *)B.ctr, (void *)B.pos})
+            dev_free(p);
         B = scry_llama_s::Batch{};
         return rc;
     }
@@ -888,26 +895,33 @@ int batch_ws(scry_llama m) {
 }
 
 // One batched decode step (the layer of record_step for n sequences): each
-// projection is one skinny matmul over the n rows, RMSNorm writes f32 rows
-// (cpu.rs:574-599), attention covers every sequence's cache in one launch,
-// and the step ends with each sequence's next token and position advance.
+// projection is one fused skinny matmul over the n rows (the RMSNorms ride in
+// them, from the residual rows' partial sums of squares, as in the
+// single-sequence step), attention covers every sequence's cache in one
+// launch, and the step ends with each sequence's next token and position
+// advance.
 int record_batch_step(scry_llama m, const DecodeSeqs &d, AttnSeqs c, int n_splits, int max_chunk, hipStream_t s) {
     auto &B = m->bd;
     const int n = d.n;
-    auto norm = [&](const float *w) {
-        return launch_norm_split(B.x, m->h, n, 1, 0, w, m->h, m->eps, nullptr, nullptr, 0, B.xn, m->h, s);
-    };
-    auto mm = [&](const Packed &w, const float *x, int ldx, float *y, int ldy, const float *resid, int swiglu) {
-        SkinnyMM a;
-        a.w = &w;
-        a.x = x;
-        a.ldx = ldx;
-        a.m = n;
-        a.resid = resid;
-        a.swiglu = swiglu;
-        a.y = y;
-        a.ldy = ldy;
-        return launch_skinny(a, B.ws, B.ws_bytes, s);
+    const int n_ss = (m->h + 127) / 128;  // partial sums per residual row (128-column tiles)
+    auto mm = [&](const Packed &w, const float *x, int ldx, const float *norm_w, int epi, float *y, int ldy) {
+        SkinnyFused f;
+        f.w = &w;
+        f.x = x;
+        f.ldx = ldx;
+        f.m = n;
+        f.norm_w = norm_w;
+        f.ss_in = B.ss;
+        f.n_ss_in = n_ss;
+        f.eps = m->eps;
+        f.epi = epi;
+        f.y = y;
+        f.ldy = ldy;
+        if (epi == SKE_RESID) f.ss_out = B.ss;
+        f.pv = B.pv;
+        f.pi = B.pi;
+        f.pn = B.pn;
+        return launch_skinny_fused(f, B.ws, B.ws_bytes, s);
     };
     AttnArgs at;
     at.q = B.q;
@@ -921,22 +935,19 @@ int record_batch_step(scry_llama m, const DecodeSeqs &d, AttnSeqs c, int n_split
     at.n_splits = n_splits;
     at.max_chunk = max_chunk;
     const float q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
-    SCRY_TRY(launch_bd_embed(m->embed, m->h, d, B.x, s));
+    SCRY_TRY(launch_bd_embed(m->embed, m->h, d, B.x, B.ss, s));
     for (int l = 0; l < m->L; l++) {
         const auto &Ly = m->layers[l];
         c.layer = l;
-        SCRY_TRY(norm(m->norm_in(l)));
-        SCRY_TRY(mm(Ly.qkv, B.xn, m->h, B.qkv, m->qkv_dim, nullptr, 0));
+        SCRY_TRY(mm(Ly.qkv, B.x, m->h, m->norm_in(l), SKE_STORE, B.qkv, m->qkv_dim));
         SCRY_TRY(launch_bd_rope_kv(B.qkv, m->qkv_dim, m->q_dim, m->kv_dim, m->hd, q_scale, d, c, B.q, s));
         SCRY_TRY(launch_attn_decode_seqs(at, c, s));
-        SCRY_TRY(mm(Ly.o, B.xa, m->q_dim, B.x, m->h, B.x, 0));
-        SCRY_TRY(norm(m->norm_post(l)));
-        SCRY_TRY(mm(Ly.gu, B.xn, m->h, B.act, m->ffn, nullptr, 1));
-        SCRY_TRY(mm(Ly.down, B.act, m->ffn, B.x, m->h, B.x, 0));
+        SCRY_TRY(mm(Ly.o, B.xa, m->q_dim, nullptr, SKE_RESID, B.x, m->h));
+        SCRY_TRY(mm(Ly.gu, B.x, m->h, m->norm_post(l), SKE_SWIGLU, B.act, m->ffn));
+        SCRY_TRY(mm(Ly.down, B.act, m->ffn, nullptr, SKE_RESID, B.x, m->h));
     }
-    SCRY_TRY(norm(m->norm_final()));
-    SCRY_TRY(mm(m->lm, B.xn, m->h, B.logits, m->V, nullptr, 0));
-    return launch_bd_argmax(B.logits, m->V, d, s);
+    SCRY_TRY(mm(m->lm, B.x, m->h, m->norm_final(), SKE_LOGITS, B.logits, m->V));
+    return launch_bd_argmax(B.logits, m->V, B.pv, B.pi, B.pn, skinny_tiles(m->lm), d, s);
 }
 
 // `steps` greedy decode steps of n sequences at once: tokens[i] is the token
@@ -950,8 +961,9 @@ int decode_batch_core(scry_llama m, scry_kv_cache *cs, int n, const int64_t *tok
         return set_error(SCRY_ERR_INVALID, "decode_batch: n_seq must be 1..%d and steps >= 1", PF_MAX_SEQS);
     if (m->lm.bf16)
         return set_error(SCRY_ERR_UNSUPPORTED, "decode_batch: int8 models only (bf16 weights decode one sequence)");
-    if (m->h % 8 || m->q_dim % 8 || m->ffn % 8)
-        return set_error(SCRY_ERR_UNSUPPORTED, "decode_batch: hidden, q and ffn sizes must be multiples of 8");
+    if (m->h % 8 || m->q_dim % 8 || m->ffn % 8 || m->h > 64 * 128)
+        return set_error(SCRY_ERR_UNSUPPORTED, "decode_batch: hidden, q and ffn sizes must be multiples of 8 "
+                         "(hidden at most 8192)");
     DecodeSeqs d{};
     AttnSeqs c{};
     int max_seq = 0;

@@ -20,6 +20,15 @@
 // MFMA blocks) covers 128 columns over KS 64-wide k blocks; the k splits of a
 // column tile write partial sums, which k_skinny_reduce adds in split order
 // (deterministic), then applies the scale and the bias.
+//
+// Fused form (the batched decode step's projections): the k splits write
+// their partials as above, and k_skinny_epi (one workgroup per column tile)
+// adds them in split order and applies the epilogue: store, residual add
+// (plus per-row partial sums of squares of the result for the next RMSNorm),
+// SwiGLU of the fused gate/up rows, or logits (plus per-row ordered argmax
+// partials).  NORM: the activation is RMSNorm(x) applied as
+// rstd * (W (x * g)) (rmsnorm.rs, cpu.rs:574-599): x * g is staged, and rstd
+// (f64, from the producer's partial sums of squares) scales the sums.
 #include "internal.h"
 #include "kdev.h"
 
@@ -44,7 +53,20 @@ struct SkArgs {
     int nb;
     float *part;  // [n_split][16][n_pad] partial sums
     int n_pad, n_split, kblocks;
+    // fused form
+    const float *g;       // NORM: RMSNorm weight [k]
+    const double *ss_in;  // NORM: per-row partial sums of squares of x [m][n_ss_in]
+    int n_ss_in;
+    float eps;
+    int tiles, n_out;
+    float scale, scale2;
+    float *y;  // output rows [m][ldy]; SKE_RESID: also the residual (in place)
+    int ldy;
+    double *ss_out;  // SKE_RESID: per-row partial sums of squares of y [m][tiles]
+    float *pv;       // SKE_LOGITS: per-row ordered argmax partials [m][tiles]
+    int *pi, *pn;
 };
+
 
 // x = h + m + l in truncated bf16 planes (bits of each plane's bf16)
 __device__ __forceinline__ void split3(float x, unsigned &h, unsigned &mi, unsigned &lo) {
@@ -86,7 +108,9 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 //               LDS read per lane and column block feeds both halves);
 //   block-32:   lane group g, half f -> k = 64 kb + 32 f + 8 g + e (each half is
 //               one 32-wide scale block).
-// LDS: A planes as 16-byte fragments [kb][plane][half][lane]; per wave a
+// LDS: A planes as 16-byte fragments [kb][plane][half][lane group][row] (rows
+// below MRT only: with at most 4 activation rows the other 12 MFMA rows are
+// zero registers, a quarter of the LDS and so more workgroups per CU); per wave a
 // [32 rows][144 B] weight tile for two 64-wide blocks (rows padded by 16 bytes
 // so the 16-byte fragment reads of 16 rows hit distinct banks) and, for
 // block-32, the wave's scales [32 columns][2 KS blocks].
@@ -97,10 +121,13 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 // (16 rows x 64 bytes per instruction) would split every line in two.
 constexpr int SK_WROW = 144;                 // bytes per weight row in the LDS tile
 constexpr int SK_WTILE = 32 * SK_WROW;       // bytes per wave
-template <int KS, bool B32>
+// MRT: activation rows kept in LDS (4: at most 4 rows; the MFMA's other A
+// rows are zero registers; 16: all of them).
+template <int KS, bool B32, bool NORM, int MRT>
 __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
     static_assert(KS % 2 == 0, "weights come in 128-byte segments of two blocks");
-    __shared__ u32x4 s_a[KS * 3 * 2 * 64];
+    static_assert(MRT == 4 || MRT == 16, "4 or 16 activation rows");
+    __shared__ u32x4 s_a[KS * 3 * 2 * 4 * MRT];
     __shared__ __attribute__((aligned(16))) unsigned char s_w[4 * SK_WTILE];
     __shared__ float s_sc[B32 ? 4 * 32 * 2 * KS : 1];
     const int split = blockIdx.x % a.n_split, tile = blockIdx.x / a.n_split;
@@ -111,16 +138,24 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
 
     // ---- 1. activation loads: unit u = (kb, row, q8) holds x[row][k0 + 64 kb + 8 q8 + 0..7];
     // eight consecutive threads read 256 contiguous bytes of one row
-    constexpr int UPT = KS * SK_ROWS * 8 / SK_NT;
+    constexpr int NU = KS * MRT * 8, UPT = (NU + SK_NT - 1) / SK_NT;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, ((size_t)(a.m - 1) * a.ldx + a.k) * 4);
     float4 xv[UPT][2];
+    float4 gv[NORM ? UPT : 1][2];
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(NORM ? a.g : a.x, NORM ? (size_t)a.k * 4 : 0);
 #pragma unroll
     for (int i = 0; i < UPT; i++) {
-        const int u = tid + SK_NT * i, kb = u >> 7, row = (u >> 3) & 15, q8 = u & 7;
+        const int u = tid + SK_NT * i, kb = u / (8 * MRT), row = (u >> 3) % MRT, q8 = u & 7;
         const int kk = k0 + kb * 64 + q8 * 8;
-        const unsigned off = (row < a.m && kb < nkb && kk < a.k) ? (unsigned)(row * a.ldx + kk) * 4 : 0x80000000u;
+        const bool in = (NU % SK_NT == 0 || u < NU) && row < a.m && kb < nkb && kk < a.k;
+        const unsigned off = in ? (unsigned)(row * a.ldx + kk) * 4 : 0x80000000u;
         xv[i][0] = bload16f(xr, off);
         xv[i][1] = bload16f(xr, off + 16);
+        if constexpr (NORM) {
+            const unsigned og = in ? (unsigned)kk * 4 : 0x80000000u;
+            gv[i][0] = bload16f(gr, og);
+            gv[i][1] = bload16f(gr, og + 16);
+        }
     }
 
     // ---- 2. the wave's 32 weight rows over this split, all requested now
@@ -147,10 +182,17 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
     // ---- 3. stage the activation planes (and the scales)
 #pragma unroll
     for (int i = 0; i < UPT; i++) {
-        const int u = tid + SK_NT * i, kb = u >> 7, row = (u >> 3) & 15, q8 = u & 7;
+        const int u = tid + SK_NT * i, kb = u / (8 * MRT), row = (u >> 3) % MRT, q8 = u & 7;
+        if (NU % SK_NT != 0 && u >= NU) break;
         const int kk = k0 + kb * 64 + q8 * 8;
         float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
                       xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+        if constexpr (NORM) {
+            const float gg8[8] = {gv[i][0].x, gv[i][0].y, gv[i][0].z, gv[i][0].w,
+                                  gv[i][1].x, gv[i][1].y, gv[i][1].z, gv[i][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = __fmul_rn(v[e], gg8[e]);
+        }
         unsigned pl[3][8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -158,7 +200,6 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
             split3(v[e], pl[0][e], pl[1][e], pl[2][e]);
         }
         const int gg = B32 ? (q8 & 3) : (q8 >> 1), f = B32 ? (q8 >> 2) : (q8 & 1);
-        const int l = row + 16 * gg;
 #pragma unroll
         for (int p = 0; p < 3; p++) {
             u32x4 q;
@@ -166,7 +207,7 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
             q.y = pl[p][2] | (pl[p][3] << 16);
             q.z = pl[p][4] | (pl[p][5] << 16);
             q.w = pl[p][6] | (pl[p][7] << 16);
-            s_a[((kb * 3 + p) * 2 + f) * 64 + l] = q;
+            s_a[(((kb * 3 + p) * 2 + f) * 4 + gg) * MRT + row] = q;
         }
     }
     float *scw = s_sc + wave * (32 * 2 * KS);  // [32 columns][2 KS blocks]
@@ -197,7 +238,10 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
 #pragma unroll
             for (int p = 0; p < 3; p++)
 #pragma unroll
-                for (int f = 0; f < 2; f++) av[p][f] = as_bf16x8(s_a[((kb * 3 + p) * 2 + f) * 64 + lane]);
+                for (int f = 0; f < 2; f++)
+                    av[p][f] = (lane & 15) < MRT
+                                   ? as_bf16x8(s_a[(((kb * 3 + p) * 2 + f) * 4 + (lane >> 4)) * MRT + (lane & 15)])
+                                   : bf16x8{};
 #pragma unroll
             for (int cb = 0; cb < 2; cb++) {
                 const unsigned char *wrow = tw + (16 * cb + nn) * SK_WROW + 64 * h;
@@ -239,6 +283,114 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
             const int row = 4 * g + r;
             if (row < a.m) a.part[((size_t)split * SK_ROWS + row) * a.n_pad + col[cb]] = acc[cb][r];
         }
+}
+
+__device__ __forceinline__ ArgAcc wave_argmax(ArgAcc a) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        ArgAcc o;
+        o.v = __shfl_xor(a.v, off);
+        o.i = __shfl_xor(a.i, off);
+        o.nan = __shfl_xor(a.nan, off);
+        a = arg_combine(a, o);
+    }
+    return a;
+}
+
+__device__ __forceinline__ void arg_push(ArgAcc &p, float v, int i) {  // sequential scan order
+    if (isnan(v)) {
+        p.nan = i;
+        return;
+    }
+    if (p.i < 0 || !(p.v > v)) {
+        p.v = v;
+        p.i = i;
+    }
+}
+
+// One workgroup per column tile: wave w takes rows w, w + 4, ...; lane l the
+// columns 2l, 2l + 1 of the tile, or (SwiGLU, lanes 0..31) the packed group
+// 4l .. 4l + 3 = gate and up of outputs 2l, 2l + 1.  Every split's partials
+// of a batch are requested before the first is used; the sums run in split
+// order.
+template <int EPI>
+__global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
+    const int tile = blockIdx.x;
+    constexpr bool SW = EPI == SKE_SWIGLU;
+    constexpr int NB = SW ? 16 : 32;  // splits per load batch
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bool act = !SW || lane < 32;
+    const int c = tile * SK_COLS + (SW ? 4 : 2) * (act ? lane : 0);
+    const size_t st = (size_t)SK_ROWS * a.n_pad;
+    for (int row = wave; row < a.m; row += SK_NT / 64) {
+        const float *p = a.part + (size_t)row * a.n_pad + c;
+        double ssq = 0.0;
+        if (a.ss_in && lane < a.n_ss_in) ssq = a.ss_in[(size_t)row * a.n_ss_in + lane];
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+        for (int i0 = 0; i0 < a.n_split; i0 += NB) {
+            float2 q0[NB], q1[SW ? NB : 1];
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                if (i0 + j < a.n_split) {
+                    q0[j] = *(const float2 *)(p + (size_t)(i0 + j) * st);
+                    if constexpr (SW) q1[j] = *(const float2 *)(p + (size_t)(i0 + j) * st + 2);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                if (i0 + j < a.n_split) {
+                    s0 += q0[j].x;
+                    s1 += q0[j].y;
+                    if constexpr (SW) {
+                        s2 += q1[j].x;
+                        s3 += q1[j].y;
+                    }
+                }
+            }
+        }
+        double rstd = 1.0;
+        if (a.ss_in) {  // RMSNorm of the input row: f64 sum of the producer's partials
+            const double v = wave_sum_d(ssq);
+            rstd = 1.0 / sqrt(v / (double)a.k + (double)a.eps);
+        }
+        float *yr = a.y + (size_t)row * a.ldy;
+        if constexpr (SW) {  // cpu.rs:666-678
+            const int j = tile * (SK_COLS / 2) + 2 * lane;
+            const float g0 = (float)((double)(s0 * a.scale) * rstd), g1 = (float)((double)(s1 * a.scale) * rstd);
+            const float u0 = (float)((double)(s2 * a.scale2) * rstd), u1 = (float)((double)(s3 * a.scale2) * rstd);
+            if (act && j < a.n_out) yr[j] = silu_f(g0) * u0;
+            if (act && j + 1 < a.n_out) yr[j + 1] = silu_f(g1) * u1;
+        } else {
+            const int c1 = c + 1;
+            const bool ok0 = c < a.n_out, ok1 = c1 < a.n_out;
+            float v0 = (float)((double)(s0 * a.scale) * rstd), v1 = (float)((double)(s1 * a.scale) * rstd);
+            if constexpr (EPI == SKE_RESID) {  // llama.rs:556-569: x + o, x + down
+                if (ok0) v0 = yr[c] + v0;
+                if (ok1) v1 = yr[c1] + v1;
+            }
+            if (ok0) yr[c] = v0;
+            if (ok1) yr[c1] = v1;
+            if constexpr (EPI == SKE_RESID) {
+                if (a.ss_out) {
+                    double q = (ok0 ? (double)v0 * (double)v0 : 0.0) + (ok1 ? (double)v1 * (double)v1 : 0.0);
+                    q = wave_sum_d(q);
+                    if (lane == 0) a.ss_out[(size_t)row * a.tiles + tile] = q;
+                }
+            }
+            if constexpr (EPI == SKE_LOGITS) {  // generate.rs:167-173, in index order
+                ArgAcc pa{0.f, -1, -1};
+                if (ok0) arg_push(pa, v0, c);
+                if (ok1) arg_push(pa, v1, c1);
+                pa = wave_argmax(pa);
+                if (lane == 0) {
+                    const size_t at = (size_t)row * a.tiles + tile;
+                    a.pv[at] = pa.v;
+                    a.pi[at] = pa.i;
+                    a.pn[at] = pa.nan;
+                }
+            }
+        }
+    }
 }
 
 // y[row][col] = scale * (sum of the splits' partials, in split order) (+ bias[col]);
@@ -295,9 +447,25 @@ SkPlan plan(int k, int n) {
     return p;
 }
 
-template <int KS, bool B32>
+template <int KS, bool B32, bool NORM = false>
 int launch_ks(const SkArgs &a, int tiles, hipStream_t s) {
-    hipLaunchKernelGGL((k_skinny<KS, B32>), dim3(tiles * a.n_split), dim3(SK_NT), 0, s, a);
+    if (a.m <= 4)
+        hipLaunchKernelGGL((k_skinny<KS, B32, NORM, 4>), dim3(tiles * a.n_split), dim3(SK_NT), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_skinny<KS, B32, NORM, 16>), dim3(tiles * a.n_split), dim3(SK_NT), 0, s, a);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
+
+template <bool NORM>
+int launch_main(const SkArgs &a, int ks, bool b32, hipStream_t s) {
+    if (ks == 8) return b32 ? launch_ks<8, true, NORM>(a, a.tiles, s) : launch_ks<8, false, NORM>(a, a.tiles, s);
+    return b32 ? launch_ks<4, true, NORM>(a, a.tiles, s) : launch_ks<4, false, NORM>(a, a.tiles, s);
+}
+
+template <int EPI>
+int launch_epi(const SkArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL((k_skinny_epi<EPI>), dim3(a.tiles), dim3(SK_NT), 0, s, a);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }
@@ -361,6 +529,66 @@ int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s)
     }
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
+}
+
+int skinny_tiles(const Packed &w) { return plan(w.k, w.rows).tiles; }
+
+int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStream_t s) {
+    const Packed &w = *f.w;
+    const bool sw = f.epi == SKE_SWIGLU;
+    if (f.epi < SKE_STORE || f.epi > SKE_LOGITS) return set_error(SCRY_ERR_INVALID, "skinny: epilogue %d", f.epi);
+    if (w.bf16 || (w.fused ? (!sw || w.rows != 2 * w.n || w.rows % 4 != 0) : (sw || w.rows != w.n)))
+        return set_error(SCRY_ERR_UNSUPPORTED,
+                         "skinny matmul: int8 weight rows only (the fused gate/up pair with the swiglu output)");
+    if (f.m < 1 || f.m > SK_ROWS || f.ldx < w.k || f.ldy < w.n || !f.x || !f.y)
+        return set_error(SCRY_ERR_INVALID, "skinny matmul: %d rows (1..%d), ldx %d, ldy %d", f.m, SK_ROWS, f.ldx,
+                         f.ldy);
+    if (w.k % 8 != 0) return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: k %% 8 != 0");
+    if (w.kp < w.k || (size_t)w.rows * w.kp > 0x7fffffffu || (size_t)f.m * f.ldx * 4 > 0x7fffffffu)
+        return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: operands above the 2 GiB buffer range");
+    if (f.norm_w && (!f.ss_in || f.n_ss_in < 1 || f.n_ss_in > 64))
+        return set_error(SCRY_ERR_INVALID, "skinny matmul: RMSNorm input needs 1..64 partial sums per row");
+    if (f.epi == SKE_LOGITS && (!f.pv || !f.pi || !f.pn))
+        return set_error(SCRY_ERR_INVALID, "skinny matmul: logits epilogue needs argmax partials");
+    const SkPlan p = plan(w.k, w.rows);
+    if (ws_bytes < skinny_ws_bytes(f.m, w.k, w.rows))
+        return set_error(SCRY_ERR_INVALID, "skinny matmul: workspace too small");
+    const bool b32 = w.s32 != nullptr;
+    SkArgs a{};
+    a.x = f.x;
+    a.ldx = f.ldx;
+    a.m = f.m;
+    a.k = w.k;
+    a.w = w.d;
+    a.kp = w.kp;
+    a.n = w.rows;
+    a.s32 = w.s32;
+    a.nb = w.nb;
+    a.part = ws;
+    a.n_pad = p.n_pad;
+    a.n_split = p.n_split;
+    a.kblocks = p.kblocks;
+    a.g = f.norm_w;
+    a.ss_in = f.norm_w ? f.ss_in : nullptr;
+    a.n_ss_in = f.n_ss_in;
+    a.eps = f.eps;
+    a.tiles = p.tiles;
+    a.n_out = w.n;
+    a.scale = b32 ? 1.f : w.scale;  // block-32 scales are applied per block
+    a.scale2 = b32 ? 1.f : (sw ? w.scale2 : w.scale);
+    a.y = f.y;
+    a.ldy = f.ldy;
+    a.ss_out = f.ss_out;
+    a.pv = f.pv;
+    a.pi = f.pi;
+    a.pn = f.pn;
+    SCRY_TRY(f.norm_w ? launch_main<true>(a, p.ks, b32, s) : launch_main<false>(a, p.ks, b32, s));
+    switch (f.epi) {
+        case SKE_STORE: return launch_epi<SKE_STORE>(a, s);
+        case SKE_RESID: return launch_epi<SKE_RESID>(a, s);
+        case SKE_SWIGLU: return launch_epi<SKE_SWIGLU>(a, s);
+        default: return launch_epi<SKE_LOGITS>(a, s);
+    }
 }
 
 }  // namespace scry

@@ -379,7 +379,8 @@ int scry_hip_llama_prefill(scry_llama m, scry_kv_cache *caches, int n_seq, const
  * every step's logits.  K/V rows seq_len .. seq_len + steps - 1 are appended
  * (seq_len advances by steps).  1 <= n_seq <= 16, distinct caches, int8
  * models (per-tensor or block-32 scales; a bf16 model returns
- * SCRY_ERR_UNSUPPORTED), hidden, q and ffn sizes multiples of 8. */
+ * SCRY_ERR_UNSUPPORTED), hidden, q and ffn sizes multiples of 8, hidden at
+ * most 8192. */
 int scry_hip_llama_decode_batch(scry_llama m, scry_kv_cache *caches, int n_seq, const int64_t *tokens,
                                 int steps, int64_t *out_tokens, float *logits);
 
