@@ -173,7 +173,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
     __syncthreads();
     __shared__ int s_last;
     if (tid == 0)
-        s_last = __hip_atomic_fetch_add(a.merge_ctr + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        s_last = __hip_atomic_fetch_add(a.merge_ctr + (size_t)g * kCtrStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (unsigned)(a.n_splits - 1);
     __syncthreads();
     if (!s_last) return;
@@ -205,7 +205,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
         }
         a.xa[(size_t)h * hd + d] = M == -INFINITY ? 0.f : v / Ls;
     }
-    if (tid == 0) a.merge_ctr[g] = 0;  // ready for the next launch on the stream
+    if (tid == 0) a.merge_ctr[(size_t)g * kCtrStride] = 0;  // ready for the next launch on the stream
 }
 
 template <int G, int NR, int NW>
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_decode_seqs(AttnArgs a, AttnSe
     s.v_cache = b.v[y] + (size_t)b.layer * b.ls[y];
     s.part_o = a.part_o + (size_t)y * a.n_heads * a.n_splits * a.head_dim;
     s.part_ml = a.part_ml + (size_t)y * a.n_heads * a.n_splits * 2;
-    s.merge_ctr = a.merge_ctr + (size_t)y * a.n_kv;
+    s.merge_ctr = a.merge_ctr + (size_t)y * a.n_kv * kCtrStride;
     s.xa = a.xa + (size_t)y * qd;
     s.fixed_len = b.pos[y] + 1;
     attn_body<G, NR, NW>(s, blockIdx.x);

@@ -230,13 +230,18 @@ const StTensor *st_find(const StShards *sh, const char *name);  // nullptr if ab
 int launch_widen(const void *src, int dtype, size_t n, float *dst, hipStream_t s);
 
 // attn.hip
+// Per-group hand-over counters sit kCtrStride words apart: each on its own
+// 256-byte block, so the atomics and polls of different groups do not queue
+// on one cache line.
+constexpr int kCtrStride = 64;
+
 struct AttnArgs {
     const float *q = nullptr;     // [n_heads*hd] pre-scaled
     const float *k_cache = nullptr, *v_cache = nullptr;  // [max_seq, n_kv*hd]
     // per (head, split) partials and per-KV-group arrival counters (zero
     // between launches)
     float *part_o = nullptr, *part_ml = nullptr;
-    unsigned *merge_ctr = nullptr;
+    unsigned *merge_ctr = nullptr;  // group g's counter at merge_ctr[g * kCtrStride]
     float *xa = nullptr;          // merged output [n_heads*hd]
     const DevState *state = nullptr;
     int n_heads = 0, n_kv = 0, head_dim = 0, n_splits = 1, max_chunk = 0;

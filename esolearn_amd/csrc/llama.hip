@@ -110,7 +110,7 @@ struct scry_kv_cache_s {
     // last split merges them), and the merged output row
     void *att_buf = nullptr;
     float *ap_o = nullptr, *ap_ml = nullptr;
-    unsigned *att_ctr = nullptr;
+    unsigned *att_ctr = nullptr;  // group g's at att_ctr[g * kCtrStride]
     float *xa = nullptr;
     float *lp_val = nullptr;
     int *lp_idx = nullptr, *lp_nan = nullptr;
@@ -403,13 +403,14 @@ int cache_new(scry_llama m, int max_seq, scry_kv_cache *out) {
         auto al = [](size_t b) { return (b + 255) / 256 * 256; };
         const size_t b_o = al(sizeof(float) * (size_t)m->nh * c->n_splits * m->hd);
         const size_t b_ml = al(sizeof(float) * (size_t)m->nh * c->n_splits * 2);
-        rc = dev_alloc(&c->att_buf, b_o + b_ml + al(sizeof(unsigned) * m->nkv));
+        const size_t n_ctr = (size_t)m->nkv * kCtrStride;  // merge arrivals
+        rc = dev_alloc(&c->att_buf, b_o + b_ml + al(sizeof(unsigned) * n_ctr));
         if (!rc) {
             char *base = (char *)c->att_buf;
             c->ap_o = (float *)base;
             c->ap_ml = (float *)(base + b_o);
             c->att_ctr = (unsigned *)(base + b_o + b_ml);
-            rc = launch_fill_u32(c->att_ctr, m->nkv, 0u, s);
+            rc = launch_fill_u32(c->att_ctr, n_ctr, 0u, s);
         }
     }
     if (!rc) rc = dev_alloc((void **)&c->lp_val, sizeof(float) * nparts);
@@ -879,8 +880,8 @@ int batch_ws(scry_llama m) {
     if (!rc) rc = dev_alloc((void **)&B.pn, sizeof(int) * R * lt);
     if (!rc) rc = dev_alloc((void **)&B.ap_o, sizeof(float) * R * m->nh * nsp * m->hd);
     if (!rc) rc = dev_alloc((void **)&B.ap_ml, sizeof(float) * R * m->nh * nsp * 2);
-    if (!rc) rc = dev_alloc((void **)&B.ctr, sizeof(unsigned) * R * m->nkv);
-    if (!rc) rc = launch_fill_u32(B.ctr, R * m->nkv, 0u, ctx().stream);  // the last split of a group resets it
+    if (!rc) rc = dev_alloc((void **)&B.ctr, sizeof(unsigned) * R * m->nkv * kCtrStride);
+    if (!rc) rc = launch_fill_u32(B.ctr, R * m->nkv * kCtrStride, 0u, ctx().stream);  // the last split of a group resets it
     if (!rc) rc = dev_alloc((void **)&B.pos, sizeof(int) * R);
     if (rc) {
         for (void *p : {(void *)B.x, (void *)B.qkv, (void *)B.q, (void *)B.xa, (void *)B.act, (void *)B.logits,

@@ -1,0 +1,517 @@
+// W8A32 quantized GEMV / skinny GEMM for gfx950, with the decode-step fusions.
+//
+// Computes, for each activation row x and output j,
+//   y[j] = scale * sum_p x[p] * q[p, j]            (matmul_i8_f32, cpu.rs:1128-1160)
+// from the GEMV stream layout (one row of kp bytes per output j, byte = q + 128).
+//
+// Work split: a workgroup of NW waves owns NW * RWT consecutive output rows,
+// each wave RWT rows over the whole k range.  Per 1024-wide k chunk a lane
+// loads 16 consecutive weight bytes of each of its rows (one wave-wide
+// buffer_load_dwordx4 reads 1 KiB contiguous) and four float4 activation
+// fragments from LDS.  Each byte is converted with a single byte-select
+// convert (v_cvt_f32_ubyte*) and FMA'd.
+//
+// Prologue (one barrier): the activation row is staged in LDS with a
+// permutation that makes the float4 reads conflict-free; while staging, each
+// quad of threads also writes the sum of the 16 values a consumer lane reads
+// per chunk.  Those per-lane sums remove the +128 bias inside the final wave
+// reduction (sum_p (q+128) x - 128 sum_p x) and are the block-32 group sums.
+// The first PF chunks of every row are requested before the staging, so the
+// weight stream is in flight during it.  Rows past the end load a valid row
+// (and are never stored): a load that is out of range for every lane can
+// complete out of order and release a partial vmcnt wait too early.
+//
+// RMSNorm (rmsnorm.rs, cpu.rs:574-599) is applied as y = rstd * (W (x*g)):
+//   PRO_NORM   stages x*g and reduces sum(x^2) itself (the first layer, whose
+//              activation is the embedding row);
+//   PRO_NORMP  stages x*g written by the producing residual GEMV, with rstd
+//              from that GEMV's per-workgroup sum(x^2) partials.
+// Both sums of squares are reduced after the staging barrier, in a fixed order.
+//
+// bf16 weights (the reference's bf16 feature, cuda.rs:1206-1290) take the
+// same path with a weight type WT = WT_BF16: rows of bf16 values (512 per
+// 1 KiB chunk), and activations normalised (with the RMSNorm prologues) and
+// rounded with the reference's bf16 cast while they are staged, since the
+// reference's bf16 matmul rounds its activation operand.  Each product of two
+// bf16 values is exact in f32; the accumulation is f32.
+//
+// Epilogues fused into the same pass (llama.rs:371-511):
+//   EPI_STORE   y = acc (+ bias)                     -- matmul_i8_f32[_bias]
+//   EPI_RESID   y = resid + acc; optionally x*g_next and sum(y^2) per workgroup
+//               for the next RMSNorm'd GEMV          -- o_proj / down_proj + residual add
+//   EPI_SWIGLU  h = silu(gate) * up on interleaved rows -- gate/up + swiglu
+//   EPI_QKV     RoPE(Q)*1/sqrt(hd), RoPE(K), K/V appended to the cache row
+//   EPI_LOGITS  logits + this workgroup's ordered argmax partial
+// The row-combining epilogues exchange row values through LDS.
+#pragma once
+#include "internal.h"
+#include "kdev.h"
+
+namespace scry {
+
+// The fields the prologue needs come first: the kernel fetches them together.
+struct KArgs {
+    const uint8_t *W;
+    const float *x;
+    const float *ss_in;
+    const float *norm_w;
+    int k, kp, rows, nch;
+    int ldx, m, n_ss;
+    float eps;
+    const float *s32;
+    int nb;
+    float scale, scale2;
+    const float *embed;
+    const int64_t *tokens;
+    DevState *state;
+    float *y;
+    int ldy;
+    const float *resid;
+    const float *bias;
+    float *xg_out;
+    const float *g_next;
+    float *ss_out;
+    float *q_out, *k_cache, *v_cache;
+    const float2 *rope_cs;
+    int q_dim, kv_dim, head_dim;
+    float q_scale;
+    float *part_val;
+    int *part_idx, *part_nan;
+};
+
+// activation prologues
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_NORMP = 2 };
+// weight types
+enum { WT_I8 = 0, WT_I8B32 = 1, WT_BF16 = 2 };
+
+// Checks a decode GEMV's arguments and fills the kernel arguments, the weight
+// type, the 1 KiB chunk count per row and the activation prologue
+// (qgemv.hip).
+int qgemv_kargs(int epi, const GemvArgs &g, KArgs *ka, int *wt, int *nch, int *pro);
+
+namespace {
+
+using namespace dev;
+constexpr int SSW = 2;  // PRO_NORMP partial sums per thread (n_ss <= SSW * threads)
+
+// Launch shape for a chunk count (0: runtime loop) and activation rows per
+// pass.  Measured on the Llama-2-7B decode shapes (one launch of 4096 x 22016
+// int8 weights: 4 rows per wave x 4 waves 17.7 us, 1 row per wave x 8 waves
+// 15.0 us): single-row waves keep more loads in flight per CU and finish
+// evenly.  The MT > 1 and runtime-k paths keep 4 rows per wave, which shares
+// each LDS activation read between 4 rows.
+struct Shape {
+    int rwt, nw, pf;  // rows per wave, waves per workgroup, chunks in flight per row
+};
+constexpr Shape shape_for(int nch, int mt) {
+    return mt > 1      ? Shape{4, 4, 4}
+           : nch == 4  ? Shape{1, 8, 4}
+           : nch == 11 ? Shape{1, 8, 8}
+           : nch == 14 ? Shape{1, 8, 7}
+           : nch == 8  ? Shape{1, 8, 8}  // bf16 rows, k = 4096
+           : nch == 22 ? Shape{1, 8, 8}  // bf16 rows, k = 11008
+           : nch == 28 ? Shape{1, 8, 7}  // bf16 rows, k = 14336
+           : nch == 0  ? Shape{1, 8, 4}  // any k, one row: 8 rows per workgroup
+                       : Shape{4, 4, 4};
+}
+
+// activation values per 1 KiB weight chunk
+constexpr int chunk_vals(int wt) { return wt == WT_BF16 ? 512 : 1024; }
+
+// Activation row source for row mr (nullptr if mr >= m).  Only the
+// self-contained RMSNorm prologue (the first layer) reads the embedding row of
+// the current token when x is null; with one row per pass the grid has
+// exactly m rows of workgroups.  Both keep argument-dependent branches (and
+// their serialized argument fetches) off the common paths.
+template <int PRO, int MT>
+__device__ __forceinline__ const float *act_row(const KArgs &a, int mr) {
+    if (MT > 1 && mr >= a.m) return nullptr;
+    if (PRO == PRO_NORM && !a.x) return a.embed + (size_t)a.tokens[a.state->pos] * a.k;
+    return a.x + (size_t)mr * a.ldx;
+}
+
+// Thread t loads the float4s f4 = p*NT + t (p < XP) of a k-vector.  A wave
+// whose float4s all lie past k loads nothing (zeros).
+template <int XP, int NT>
+__device__ __forceinline__ void load_vec(const float *src, int k, int tot4, float4 (&v)[XP]) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(src, src ? (size_t)k * 4 : 0);
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int p = 0; p < XP; p++) {
+        const int f4 = p * NT + tid;
+        v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (src && f4 < tot4 && (f4 & ~63) * 4 < k) v[p] = bload16f(r, (unsigned)f4 << 4);
+    }
+}
+
+// One 1024-wide k chunk for RWT rows and MT activation rows.
+template <int MT, int WT, int RWT>
+__device__ __forceinline__ void chunk_fma(const u32x4 (&w)[RWT], int c, const float *xs, int kc,
+                                          const float *xsum, __amdgpu_buffer_rsrc_t sr, int nb,
+                                          const int (&wrow)[RWT], int lane, float (&acc)[MT][RWT],
+                                          int kp) {
+    constexpr bool B32 = WT == WT_I8B32;
+    if constexpr (WT == WT_BF16) {
+        // lane L holds bf16 values 8L .. 8L+7 of chunk c: x at c*512 + 4L (+256)
+        if ((c << 10) + (lane << 4) >= kp) return;  // past the row (the next row's bytes)
+#pragma unroll
+        for (int mi = 0; mi < MT; mi++) {
+            const float *xb = xs + mi * kc + (c << 9) + (lane << 2);
+            const float4 x0 = *(const float4 *)(xb);
+            const float4 x1 = *(const float4 *)(xb + 256);
+#pragma unroll
+            for (int r = 0; r < RWT; r++) acc[mi][r] = dot8_bf16(w[r], x0, x1, acc[mi][r]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++) {
+        const float *xb = xs + mi * kc + (c << 10) + (lane << 2);
+        const float4 x0 = *(const float4 *)(xb);
+        const float4 x1 = *(const float4 *)(xb + 256);
+        const float4 x2 = *(const float4 *)(xb + 512);
+        const float4 x3 = *(const float4 *)(xb + 768);
+        if (!B32) {
+#pragma unroll
+            for (int r = 0; r < RWT; r++) acc[mi][r] = dot16(w[r], x0, x1, x2, x3, acc[mi][r]);
+        } else {
+            // block-32: this lane's 16 bytes are half of k-block blk
+            const float gs = xsum[mi * (kc >> 4) + (c << 6) + lane];
+            const int blk = ((c << 10) + (lane << 4)) >> 5;
+#pragma unroll
+            for (int r = 0; r < RWT; r++) {
+                const float p = dot16(w[r], x0, x1, x2, x3, 0.f);
+                const float sc = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(sr, (wrow[r] * nb + blk) * 4, 0, 0));
+                acc[mi][r] = fmaf(sc, fmaf(-128.f, gs, p), acc[mi][r]);
+            }
+        }
+    }
+}
+
+// One workgroup's rows: workgroup bx of the row blocks, by of the activation
+// row groups (a kernel's blockIdx, or a fused kernel's own block mapping).
+template <int EPI, int PRO, int WT, int MT, int NCH>
+__device__ __forceinline__ void qgemv_block(const KArgs &a, const int bx, const int by) {
+    constexpr Shape S = shape_for(NCH, MT);
+    constexpr int RWT = S.rwt, NW = S.nw, PF = S.pf, RPW = RWT * NW, NT = 64 * NW;
+    constexpr bool B32 = WT == WT_I8B32, WB = WT == WT_BF16;
+    constexpr int CV = chunk_vals(WT);  // activation values per chunk
+    constexpr int XP = ((NCH > 0 ? NCH : (WB ? 32 : 16)) * (CV / 4) + NT - 1) / NT;  // float4 per thread per row
+    constexpr bool NORM = PRO != PRO_PLAIN;
+    static_assert(!WB || MT == 1, "bf16 weights take one activation row per pass");
+    static_assert(!NORM || MT == 1, "the RMSNorm prologues take one activation row");
+    static_assert(EPI == EPI_STORE || MT == 1, "only the store epilogue takes several rows");
+    static_assert(EPI == EPI_STORE || EPI == EPI_RESID || RPW % 4 == 0,
+                  "the SwiGLU, QKV and logits epilogues combine rows in groups of 4");
+    extern __shared__ float4 dyn4[];
+    const int nch = NCH > 0 ? NCH : a.nch;
+    const int kc = nch * CV;
+    const int tot4 = kc >> 2;  // float4 slots of one staged activation row
+    float *xs = reinterpret_cast<float *>(dyn4);  // [MT][kc] permuted activation rows
+    float *xsum = xs + MT * kc;                    // [MT][nch][64] per-lane 16-value sums (int8)
+    __shared__ double s_ss[NW];  // per-wave sums of squares for the RMSNorm
+    __shared__ float s_rstd;
+    __shared__ float s_val[MT * RPW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rb = bx * RPW, row0 = rb + wave * RWT;
+    const int m0 = by * MT;
+
+    // ---- 1. activation loads (and the RMSNorm inputs), then the first PF
+    // chunks of every row: waiting for the activations leaves the weight
+    // stream in flight
+    float4 xr[XP];
+    load_vec<XP, NT>(act_row<PRO, MT>(a, m0), a.k, tot4, xr);
+    float4 gw[PRO == PRO_NORM ? XP : 1];
+    if constexpr (PRO == PRO_NORM) load_vec<XP, NT>(a.norm_w, a.k, tot4, gw);
+    // PRO_NORMP: this thread's share of the producer's partial sums
+    // (unconditional clamped loads: no wait inside a branch)
+    float ssv[PRO == PRO_NORMP ? SSW : 1];
+    if constexpr (PRO == PRO_NORMP) {
+#pragma unroll
+        for (int j = 0; j < SSW; j++) ssv[j] = a.ss_in[min(tid + NT * j, a.n_ss - 1)];
+    }
+
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.W, (size_t)a.rows * a.kp);
+    int wrow[RWT];
+    unsigned woff[RWT];
+#pragma unroll
+    for (int r = 0; r < RWT; r++) {
+        wrow[r] = min(row0 + r, a.rows - 1);
+        woff[r] = (unsigned)(wrow[r] * a.kp + (lane << 4));
+    }
+    u32x4 wb[PF][RWT];
+#pragma unroll
+    for (int d = 0; d < PF; d++)
+        if (NCH > 0 || d < nch) {
+#pragma unroll
+            for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + (d << 10));
+        }
+    // EPI_RESID: the residual and the next norm's weight of the row this lane
+    // stores, requested now (they are used after the weight stream; the row
+    // is read and written by this lane only)
+    float pre_r[RWT], pre_g[RWT];
+    if constexpr (EPI == EPI_RESID) {
+        const float *R = a.resid ? a.resid : a.embed + (size_t)a.tokens[a.state->pos] * a.rows;
+#pragma unroll
+        for (int r = 0; r < RWT; r++) {
+            pre_r[r] = pre_g[r] = 0.f;
+            if (lane == r) {
+                pre_r[r] = R[wrow[r]];
+                if (a.xg_out) pre_g[r] = a.g_next[wrow[r]];
+            }
+        }
+    }
+
+    // ---- 2. stage the activation rows into LDS with the per-lane sums
+    double ssp = 0.0;
+    if constexpr (WB) {
+        // bf16: the RMSNorm scale first (cpu.rs:574-599; f64 sum of squares,
+        // reduced in a fixed order), then each value normalised and rounded
+        // with the reference's cast as it is staged
+        double rstd = 1.0;
+        if constexpr (NORM) {
+            if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+                for (int p = 0; p < XP; p++) {
+                    const float4 v = xr[p];
+                    ssp += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < SSW; j++)
+                    if (tid + NT * j < a.n_ss) ssp += ssv[j];
+            }
+            ssp = wave_sum_d_dpp(ssp);
+            if (lane == 0) s_ss[wave] = ssp;
+            __syncthreads();
+            double t = 0.0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) t += s_ss[w];
+            rstd = 1.0 / sqrt(t / (double)a.k + (double)a.eps);
+        }
+#pragma unroll
+        for (int p = 0; p < XP; p++) {
+            const int f4 = p * NT + tid;
+            if (f4 < tot4) {
+                float4 v = xr[p];
+                if constexpr (PRO == PRO_NORM) {  // f32(f64(x) * rstd * f64(w))
+                    v.x = (float)((double)v.x * rstd * (double)gw[p].x);
+                    v.y = (float)((double)v.y * rstd * (double)gw[p].y);
+                    v.z = (float)((double)v.z * rstd * (double)gw[p].z);
+                    v.w = (float)((double)v.w * rstd * (double)gw[p].w);
+                } else if constexpr (PRO == PRO_NORMP) {  // the producer's x * w, times rstd
+                    v.x = (float)((double)v.x * rstd);
+                    v.y = (float)((double)v.y * rstd);
+                    v.z = (float)((double)v.z * rstd);
+                    v.w = (float)((double)v.w * rstd);
+                }
+                v.x = bf16_cast(v.x);
+                v.y = bf16_cast(v.y);
+                v.z = bf16_cast(v.z);
+                v.w = bf16_cast(v.w);
+                // value 512c + 8L + 4j + e (lane L's j-th float4 of chunk c)
+                const int c = f4 >> 7, w = f4 & 127;
+                *(float4 *)(xs + (c << 9) + ((w & 1) << 8) + ((w >> 1) << 2)) = v;
+            }
+        }
+    } else {
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++) {
+        if (mi > 0) load_vec<XP, NT>(act_row<PRO, MT>(a, m0 + mi), a.k, tot4, xr);
+#pragma unroll
+        for (int p = 0; p < XP; p++) {
+            const int f4 = p * NT + tid;
+            if (f4 < nch * 256) {  // whole waves: nch * 256 is a multiple of 64
+                float4 v = xr[p];
+                if constexpr (PRO == PRO_NORM) {
+                    ssp += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+                    v.x *= gw[p].x;
+                    v.y *= gw[p].y;
+                    v.z *= gw[p].z;
+                    v.w *= gw[p].w;
+                }
+                *(float4 *)(xs + mi * kc + xslot(f4 >> 8, f4 & 255)) = v;
+                // consumer lane L of chunk c reads float4s c*256 + 4L .. 4L+3:
+                // the quad of threads staging them sums its 16 values
+                float s = (v.x + v.y) + (v.z + v.w);
+                s += __shfl_xor(s, 1);
+                s += __shfl_xor(s, 2);
+                if ((tid & 3) == 0) xsum[mi * (kc >> 4) + ((f4 >> 8) << 6) + ((f4 & 255) >> 2)] = s;
+            }
+        }
+    }
+    if constexpr (NORM) {
+        if constexpr (PRO == PRO_NORMP) {
+#pragma unroll
+            for (int j = 0; j < SSW; j++)
+                if (tid + NT * j < a.n_ss) ssp += ssv[j];
+        }
+        ssp = wave_sum_d_dpp(ssp);
+        if (lane == 0) s_ss[wave] = ssp;
+    }
+    }  // int8 staging
+    __syncthreads();
+    if (NORM && !WB && wave == 0) {
+        // cpu.rs:574-599: rstd = 1/sqrt(mean(x^2) + eps) in f64 (waves in order)
+        double t = 0.0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) t += s_ss[w];
+        if (lane == 0) s_rstd = (float)(1.0 / sqrt(t / (double)a.k + (double)a.eps));
+    }
+
+    // ---- 3. stream the weights
+    float acc[MT][RWT];
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++)
+#pragma unroll
+        for (int r = 0; r < RWT; r++) acc[mi][r] = 0.f;
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(a.s32, B32 ? (size_t)a.rows * a.nb * sizeof(float) : 0);
+
+    if constexpr (NCH > 0) {
+        // straight-line stream: chunk c computes from wb[c % PF], then refills it
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            chunk_fma<MT, WT, RWT>(wb[c % PF], c, xs, kc, xsum, sr, a.nb, wrow, lane, acc, a.kp);
+            if (c + PF < NCH) {
+#pragma unroll
+                for (int r = 0; r < RWT; r++) wb[c % PF][r] = bload16(wr, woff[r] + ((c + PF) << 10));
+            }
+        }
+    } else {
+        for (int c0 = 0; c0 < nch; c0 += PF) {
+#pragma unroll
+            for (int d = 0; d < PF; d++) {
+                const int c = c0 + d;
+                if (c < nch) {
+                    chunk_fma<MT, WT, RWT>(wb[d], c, xs, kc, xsum, sr, a.nb, wrow, lane, acc, a.kp);
+                    if (c + PF < nch) {
+#pragma unroll
+                        for (int r = 0; r < RWT; r++) wb[d][r] = bload16(wr, woff[r] + ((c + PF) << 10));
+                    }
+                }
+            }
+        }
+    }
+
+
+    // ---- 4. remove the +128 bias inside the wave reduction, apply the scales
+    float val[MT][RWT];
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++) {
+        float sxl = 0.f;
+        if (WT == WT_I8)
+            for (int c = 0; c < nch; c++) sxl += xsum[mi * (kc >> 4) + (c << 6) + lane];
+#pragma unroll
+        for (int r = 0; r < RWT; r++) {
+            const float s = wave_sum(WT == WT_I8 ? fmaf(-128.f, sxl, acc[mi][r]) : acc[mi][r]);
+            // fused gate/up rows come as gate, gate, up, up
+            const float sc = WT != WT_I8 ? 1.f : (EPI == EPI_SWIGLU && ((row0 + r) & 2)) ? a.scale2 : a.scale;
+            val[mi][r] = sc * s;
+        }
+    }
+
+    // ---- 5. epilogues
+    if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {
+#pragma unroll
+        for (int mi = 0; mi < MT; mi++) {
+            const int mr = m0 + mi;
+            // lane r stores row r (static indices: no private-array select)
+#pragma unroll
+            for (int r = 0; r < RWT; r++) {
+                const int row = row0 + r;
+                if (lane == r && mr < a.m && row < a.rows) {
+                    float v = val[mi][r];
+                    if constexpr (EPI == EPI_STORE) {
+                        if (a.bias) v = v + a.bias[row];
+                    } else {
+                        v = pre_r[r] + v;  // (EPI_RESID has one activation row: mr == 0)
+                        if (a.xg_out) a.xg_out[row] = v * pre_g[r];
+                        s_val[wave * RWT + r] = v;
+                    }
+                    a.y[(size_t)mr * a.ldy + row] = v;
+                }
+            }
+        }
+        if constexpr (EPI == EPI_RESID) {
+            if (a.ss_out) {  // uniform: the next RMSNorm's sum of squares, in row order
+                __syncthreads();
+                if (tid == 0) {
+                    double t = 0.0;
+                    for (int i = 0; i < RPW && rb + i < a.rows; i++) t += (double)s_val[i] * s_val[i];
+                    a.ss_out[bx] = (float)t;
+                }
+            }
+        }
+        return;
+    } else {
+#pragma unroll
+        for (int r = 0; r < RWT; r++)
+            if (lane == r) s_val[wave * RWT + r] = val[0][r];
+        __syncthreads();
+    }
+    const float rs = (NORM && !WB) ? s_rstd : 1.f;  // bf16: normalised while staged
+    if constexpr (EPI == EPI_SWIGLU) {
+        // rows 4i..4i+3 = gate[2i], gate[2i+1], up[2i], up[2i+1]
+        if (tid < RPW / 2 && rb + 2 * tid < a.rows) {
+            const int q = (tid >> 1) * 4 + (tid & 1);
+            a.y[(rb >> 1) + tid] = silu_f(s_val[q] * rs) * (s_val[q + 2] * rs);
+        }
+    } else if constexpr (EPI == EPI_QKV) {
+        const int j = rb + 2 * tid;
+        if (tid < RPW / 2 && j < a.rows) {
+            const float x0 = s_val[2 * tid] * rs, x1 = s_val[2 * tid + 1] * rs;
+            const int pos = a.state->pos, crow = a.state->cache_len;
+            const int hh = a.head_dim >> 1;
+            if (j < a.q_dim + a.kv_dim) {
+                const bool isq = j < a.q_dim;
+                const int jj = isq ? j : j - a.q_dim;
+                const float2 cs = a.rope_cs[(size_t)pos * hh + ((jj % a.head_dim) >> 1)];
+                // cpu.rs:655-658 in f32, no contraction
+                const float r0 = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
+                const float r1 = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+                if (isq) {
+                    a.q_out[jj] = __fmul_rn(r0, a.q_scale);
+                    a.q_out[jj + 1] = __fmul_rn(r1, a.q_scale);
+                } else {
+                    float *kr = a.k_cache + (size_t)crow * a.kv_dim;
+                    kr[jj] = r0;
+                    kr[jj + 1] = r1;
+                }
+            } else {
+                const int jj = j - a.q_dim - a.kv_dim;
+                float *vr = a.v_cache + (size_t)crow * a.kv_dim;
+                vr[jj] = x0;
+                vr[jj + 1] = x1;
+            }
+        }
+    } else if constexpr (EPI == EPI_LOGITS) {
+        // logits + this workgroup's ordered argmax partial (no fences: the
+        // finish kernel that reduces the partials is the next launch)
+        if (tid < RPW && rb + tid < a.rows) a.y[rb + tid] = s_val[tid] * rs;
+        if (tid == 0) {
+            ArgAcc p{0.f, -1, -1};
+            for (int t = 0; t < RPW; t++) {
+                const int row = rb + t;
+                if (row >= a.rows) break;
+                const float v = s_val[t] * rs;
+                if (isnan(v)) {
+                    p.nan = row;
+                    continue;
+                }
+                if (p.i < 0 || !(p.v > v)) {
+                    p.v = v;
+                    p.i = row;
+                }
+            }
+            a.part_val[bx] = p.v;
+            a.part_idx[bx] = p.i;
+            a.part_nan[bx] = p.nan;
+        }
+    }
+}
+
+}  // namespace
+}  // namespace scry
