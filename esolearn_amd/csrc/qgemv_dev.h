@@ -106,7 +106,7 @@ struct Shape {
 constexpr Shape shape_for(int nch, int mt) {
     return mt > 1      ? Shape{4, 4, 4}
            : nch == 4  ? Shape{1, 8, 4}
-           : nch == 11 ? Shape{1, 8, 8}
+           : nch == 11 ? Shape{1, 8, 11}  // down (k = 11008): every chunk in flight
            : nch == 14 ? Shape{1, 8, 7}
            : nch == 8  ? Shape{1, 8, 8}  // bf16 rows, k = 4096
            : nch == 22 ? Shape{1, 8, 8}  // bf16 rows, k = 11008
