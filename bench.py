@@ -33,7 +33,8 @@ Also reported:
                 copies: median / p10 / p90 per-launch device time
 
 Profiling modes (no JSON line): --pmc-probe runs a 256 MiB device copy (the
-counter calibration) and each decode projection kernel over all layers;
+counter calibration), each decode projection kernel over all layers and
+decode attention at 640 cached rows;
 --prefill-profile runs the config-5 batched prefill twice without decode;
 --prefill-only runs the config-5 measurement alone; --gemv-only the
 configs 2 / 3 micro-benchmark alone.
@@ -128,7 +129,8 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
 
 
 def pmc_probe(E) -> None:
-    """The workload of the committed PMC summary: calibration copy + projections."""
+    """The workload of the committed PMC summaries: calibration copy, the decode
+    projections, and decode attention at 640 cached rows."""
     import esolearn_amd.llama as EL
     B = E.HipBackend
     src = B.zeros(64 * 1024 * 1024)  # 256 MiB
@@ -143,6 +145,8 @@ def pmc_probe(E) -> None:
                       ("down", EL.T_DOWN), ("lm_head", EL.T_LM_HEAD)):
         us, b = m.time_projection(tid, 32)
         print(f"[probe] {name} {us:.2f} us {b:.0f} B", flush=True)
+    us, b = m.time_attention(640, 32)
+    print(f"[probe] attention (640 rows) {us:.2f} us {b:.0f} B", flush=True)
     m.free()
 
 
