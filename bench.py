@@ -88,6 +88,9 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
     prompts = [E.synth.prompt_ids(s + 1, n_prompt, cfg.vocab_size) for s in range(n_seq)]
     import numpy as np
     pm, dm, toks = m.bench_prefill(np.stack(prompts), decode_steps)
+    # the same prefill, then the four sequences decoded together per step
+    # (one skinny matrix-core pass per projection over the 4 rows)
+    pm_b, dm_b, toks_b = m.bench_prefill(np.stack(prompts), decode_steps, batched=True)
     m.free()
     mb = E.LlamaModel.new_random(cfg, seed=0, quant_mode=EL.QUANT_BF16, init_on_device=True)
     pm_bf16, _, toks_bf16 = mb.bench_prefill(np.stack(prompts), 1)
@@ -101,7 +104,8 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
     attn = 4.0 * n_seq * L * cfg.n_heads * (s * (s + 1) / 2) * hd
     tf = proj / (pm / 1e3) / 1e12
     print(f"[bench] prefill {n_seq}x{s}: {pm:.1f} ms ({rows / pm * 1e3:.0f} tok/s, projections "
-          f"{tf:.1f} TFLOP/s); decode {n_seq}x{decode_steps}: {dm:.1f} ms; init {t_init:.1f} s; "
+          f"{tf:.1f} TFLOP/s); decode {n_seq}x{decode_steps}: {dm:.1f} ms, batched {dm_b:.1f} ms "
+          f"(tokens equal: {bool((toks_b == toks).all())}); init {t_init:.1f} s; "
           f"bf16 model prefill {pm_bf16:.1f} ms", file=sys.stderr, flush=True)
     return {
         "workload": "llama3-8b-shape int8: 4 x 2048-token prompts, batched prefill of the first "
@@ -121,6 +125,13 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
         "mfma_busy_counters": PREFILL_MFMA_BUSY_PROFILE,
         "decode_ms": round(dm, 2),
         "decode_tok_s": round(n_seq * decode_steps / (dm / 1e3), 1),
+        "decode_batched": {
+            "mode": f"{n_seq} sequences per step (skinny matrix-core projections, one attention launch over all caches)",
+            "decode_ms": round(dm_b, 2),
+            "decode_tok_s": round(n_seq * decode_steps / (dm_b / 1e3), 1),
+            "prefill_ms": round(pm_b, 2),
+            "tokens_equal_per_sequence_decode": bool((toks_b == toks).all()),
+        },
         "greedy_tokens_head": [[int(t) for t in row[:4]] for row in toks],
         "bf16_model_prefill_ms": round(pm_bf16, 2),
         "bf16_model_prefill_tok_s": round(rows / (pm_bf16 / 1e3), 1),
