@@ -43,6 +43,9 @@
 //   EPI_QKV     RoPE(Q)*1/sqrt(hd), RoPE(K), K/V appended to the cache row
 //   EPI_LOGITS  logits + this workgroup's ordered argmax partial
 // The row-combining epilogues exchange row values through LDS.
+//
+// This header holds the workgroup body (qgemv_block) and its argument block;
+// qgemv.hip wraps the body in the k_qgemv kernel and holds the launchers.
 #pragma once
 #include "internal.h"
 #include "kdev.h"
