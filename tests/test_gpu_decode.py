@@ -73,6 +73,40 @@ def test_7b_dims_long_prompt_vs_oracle(orc, hip):
     assert (kt == ref_t).all() and (pt == ref_t).all()
 
 
+def test_7b_dims_long_context_vs_oracle(orc, hip):
+    """Config-4 shapes, 2 layers, a 1600-token prompt: with 16 splits per KV
+    group each split walks 100 cached rows, more than one step of its
+    workgroup (96 rows), so the split loop runs twice.  Token by token and
+    with the batched prefill, 6 greedy steps, against the oracle on the GPU
+    model's own weights."""
+    print("[case] 7B dims, 2 layers, prompt 1600, 6 greedy", flush=True)
+    cfg = dict(vocab_size=32000, hidden_size=4096, intermediate_size=11008, n_layers=2,
+               n_heads=32, n_kv_heads=32, max_seq_len=2048, rope_theta=10000.0,
+               tie_word_embeddings=False)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), 0, init_on_device=True)
+    prompt = hip.synth.prompt_ids(5, 1600, 32000)
+    kt, kl = hm.generate_greedy(prompt, 6, want_logits=True)
+    pt, pl = hm.generate_greedy(prompt, 6, want_logits=True, prefill=True)
+    orc.set_threads(16)
+    om = orc.Llama(orc.LlamaConfig(**cfg), None)
+    for layer in range(2):
+        for tid in (orc.T_QKV, orc.T_O, orc.T_GATE, orc.T_UP, orc.T_DOWN):
+            q, s = hm.qtensor(tid, layer)
+            om.set_qtensor(tid, layer, q, s)
+    q, s = hm.qtensor(orc.T_LM_HEAD)
+    om.set_qtensor(orc.T_LM_HEAD, 0, q, s)
+    om.set_embed(hm.embed())
+    hm.free()
+    ref_t, ref_l = om.generate_greedy_fast(prompt, 6, want_logits=True)
+    om.close()
+    orc.set_threads(0)
+    ek = max(rel_err(kl[i], ref_l[i]) for i in range(6))
+    ep = max(rel_err(pl[i], ref_l[i]) for i in range(6))
+    print(f"[err] token by token {ek:.3e}, prefill {ep:.3e}", flush=True)
+    assert ek < LOGIT_TOL and ep < LOGIT_TOL
+    assert (kt == ref_t).all() and (pt == ref_t).all()
+
+
 @pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 4), (4, 1, 128), (16, 4, 64)])
 def test_gqa_decode_vs_oracle(orc, hip, nh, nkv, hd):
     print(f"[case] GQA nh={nh} nkv={nkv} hd={hd}", flush=True)
