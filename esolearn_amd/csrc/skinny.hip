@@ -22,7 +22,9 @@
 // (deterministic), then applies the scale and the bias.
 //
 // Fused form (the batched decode step's projections): the k splits write
-// their partials as above, and k_skinny_epi (one workgroup per column tile)
+// their partials as above -- per-tensor weights through k_skinny_dg, on the
+// int8 matrix cores with the activations as int8 digits (below) -- and
+// k_skinny_epi (one workgroup per column tile)
 // adds them in split order and applies the epilogue: store, residual add
 // (plus per-row partial sums of squares of the result for the next RMSNorm),
 // SwiGLU of the fused gate/up rows, or logits (plus per-row ordered argmax
@@ -285,6 +287,214 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
         }
 }
 
+// The fused form with per-tensor int8 weights (the batched decode step's
+// projections) on the int8 matrix cores.  The workgroup's activation segment
+// (its KS 64-wide blocks of each row, x * g for the RMSNorm'd inputs) is
+// carried as fixed point per row: E with max|v| 2^E <= 2^23 - 2^16 - 1 over
+// the segment, X = rint(v 2^E) (a power-of-two scaling, one rounding:
+// |v - X 2^-E| <= 2^-24 max|v|), and X = d0 + 2^8 d1 + 2^16 d2 in balanced
+// int8 digits.  Three v_mfma_i32_16x16x64_i8 per 64-wide block and 16
+// columns (one per digit plane) against the weight bytes as they are
+// (q = byte XOR 0x80) give exact integer sums (|d q| <= 2^14, 512 values per
+// segment); the split's partial is f32(S 2^-E) with S = A2 2^16 + A1 2^8 + A0
+// formed exactly in f64.  A segment holding a NaN or an infinity gives NaN
+// partials for its row (the prefill digit GEMM does the same).
+// LDS: digit fragments [kb][plane][lane group][row] of 16 bytes (rows below
+// MRT), the per-wave weight tile of k_skinny, per-(wave, row) maxima.
+constexpr int SK_DG_NONFINITE = 0x7fffffff;
+constexpr double SK_DG_XMAX = 8323071.0;  // 2^23 - 2^16 - 1
+
+template <int KS, bool NORM, int MRT>
+__global__ __launch_bounds__(SK_NT) void k_skinny_dg(SkArgs a) {
+    static_assert(KS % 2 == 0, "weights come in 128-byte segments of two blocks");
+    static_assert(MRT == 4 || MRT == 16, "4 or 16 activation rows");
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    __shared__ u32x4 s_d[KS * 3 * 4 * MRT];
+    __shared__ __attribute__((aligned(16))) unsigned char s_w[4 * SK_WTILE];
+    __shared__ float s_wmax[4][MRT];
+    __shared__ int s_wbad[4][MRT];
+    __shared__ int s_e[MRT];
+    const int split = blockIdx.x % a.n_split, tile = blockIdx.x / a.n_split;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kb0 = split * KS;
+    const int nkb = min(KS, a.kblocks - kb0);
+    const int k0 = kb0 * 64;
+
+    // ---- 1. activation loads: unit u = (kb, row, q8) holds x[row][k0 + 64 kb + 8 q8 + 0..7];
+    // every unit of a thread has the same row, (tid / 8) % MRT
+    constexpr int NU = KS * MRT * 8, UPT = (NU + SK_NT - 1) / SK_NT;
+    const int myrow = (tid >> 3) % MRT;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, ((size_t)(a.m - 1) * a.ldx + a.k) * 4);
+    float4 xv[UPT][2];
+    float4 gv[NORM ? UPT : 1][2];
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(NORM ? a.g : a.x, NORM ? (size_t)a.k * 4 : 0);
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = tid + SK_NT * i, kb = u / (8 * MRT), q8 = u & 7;
+        const int kk = k0 + kb * 64 + q8 * 8;
+        const bool in = (NU % SK_NT == 0 || u < NU) && myrow < a.m && kb < nkb && kk < a.k;
+        const unsigned off = in ? (unsigned)(myrow * a.ldx + kk) * 4 : 0x80000000u;
+        xv[i][0] = bload16f(xr, off);
+        xv[i][1] = bload16f(xr, off + 16);
+        if constexpr (NORM) {
+            const unsigned og = in ? (unsigned)kk * 4 : 0x80000000u;
+            gv[i][0] = bload16f(gr, og);
+            gv[i][1] = bload16f(gr, og + 16);
+        }
+    }
+
+    // ---- 2. the wave's 32 weight rows over this split, all requested now
+    const int cw = tile * SK_COLS + wave * 32;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, (size_t)a.n * a.kp);
+    constexpr int NSEG = KS / 2;
+    u32x4 wv[NSEG][4];
+#pragma unroll
+    for (int sg = 0; sg < NSEG; sg++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = cw + 8 * j + (lane >> 3);
+            const bool ok = 2 * sg < nkb && row < a.n;
+            wv[sg][j] = bload16(wr, ok ? (unsigned)row * a.kp + k0 + 128 * sg + 16 * (lane & 7) : 0x80000000u);
+        }
+
+    // ---- 3. the values, the segment maximum of each row, the digit planes
+    float v[UPT][8];
+    float amax = 0.f;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = tid + SK_NT * i, kb = u / (8 * MRT), q8 = u & 7;
+        const int kk = k0 + kb * 64 + q8 * 8;
+        const float xs[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                             xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float t = xs[e];
+            if constexpr (NORM) {
+                const float gg8[8] = {gv[i][0].x, gv[i][0].y, gv[i][0].z, gv[i][0].w,
+                                      gv[i][1].x, gv[i][1].y, gv[i][1].z, gv[i][1].w};
+                t = __fmul_rn(t, gg8[e]);
+            }
+            if (kk + e >= a.k || (NU % SK_NT != 0 && u >= NU)) t = 0.f;  // past the row / no unit
+            v[i][e] = t;
+            amax = fmaxf(amax, fabsf(t));
+            bad |= !isfinite(t);
+        }
+    }
+    // lanes of one row: MRT 4: lane bits 0-2 and 5 vary; MRT 16: bits 0-2
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off));
+        bad |= __shfl_xor(bad, off);
+    }
+    if constexpr (MRT == 4) {
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        bad |= __shfl_xor(bad, 32);
+    }
+    if ((lane & 7) == 0 && (MRT == 16 || lane < 32)) {
+        s_wmax[wave][myrow] = amax;
+        s_wbad[wave][myrow] = bad;
+    }
+    __syncthreads();
+    if (tid < MRT) {  // waves holding row tid: all four (MRT 4), or tid / 8 and tid / 8 + 2
+        float m = 0.f;
+        int b = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            if (MRT == 4 || (w & 1) == (tid >> 3)) {
+                m = fmaxf(m, s_wmax[w][tid]);
+                b |= s_wbad[w][tid];
+            }
+        int E = 0;
+        if (b) {
+            E = SK_DG_NONFINITE;
+        } else if (m > 0.f) {
+            int ex;
+            frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
+            E = 23 - ex;
+            if (ldexp((double)m, E) > SK_DG_XMAX) E--;
+        }
+        s_e[tid] = E;
+    }
+    __syncthreads();
+    {
+        const int E = s_e[myrow];
+        const int Es = E == SK_DG_NONFINITE ? 0 : E;
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = tid + SK_NT * i, kb = u / (8 * MRT), q8 = u & 7;
+            if (NU % SK_NT != 0 && u >= NU) break;
+            unsigned b[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                // v 2^E is exact in f32 (a power-of-two scaling to at most 2^23), rint then exact
+                const int X = E == SK_DG_NONFINITE ? 0 : (int)rintf(ldexpf(v[i][e], Es));
+                const int X1 = (X - (int)(signed char)X) >> 8;
+                const int X2 = (X1 - (int)(signed char)X1) >> 8;
+                const int sh = 8 * (e & 3);
+                b[0][e >> 2] |= (unsigned)(X & 255) << sh;
+                b[1][e >> 2] |= (unsigned)(X1 & 255) << sh;
+                b[2][e >> 2] |= (unsigned)(X2 & 255) << sh;
+            }
+            // k = 64 kb + 16 g + 8 h + e: lane group g = q8 / 2, half h = q8 % 2
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                unsigned char *frag = reinterpret_cast<unsigned char *>(&s_d[((kb * 3 + p) * 4 + (q8 >> 1)) * MRT + myrow]);
+                *reinterpret_cast<uint2 *>(frag + 8 * (q8 & 1)) = make_uint2(b[p][0], b[p][1]);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 4. per 128-byte segment: weights through the wave's LDS tile, then
+    // three int8 matrix-core passes (one per digit plane) per block and 16 columns
+    unsigned char *tw = s_w + wave * SK_WTILE;
+    const int nn = lane & 15, g = lane >> 4;
+    i32x4 acc[3][2];
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++) acc[p][cb] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int sg = 0; sg < NSEG; sg++) {
+        if (2 * sg >= nkb) break;  // uniform
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *(u32x4 *)(tw + (8 * j + (lane >> 3)) * SK_WROW + 16 * (lane & 7)) = wv[sg][j];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int kb = 2 * sg + h;
+            if (kb >= nkb) break;  // uniform
+            i32x4 ad[3];
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+                ad[p] = nn < MRT ? __builtin_bit_cast(i32x4, s_d[((kb * 3 + p) * 4 + g) * MRT + nn]) : i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++) {
+                const u32x4 w = *(const u32x4 *)(tw + (16 * cb + nn) * SK_WROW + 64 * h + 16 * g) ^ 0x80808080u;
+                const i32x4 bq = __builtin_bit_cast(i32x4, w);
+#pragma unroll
+                for (int p = 0; p < 3; p++)
+                    acc[p][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ad[p], bq, acc[p][cb], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- 5. this split's partial sums: lane holds rows 4 g + r of column cw + 16 cb + nn
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int row = 4 * g + r;
+        if (row >= a.m) continue;
+        const int E = s_e[row < MRT ? row : 0];
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++) {
+            const double S = (double)acc[2][cb][r] * 65536.0 + (double)acc[1][cb][r] * 256.0 + (double)acc[0][cb][r];
+            const float val = E == SK_DG_NONFINITE ? __builtin_nanf("") : (float)(S * ldexp(1.0, -E));
+            a.part[((size_t)split * SK_ROWS + row) * a.n_pad + cw + 16 * cb + nn] = val;
+        }
+    }
+}
+
 __device__ __forceinline__ ArgAcc wave_argmax(ArgAcc a) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -457,8 +667,20 @@ int launch_ks(const SkArgs &a, int tiles, hipStream_t s) {
     return SCRY_OK;
 }
 
+template <int KS, bool NORM>
+int launch_dg(const SkArgs &a, hipStream_t s) {
+    const dim3 grid(a.tiles * a.n_split);
+    if (a.m <= 4)
+        hipLaunchKernelGGL((k_skinny_dg<KS, NORM, 4>), grid, dim3(SK_NT), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_skinny_dg<KS, NORM, 16>), grid, dim3(SK_NT), 0, s, a);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
+
 template <bool NORM>
 int launch_main(const SkArgs &a, int ks, bool b32, hipStream_t s) {
+    if (!b32) return ks == 8 ? launch_dg<8, NORM>(a, s) : launch_dg<4, NORM>(a, s);
     if (ks == 8) return b32 ? launch_ks<8, true, NORM>(a, a.tiles, s) : launch_ks<8, false, NORM>(a, a.tiles, s);
     return b32 ? launch_ks<4, true, NORM>(a, a.tiles, s) : launch_ks<4, false, NORM>(a, a.tiles, s);
 }
