@@ -103,14 +103,20 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
             if (r >= nrep) break;
             float sc[U];
             float mx = m[r];
+            bool any = false;
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 float d = qf[r].x * kv[u].x + qf[r].y * kv[u].y + qf[r].z * kv[u].z + qf[r].w * kv[u].w;
                 d = group_sum<G>(d);
-                sc[u] = (tb + u * P + sub < t1) ? d : -INFINITY;
+                const bool in = tb + u * P + sub < t1;
+                any |= in;
+                sc[u] = in ? d : -INFINITY;
                 mx = fmaxf(mx, sc[u]);
             }
-            if (mx == -INFINITY) continue;  // this lane group has no position yet
+            // no position of this lane group in the step; a step of NaN scores
+            // only is not skipped: with mx = -inf its sum becomes NaN (the
+            // reference's softmax of a NaN score is NaN, cpu.rs:336-366)
+            if (!any) continue;
             const float f = expf(m[r] - mx);
             l[r] *= f;
             o[r].x *= f;
@@ -143,9 +149,14 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
     const bool single = a.n_splits == 1;
     for (int idx = tid; idx < nrep * hd; idx += NT) {
         const int r = idx / hd, d = idx % hd;
+        // a lane group that saw only NaN scores has max -inf and a NaN sum
         float M = -INFINITY;
+        bool poison = false;
 #pragma unroll
-        for (int q = 0; q < SLOTS; q++) M = fmaxf(M, s_m[q][r]);
+        for (int q = 0; q < SLOTS; q++) {
+            M = fmaxf(M, s_m[q][r]);
+            poison |= isnan(s_l[q][r]);
+        }
         float lsum = 0.f, osum = 0.f;
         if (M != -INFINITY) {
 #pragma unroll
@@ -156,8 +167,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
                 osum += s_o[((size_t)q * NR + r) * hd + d] * f;
             }
         }
+        if (poison) lsum = osum = __builtin_nanf("");
         if (single) {  // the whole sequence: softmax-normalised row
-            a.xa[(size_t)(g * nrep + r) * hd + d] = M == -INFINITY ? 0.f : osum / lsum;
+            a.xa[(size_t)(g * nrep + r) * hd + d] = M == -INFINITY && !poison ? 0.f : osum / lsum;
             continue;
         }
         const size_t ph = (size_t)(g * nrep + r) * a.n_splits + split;
@@ -192,8 +204,12 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
             oq[q] = q < ns ? cload(po + (size_t)q * hd) : 0.f;
         }
         float M = -INFINITY;
+        bool poison = false;
 #pragma unroll
-        for (int q = 0; q < MAX_SPLITS; q++) M = fmaxf(M, mq[q]);
+        for (int q = 0; q < MAX_SPLITS; q++) {
+            M = fmaxf(M, mq[q]);
+            poison |= isnan(lq[q]);
+        }
         float Ls = 0.f, v = 0.f;
 #pragma unroll
         for (int q = 0; q < MAX_SPLITS; q++) {
@@ -203,7 +219,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
                 v += oq[q] * e;
             }
         }
-        a.xa[(size_t)h * hd + d] = M == -INFINITY ? 0.f : v / Ls;
+        a.xa[(size_t)h * hd + d] = poison ? __builtin_nanf("") : M == -INFINITY ? 0.f : v / Ls;
     }
     if (tid == 0) a.merge_ctr[(size_t)g * kCtrStride] = 0;  // ready for the next launch on the stream
 }

@@ -281,3 +281,29 @@ def test_forward_nonfinite_norm_output(tmp_path, orc, hip):
     assert np.isnan(fr).all() and np.isnan(fg).all()
     hm.free()
     om.close()
+
+
+def test_decode_batch_nonfinite_norm_output(tmp_path, orc, hip):
+    """The batched decode step with an infinite RMSNorm weight: its int8-digit
+    projections mark the row segment holding the infinity and give NaN, as
+    the reference's sums of inf * q do; every logit of the first step is NaN
+    on both sides (one-token prompts: no prefill)."""
+    cfg = dict(BASE, n_layers=1)
+    _, tensors = make_checkpoint(tmp_path, cfg, 23, False, [torch.float32])
+    paths, t2 = _with_norm_weights(tmp_path, cfg, tensors,
+                                   {("model.layers.0.input_layernorm.weight", 5): float("inf")})
+    print("[case] decode_batch with an infinite norm weight", flush=True)
+    hm = hip.LlamaModel.from_safetensors(hip.LlamaConfig(**dict(cfg, tie_word_embeddings=False)), paths)
+    om = oracle_model(orc, cfg, t2, False)
+    prompts = [orc.prompt_ids(7 + i, 1, cfg["vocab_size"]) for i in range(3)]
+    caches = [hm.new_llama_kv_cache(16) for _ in prompts]
+    _, lg = hm.decode_batch(caches, [int(p[0]) for p in prompts], 2, want_logits=True)
+    for c in caches:
+        c.free()
+    for i, p in enumerate(prompts):
+        _, rl = om.generate_greedy(np.asarray(p, np.int64), 2, mode=1, want_logits=True)
+        print(f"[nan] sequence {i}: oracle {np.isnan(np.asarray(rl[0])).mean():.3f} "
+              f"gpu {np.isnan(lg[0, i]).mean():.3f}", flush=True)
+        assert np.isnan(np.asarray(rl[0])).all() and np.isnan(lg[0, i]).all()
+    hm.free()
+    om.close()
