@@ -415,6 +415,40 @@ __device__ __forceinline__ void qgemv_block(const KArgs &a, const int bx, const 
             val[mi][r] = sc * s;
         }
     }
+    if constexpr (!WB && (EPI == EPI_STORE || EPI == EPI_LOGITS)) {
+        // An activation row holding an infinity or a NaN: the +128 bias
+        // removal made the sum NaN (inf - inf), while the reference's sum of
+        // q x is +-inf unless a NaN term or both infinities occur.  Only the
+        // terms of the non-finite values decide it, so a NaN sum (uniform in
+        // the wave; never the case for finite rows) scans the row's staged
+        // values and classifies those terms.  Done where the sums are final
+        // (matmul_i8_f32, the logits); the decode step's other projections
+        // feed an RMSNorm or a softmax, which make +-inf and NaN alike NaN.
+        {
+#pragma unroll
+            for (int mi = 0; mi < MT; mi++) {
+#pragma unroll
+                for (int r = 0; r < RWT; r++) {
+                    if (!isnan(val[mi][r])) continue;
+                    const float sc = WT != WT_I8 ? 1.f : (EPI == EPI_SWIGLU && ((row0 + r) & 2)) ? a.scale2 : a.scale;
+                    int cls = 0;  // +inf, -inf, NaN terms seen
+#pragma unroll 1
+                    for (int j = lane; j < a.k; j += 64) {
+                        const float x = xs[mi * kc + xslot(j >> 10, (j >> 2) & 255) + (j & 3)];
+                        if (!isfinite(x)) {
+                            const int q = (int)(signed char)(a.W[(size_t)wrow[r] * a.kp + j] ^ 0x80);
+                            const float ws = B32 ? a.s32[(size_t)wrow[r] * a.nb + (j >> 5)] : sc;
+                            const float t = x * ((float)q * ws);
+                            cls |= isnan(t) ? 4 : t > 0.f ? 1 : 2;
+                        }
+                    }
+#pragma unroll
+                    for (int off = 32; off > 0; off >>= 1) cls |= __shfl_xor(cls, off);
+                    if (cls) val[mi][r] = (cls & 4) || cls == 3 ? __builtin_nanf("") : cls == 1 ? INFINITY : -INFINITY;
+                }
+            }
+        }
+    }
 
     // ---- 5. epilogues
     if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {

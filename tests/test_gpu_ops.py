@@ -223,6 +223,31 @@ def test_skinny_matmul_nonfinite(hip, orc):
     assert rel_err(out[fin], ref[fin]) < 2e-5
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 512), (2, 4096, 512), (1, 11008, 256), (1, 300, 64)])
+def test_gemv_matmul_nonfinite(hip, orc, m, k, n):
+    """The GEMV rows (m <= 2) with Inf and NaN activations, as the skinny test
+    above: Inf times a nonzero weight stays infinite, times 0 is NaN."""
+    B = hip.HipBackend
+    rng = np.random.default_rng(31 + m + k)
+    a = rng.normal(0, 1, (m, k)).astype(F)
+    a[0, 3] = np.inf
+    a[0, 900 % k] = np.nan if m == 1 and k == 11008 else a[0, 900 % k]
+    if m > 1:
+        a[1, 100] = -np.inf
+    q = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    q[3, :16] = 0
+    ref = orc.matmul_i8_f32(a, q, 0.01, m, k, n)
+    out = B.matmul_i8_f32(B.from_vec(a), B.i8_from_vec(q), 0.01, m, k, n).to_vec().reshape(m, n)
+    print(f"[nf] m={m} k={k}: inf gpu {int(np.isinf(out).sum())} ref {int(np.isinf(ref).sum())}, "
+          f"nan gpu {int(np.isnan(out).sum())} ref {int(np.isnan(ref).sum())}", flush=True)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    assert np.array_equal(np.isinf(out), np.isinf(ref))
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.sign(out[np.isinf(out)]), np.sign(ref[np.isinf(ref)]))
+    if fin.any():
+        assert rel_err(out[fin], ref[fin]) < 2e-5
+
+
 def test_matmul_shape_errors(hip):
     B = hip.HipBackend
     with pytest.raises(hip.ScryHipError) as ei:
