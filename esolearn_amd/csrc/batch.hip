@@ -37,36 +37,6 @@ __global__ __launch_bounds__(128) void k_bd_embed(const float *__restrict__ embe
     if (threadIdx.x == 0) ss[(size_t)y * n_ss + blockIdx.x] = sh[0] + sh[1];
 }
 
-// Thread e of row y: q pair e (e < qd/2), k pair e - qd/2 (< kvd/2), or the v
-// pair after them.  Rotation in f32 without contraction, as the step's QKV
-// epilogue.
-__global__ __launch_bounds__(256) void k_bd_rope_kv(const float *__restrict__ qkv, int ldq, int qd, int kvd,
-                                                    int hd, float q_scale, DecodeSeqs d, AttnSeqs c,
-                                                    float *__restrict__ q_out) {
-    const int y = blockIdx.y, e = blockIdx.x * 256 + threadIdx.x;
-    const int nq = qd >> 1, nk = kvd >> 1;
-    if (e >= nq + 2 * nk) return;
-    const int pos = d.pos[y];
-    const float *row = qkv + (size_t)y * ldq;
-    const size_t at = (size_t)c.layer * c.ls[y] + (size_t)pos * kvd;
-    if (e >= nq + nk) {
-        const int j = 2 * (e - nq - nk);
-        *(float2 *)(c.v[y] + at + j) = *(const float2 *)(row + qd + kvd + j);
-        return;
-    }
-    const bool isq = e < nq;
-    const int j = isq ? 2 * e : 2 * (e - nq);
-    const float2 cs = d.rope[y][(size_t)pos * (hd >> 1) + ((j % hd) >> 1)];
-    const float2 xv = *(const float2 *)(row + (isq ? 0 : qd) + j);
-    const float r0 = __fsub_rn(__fmul_rn(xv.x, cs.x), __fmul_rn(xv.y, cs.y));
-    const float r1 = __fadd_rn(__fmul_rn(xv.x, cs.y), __fmul_rn(xv.y, cs.x));
-    if (isq) {
-        *(float2 *)(q_out + (size_t)y * qd + j) = make_float2(__fmul_rn(r0, q_scale), __fmul_rn(r1, q_scale));
-    } else {
-        *(float2 *)(c.k[y] + at + j) = make_float2(r0, r1);
-    }
-}
-
 // One workgroup per sequence: the ordered argmax of its logits row (from the
 // LM head's per-tile partials, combined in any order) becomes the token at
 // pos + 1, and the position advances.
@@ -105,19 +75,6 @@ int launch_bd_embed(const float *embed, int h, const DecodeSeqs &d, float *x, do
     if (d.n < 1 || d.n > PF_MAX_SEQS) return set_error(SCRY_ERR_INVALID, "batched decode: %d sequences", d.n);
     const int n_ss = (h + 127) / 128;
     hipLaunchKernelGGL(k_bd_embed, dim3(n_ss, d.n), dim3(128), 0, s, embed, h, d, x, ss, n_ss);
-    SCRY_HIP(hipGetLastError());
-    return SCRY_OK;
-}
-
-int launch_bd_rope_kv(const float *qkv, int ldq, int qd, int kvd, int hd, float q_scale, const DecodeSeqs &d,
-                      const AttnSeqs &c, float *q_out, hipStream_t s) {
-    if (d.n < 1 || d.n > PF_MAX_SEQS || c.n != d.n)
-        return set_error(SCRY_ERR_INVALID, "batched decode: %d sequences", d.n);
-    if (hd % 2 || qd % hd || kvd % hd || ldq % 2 || (uintptr_t)qkv % 8 || (uintptr_t)q_out % 8)
-        return set_error(SCRY_ERR_INVALID, "batched decode: bad head dims or alignment for rope_kv");
-    const int n = (qd >> 1) + kvd;
-    hipLaunchKernelGGL(k_bd_rope_kv, dim3((n + 255) / 256, d.n), dim3(256), 0, s, qkv, ldq, qd, kvd, hd, q_scale,
-                       d, c, q_out);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }

@@ -178,6 +178,8 @@ size_t skinny_ws_bytes(int m, int k, int n);  // n: packed weight rows (2 n for 
 // in the activation staging, and one workgroup per 128-column tile adds the
 // k splits' partials in split order and applies the epilogue.
 enum { SKE_STORE = 1, SKE_RESID = 2, SKE_SWIGLU = 3, SKE_LOGITS = 4 };
+struct DecodeSeqs;
+struct AttnSeqs;
 struct SkinnyFused {
     const Packed *w = nullptr;
     const float *x = nullptr;
@@ -194,6 +196,15 @@ struct SkinnyFused {
     double *ss_out = nullptr;  // RESID (may be null): [m][skinny_tiles(w)] partial sums of squares of y
     float *pv = nullptr;       // LOGITS: [m][skinny_tiles(w)] ordered argmax partials
     int *pi = nullptr, *pn = nullptr;
+    // STORE of the qkv rows of a batched decode step (row i = sequence i):
+    // with rope_d, y is not written; q is rotated and scaled into q_out
+    // [m][qd], k rotated and v stored into the caches of rope_c at each
+    // sequence's position
+    const DecodeSeqs *rope_d = nullptr;
+    const AttnSeqs *rope_c = nullptr;
+    float *q_out = nullptr;
+    int qd = 0, kvd = 0, hd = 0;
+    float q_scale = 1.f;
 };
 int skinny_tiles(const Packed &w);  // 128-row tiles of the packed rows
 int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStream_t s);
@@ -325,10 +336,6 @@ struct DecodeSeqs {
 // x [n][h] = the embedding rows of the current tokens; ss [n][ceil(h / 128)]
 // their partial sums of squares (f64) for the first RMSNorm
 int launch_bd_embed(const float *embed, int h, const DecodeSeqs &d, float *x, double *ss, hipStream_t s);
-// RoPE of q (then times q_scale, into q_out [n][qd]) and k; the K / V rows are
-// written at pos into layer c.layer of each cache
-int launch_bd_rope_kv(const float *qkv, int ldq, int qd, int kvd, int hd, float q_scale, const DecodeSeqs &d,
-                      const AttnSeqs &c, float *q_out, hipStream_t s);
 // ordered argmax of logits [n][V] per sequence (from the np per-row argmax
 // partials of the LM head's fused skinny launch) -> tokens[pos + 1]; pos += 1
 int launch_bd_argmax(const float *logits, int V, const float *pv, const int *pi, const int *pn, int np,

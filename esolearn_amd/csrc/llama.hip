@@ -905,8 +905,19 @@ int record_batch_step(scry_llama m, const DecodeSeqs &d, AttnSeqs c, int n_split
     auto &B = m->bd;
     const int n = d.n;
     const int n_ss = (m->h + 127) / 128;  // partial sums per residual row (128-column tiles)
-    auto mm = [&](const Packed &w, const float *x, int ldx, const float *norm_w, int epi, float *y, int ldy) {
+    const float q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
+    auto mm = [&](const Packed &w, const float *x, int ldx, const float *norm_w, int epi, float *y, int ldy,
+                  bool rope = false) {
         SkinnyFused f;
+        if (rope) {  // RoPE and the K / V append in the epilogue
+            f.rope_d = &d;
+            f.rope_c = &c;
+            f.q_out = B.q;
+            f.qd = m->q_dim;
+            f.kvd = m->kv_dim;
+            f.hd = m->hd;
+            f.q_scale = q_scale;
+        }
         f.w = &w;
         f.x = x;
         f.ldx = ldx;
@@ -935,13 +946,11 @@ int record_batch_step(scry_llama m, const DecodeSeqs &d, AttnSeqs c, int n_split
     at.head_dim = m->hd;
     at.n_splits = n_splits;
     at.max_chunk = max_chunk;
-    const float q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
     SCRY_TRY(launch_bd_embed(m->embed, m->h, d, B.x, B.ss, s));
     for (int l = 0; l < m->L; l++) {
         const auto &Ly = m->layers[l];
         c.layer = l;
-        SCRY_TRY(mm(Ly.qkv, B.x, m->h, m->norm_in(l), SKE_STORE, B.qkv, m->qkv_dim));
-        SCRY_TRY(launch_bd_rope_kv(B.qkv, m->qkv_dim, m->q_dim, m->kv_dim, m->hd, q_scale, d, c, B.q, s));
+        SCRY_TRY(mm(Ly.qkv, B.x, m->h, m->norm_in(l), SKE_STORE, B.qkv, m->qkv_dim, true));
         SCRY_TRY(launch_attn_decode_seqs(at, c, s));
         SCRY_TRY(mm(Ly.o, B.xa, m->q_dim, nullptr, SKE_RESID, B.x, m->h));
         SCRY_TRY(mm(Ly.gu, B.x, m->h, m->norm_post(l), SKE_SWIGLU, B.act, m->ffn));

@@ -67,6 +67,11 @@ struct SkArgs {
     double *ss_out;  // SKE_RESID: per-row partial sums of squares of y [m][tiles]
     float *pv;       // SKE_LOGITS: per-row ordered argmax partials [m][tiles]
     int *pi, *pn;
+    // k_skinny_epi_rope: q (rotated, times q_scale) into q_out [m][qd]; k
+    // (rotated) and v into the K / V caches of the batched decode sequences
+    float *q_out;
+    int qd, kvd, hd;
+    float q_scale;
 };
 
 
@@ -522,9 +527,12 @@ __device__ __forceinline__ void arg_push(ArgAcc &p, float v, int i) {  // sequen
 // columns 2l, 2l + 1 of the tile, or (SwiGLU, lanes 0..31) the packed group
 // 4l .. 4l + 3 = gate and up of outputs 2l, 2l + 1.  Every split's partials
 // of a batch are requested before the first is used; the sums run in split
-// order.
-template <int EPI>
-__global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
+// order.  ROPE (STORE of the qkv rows of a batched decode step, row = the
+// sequence): the lane's column pair is a RoPE pair; q and k are rotated in
+// f32 without contraction (as the single-sequence step's QKV epilogue) and q
+// scaled, and k and v go to the caches at the row's position.
+template <int EPI, bool ROPE>
+__device__ __forceinline__ void skinny_epi_body(const SkArgs &a, const DecodeSeqs *rd, const AttnSeqs *rc) {
     const int tile = blockIdx.x;
     constexpr bool SW = EPI == SKE_SWIGLU;
     constexpr int NB = SW ? 16 : 32;  // splits per load batch
@@ -578,8 +586,29 @@ __global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
                 if (ok0) v0 = yr[c] + v0;
                 if (ok1) v1 = yr[c1] + v1;
             }
-            if (ok0) yr[c] = v0;
-            if (ok1) yr[c1] = v1;
+            if constexpr (ROPE) {  // llama.rs:384-396 (apply_rotary_emb on the adjacent pair)
+                if (ok1) {  // c is even and the row length qd + 2 kvd is even: the pair is whole
+                    const int pos = rd->pos[row];
+                    const size_t at = (size_t)rc->layer * rc->ls[row] + (size_t)pos * a.kvd;
+                    if (c >= a.qd + a.kvd) {
+                        *(float2 *)(rc->v[row] + at + (c - a.qd - a.kvd)) = make_float2(v0, v1);
+                    } else {
+                        const bool isq = c < a.qd;
+                        const int j = isq ? c : c - a.qd;
+                        const float2 cs = rd->rope[row][(size_t)pos * (a.hd >> 1) + ((j % a.hd) >> 1)];
+                        const float r0 = __fsub_rn(__fmul_rn(v0, cs.x), __fmul_rn(v1, cs.y));
+                        const float r1 = __fadd_rn(__fmul_rn(v0, cs.y), __fmul_rn(v1, cs.x));
+                        if (isq)
+                            *(float2 *)(a.q_out + (size_t)row * a.qd + j) =
+                                make_float2(__fmul_rn(r0, a.q_scale), __fmul_rn(r1, a.q_scale));
+                        else
+                            *(float2 *)(rc->k[row] + at + j) = make_float2(r0, r1);
+                    }
+                }
+            } else {
+                if (ok0) yr[c] = v0;
+                if (ok1) yr[c1] = v1;
+            }
             if constexpr (EPI == SKE_RESID) {
                 if (a.ss_out) {
                     double q = (ok0 ? (double)v0 * (double)v0 : 0.0) + (ok1 ? (double)v1 * (double)v1 : 0.0);
@@ -601,6 +630,15 @@ __global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
             }
         }
     }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
+    skinny_epi_body<EPI, false>(a, nullptr, nullptr);
+}
+
+__global__ __launch_bounds__(SK_NT) void k_skinny_epi_rope(SkArgs a, DecodeSeqs d, AttnSeqs c) {
+    skinny_epi_body<SKE_STORE, true>(a, &d, &c);
 }
 
 // y[row][col] = scale * (sum of the splits' partials, in split order) (+ bias[col]);
@@ -772,6 +810,13 @@ int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStr
         return set_error(SCRY_ERR_INVALID, "skinny matmul: RMSNorm input needs 1..64 partial sums per row");
     if (f.epi == SKE_LOGITS && (!f.pv || !f.pi || !f.pn))
         return set_error(SCRY_ERR_INVALID, "skinny matmul: logits epilogue needs argmax partials");
+    if (f.rope_d) {
+        const DecodeSeqs &d = *f.rope_d;
+        const AttnSeqs &c = *f.rope_c;
+        if (f.epi != SKE_STORE || !f.rope_c || !f.q_out || c.n != d.n || d.n != f.m || !d.pos || f.hd < 2 ||
+            f.hd % 2 || f.qd % f.hd || f.kvd % f.hd || w.n != f.qd + 2 * f.kvd || (uintptr_t)f.q_out % 8)
+            return set_error(SCRY_ERR_INVALID, "skinny matmul: rope epilogue needs the qkv rows of the batched step");
+    }
     const SkPlan p = plan(w.k, w.rows);
     if (ws_bytes < skinny_ws_bytes(f.m, w.k, w.rows))
         return set_error(SCRY_ERR_INVALID, "skinny matmul: workspace too small");
@@ -804,7 +849,17 @@ int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStr
     a.pv = f.pv;
     a.pi = f.pi;
     a.pn = f.pn;
+    a.q_out = f.q_out;
+    a.qd = f.qd;
+    a.kvd = f.kvd;
+    a.hd = f.hd;
+    a.q_scale = f.q_scale;
     SCRY_TRY(f.norm_w ? launch_main<true>(a, p.ks, b32, s) : launch_main<false>(a, p.ks, b32, s));
+    if (f.rope_d) {
+        hipLaunchKernelGGL(k_skinny_epi_rope, dim3(a.tiles), dim3(SK_NT), 0, s, a, *f.rope_d, *f.rope_c);
+        SCRY_HIP(hipGetLastError());
+        return SCRY_OK;
+    }
     switch (f.epi) {
         case SKE_STORE: return launch_epi<SKE_STORE>(a, s);
         case SKE_RESID: return launch_epi<SKE_RESID>(a, s);
