@@ -684,13 +684,18 @@ struct SkPlan {
     int ks, kblocks, n_split, tiles, n_pad;
 };
 
-SkPlan plan(int k, int n) {
+// min_wg: below this many workgroups at 8 k-blocks per split, splits take 4.
+// The bf16-plane kernel was tuned at 512. The int8-digit kernel of the fused
+// form at 256: its qkv and o launches (4 rows, Llama-3-8B shape) then run with
+// 8 partials per column instead of 16, 4 x 64 batched decode 197.65 ->
+// 195.7 ms.
+SkPlan plan(int k, int n, size_t min_wg = 512) {
     SkPlan p;
     p.kblocks = (k + 63) / 64;
     p.tiles = (n + SK_COLS - 1) / SK_COLS;
     p.n_pad = p.tiles * SK_COLS;
     p.ks = 8;
-    if ((size_t)p.tiles * ((p.kblocks + 7) / 8) < 512) p.ks = 4;  // enough workgroups to stream the weights
+    if ((size_t)p.tiles * ((p.kblocks + 7) / 8) < min_wg) p.ks = 4;  // enough workgroups to stream the weights
     p.n_split = (p.kblocks + p.ks - 1) / p.ks;
     return p;
 }
@@ -817,7 +822,8 @@ int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStr
             f.hd % 2 || f.qd % f.hd || f.kvd % f.hd || w.n != f.qd + 2 * f.kvd || (uintptr_t)f.q_out % 8)
             return set_error(SCRY_ERR_INVALID, "skinny matmul: rope epilogue needs the qkv rows of the batched step");
     }
-    const SkPlan p = plan(w.k, w.rows);
+    // the workspace bound below holds: 256 gives no more splits than 512
+    const SkPlan p = plan(w.k, w.rows, w.s32 ? 512 : 256);
     if (ws_bytes < skinny_ws_bytes(f.m, w.k, w.rows))
         return set_error(SCRY_ERR_INVALID, "skinny matmul: workspace too small");
     const bool b32 = w.s32 != nullptr;
