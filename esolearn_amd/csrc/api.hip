@@ -351,6 +351,16 @@ int scry_hip_init(int device) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return set_error(SCRY_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only",
                          device, prop.gcnArchName);
+    // Decode attention hands its split partials over inside one XCD's L2: it
+    // relies on the whole MI355X (8 XCDs of 32 CUs, one partition), whose
+    // dispatcher gives workgroup b to XCD b % 8.  A partitioned device (fewer
+    // CUs per agent) may map blocks to XCDs otherwise, which would read stale
+    // partials instead of faulting, so it is refused.
+    if (prop.multiProcessorCount != 256)
+        return set_error(SCRY_ERR_UNSUPPORTED,
+                         "device %d has %d CUs; the decode attention exchange needs the 256-CU, 8-XCD "
+                         "MI355X in one partition",
+                         device, prop.multiProcessorCount);
     SCRY_TRY(noalloc_setup(device));  // the device address of the static sampler scratch
     SCRY_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
     c.bf16 = false;

@@ -4,6 +4,7 @@
 // and attention kernels.  These serve the per-op API (a Rust HipBackend's
 // trait methods) and the parity tests.
 #include "internal.h"
+#include "kdev.h"
 
 namespace scry {
 namespace {
@@ -167,6 +168,61 @@ __global__ void k_matmul_f32(const float *__restrict__ a, const float *__restric
     }
 }
 
+// Logits of the int8 LM head for rows whose normalised input holds an
+// infinity or a NaN.  The prefill GEMMs mark such a row and give NaN for all
+// of it, while the reference's sum of f64(a) (q s) over k (cpu.rs:1128-1160)
+// is +-inf per column unless a NaN term or both infinities occur; only the
+// terms of the non-finite inputs decide it.  One workgroup per row:
+// RMSNorm's f64 scale (cpu.rs:574-599) and the normalised values
+// f32(f64(x) rstd f64(g)); a row with none non-finite is left as it is;
+// otherwise each 256-position chunk's non-finite values (at most 256) are
+// gathered in LDS and every column's class is folded into its logit (the
+// classes combine in any order).
+__global__ __launch_bounds__(256) void k_logits_nonfinite(const float *__restrict__ x, int ldx,
+                                                          const float *__restrict__ g, float eps, int k,
+                                                          const uint8_t *__restrict__ W, int kp,
+                                                          const float *__restrict__ s32, int nb, float scale,
+                                                          int n, float *__restrict__ y, int ldy) {
+    __shared__ double red[4];
+    __shared__ int s_cnt;
+    __shared__ int s_idx[256];
+    __shared__ float s_val[256];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *xr = x + (size_t)row * ldx;
+    float *yr = y + (size_t)row * ldy;
+    double ss = 0.0;
+    for (int p = tid; p < k; p += 256) ss += (double)xr[p] * (double)xr[p];
+    ss = dev::block_sum_d(ss, red);
+    const double rstd = 1.0 / sqrt(ss / (double)k + (double)eps);
+    bool seen = false;  // uniform: a chunk with non-finite values was folded in
+    for (int p0 = 0; p0 < k; p0 += 256) {
+        const int p = p0 + tid;
+        float t = 0.f;
+        if (p < k) t = g ? (float)((double)xr[p] * rstd * (double)g[p]) : xr[p];
+        __syncthreads();
+        if (tid == 0) s_cnt = 0;
+        __syncthreads();
+        if (p < k && !isfinite(t)) {
+            const int i = atomicAdd(&s_cnt, 1);
+            s_idx[i] = p;
+            s_val[i] = t;
+        }
+        __syncthreads();
+        const int cnt = s_cnt;
+        if (cnt == 0) continue;
+        for (int j = tid; j < n; j += 256) {
+            int cls = seen ? dev::nonfinite_class(yr[j]) : 0;
+            const uint8_t *wr = W + (size_t)j * kp;
+            for (int i = 0; i < cnt; i++) {
+                const int q = s_idx[i];
+                cls |= dev::nonfinite_term(s_val[i], wr[q], s32 ? s32[(size_t)j * nb + (q >> 5)] : scale);
+            }
+            yr[j] = dev::nonfinite_value(cls);
+        }
+        seen = true;
+    }
+}
+
 __global__ void k_fill_f32(float *p, size_t n, float v) { GRID_STRIDE(i, n) p[i] = v; }
 __global__ void k_fill_u32(unsigned int *p, size_t n, unsigned int v) { GRID_STRIDE(i, n) p[i] = v; }
 
@@ -253,6 +309,14 @@ int launch_matmul_f32(const float *a, const float *b, int batch, int m, int k, i
     if (total == 0) return SCRY_OK;
     hipLaunchKernelGGL(k_matmul_f32, dim3(grid1(total)), dim3(256), 0, s, a, b, batch, m, k, n, ta,
                        tb, c);
+    LAUNCH_CHECK();
+}
+
+int launch_logits_nonfinite(const float *x, int ldx, int rows, const float *norm_w, float eps, const Packed &w,
+                            float *y, int ldy, hipStream_t s) {
+    if (rows <= 0 || w.bf16) return SCRY_OK;  // bf16 rows: the GEMM's products already give +-inf
+    hipLaunchKernelGGL(k_logits_nonfinite, dim3(rows), dim3(256), 0, s, x, ldx, norm_w, eps, w.k, w.d, w.kp, w.s32,
+                       w.nb, w.scale, w.rows, y, ldy);
     LAUNCH_CHECK();
 }
 

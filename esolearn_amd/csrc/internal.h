@@ -282,6 +282,10 @@ int launch_matmul_f32(const float *a, const float *b, int batch, int m, int k, i
 int launch_argmax(const float *x, int64_t n, int64_t *out, hipStream_t s);
 int launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
 int launch_fill_u32(unsigned int *p, size_t n, unsigned int v, hipStream_t s);
+// Rows of int8 LM-head logits whose RMSNorm'd input holds a non-finite value:
+// the reference's per-column +-inf / NaN in place of the prefill GEMM's NaN row.
+int launch_logits_nonfinite(const float *x, int ldx, int rows, const float *norm_w, float eps, const Packed &w,
+                            float *y, int ldy, hipStream_t s);
 
 // ops.hip -- the rest of the trait surface
 int launch_layernorm(const float *x, const float *g, const float *b, int rows, int d, float eps, float *out,

@@ -99,6 +99,20 @@ __device__ __forceinline__ double block_sum_d(double v, double *red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
+// Class of one term f64(a) * (f64(q) * f64(s)) of matmul_i8_f32
+// (cpu.rs:1128-1160) with a non-finite activation a, from the stream byte
+// b = q XOR 0x80: 1 = +inf, 2 = -inf, 4 = NaN (q s = 0 or a NaN).
+__device__ __forceinline__ int nonfinite_term(float a, uint8_t b, float s) {
+    const float t = a * ((float)(int)(signed char)(b ^ 0x80u) * s);
+    return isnan(t) ? 4 : t > 0.f ? 1 : 2;
+}
+// The f32 sum of terms of these classes (finite terms cannot change it): NaN
+// when a NaN term or both infinities occur, else the infinity.
+__device__ __forceinline__ float nonfinite_value(int cls) {
+    return (cls & 4) || cls == 3 ? __builtin_nanf("") : cls == 1 ? INFINITY : -INFINITY;
+}
+__device__ __forceinline__ int nonfinite_class(float v) { return isnan(v) ? 4 : v > 0.f ? 1 : 2; }
+
 __device__ __forceinline__ float silu_f(float g) {
     double x = (double)g;  // cpu.rs:1119-1122: computed in f64, rounded once
     return (float)(x / (1.0 + exp(-x)));

@@ -830,6 +830,7 @@ int prefill_core(scry_llama m, scry_kv_cache *cs, int n_seq, const int64_t *toke
         g.c = all_logits;
         g.ldc = m->V;
         SCRY_TRY(launch_gemm(PF_STORE, g, s));
+        SCRY_TRY(launch_logits_nonfinite(P.x, m->h, M, m->norm_final(), eps, m->lm, all_logits, m->V, s));
     }
     if (last_logits) {
         // the last row of each sequence: RMSNorm, then the LM-head GEMV

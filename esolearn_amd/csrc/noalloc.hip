@@ -1,5 +1,7 @@
-// sample_token without any device allocation, for callers that cannot call
-// hipMalloc (code under HIP graph capture, tight serving loops).
+// sample_token without any device allocation, for callers that must not call
+// hipMalloc (between replays of a captured graph, tight serving loops).  It
+// waits for the stream and reads the token and the rng state back on the
+// host, so it cannot itself be captured: call it outside stream capture.
 //
 // scry_hip_sample_token allocates its scratch on every call: the step state
 // and token slots, the wyrand state, an f64 workspace of V entries and, for

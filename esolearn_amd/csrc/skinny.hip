@@ -617,6 +617,39 @@ __device__ __forceinline__ void skinny_epi_body(const SkArgs &a, const DecodeSeq
                 }
             }
             if constexpr (EPI == SKE_LOGITS) {  // generate.rs:167-173, in index order
+                // A row segment holding an infinity or a NaN makes the digit
+                // kernel's partials NaN, while the reference's sum of
+                // f64(a) (q s) over k (cpu.rs:1128-1160) is +-inf per column
+                // unless a NaN term or both infinities occur.  Only the terms
+                // of the non-finite normalised inputs decide it, so a NaN sum
+                // (uniform over the row; never the case for finite rows)
+                // classifies those terms, as the GEMV's logits epilogue does.
+                const bool n0 = ok0 && isnan(v0), n1 = ok1 && isnan(v1);
+                if (__builtin_amdgcn_ballot_w64(n0 || n1)) {
+                    int cls0 = 0, cls1 = 0;
+                    const float *xr = a.x + (size_t)row * a.ldx;
+                    for (int p0 = 0; p0 < a.k; p0 += 64) {
+                        const int p = p0 + lane;
+                        float t = 0.f;
+                        if (p < a.k) {  // rmsnorm (cpu.rs:574-599): f32(f64(x) rstd f64(w))
+                            t = xr[p];
+                            if (a.g) t = (float)((double)t * rstd * (double)a.g[p]);
+                        }
+                        unsigned long long mk = __builtin_amdgcn_ballot_w64(p < a.k && !isfinite(t));
+                        while (mk) {
+                            const int l = __builtin_ctzll(mk);
+                            mk &= mk - 1;
+                            const float tt = __shfl(t, l);
+                            const int pp = p0 + l;
+                            if (n0) cls0 |= nonfinite_term(tt, a.w[(size_t)c * a.kp + pp], a.s32 ? a.s32[(size_t)c * a.nb + (pp >> 5)] : a.scale);
+                            if (n1) cls1 |= nonfinite_term(tt, a.w[(size_t)c1 * a.kp + pp], a.s32 ? a.s32[(size_t)c1 * a.nb + (pp >> 5)] : a.scale);
+                        }
+                    }
+                    if (n0 && cls0) v0 = nonfinite_value(cls0);
+                    if (n1 && cls1) v1 = nonfinite_value(cls1);
+                    if (ok0) yr[c] = v0;
+                    if (ok1) yr[c1] = v1;
+                }
                 ArgAcc pa{0.f, -1, -1};
                 if (ok0) arg_push(pa, v0, c);
                 if (ok1) arg_push(pa, v1, c1);

@@ -175,11 +175,14 @@ int scry_hip_normal_vec(uint64_t *rng_state, size_t n, float mean, float std_dev
 int scry_hip_sample_token(scry_buf logits, const scry_sampling_config *cfg, uint64_t *rng_state,
                           int64_t *out);
 /* No counterpart in the reference: scry_hip_sample_token without any device
- * allocation, for callers that cannot allocate (code under HIP graph capture,
- * tight serving loops).  Same arguments, results and rng advance.  Its scratch
- * is a static device array of about 2 MiB per GPU, held until the process
- * ends; vocabularies above 262144 entries are refused (SCRY_ERR_UNSUPPORTED).
- * All calls on one GPU share that array: calls that overlap on one GPU race. */
+ * allocation, for callers that must not allocate device memory (between
+ * replays of a captured graph, tight serving loops).  Same arguments, results
+ * and rng advance.  It waits for the stream and copies the token and the rng
+ * state back to the host, so it must be called outside stream capture.  Its
+ * scratch is a static device array of about 2 MiB per GPU, held until the
+ * process ends; vocabularies above 262144 entries are refused
+ * (SCRY_ERR_UNSUPPORTED).  All calls on one GPU share that array: calls that
+ * overlap on one GPU race. */
 int scry_hip_sample_token_noalloc(scry_buf logits, const scry_sampling_config *cfg, uint64_t *rng_state,
                                   int64_t *out);
 

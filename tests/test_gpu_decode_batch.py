@@ -5,10 +5,14 @@ every sequence is checked against the oracle's own greedy run of that
 sequence, on the same seeded synthetic weights and token ids.
 
 Bars: each step's logits within 1e-3 relative of the oracle's for that
-sequence and position (the projections run as matrix-core products of exact
-bf16 terms with f32 accumulation: f32 rounding only); greedy tokens
-identical; and against the GPU's single-sequence decode step, identical
-tokens and logits within the same bar.
+sequence and position; greedy tokens identical; and against the GPU's
+single-sequence decode step, identical tokens and logits within the same bar.
+With per-tensor int8 weights the projections run on the int8 matrix cores:
+each activation row's 512-value segment becomes 24-bit fixed point scaled to
+the segment's largest value (one rounding, at most 2^-24 of that maximum per
+value), the products with the weight bytes are summed exactly in i32, and
+each split's partial is rounded once to f32.  Block-32 weights take three
+exact bf16 planes of each value with f32 accumulation.
 """
 import numpy as np
 import pytest

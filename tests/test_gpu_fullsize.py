@@ -14,11 +14,14 @@ computes at step t whenever the tokens before t agree.  Since every earlier
 step's argmax also agrees, its own greedy run produces the same 256 tokens
 (induction on t).
 
-Config 5 (Llama-3-8B shape) is checked twice:
+Config 5 (Llama-3-8B shape) is checked three ways:
   - at its dimensions with 2 layers against the oracle (batched prefill of 4
-    sequences, then greedy steps);
-  - at full size against the GPU's own token-by-token path.  The oracle would
-    need ~6e13 multiply-adds for 4 x 2048 prompts.
+    sequences then greedy steps; the batched decode of 4 and of 8 sequences);
+  - at full depth (32 layers) against the oracle on one sequence: a 64-token
+    batched prefill and 8 greedy steps;
+  - at full size (4 x 2048 prompts, 64 greedy steps) against the GPU's own
+    token-by-token path.  The oracle would need ~6e13 multiply-adds for the
+    4 x 2048 prompts.
 """
 import numpy as np
 import pytest
@@ -153,39 +156,67 @@ def test_config4_full_depth_vs_oracle(hip, orc, model7b):
 
 def test_config5_dims_two_layers_vs_oracle(hip, orc):
     """Config-5 tensor shapes (h4096, 32:8 GQA, ffn 14336, V 128256, theta 5e5)
-    with 2 layers: the batched prefill of 4 x 255 tokens (seeds 1-4) and 16
-    greedy steps per sequence against the oracle."""
+    with 2 layers, against the oracle:
+      - the batched prefill of 4 x 255 tokens (seeds 1-4), then 16 greedy
+        steps per sequence, token by token;
+      - the batched decode step (decode_batch, llama.rs:744-763 per row) of the
+        same 4 sequences, and of 8 sequences (seeds 1-8).  From 5 rows on,
+        every projection and the LM head run the 16-row int8-digit matrix-core
+        kernel with 8 k-blocks per split; at 4 rows the 4-row kernel.
+    Identical greedy tokens, logits within 1e-3 at every step."""
     cfg = dict(LLAMA3_8B, n_layers=2)
-    print("[case] config-5 dims, 2 layers: batched prefill 4 x 255 + 16 greedy", flush=True)
+    NS = 16
+    print("[case] config-5 dims, 2 layers: batched prefill 4 x 255 + 16 greedy; decode_batch 4 and 8",
+          flush=True)
     hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), seed=0, init_on_device=True)
     V = cfg["vocab_size"]
-    prompts = np.stack([orc.prompt_ids(s + 1, 256, V) for s in range(4)])
+    prompts = np.stack([orc.prompt_ids(s + 1, 256, V) for s in range(8)])
     try:
-        caches = [hm.new_llama_kv_cache(256 + 16) for _ in range(4)]
-        last = hm.prefill(caches, prompts[:, :255])
+        caches = [hm.new_llama_kv_cache(256 + NS) for _ in range(4)]
+        last = hm.prefill(caches, prompts[:4, :255])
         gpu_lg, gpu_tok = [], []
         for s in range(4):
             tok, pos, lgs, ts = int(prompts[s, 255]), 255, [], []
-            for _ in range(16):
+            for _ in range(NS):
                 lg, am = hm.forward_with_llama_cache(tok, pos, caches[s])
                 lgs.append(lg)
                 ts.append(am)
                 tok, pos = am, pos + 1
             gpu_lg.append(np.stack(lgs))
             gpu_tok.append(np.array(ts))
+            caches[s].free()
+        batched = {}
+        for n in (4, 8):
+            print(f"[case] config-5 dims, 2 layers: decode_batch of {n} sequences", flush=True)
+            cs = [hm.new_llama_kv_cache(256 + NS) for _ in range(n)]
+            hm.prefill(cs, prompts[:n, :255], want_logits=False)
+            batched[n] = hm.decode_batch(cs, prompts[:n, 255], NS, want_logits=True)
+            for c in cs:
+                c.free()
         orc.set_threads(16)
         om = oracle_from_gpu(orc, hm, cfg)
     finally:
         hm.free()
     try:
-        for s in range(4):
-            seq = np.concatenate([prompts[s], gpu_tok[s][:-1]])  # 271 rows
+        for s in range(8):
+            toks_s = gpu_tok[s] if s < 4 else batched[8][0][s]
+            seq = np.concatenate([prompts[s], toks_s[:-1]])  # 271 rows
             cache = om.new_cache(len(seq))
-            ref = om.forward_cache_seq(cache, seq, 0, n_logits=17)
+            ref = om.forward_cache_seq(cache, seq, 0, n_logits=NS + 1)  # rows 254..270
             del cache
+            ref_toks = np.array([orc.argmax(ref[i + 1]) for i in range(NS)])
+            for n in (4, 8):
+                if s >= n:
+                    continue
+                bt, bl = batched[n]
+                e = max(rel_err(bl[i, s], ref[i + 1]) for i in range(NS))
+                print(f"[err] config-5 dims seq {s}: decode_batch of {n}, max {e:.3e}", flush=True)
+                assert e < LOGIT_TOL
+                assert (bt[s] == ref_toks).all()
+            if s >= 4:
+                continue
             e_pre = rel_err(last[s], ref[0])
-            errs = [rel_err(gpu_lg[s][i], ref[i + 1]) for i in range(16)]
-            ref_toks = np.array([orc.argmax(ref[i + 1]) for i in range(16)])
+            errs = [rel_err(gpu_lg[s][i], ref[i + 1]) for i in range(NS)]
             print(f"[err] config-5 dims seq {s}: prefill last logits {e_pre:.3e}, "
                   f"decode max {max(errs):.3e}", flush=True)
             assert e_pre < LOGIT_TOL
@@ -196,7 +227,46 @@ def test_config5_dims_two_layers_vs_oracle(hip, orc):
         orc.set_threads(0)
 
 
-def test_config5_full_batched_prefill_vs_token_by_token(hip, orc):
+@pytest.fixture(scope="module")
+def model8b(hip):
+    print("[case] config 5 model: Llama-3-8B shape, seed 0, device init (as bench.py)", flush=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**LLAMA3_8B), seed=0, init_on_device=True)
+    yield hm
+    hm.free()
+
+
+def test_config5_full_depth_one_sequence_vs_oracle(hip, orc, model8b):
+    """BASELINE config 5 at full depth (32 layers, GQA 32:8, ffn 14336,
+    V 128256; nn/llama.rs:683-700, 744-763) on one sequence: a 65-token seeded
+    prompt (seed 1), its first 64 tokens through the batched prefill, then 8
+    greedy steps (generate.rs:51-89) -- against the oracle on the GPU model's
+    own int8 weights: identical tokens, logits within 1e-3 at every step."""
+    cfg = LLAMA3_8B
+    V = cfg["vocab_size"]
+    prompt = orc.prompt_ids(1, 65, V)
+    print("[case] config 5 full depth: 64-token batched prefill + 8 greedy", flush=True)
+    toks, lg = model8b.generate_greedy(prompt, 8, want_logits=True, prefill=True)
+    assert len(toks) == 8
+    orc.set_threads(16)
+    om = oracle_from_gpu(orc, model8b, cfg)
+    try:
+        seq = np.concatenate([prompt, toks[:-1]])  # 72 rows; row 64 + i gives step i
+        cache = om.new_cache(len(seq))
+        print("[case] config 5 oracle: layer-major cache path over 72 rows", flush=True)
+        ref = om.forward_cache_seq(cache, seq, 0, n_logits=8)
+        del cache
+    finally:
+        om.close()
+        orc.set_threads(0)
+    errs = np.array([rel_err(lg[i], ref[i]) for i in range(8)])
+    ref_toks = np.array([orc.argmax(ref[i]) for i in range(8)])
+    print(f"[err] config 5 full depth: max step rel err {errs.max():.3e}; tokens {toks.tolist()}; "
+          f"smallest top-1/top-2 margin {min(top2_margin(ref[i]) for i in range(8)):.4g}", flush=True)
+    assert errs.max() < LOGIT_TOL
+    assert (ref_toks == toks).all()
+
+
+def test_config5_full_batched_prefill_vs_token_by_token(hip, orc, model8b):
     """BASELINE config 5 at full size: 4 x 2048-token prompts (seeds 1-4), the
     first 2047 tokens of each through one batched prefill, then 64 greedy
     steps per sequence -- against the GPU's token-by-token cache path of each
@@ -204,9 +274,10 @@ def test_config5_full_batched_prefill_vs_token_by_token(hip, orc):
     cfg = LLAMA3_8B
     print("[case] config 5 full: batched prefill 4 x 2047 + 64 greedy vs token by token",
           flush=True)
-    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), seed=0, init_on_device=True)
+    hm = model8b
     V = cfg["vocab_size"]
     prompts = np.stack([orc.prompt_ids(s + 1, 2048, V) for s in range(4)])
+    caches = []
     try:
         caches = [hm.new_llama_kv_cache(2048 + 64) for _ in range(4)]
         hm.prefill(caches, prompts[:, :2047], want_logits=False)
@@ -226,4 +297,5 @@ def test_config5_full_batched_prefill_vs_token_by_token(hip, orc):
             assert err < LOGIT_TOL
             assert (np.array(ts) == ref_tok).all()
     finally:
-        hm.free()
+        for c in caches:
+            c.free()

@@ -284,10 +284,12 @@ def test_forward_nonfinite_norm_output(tmp_path, orc, hip):
 
 
 def test_decode_batch_nonfinite_norm_output(tmp_path, orc, hip):
-    """The batched decode step with an infinite RMSNorm weight: its int8-digit
-    projections mark the row segment holding the infinity and give NaN, as
-    the reference's sums of inf * q do; every logit of the first step is NaN
-    on both sides (one-token prompts: no prefill)."""
+    """The batched decode step with an infinite input RMSNorm weight in the
+    first layer: q, k and v of every row hold infinities or NaN (the int8-digit
+    projections give NaN for the row segment holding the infinity, the
+    reference +-inf or NaN per column), the attention softmax makes both NaN
+    (cpu.rs:336-366), and every logit of the first step is NaN on both sides
+    (one-token prompts: no prefill)."""
     cfg = dict(BASE, n_layers=1)
     _, tensors = make_checkpoint(tmp_path, cfg, 23, False, [torch.float32])
     paths, t2 = _with_norm_weights(tmp_path, cfg, tensors,
@@ -305,5 +307,51 @@ def test_decode_batch_nonfinite_norm_output(tmp_path, orc, hip):
         print(f"[nan] sequence {i}: oracle {np.isnan(np.asarray(rl[0])).mean():.3f} "
               f"gpu {np.isnan(lg[0, i]).mean():.3f}", flush=True)
         assert np.isnan(np.asarray(rl[0])).all() and np.isnan(lg[0, i]).all()
+    hm.free()
+    om.close()
+
+
+def _same_nonfinite(g, r):
+    """Equal NaN positions and equal values elsewhere (infinities included)."""
+    g, r = np.asarray(g), np.asarray(r)
+    ng, nr = np.isnan(g), np.isnan(r)
+    return np.array_equal(ng, nr) and np.array_equal(g[~ng], r[~nr])
+
+
+def test_nonfinite_final_norm_logits(tmp_path, orc, hip):
+    """An infinite final-norm weight: every LM-head column sums one infinite
+    term, so the reference's logits are +inf, -inf or NaN per column (NaN where
+    q = 0; cpu.rs:1128-1160).  The single-sequence GEMV, the batched decode's
+    int8-digit LM head and the prefill GEMM of forward() give exactly that
+    pattern, and the greedy tokens (generate.rs:167-173) agree."""
+    cfg = dict(BASE, n_layers=1)
+    V = cfg["vocab_size"]
+    _, tensors = make_checkpoint(tmp_path, cfg, 29, False, [torch.float32])
+    paths, t2 = _with_norm_weights(tmp_path, cfg, tensors, {("model.norm.weight", 9): float("inf")})
+    print("[case] infinite final-norm weight: decode, decode_batch, forward", flush=True)
+    hm = hip.LlamaModel.from_safetensors(hip.LlamaConfig(**dict(cfg, tie_word_embeddings=False)), paths)
+    om = oracle_model(orc, cfg, t2, False)
+    prompts = [orc.prompt_ids(31 + i, 1, V) for i in range(3)]
+    caches = [hm.new_llama_kv_cache(16) for _ in prompts]
+    bt, bl = hm.decode_batch(caches, [int(p[0]) for p in prompts], 3, want_logits=True)
+    for c in caches:
+        c.free()
+    for i, p in enumerate(prompts):
+        rt, rl = om.generate_greedy(np.asarray(p, np.int64), 3, mode=1, want_logits=True)
+        st, sl = hm.generate_greedy(p, 3, want_logits=True)
+        r0 = np.asarray(rl[0])
+        print(f"[nan] sequence {i}: oracle +inf {np.isposinf(r0).mean():.3f} -inf {np.isneginf(r0).mean():.3f} "
+              f"NaN {np.isnan(r0).mean():.3f}; tokens {list(rt)} gpu {list(st)} batched {list(bt[i])}", flush=True)
+        assert np.isinf(r0).any()
+        for t in range(3):
+            assert _same_nonfinite(sl[t], rl[t]), (i, t)
+            assert _same_nonfinite(bl[t, i], rl[t]), (i, t)
+        assert (np.asarray(st) == np.asarray(rt)).all()
+        assert (bt[i] == np.asarray(rt)).all()
+    toks = orc.prompt_ids(37, 6, V)
+    fr = np.asarray(om.forward(toks, mode=1))
+    fg = np.asarray(hm.forward(toks))
+    for i in range(len(toks)):
+        assert _same_nonfinite(fg[i], fr[i]), i
     hm.free()
     om.close()
