@@ -284,6 +284,37 @@ def gemv_micro(EL, iters: int = 1000, n_bufs: int = 32) -> list:
     return out
 
 
+def step_profile(model, cfg, prompt, steps: int) -> dict:
+    """Per-launch durations and gaps of the graph-replayed decode step
+    (scry_hip_llama_profile_step: the step graph captured with per-workgroup
+    s_memrealtime stamps, 100 MHz).  A launch's duration is its latest
+    workgroup end minus its earliest workgroup start; its gap is its earliest
+    start minus the previous launch's latest end.  Steps 2.. of the run
+    (the first replay is excluded)."""
+    import numpy as np
+
+    st, en = model.profile_step(prompt, steps)
+    st, en = st[1:], en[1:]
+    L = cfg.n_layers
+    kinds = ["qkv", "attention", "o", "gate_up", "down"]
+    dur = en - st
+    gap = np.zeros_like(st)
+    gap[:, 1:] = st[:, 1:] - en[:, :-1]
+    out = {"steps": int(st.shape[0]), "context": [len(prompt), len(prompt) + steps],
+           "step_span_us": round(float(np.mean(en[:, -1])), 2),
+           "sum_kernel_us": round(float(np.mean(dur.sum(axis=1))), 2),
+           "sum_gap_us": round(float(np.mean(gap.sum(axis=1))), 2), "launches": {}}
+    for j, k in enumerate(kinds):
+        idx = [5 * l + j for l in range(L) if not (j == 0 and l == 0)]
+        out["launches"][k] = {"count": len(idx), "mean_us": round(float(dur[:, idx].mean()), 2),
+                              "mean_gap_before_us": round(float(gap[:, idx].mean()), 2),
+                              "per_step_us": round(float(dur[:, idx].sum(axis=1).mean()), 1)}
+    for name, i in (("qkv_layer0", 0), ("lm_head", 5 * L), ("finish", 5 * L + 1)):
+        out["launches"][name] = {"count": 1, "mean_us": round(float(dur[:, i].mean()), 2),
+                                 "mean_gap_before_us": round(float(gap[:, i].mean()), 2)}
+    return out
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -409,6 +440,8 @@ def main() -> int:
                     help="the config 2 / 3 isolated GEMV micro-benchmark only")
     ap.add_argument("--no-gemv", action="store_true", help="skip the config 2 / 3 micro-benchmark")
     ap.add_argument("--no-bf16-decode", action="store_true", help="skip the bf16-model decode line")
+    ap.add_argument("--step-profile", action="store_true",
+                    help="per-launch durations and gaps of the graph-replayed decode step only")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -452,6 +485,16 @@ def main() -> int:
     if args.sampling_only:
         print(json.dumps({"sampling": sampling_sweep(E, EL, model, prompt, args.warmup, args.steps),
                           "prompt_tokens": args.prompt_len, "steps": args.steps}), flush=True)
+        model.free()
+        return 0
+    if args.step_profile:
+        ms, _ = model.bench_decode(prompt, args.warmup, args.steps)
+        prof = step_profile(model, cfg, prompt, args.steps)
+        prof["bench_ms_per_step"] = round(ms / args.steps, 4)
+        from esolearn_amd import _lib
+
+        prof["graph_replay"] = bool(_lib.load().scry_hip_graph_replay())
+        print(json.dumps({"step_profile": prof}), flush=True)
         model.free()
         return 0
     E.HipBackend.synchronize()

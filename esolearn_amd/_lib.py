@@ -130,6 +130,8 @@ SIGNATURES = {
     "scry_hip_llama_decode_batch": [vp, vp, i32, vp, i32, vp, vp],
     "scry_hip_llama_bench_prefill": [vp, vp, i32, i32, i32, vp, P(f64), P(f64)],
     "scry_hip_llama_bench_prefill_batch": [vp, vp, i32, i32, i32, vp, P(f64), P(f64)],
+    "scry_hip_graph_replay": [],
+    "scry_hip_llama_profile_step": [vp, vp, i32, i32, i32, P(i32), vp, vp],
     "scry_hip_llama_bench_decode": [vp, vp, i32, i32, i32, vp, P(f64)],
     "scry_hip_llama_bench_decode_sampled": [vp, vp, i32, i32, i32, P(SamplingConfigC), u64, vp, P(f64)],
     "scry_hip_llama_time_projection": [vp, i32, i32, i32, P(f64), P(f64)],

@@ -252,7 +252,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
 
 template <int G, int NR, int NW>
 __global__ __launch_bounds__(64 * NW) void k_attn_decode(AttnArgs a) {
+    if (a.ts) wg_stamp_begin(a.ts);
     attn_body<G, NR, NW>(a, blockIdx.x);
+    if (a.ts) wg_stamp_end(a.ts);
 }
 
 // Several sequences, one per blockIdx.y, each with its own cache, length and

@@ -151,9 +151,12 @@ struct GemvArgs {
     int64_t *tokens_rw = nullptr;
     int64_t *argmax_out = nullptr;
     int advance = 0;
+    unsigned long long *ts = nullptr;  // step profile: per-workgroup start / end stamps (null: off)
 };
 
 int launch_qgemv(int epi, const GemvArgs &a, hipStream_t s);
+// Whether decode steps replay their captured graphs (llama.hip).
+bool graph_replay();
 // workgroups of one launch_qgemv launch (= EPI_LOGITS argmax partials, EPI_RESID
 // sum-of-squares partials)
 int qgemv_blocks(int epi, const Packed &w, int m);
@@ -257,6 +260,7 @@ struct AttnArgs {
     const DevState *state = nullptr;
     int n_heads = 0, n_kv = 0, head_dim = 0, n_splits = 1, max_chunk = 0;
     int fixed_len = -1;  // >= 0: use this length instead of state->cache_len + 1
+    unsigned long long *ts = nullptr;  // step profile: per-workgroup start / end stamps (null: off)
 };
 int launch_attn_decode(const AttnArgs &a, hipStream_t s);
 int attn_pick_splits(int n_kv, int max_seq, int *n_splits, int *max_chunk);

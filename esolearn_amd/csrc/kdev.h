@@ -190,6 +190,20 @@ __device__ inline int argmax_finish(ArgAcc r, const float *x, int n, ArgAcc *sh)
     return s.i;
 }
 
+// Step profile: workgroup b of a launch writes the 100 MHz constant clock to
+// ts[2b] on entry and to ts[2b + 1] once all its waves are done (the host
+// takes the earliest start and latest end of each launch).
+__device__ __forceinline__ unsigned wg_linear_id() {
+    return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+}
+__device__ __forceinline__ void wg_stamp_begin(unsigned long long *ts) {
+    if (threadIdx.x == 0) ts[2 * wg_linear_id()] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ void wg_stamp_end(unsigned long long *ts) {
+    __syncthreads();
+    if (threadIdx.x == 0) ts[2 * wg_linear_id() + 1] = __builtin_amdgcn_s_memrealtime();
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, size_t bytes) {
     const int n = bytes > 0x7fffffffu ? 0x7fffffff : (int)bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);

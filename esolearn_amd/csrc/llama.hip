@@ -564,29 +564,64 @@ GemvArgs lm_args(scry_kv_cache c, int advance) {
     return g;
 }
 
-int record_step(scry_kv_cache c, hipStream_t s) {
+// The step's launches in order.  ts (step profile, may be null): launch i
+// writes its workgroups' start / end stamps at ts + 2 * ts_slots * i.
+int record_step(scry_kv_cache c, hipStream_t s, unsigned long long *ts = nullptr, size_t ts_slots = 0) {
     scry_llama m = c->m;
+    int li = 0;
+    auto slot = [&]() { return ts ? ts + 2 * ts_slots * (size_t)li++ : nullptr; };
     for (int l = 0; l < m->L; l++) {
-        SCRY_TRY(launch_qgemv(EPI_QKV, qkv_args(c, l), s));
-        SCRY_TRY(launch_attn_decode(attn_args(c, l), s));
-        SCRY_TRY(launch_qgemv(EPI_RESID, o_args(c, l), s));
-        SCRY_TRY(launch_qgemv(EPI_SWIGLU, gu_args(c, l), s));
-        SCRY_TRY(launch_qgemv(EPI_RESID, down_args(c, l), s));
+        GemvArgs q = qkv_args(c, l);
+        q.ts = slot();
+        SCRY_TRY(launch_qgemv(EPI_QKV, q, s));
+        AttnArgs at = attn_args(c, l);
+        at.ts = slot();
+        SCRY_TRY(launch_attn_decode(at, s));
+        GemvArgs o = o_args(c, l);
+        o.ts = slot();
+        SCRY_TRY(launch_qgemv(EPI_RESID, o, s));
+        GemvArgs gu = gu_args(c, l);
+        gu.ts = slot();
+        SCRY_TRY(launch_qgemv(EPI_SWIGLU, gu, s));
+        GemvArgs dn = down_args(c, l);
+        dn.ts = slot();
+        SCRY_TRY(launch_qgemv(EPI_RESID, dn, s));
     }
-    const GemvArgs lg = lm_args(c, 1);
+    GemvArgs lg = lm_args(c, 1);
+    lg.ts = slot();
     SCRY_TRY(launch_qgemv(EPI_LOGITS, lg, s));
     if (c->sampling)
         return launch_sample(c->logits, m->V, c->samp, c->samp_ws, c->rng, c->state, c->tokens, c->samp_prep, s);
+    lg.ts = slot();
     return launch_logits_finish(lg, s);
 }
 
-// One decode step: the captured graph when available, else direct launches.
-// SCRY_HIP_NO_GRAPH=1 forces direct launches (same kernels), for tools that
-// do not follow graph launches.
+}  // namespace
+
+// Graph replay of the decode steps, unless SCRY_HIP_NO_GRAPH is set or a
+// rocprofiler tool is attached to the process (rocprofv3 names its tool
+// library in ROCP_TOOL_LIBRARIES).  Under rocprofv3 --kernel-trace the
+// process faulted on the host inside the profiler's hipGraphLaunch
+// interception (SIGSEGV below run_step -> hipGraphLaunch, in frames of the
+// runtime and the tool), while the same graphs replay without a profiler in
+// every test and bench run; so profiled runs take the same kernels as direct
+// launches.
+bool scry::graph_replay() {
+    static const bool on = [] {
+        if (std::getenv("SCRY_HIP_NO_GRAPH")) return false;
+        const char *tool = std::getenv("ROCP_TOOL_LIBRARIES");
+        return !(tool && *tool);
+    }();
+    return on;
+}
+
+namespace {
+
+// One decode step: the captured graph when available, else direct launches
+// (graph_replay()).
 int run_step(scry_kv_cache c) {
     hipStream_t s = ctx().stream;
-    static const bool no_graph = std::getenv("SCRY_HIP_NO_GRAPH") != nullptr;
-    if (no_graph) return record_step(c, s);
+    if (!graph_replay()) return record_step(c, s);
     if (!c->gexec) {
         hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
         if (e == hipSuccess) {
@@ -1017,7 +1052,7 @@ int decode_batch_core(scry_llama m, scry_kv_cache *cs, int n, const int64_t *tok
         SCRY_HIP(hipMemcpyAsync(cs[i]->tokens + pos0[i], tokens + i, sizeof(int64_t), hipMemcpyHostToDevice, s));
     SCRY_HIP(hipMemcpyAsync(B.pos, pos0.data(), sizeof(int) * n, hipMemcpyHostToDevice, s));
     SCRY_TRY(sync_stream());
-    static const bool no_graph = std::getenv("SCRY_HIP_NO_GRAPH") != nullptr;
+    const bool no_graph = !graph_replay();
     hipGraph_t g = nullptr;
     hipGraphExec_t gx = nullptr;
     if (!no_graph) {
@@ -1662,9 +1697,105 @@ int bench_decode_impl(scry_llama m, const int64_t *prompt, int n_prompt, int war
     return rc;
 }
 
+// Step profile: the prompt through the cache path, then `steps` replays of
+// the decode step captured with per-workgroup start / end stamps (the same
+// launches as the bench's graph; direct launches when graphs are off).  For
+// each step and launch: the earliest workgroup start and the latest end, in
+// us from the step's first start.
+int profile_step_impl(scry_llama m, const int64_t *prompt, int n_prompt, int steps, int max_launches,
+                      int *n_launches, double *start_us, double *end_us) {
+    SCRY_REQUIRE_INIT();
+    if (!m || !prompt || n_prompt <= 0 || steps <= 0 || !n_launches || !start_us || !end_us)
+        return set_error(SCRY_ERR_INVALID, "profile_step: bad arguments");
+    const int nl = 5 * m->L + 2;
+    *n_launches = nl;
+    if (max_launches < nl) return set_error(SCRY_ERR_INVALID, "profile_step: %d launches per step > %d", nl, max_launches);
+    SCRY_TRY(check_ids(m, prompt, n_prompt));
+    scry_kv_cache c = nullptr;
+    SCRY_TRY(cache_new(m, n_prompt + steps + 1, &c));
+    // stamp slots per launch: the largest grid of the step
+    size_t slots = (size_t)qgemv_blocks(EPI_LOGITS, m->lm, 1);
+    for (const auto &Ly : m->layers)
+        for (const Packed *w : {&Ly.qkv, &Ly.o, &Ly.gu, &Ly.down})
+            slots = std::max(slots, (size_t)qgemv_blocks(EPI_RESID, *w, 1));
+    slots = std::max(slots, (size_t)8 * ((m->nkv + 7) / 8) * c->n_splits);
+    slots = std::max(slots, (size_t)1);
+    const size_t bytes = 2 * slots * nl * sizeof(unsigned long long);
+    hipStream_t s = ctx().stream;
+    unsigned long long *ts = nullptr;
+    std::vector<unsigned long long> h;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t gx = nullptr;
+    hipError_t e = hipSuccess;
+    int rc = dev_alloc((void **)&ts, bytes);
+    if (!rc) {
+        e = hipMemcpyAsync(c->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) rc = hip_fail(e, "prompt upload", __FILE__, __LINE__);
+    }
+    if (!rc) rc = set_state(c, 0, 0, n_prompt);
+    for (int t = 0; t < n_prompt && !rc; t++) rc = run_step(c);
+    if (!rc && graph_replay()) {
+        e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            rc = record_step(c, s, ts, slots);
+            e = hipStreamEndCapture(s, &g);
+            if (!rc && e == hipSuccess) e = hipGraphInstantiate(&gx, g, nullptr, nullptr, 0);
+        }
+        if (!rc && e != hipSuccess) rc = hip_fail(e, "profile graph capture", __FILE__, __LINE__);
+    }
+    if (!rc) {
+        try {
+            h.resize(bytes / sizeof(unsigned long long));
+        } catch (...) {
+            rc = set_error(SCRY_ERR_OOM, "profile_step: host buffer of %zu bytes", bytes);
+        }
+    }
+    for (int t = 0; t < steps && !rc; t++) {
+        e = hipMemsetAsync(ts, 0, bytes, s);  // outside the captured graph
+        if (e == hipSuccess) e = gx ? hipGraphLaunch(gx, s) : hipSuccess;
+        if (e != hipSuccess) {
+            rc = hip_fail(e, "profile replay", __FILE__, __LINE__);
+            break;
+        }
+        if (!gx) rc = record_step(c, s, ts, slots);
+        if (!rc) e = hipMemcpyAsync(h.data(), ts, bytes, hipMemcpyDeviceToHost, s);
+        if (!rc && e == hipSuccess) e = hipStreamSynchronize(s);
+        if (!rc && e != hipSuccess) rc = hip_fail(e, "profile readback", __FILE__, __LINE__);
+        if (rc) break;
+        unsigned long long t0 = ~0ull;
+        std::vector<unsigned long long> lo(nl, ~0ull), hi(nl, 0);
+        for (int i = 0; i < nl; i++) {
+            const unsigned long long *p = h.data() + 2 * slots * i;
+            for (size_t b = 0; b < slots; b++) {
+                if (p[2 * b]) lo[i] = std::min(lo[i], p[2 * b]);
+                hi[i] = std::max(hi[i], p[2 * b + 1]);
+            }
+            t0 = std::min(t0, lo[i]);
+        }
+        for (int i = 0; i < nl; i++) {  // s_memrealtime: 100 MHz
+            start_us[(size_t)t * max_launches + i] = lo[i] == ~0ull ? -1.0 : (double)(lo[i] - t0) * 0.01;
+            end_us[(size_t)t * max_launches + i] = hi[i] == 0 ? -1.0 : (double)(hi[i] - t0) * 0.01;
+        }
+    }
+    if (gx) (void)hipGraphExecDestroy(gx);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamSynchronize(s);
+    dev_free(ts);
+    cache_free(c);
+    return rc;
+}
+
 }  // namespace
 
 extern "C" {
+
+int scry_hip_graph_replay(void) { return graph_replay() ? 1 : 0; }
+
+int scry_hip_llama_profile_step(scry_llama m, const int64_t *prompt, int n_prompt, int steps, int max_launches,
+                                int *n_launches, double *start_us, double *end_us) {
+    API_LOCK;
+    return profile_step_impl(m, prompt, n_prompt, steps, max_launches, n_launches, start_us, end_us);
+}
 
 int scry_hip_llama_bench_decode(scry_llama m, const int64_t *prompt, int n_prompt, int warmup,
                                 int steps, int64_t *out_tokens, double *ms) {

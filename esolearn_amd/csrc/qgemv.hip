@@ -9,7 +9,9 @@ using namespace dev;
 
 template <int EPI, int PRO, int WT, int MT, int NCH>
 __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
+    if (a.ts) wg_stamp_begin(a.ts);
     qgemv_block<EPI, PRO, WT, MT, NCH>(a, blockIdx.x, blockIdx.y);
+    if (a.ts) wg_stamp_end(a.ts);
 }
 
 // Compile-time chunk count (straight-line stream) for the k on the Llama
@@ -195,6 +197,7 @@ int qgemv_kargs(int epi, const GemvArgs &g, KArgs *out, int *wt_out, int *nch_ou
     ka.part_val = g.part_val;
     ka.part_idx = g.part_idx;
     ka.part_nan = g.part_nan;
+    ka.ts = g.ts;
     *out = ka;
     *wt_out = wt;
     *nch_out = nch;
@@ -235,7 +238,9 @@ __global__ __launch_bounds__(TPB) void k_logits_finish(const float *__restrict__
                                                        const int *__restrict__ pi,
                                                        const int *__restrict__ pn, int np,
                                                        DevState *st, int64_t *tokens,
-                                                       int64_t *argmax_out, int advance) {
+                                                       int64_t *argmax_out, int advance,
+                                                       unsigned long long *ts) {
+    if (ts) wg_stamp_begin(ts);
     __shared__ ArgAcc sh[TPB];
     const int tid = threadIdx.x;
     // thread t combines partials t, t + TPB, ... (coalesced; arg_combine is
@@ -264,13 +269,14 @@ __global__ __launch_bounds__(TPB) void k_logits_finish(const float *__restrict__
             st->cache_len = st->cache_len + 1;
         }
     }
+    if (ts) wg_stamp_end(ts);
 }
 }  // namespace
 
 int launch_logits_finish(const GemvArgs &g, hipStream_t s) {
     const int np = qgemv_blocks(EPI_LOGITS, *g.w, 1);
     hipLaunchKernelGGL(k_logits_finish, dim3(1), dim3(TPB), 0, s, g.y, g.w->rows, g.part_val,
-                       g.part_idx, g.part_nan, np, g.state, g.tokens_rw, g.argmax_out, g.advance);
+                       g.part_idx, g.part_nan, np, g.state, g.tokens_rw, g.argmax_out, g.advance, g.ts);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }

@@ -80,6 +80,7 @@ struct KArgs {
     float q_scale;
     float *part_val;
     int *part_idx, *part_nan;
+    unsigned long long *ts;  // step profile stamps (null: off)
 };
 
 // activation prologues

@@ -260,6 +260,20 @@ class LlamaModel:
              toks.ctypes.data, C.byref(ms))
         return ms.value, toks
 
+    def profile_step(self, prompt, steps: int):
+        """Per-launch (start, end) in us from each step's first start, for
+        `steps` replays of the stamped decode step after the prompt: two arrays
+        [steps, 5 L + 2] (per layer qkv, attention, o, gate/up, down; then the
+        LM head and the argmax finish)."""
+        p = np.ascontiguousarray(prompt, dtype=np.int64)
+        nl = 5 * self.cfg.n_layers + 2
+        st = np.empty((steps, nl), np.float64)
+        en = np.empty((steps, nl), np.float64)
+        n = C.c_int()
+        call("scry_hip_llama_profile_step", self.h, p.ctypes.data, p.size, steps, nl, C.byref(n),
+             st.ctypes.data, en.ctypes.data)
+        return st, en
+
     def bench_decode_sampled(self, prompt, warmup: int, steps: int, config: "SamplingConfig",
                              seed: int = 0):
         """bench_decode with the device sampler after every LM head."""

@@ -388,6 +388,20 @@ int scry_hip_llama_decode_batch(scry_llama m, scry_kv_cache *caches, int n_seq, 
                                 int steps, int64_t *out_tokens, float *logits);
 
 /* ------------------------------------------------ measurement helpers */
+/* No counterpart in the reference: 1 when decode steps replay their captured
+ * graphs, 0 when they are direct launches (SCRY_HIP_NO_GRAPH set, or a
+ * rocprofiler tool attached: ROCP_TOOL_LIBRARIES non-empty, as rocprofv3
+ * sets it).  Needs no device. */
+int scry_hip_graph_replay(void);
+/* No counterpart in the reference: step profile of the graph-replayed decode
+ * step.  Feeds the prompt, then replays `steps` decode steps captured with
+ * per-workgroup stamps of the 100 MHz constant clock.  Launch i of step t
+ * (per layer qkv, attention, o, gate/up, down; then the LM head and the
+ * argmax finish: 5 L + 2 launches) gets its earliest workgroup start and
+ * latest end, in us from the step's first start, at start_us / end_us
+ * [t * max_launches + i].  *n_launches = 5 L + 2. */
+int scry_hip_llama_profile_step(scry_llama m, const int64_t *prompt, int n_prompt, int steps, int max_launches,
+                                int *n_launches, double *start_us, double *end_us);
 /* Decode-step session for benchmarks: binds a model and cache, feeds the
  * prompt, then runs `steps` greedy decode steps as graph replays.  The time of
  * the decode steps (HIP events on the launch stream) is returned in *ms. */

@@ -42,3 +42,30 @@ def test_calls_before_init_fail_cleanly():
     assert ei.value.code == 4
     assert "scry_hip_init not called" in str(ei.value)
     assert b"not called" in _lib.load().scry_hip_last_error()
+
+
+@pytest.mark.parametrize("env,want", [
+    ({}, 1),
+    ({"SCRY_HIP_NO_GRAPH": "1"}, 0),
+    ({"ROCP_TOOL_LIBRARIES": "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so"}, 0),
+    ({"ROCP_TOOL_LIBRARIES": ""}, 1),
+])
+def test_graph_replay_off_under_a_profiler_tool(env, want):
+    """Decode steps replay captured graphs unless SCRY_HIP_NO_GRAPH is set or
+    a rocprofiler tool is attached (rocprofv3 sets ROCP_TOOL_LIBRARIES): the
+    profiler's hipGraphLaunch interception faulted the process, so profiled
+    runs take direct launches.  Decided from the environment once per process,
+    so each case runs in a fresh interpreter; no device is used."""
+    import os
+    import subprocess
+    import sys
+
+    from esolearn_amd import _lib
+
+    base = {k: v for k, v in os.environ.items() if k not in ("SCRY_HIP_NO_GRAPH", "ROCP_TOOL_LIBRARIES")}
+    code = ("import ctypes, sys; L = ctypes.CDLL(sys.argv[1]); "
+            "print(L.scry_hip_graph_replay())")
+    out = subprocess.run([sys.executable, "-c", code, _lib.LIB_PATH], env={**base, **env},
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert int(out.stdout.strip().splitlines()[-1]) == want
