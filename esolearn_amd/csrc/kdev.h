@@ -196,12 +196,16 @@ __device__ inline int argmax_finish(ArgAcc r, const float *x, int n, ArgAcc *sh)
 __device__ __forceinline__ unsigned wg_linear_id() {
     return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
 }
+// Wave 0 stores (every lane the same value): a branch uniform in the wave,
+// so the kernel's values derived from its arguments stay uniform.
 __device__ __forceinline__ void wg_stamp_begin(unsigned long long *ts) {
-    if (threadIdx.x == 0) ts[2 * wg_linear_id()] = __builtin_amdgcn_s_memrealtime();
+    if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) == 0)
+        ts[2 * wg_linear_id()] = __builtin_amdgcn_s_memrealtime();
 }
 __device__ __forceinline__ void wg_stamp_end(unsigned long long *ts) {
     __syncthreads();
-    if (threadIdx.x == 0) ts[2 * wg_linear_id() + 1] = __builtin_amdgcn_s_memrealtime();
+    if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) == 0)
+        ts[2 * wg_linear_id() + 1] = __builtin_amdgcn_s_memrealtime();
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, size_t bytes) {
