@@ -309,11 +309,51 @@ __global__ __launch_bounds__(SK_NT) void k_skinny(SkArgs a) {
 constexpr int SK_DG_NONFINITE = 0x7fffffff;
 constexpr double SK_DG_XMAX = 8323071.0;  // 2^23 - 2^16 - 1
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// A row segment's exponent from its maximum magnitude m and whether it holds a
+// NaN or an infinity
+__device__ __forceinline__ int dg_exponent(float m, bool bad) {
+    int E = 0;
+    if (bad) {
+        E = SK_DG_NONFINITE;
+    } else if (m > 0.f) {
+        int ex;
+        frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
+        E = 23 - ex;
+        if (ldexp((double)m, E) > SK_DG_XMAX) E--;
+    }
+    return E;
+}
+
+// Eight values -> their bytes in the three digit planes (b[p][e / 4], byte e % 4)
+__device__ __forceinline__ void dg_digits(const float (&v)[8], int E, unsigned (&b)[3][2]) {
+    const int Es = E == SK_DG_NONFINITE ? 0 : E;
+#pragma unroll
+    for (int p = 0; p < 3; p++) b[p][0] = b[p][1] = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        // v 2^E is exact in f32 (a power-of-two scaling to at most 2^23), rint then exact
+        const int X = E == SK_DG_NONFINITE ? 0 : (int)rintf(ldexpf(v[e], Es));
+        const int X1 = (X - (int)(signed char)X) >> 8;
+        const int X2 = (X1 - (int)(signed char)X1) >> 8;
+        const int sh = 8 * (e & 3);
+        b[0][e >> 2] |= (unsigned)(X & 255) << sh;
+        b[1][e >> 2] |= (unsigned)(X1 & 255) << sh;
+        b[2][e >> 2] |= (unsigned)(X2 & 255) << sh;
+    }
+}
+
+// A split's partial of one row from the digit planes' integer sums
+__device__ __forceinline__ float dg_partial(int a0, int a1, int a2, int E) {
+    const double S = (double)a2 * 65536.0 + (double)a1 * 256.0 + (double)a0;
+    return E == SK_DG_NONFINITE ? __builtin_nanf("") : (float)(S * ldexp(1.0, -E));
+}
+
 template <int KS, bool NORM, int MRT>
 __global__ __launch_bounds__(SK_NT) void k_skinny_dg(SkArgs a) {
     static_assert(KS % 2 == 0, "weights come in 128-byte segments of two blocks");
     static_assert(MRT == 4 || MRT == 16, "4 or 16 activation rows");
-    typedef int i32x4 __attribute__((ext_vector_type(4)));
     __shared__ u32x4 s_d[KS * 3 * 4 * MRT];
     __shared__ __attribute__((aligned(16))) unsigned char s_w[4 * SK_WTILE];
     __shared__ float s_wmax[4][MRT];
@@ -410,37 +450,17 @@ __global__ __launch_bounds__(SK_NT) void k_skinny_dg(SkArgs a) {
                 m = fmaxf(m, s_wmax[w][tid]);
                 b |= s_wbad[w][tid];
             }
-        int E = 0;
-        if (b) {
-            E = SK_DG_NONFINITE;
-        } else if (m > 0.f) {
-            int ex;
-            frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
-            E = 23 - ex;
-            if (ldexp((double)m, E) > SK_DG_XMAX) E--;
-        }
-        s_e[tid] = E;
+        s_e[tid] = dg_exponent(m, b != 0);
     }
     __syncthreads();
     {
         const int E = s_e[myrow];
-        const int Es = E == SK_DG_NONFINITE ? 0 : E;
 #pragma unroll
         for (int i = 0; i < UPT; i++) {
             const int u = tid + SK_NT * i, kb = u / (8 * MRT), q8 = u & 7;
             if (NU % SK_NT != 0 && u >= NU) break;
-            unsigned b[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                // v 2^E is exact in f32 (a power-of-two scaling to at most 2^23), rint then exact
-                const int X = E == SK_DG_NONFINITE ? 0 : (int)rintf(ldexpf(v[i][e], Es));
-                const int X1 = (X - (int)(signed char)X) >> 8;
-                const int X2 = (X1 - (int)(signed char)X1) >> 8;
-                const int sh = 8 * (e & 3);
-                b[0][e >> 2] |= (unsigned)(X & 255) << sh;
-                b[1][e >> 2] |= (unsigned)(X1 & 255) << sh;
-                b[2][e >> 2] |= (unsigned)(X2 & 255) << sh;
-            }
+            unsigned b[3][2];
+            dg_digits(v[i], E, b);
             // k = 64 kb + 16 g + 8 h + e: lane group g = q8 / 2, half h = q8 % 2
 #pragma unroll
             for (int p = 0; p < 3; p++) {
@@ -492,12 +512,34 @@ __global__ __launch_bounds__(SK_NT) void k_skinny_dg(SkArgs a) {
         if (row >= a.m) continue;
         const int E = s_e[row < MRT ? row : 0];
 #pragma unroll
-        for (int cb = 0; cb < 2; cb++) {
-            const double S = (double)acc[2][cb][r] * 65536.0 + (double)acc[1][cb][r] * 256.0 + (double)acc[0][cb][r];
-            const float val = E == SK_DG_NONFINITE ? __builtin_nanf("") : (float)(S * ldexp(1.0, -E));
-            a.part[((size_t)split * SK_ROWS + row) * a.n_pad + cw + 16 * cb + nn] = val;
-        }
+        for (int cb = 0; cb < 2; cb++)
+            a.part[((size_t)split * SK_ROWS + row) * a.n_pad + cw + 16 * cb + nn] =
+                dg_partial(acc[0][cb][r], acc[1][cb][r], acc[2][cb][r], E);
     }
+}
+
+// RoPE and the K / V append of the batched decode step's qkv rows (row = the
+// sequence) for the column pair (c, c + 1), c even (llama.rs:384-396,
+// apply_rotary_emb on the adjacent pair): q and k are rotated in f32 without
+// contraction (as the single-sequence step's QKV epilogue) and q scaled; k and
+// v go to the caches at the row's position.
+__device__ __forceinline__ void rope_store(const SkArgs &a, const DecodeSeqs &rd, const AttnSeqs &rc, int row, int c,
+                                           float v0, float v1) {
+    const int pos = rd.pos[row];
+    const size_t at = (size_t)rc.layer * rc.ls[row] + (size_t)pos * a.kvd;
+    if (c >= a.qd + a.kvd) {
+        *(float2 *)(rc.v[row] + at + (c - a.qd - a.kvd)) = make_float2(v0, v1);
+        return;
+    }
+    const bool isq = c < a.qd;
+    const int j = isq ? c : c - a.qd;
+    const float2 cs = rd.rope[row][(size_t)pos * (a.hd >> 1) + ((j % a.hd) >> 1)];
+    const float r0 = __fsub_rn(__fmul_rn(v0, cs.x), __fmul_rn(v1, cs.y));
+    const float r1 = __fadd_rn(__fmul_rn(v0, cs.y), __fmul_rn(v1, cs.x));
+    if (isq)
+        *(float2 *)(a.q_out + (size_t)row * a.qd + j) = make_float2(__fmul_rn(r0, a.q_scale), __fmul_rn(r1, a.q_scale));
+    else
+        *(float2 *)(rc.k[row] + at + j) = make_float2(r0, r1);
 }
 
 __device__ __forceinline__ ArgAcc wave_argmax(ArgAcc a) {
@@ -586,25 +628,8 @@ __device__ __forceinline__ void skinny_epi_body(const SkArgs &a, const DecodeSeq
                 if (ok0) v0 = yr[c] + v0;
                 if (ok1) v1 = yr[c1] + v1;
             }
-            if constexpr (ROPE) {  // llama.rs:384-396 (apply_rotary_emb on the adjacent pair)
-                if (ok1) {  // c is even and the row length qd + 2 kvd is even: the pair is whole
-                    const int pos = rd->pos[row];
-                    const size_t at = (size_t)rc->layer * rc->ls[row] + (size_t)pos * a.kvd;
-                    if (c >= a.qd + a.kvd) {
-                        *(float2 *)(rc->v[row] + at + (c - a.qd - a.kvd)) = make_float2(v0, v1);
-                    } else {
-                        const bool isq = c < a.qd;
-                        const int j = isq ? c : c - a.qd;
-                        const float2 cs = rd->rope[row][(size_t)pos * (a.hd >> 1) + ((j % a.hd) >> 1)];
-                        const float r0 = __fsub_rn(__fmul_rn(v0, cs.x), __fmul_rn(v1, cs.y));
-                        const float r1 = __fadd_rn(__fmul_rn(v0, cs.y), __fmul_rn(v1, cs.x));
-                        if (isq)
-                            *(float2 *)(a.q_out + (size_t)row * a.qd + j) =
-                                make_float2(__fmul_rn(r0, a.q_scale), __fmul_rn(r1, a.q_scale));
-                        else
-                            *(float2 *)(rc->k[row] + at + j) = make_float2(r0, r1);
-                    }
-                }
+            if constexpr (ROPE) {  // c is even and the row length qd + 2 kvd is even: the pair is whole
+                if (ok1) rope_store(a, *rd, *rc, row, c, v0, v1);
             } else {
                 if (ok0) yr[c] = v0;
                 if (ok1) yr[c1] = v1;
