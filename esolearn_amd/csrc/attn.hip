@@ -75,8 +75,13 @@ __device__ __forceinline__ float group_sum(float v) {
 // per lane group.  The NW*P lane groups of the workgroup are merged through
 // LDS into one partial per (query head, split); with a single split that is
 // the attention row itself.
-template <int G, int NR, int NW>
-__device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
+// PRO: a callable run by every thread after the position range is known and
+// before the queries are read; it returns the LDS queries [nrep][hd] or null
+// (a.q).  PRE: the first step's K / V rows are requested before it, unless the
+// new position (written by the prologue of the split holding it) is among
+// them.
+template <int G, int NR, int NW, bool PRE, class PRO>
+__device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk, PRO &&pro) {
     constexpr int NT = 64 * NW;
     constexpr int P = 64 / G;  // positions per load instruction
     // load instructions per step: 12 keeps the most K/V rows in flight; with
@@ -104,19 +109,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v_cache, (size_t)t1 * kv_dim * 4);
     const unsigned col = (unsigned)(g * hd + gl * 4) * 4;
 
-    float4 qf[NR];
-    float m[NR], l[NR];
-    float4 o[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-        qf[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (r < nrep && dact) qf[r] = *(const float4 *)(a.q + (size_t)(g * nrep + r) * hd + gl * 4);
-        m[r] = -INFINITY;
-        l[r] = 0.f;
-        o[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    for (int tb = t0 + wave * PI; tb < t1; tb += NW * PI) {
-        float4 kv[U], vv[U];
+    auto load = [&](float4(&kv)[U], float4(&vv)[U], int tb) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int t = tb + u * P + sub;
@@ -124,6 +117,31 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
             kv[u] = bload16f(kr, off);
             vv[u] = bload16f(vr, off);
         }
+    };
+    const int tb0 = t0 + wave * PI;
+    float4 kv0[U], vv0[U];
+    bool pre = false;
+    if constexpr (PRE) {
+        const bool holder = t1 == L && t0 < t1;
+        pre = tb0 < t1 && (!holder || t1 - 1 >= t0 + NW * PI);
+        if (pre) load(kv0, vv0, tb0);
+    }
+    const float *q_lds = pro();
+
+    float4 qf[NR];
+    float m[NR], l[NR];
+    float4 o[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        qf[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < nrep && dact)
+            qf[r] = q_lds ? *(const float4 *)(q_lds + r * hd + gl * 4)
+                          : *(const float4 *)(a.q + (size_t)(g * nrep + r) * hd + gl * 4);
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+        o[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    auto step = [&](const float4(&kv)[U], const float4(&vv)[U], int tb) {
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             if (r >= nrep) break;
@@ -160,6 +178,16 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
             }
             m[r] = mx;
         }
+    };
+    int tbs = tb0;
+    if (pre) {
+        step(kv0, vv0, tb0);
+        tbs += NW * PI;
+    }
+    for (int tb = tbs; tb < t1; tb += NW * PI) {
+        float4 kv[U], vv[U];
+        load(kv, vv, tb);
+        step(kv, vv, tb);
     }
     const int slot = wave * P + sub;
 #pragma unroll
@@ -253,16 +281,93 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk) {
 template <int G, int NR, int NW>
 __global__ __launch_bounds__(64 * NW) void k_attn_decode(AttnArgs a) {
     if (a.ts) wg_stamp_begin(a.ts);
-    attn_body<G, NR, NW>(a, blockIdx.x);
+    attn_body<G, NR, NW, false>(a, blockIdx.x, [] { return (const float *)nullptr; });
     if (a.ts) wg_stamp_end(a.ts);
+}
+
+// The qkv epilogue of the batched decode step for sequence y and the
+// workgroup's KV group (QkvPro): its query heads into s_q [nrep][hd], and, in
+// the split holding the new position, that position's K / V row into the
+// cache.  One element per thread and pass; a RoPE pair is two neighbouring
+// lanes.  The sums, scaling and rotation are the fused STORE epilogue's.
+constexpr int QP_MAX_SPLIT = 16;  // qkv partials per column (launch_attn_decode_seqs checks)
+
+template <int NW>
+__device__ __forceinline__ void qkv_prologue(const AttnArgs &a, const AttnSeqs &b, const QkvPro &qp, int y, int blk,
+                                             float *s_q) {
+    constexpr int NT = 64 * NW;
+    __shared__ double s_rstd;
+    const int bi = blk >> 3;
+    const int g = (blk & 7) + 8 * (bi / a.n_splits), split = bi % a.n_splits;
+    if (g >= a.n_kv) return;  // padding of the last row of 8 groups (attn_body returns too)
+    const int tid = threadIdx.x, nrep = a.n_heads / a.n_kv, hd = a.head_dim;
+    const int qd = a.n_heads * hd, kvd = a.n_kv * hd;
+    const int pos = b.pos[y], L = pos + 1, chunk = (L + a.n_splits - 1) / a.n_splits;
+    const int t0 = min(L, split * chunk), t1 = min(L, t0 + chunk);
+    const bool holder = t0 <= pos && pos < t1;
+    const float *pr = qp.part + (size_t)y * qp.n_pad;
+    const size_t st = (size_t)16 * qp.n_pad;  // one split's 16 rows
+    const float2 *rope = qp.rope[y] + (size_t)pos * (hd >> 1);
+    // items: the group's query values (nq), then in the holder k and v (2 hd);
+    // item i's column and RoPE dimension
+    const int nq = nrep * hd, ni = nq + (holder ? 2 * hd : 0);
+    auto col = [&](int i) {
+        return i < nq ? g * nrep * hd + i : i < nq + hd ? qd + g * hd + (i - nq) : qd + kvd + g * hd + (i - nq - hd);
+    };
+    // every load of a pass is issued before the first use (one memory round trip)
+    float pv[QP_MAX_SPLIT];
+    float2 cs;
+    auto load = [&](int i) {
+        const int ii = min(i, ni - 1), c = col(ii);
+#pragma unroll
+        for (int sp = 0; sp < QP_MAX_SPLIT; sp++) pv[sp] = sp < qp.n_split ? pr[sp * st + c] : 0.f;
+        cs = rope[((ii < nq ? ii : ii - nq) % hd) >> 1];
+    };
+    // finish item i: the split sum in split order, the scales, the rotation of
+    // the pair (c, c + 1) held by lanes 2j, 2j + 1 (llama.rs:384-396)
+    auto finish = [&](int i, double rstd) {
+        float sum = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < QP_MAX_SPLIT; sp++)
+            if (sp < qp.n_split) sum += pv[sp];
+        const bool in = i < ni;
+        const float v = in ? (float)((double)(sum * qp.scale) * rstd) : 0.f;
+        const float w = __shfl_xor(v, 1);
+        const float r = (i & 1) ? __fadd_rn(__fmul_rn(w, cs.y), __fmul_rn(v, cs.x))
+                                : __fsub_rn(__fmul_rn(v, cs.x), __fmul_rn(w, cs.y));
+        if (!in) return;
+        if (i < nq) {
+            s_q[i] = __fmul_rn(r, qp.q_scale);
+        } else {
+            const size_t at = (size_t)b.layer * b.ls[y] + (size_t)pos * kvd + (size_t)g * hd;
+            if (i < nq + hd) b.k[y][at + (i - nq)] = r;
+            else b.v[y][at + (i - nq - hd)] = v;
+        }
+    };
+    load(tid);
+    if (tid < 64) {  // RMSNorm scale of row y (rmsnorm.rs, cpu.rs:574-599), f64
+        const double q = tid < qp.n_ss_in ? qp.ss_in[(size_t)y * qp.n_ss_in + tid] : 0.0;
+        const double v = wave_sum_d(q);
+        if (tid == 0) s_rstd = 1.0 / sqrt(v / (double)qp.k + (double)qp.eps);
+    }
+    __syncthreads();
+    const double rstd = s_rstd;
+    finish(tid, rstd);
+    for (int i = tid + NT; i - tid < ni; i += NT) {  // more items than threads (uniform trip count)
+        load(i);
+        finish(i, rstd);
+    }
+    if (holder) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the new row is in memory before the workgroup reads it
+    __syncthreads();
 }
 
 // Several sequences, one per blockIdx.y, each with its own cache, length and
 // partial buffers (the rows of a batched decode step).  The linear block id is
 // blockIdx.x + gridDim.x * blockIdx.y with gridDim.x a multiple of 8, so the
 // XCD of a workgroup is still blockIdx.x % 8 and the exchange stays in one L2.
-template <int G, int NR, int NW>
-__global__ __launch_bounds__(64 * NW) void k_attn_decode_seqs(AttnArgs a, AttnSeqs b) {
+// QP: the queries and the new K / V rows come from the qkv partials (QkvPro).
+template <int G, int NR, int NW, bool QP>
+__global__ __launch_bounds__(64 * NW) void k_attn_decode_seqs(AttnArgs a, AttnSeqs b, QkvPro qp) {
     const int y = blockIdx.y;
     const int qd = a.n_heads * a.head_dim;
     AttnArgs s = a;
@@ -274,32 +379,43 @@ __global__ __launch_bounds__(64 * NW) void k_attn_decode_seqs(AttnArgs a, AttnSe
     s.merge_ctr = a.merge_ctr + (size_t)y * a.n_kv * kCtrStride;
     s.xa = a.xa + (size_t)y * qd;
     s.fixed_len = b.pos[y] + 1;
-    attn_body<G, NR, NW>(s, blockIdx.x);
+    if constexpr (QP) {
+        __shared__ float s_q[NR * 256];  // head_dim <= 256
+        attn_body<G, NR, NW, true>(s, blockIdx.x, [&] {
+            qkv_prologue<NW>(a, b, qp, y, blockIdx.x, s_q);
+            return (const float *)s_q;
+        });
+    } else {
+        attn_body<G, NR, NW, false>(s, blockIdx.x, [] { return (const float *)nullptr; });
+    }
 }
 
 template <int G, int NR, int NW>
-void launch_k(const AttnArgs &a, const AttnSeqs *b, dim3 grid, size_t lds, hipStream_t s) {
+void launch_k(const AttnArgs &a, const AttnSeqs *b, const QkvPro *qp, dim3 grid, size_t lds, hipStream_t s) {
     if (b) {
         grid.y = b->n;
-        hipLaunchKernelGGL((k_attn_decode_seqs<G, NR, NW>), grid, dim3(64 * NW), lds, s, a, *b);
+        if (qp)
+            hipLaunchKernelGGL((k_attn_decode_seqs<G, NR, NW, true>), grid, dim3(64 * NW), lds, s, a, *b, *qp);
+        else
+            hipLaunchKernelGGL((k_attn_decode_seqs<G, NR, NW, false>), grid, dim3(64 * NW), lds, s, a, *b, QkvPro{});
     } else {
         hipLaunchKernelGGL((k_attn_decode<G, NR, NW>), grid, dim3(64 * NW), lds, s, a);
     }
 }
 
 template <int G, int NW>
-int launch_gw(const AttnArgs &a, const AttnSeqs *b, int nrep, hipStream_t s) {
+int launch_gw(const AttnArgs &a, const AttnSeqs *b, const QkvPro *qp, int nrep, hipStream_t s) {
     const int P = 64 / G;
     auto lds = [&](int nr) { return (size_t)NW * P * nr * a.head_dim * 4; };
     dim3 grid(8 * ((a.n_kv + 7) / 8) * a.n_splits);
     if (nrep <= 1) {
-        launch_k<G, 1, NW>(a, b, grid, lds(1), s);
+        launch_k<G, 1, NW>(a, b, qp, grid, lds(1), s);
     } else if (nrep <= 2) {
-        launch_k<G, 2, NW>(a, b, grid, lds(2), s);
+        launch_k<G, 2, NW>(a, b, qp, grid, lds(2), s);
     } else if (nrep <= 4) {
-        launch_k<G, 4, NW>(a, b, grid, lds(4), s);
+        launch_k<G, 4, NW>(a, b, qp, grid, lds(4), s);
     } else if (nrep <= 8) {
-        launch_k<G, 8, NW>(a, b, grid, lds(8), s);
+        launch_k<G, 8, NW>(a, b, qp, grid, lds(8), s);
     } else {
         return set_error(SCRY_ERR_UNSUPPORTED, "attention: n_heads/n_kv = %d > 8", nrep);
     }
@@ -314,9 +430,9 @@ int launch_gw(const AttnArgs &a, const AttnSeqs *b, int nrep, hipStream_t s) {
 // 212.0 -> 203.5 ms, one sequence at a time 571.7 -> 531.5 ms; 8 waves at one
 // head per KV head (Llama-2-7B) were 0.2% slower.
 template <int G>
-int launch_g(const AttnArgs &a, const AttnSeqs *b, int nrep, hipStream_t s) {
-    if (a.n_splits == 1) return launch_gw<G, 16>(a, b, nrep, s);
-    return nrep >= 3 ? launch_gw<G, 8>(a, b, nrep, s) : launch_gw<G, 4>(a, b, nrep, s);
+int launch_g(const AttnArgs &a, const AttnSeqs *b, const QkvPro *qp, int nrep, hipStream_t s) {
+    if (a.n_splits == 1) return launch_gw<G, 16>(a, b, qp, nrep, s);
+    return nrep >= 3 ? launch_gw<G, 8>(a, b, qp, nrep, s) : launch_gw<G, 4>(a, b, qp, nrep, s);
 }
 
 }  // namespace
@@ -337,7 +453,7 @@ int attn_pick_splits(int n_kv, int max_seq, int *n_splits, int *max_chunk) {
 }
 
 namespace {
-int launch_attn(const AttnArgs &a, const AttnSeqs *b, hipStream_t s) {
+int launch_attn(const AttnArgs &a, const AttnSeqs *b, const QkvPro *qp, hipStream_t s) {
     if (!a.xa || (a.n_splits > 1 && (!a.merge_ctr || !a.part_o || !a.part_ml)))
         return set_error(SCRY_ERR_INVALID, "attention: missing output / partial / merge buffers");
     if (a.n_splits < 1 || a.n_splits > MAX_SPLITS)
@@ -349,23 +465,31 @@ int launch_attn(const AttnArgs &a, const AttnSeqs *b, hipStream_t s) {
                          a.head_dim);
     const int nrep = a.n_heads / a.n_kv;
     const int lanes = a.head_dim / 4;
-    if (lanes <= 1) return launch_g<1>(a, b, nrep, s);
-    if (lanes <= 2) return launch_g<2>(a, b, nrep, s);
-    if (lanes <= 4) return launch_g<4>(a, b, nrep, s);
-    if (lanes <= 8) return launch_g<8>(a, b, nrep, s);
-    if (lanes <= 16) return launch_g<16>(a, b, nrep, s);
-    if (lanes <= 32) return launch_g<32>(a, b, nrep, s);
-    return launch_g<64>(a, b, nrep, s);
+    if (lanes <= 1) return launch_g<1>(a, b, qp, nrep, s);
+    if (lanes <= 2) return launch_g<2>(a, b, qp, nrep, s);
+    if (lanes <= 4) return launch_g<4>(a, b, qp, nrep, s);
+    if (lanes <= 8) return launch_g<8>(a, b, qp, nrep, s);
+    if (lanes <= 16) return launch_g<16>(a, b, qp, nrep, s);
+    if (lanes <= 32) return launch_g<32>(a, b, qp, nrep, s);
+    return launch_g<64>(a, b, qp, nrep, s);
 }
 }  // namespace
 
-int launch_attn_decode(const AttnArgs &a, hipStream_t s) { return launch_attn(a, nullptr, s); }
+int launch_attn_decode(const AttnArgs &a, hipStream_t s) { return launch_attn(a, nullptr, nullptr, s); }
 
-int launch_attn_decode_seqs(const AttnArgs &a, const AttnSeqs &b, hipStream_t s) {
-    if (b.n < 1 || b.n > PF_MAX_SEQS || !b.pos || !a.q)
+int launch_attn_decode_seqs(const AttnArgs &a, const AttnSeqs &b, hipStream_t s, const QkvPro *pro) {
+    if (b.n < 1 || b.n > PF_MAX_SEQS || !b.pos || (!pro && !a.q))
         return set_error(SCRY_ERR_INVALID, "attention: %d sequences (1..%d) with positions and queries", b.n,
                          PF_MAX_SEQS);
-    return launch_attn(a, &b, s);
+    if (pro) {
+        bool ok = pro->part && pro->n_split >= 1 && pro->n_split <= QP_MAX_SPLIT && pro->ss_in && pro->n_ss_in >= 1 &&
+                  pro->n_ss_in <= 64 &&
+                  pro->k >= 1 && a.head_dim % 2 == 0 && a.head_dim <= 256 &&
+                  pro->n_pad >= (a.n_heads + 2 * a.n_kv) * a.head_dim;
+        for (int i = 0; ok && i < b.n; i++) ok = pro->rope[i] != nullptr;
+        if (!ok) return set_error(SCRY_ERR_INVALID, "attention: qkv partials, norm partials and RoPE tables");
+    }
+    return launch_attn(a, &b, pro, s);
 }
 
 }  // namespace scry

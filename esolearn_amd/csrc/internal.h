@@ -180,7 +180,7 @@ size_t skinny_ws_bytes(int m, int k, int n);  // n: packed weight rows (2 n for 
 // The fused form (the batched decode step's projections): the RMSNorm rides
 // in the activation staging, and one workgroup per 128-column tile adds the
 // k splits' partials in split order and applies the epilogue.
-enum { SKE_STORE = 1, SKE_RESID = 2, SKE_SWIGLU = 3, SKE_LOGITS = 4 };
+enum { SKE_NONE = 0, SKE_STORE = 1, SKE_RESID = 2, SKE_SWIGLU = 3, SKE_LOGITS = 4 };
 struct DecodeSeqs;
 struct AttnSeqs;
 struct SkinnyFused {
@@ -193,24 +193,23 @@ struct SkinnyFused {
     const double *ss_in = nullptr;
     int n_ss_in = 0;
     float eps = 1e-5f;
-    int epi = SKE_STORE;  // STORE, RESID (y += x W), SWIGLU (fused gate/up rows), LOGITS
+    int epi = SKE_STORE;  // NONE (the split partials only), STORE, RESID (y += x W), SWIGLU (fused gate/up rows), LOGITS
     float *y = nullptr;
     int ldy = 0;
     double *ss_out = nullptr;  // RESID (may be null): [m][skinny_tiles(w)] partial sums of squares of y
     float *pv = nullptr;       // LOGITS: [m][skinny_tiles(w)] ordered argmax partials
     int *pi = nullptr, *pn = nullptr;
-    // STORE of the qkv rows of a batched decode step (row i = sequence i):
-    // with rope_d, y is not written; q is rotated and scaled into q_out
-    // [m][qd], k rotated and v stored into the caches of rope_c at each
-    // sequence's position
-    const DecodeSeqs *rope_d = nullptr;
-    const AttnSeqs *rope_c = nullptr;
-    float *q_out = nullptr;
-    int qd = 0, kvd = 0, hd = 0;
-    float q_scale = 1.f;
 };
 int skinny_tiles(const Packed &w);  // 128-row tiles of the packed rows
-int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStream_t s);
+// SKE_NONE: the split partials of rows [m] in ws as part[n_split][16][n_pad];
+// y[i][j] = scale * (sum over the splits of part[s][i][j], in split order)
+// (times the row's RMSNorm scale under norm_w)
+struct SkinnyParts {
+    int n_split = 0, n_pad = 0;
+    float scale = 1.f;
+};
+int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStream_t s,
+                        SkinnyParts *parts = nullptr);
 int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s);
 int launch_logits_finish(const GemvArgs &a, hipStream_t s);
 // sample_token on the device (sample.hip): logits [V] -> tokens[pos + 1] when
@@ -332,7 +331,24 @@ struct AttnSeqs {
     const int *pos;                                // device [n]: rows cached before this token
     int layer, n;
 };
-int launch_attn_decode_seqs(const AttnArgs &a, const AttnSeqs &b, hipStream_t s);
+// The batched decode step's qkv epilogue, done by the attention launch: the
+// qkv rows' split partials (SKE_NONE, row = the sequence) are summed in split
+// order and scaled (scale, then the row's RMSNorm rstd from ss_in [n][n_ss_in]
+// over k); each workgroup rotates its group's query heads (RoPE on adjacent
+// pairs at the sequence's position, llama.rs:384-396) and multiplies them by
+// q_scale, and the workgroup whose split holds the position rotates k and
+// writes k and v into that row of the cache.  The arithmetic is the fused
+// STORE epilogue's, so q, k and v are the same values.
+struct QkvPro {
+    const float *part = nullptr;
+    int n_split = 0, n_pad = 0;
+    float scale = 1.f;
+    const double *ss_in = nullptr;
+    int n_ss_in = 0, k = 0;
+    float eps = 0.f, q_scale = 1.f;
+    const float2 *rope[PF_MAX_SEQS] = {};
+};
+int launch_attn_decode_seqs(const AttnArgs &a, const AttnSeqs &b, hipStream_t s, const QkvPro *pro = nullptr);
 
 // batch.hip -- glue of the batched decode step (n sequences, one token each)
 struct DecodeSeqs {

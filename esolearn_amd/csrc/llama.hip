@@ -71,7 +71,7 @@ struct scry_llama_s {
     // partials; the LM head's argmax partials; per-sequence
     // attention partials and arrival counters; the device positions
     struct Batch {
-        float *x = nullptr, *qkv = nullptr, *q = nullptr, *xa = nullptr, *act = nullptr, *logits = nullptr;
+        float *x = nullptr, *xa = nullptr, *act = nullptr, *logits = nullptr;
         double *ss = nullptr;
         float *ws = nullptr;
         size_t ws_bytes = 0;
@@ -262,7 +262,7 @@ void model_free(scry_llama m) {
     dev_free(m->pf.dg);
     dev_free(m->pf.de);
     dev_free(m->kvp);
-    for (void *p : {(void *)m->bd.x, (void *)m->bd.qkv, (void *)m->bd.q, (void *)m->bd.xa, (void *)m->bd.act,
+    for (void *p : {(void *)m->bd.x, (void *)m->bd.xa, (void *)m->bd.act,
                     (void *)m->bd.logits, (void *)m->bd.ss, (void *)m->bd.ws, (void *)m->bd.pv, (void *)m->bd.pi, (void *)m->bd.pn, (void *)m->bd.ap_o, (void *)m->bd.ap_ml,
                     (void *)m->bd.ctr, (void *)m->bd.pos})
         dev_free(p);
@@ -904,8 +904,6 @@ int batch_ws(scry_llama m) {
     const int lt = skinny_tiles(m->lm);
     const size_t nsp = 16;  // attention splits: attn_pick_splits picks at most 16
     int rc = dev_alloc((void **)&B.x, sizeof(float) * R * m->h);
-    if (!rc) rc = dev_alloc((void **)&B.qkv, sizeof(float) * R * m->qkv_dim);
-    if (!rc) rc = dev_alloc((void **)&B.q, sizeof(float) * R * m->q_dim);
     if (!rc) rc = dev_alloc((void **)&B.xa, sizeof(float) * R * m->q_dim);
     if (!rc) rc = dev_alloc((void **)&B.act, sizeof(float) * R * m->ffn);
     if (!rc) rc = dev_alloc((void **)&B.logits, sizeof(float) * R * m->V);
@@ -920,7 +918,7 @@ int batch_ws(scry_llama m) {
     if (!rc) rc = launch_fill_u32(B.ctr, R * m->nkv * kCtrStride, 0u, ctx().stream);  // the last split of a group resets it
     if (!rc) rc = dev_alloc((void **)&B.pos, sizeof(int) * R);
     if (rc) {
-        for (void *p : {(void *)B.x, (void *)B.qkv, (void *)B.q, (void *)B.xa, (void *)B.act, (void *)B.logits,
+        for (void *p : {(void *)B.x, (void *)B.xa, (void *)B.act, (void *)B.logits,
                         (void *)B.ss, (void *)B.ws, (void *)B.pv, (void *)B.pi, (void *)B.pn,
                         (void *)B.ap_o, (void *)B.ap_ml, (void *)B.ctr, (void *)B.pos})
             dev_free(p);
@@ -934,26 +932,17 @@ int batch_ws(scry_llama m) {
 // One batched decode step (the layer of record_step for n sequences): each
 // projection is one fused skinny matmul over the n rows (the RMSNorms ride in
 // them, from the residual rows' partial sums of squares, as in the
-// single-sequence step), attention covers every sequence's cache in one
-// launch, and the step ends with each sequence's next token and position
-// advance.
+// single-sequence step); attention covers every sequence's cache in one
+// launch and forms the queries and the new K / V rows from the qkv rows'
+// split partials itself (QkvPro); the step ends with each sequence's next
+// token and position advance.
 int record_batch_step(scry_llama m, const DecodeSeqs &d, AttnSeqs c, int n_splits, int max_chunk, hipStream_t s) {
     auto &B = m->bd;
     const int n = d.n;
     const int n_ss = (m->h + 127) / 128;  // partial sums per residual row (128-column tiles)
     const float q_scale = (float)(1.0 / std::sqrt((double)m->hd));  // llama.rs:394
-    auto mm = [&](const Packed &w, const float *x, int ldx, const float *norm_w, int epi, float *y, int ldy,
-                  bool rope = false) {
+    auto mm = [&](const Packed &w, const float *x, int ldx, const float *norm_w, int epi, float *y, int ldy) {
         SkinnyFused f;
-        if (rope) {  // RoPE and the K / V append in the epilogue
-            f.rope_d = &d;
-            f.rope_c = &c;
-            f.q_out = B.q;
-            f.qd = m->q_dim;
-            f.kvd = m->kv_dim;
-            f.hd = m->hd;
-            f.q_scale = q_scale;
-        }
         f.w = &w;
         f.x = x;
         f.ldx = ldx;
@@ -972,7 +961,6 @@ int record_batch_step(scry_llama m, const DecodeSeqs &d, AttnSeqs c, int n_split
         return launch_skinny_fused(f, B.ws, B.ws_bytes, s);
     };
     AttnArgs at;
-    at.q = B.q;
     at.part_o = B.ap_o;
     at.part_ml = B.ap_ml;
     at.merge_ctr = B.ctr;
@@ -982,12 +970,36 @@ int record_batch_step(scry_llama m, const DecodeSeqs &d, AttnSeqs c, int n_split
     at.head_dim = m->hd;
     at.n_splits = n_splits;
     at.max_chunk = max_chunk;
+    QkvPro qp;
+    qp.ss_in = B.ss;
+    qp.n_ss_in = n_ss;
+    qp.k = m->h;
+    qp.eps = m->eps;
+    qp.q_scale = q_scale;
+    for (int i = 0; i < n; i++) qp.rope[i] = d.rope[i];
     SCRY_TRY(launch_bd_embed(m->embed, m->h, d, B.x, B.ss, s));
     for (int l = 0; l < m->L; l++) {
         const auto &Ly = m->layers[l];
         c.layer = l;
-        SCRY_TRY(mm(Ly.qkv, B.x, m->h, m->norm_in(l), SKE_STORE, B.qkv, m->qkv_dim, true));
-        SCRY_TRY(launch_attn_decode_seqs(at, c, s));
+        {  // the qkv rows' split partials; the attention launch sums them (RoPE, K / V append)
+            SkinnyFused f;
+            f.w = &Ly.qkv;
+            f.x = B.x;
+            f.ldx = m->h;
+            f.m = n;
+            f.norm_w = m->norm_in(l);
+            f.ss_in = B.ss;
+            f.n_ss_in = n_ss;
+            f.eps = m->eps;
+            f.epi = SKE_NONE;
+            SkinnyParts sp;
+            SCRY_TRY(launch_skinny_fused(f, B.ws, B.ws_bytes, s, &sp));
+            qp.part = B.ws;
+            qp.n_split = sp.n_split;
+            qp.n_pad = sp.n_pad;
+            qp.scale = sp.scale;
+        }
+        SCRY_TRY(launch_attn_decode_seqs(at, c, s, &qp));
         SCRY_TRY(mm(Ly.o, B.xa, m->q_dim, nullptr, SKE_RESID, B.x, m->h));
         SCRY_TRY(mm(Ly.gu, B.x, m->h, m->norm_post(l), SKE_SWIGLU, B.act, m->ffn));
         SCRY_TRY(mm(Ly.down, B.act, m->ffn, nullptr, SKE_RESID, B.x, m->h));

@@ -28,7 +28,8 @@
 // adds them in split order and applies the epilogue: store, residual add
 // (plus per-row partial sums of squares of the result for the next RMSNorm),
 // SwiGLU of the fused gate/up rows, or logits (plus per-row ordered argmax
-// partials).  NORM: the activation is RMSNorm(x) applied as
+// partials); or no epilogue (SKE_NONE: the batched decode step's qkv rows,
+// whose partials the attention launch sums).  NORM: the activation is RMSNorm(x) applied as
 // rstd * (W (x * g)) (rmsnorm.rs, cpu.rs:574-599): x * g is staged, and rstd
 // (f64, from the producer's partial sums of squares) scales the sums.
 #include "internal.h"
@@ -67,11 +68,6 @@ struct SkArgs {
     double *ss_out;  // SKE_RESID: per-row partial sums of squares of y [m][tiles]
     float *pv;       // SKE_LOGITS: per-row ordered argmax partials [m][tiles]
     int *pi, *pn;
-    // k_skinny_epi_rope: q (rotated, times q_scale) into q_out [m][qd]; k
-    // (rotated) and v into the K / V caches of the batched decode sequences
-    float *q_out;
-    int qd, kvd, hd;
-    float q_scale;
 };
 
 
@@ -518,30 +514,6 @@ __global__ __launch_bounds__(SK_NT) void k_skinny_dg(SkArgs a) {
     }
 }
 
-// RoPE and the K / V append of the batched decode step's qkv rows (row = the
-// sequence) for the column pair (c, c + 1), c even (llama.rs:384-396,
-// apply_rotary_emb on the adjacent pair): q and k are rotated in f32 without
-// contraction (as the single-sequence step's QKV epilogue) and q scaled; k and
-// v go to the caches at the row's position.
-__device__ __forceinline__ void rope_store(const SkArgs &a, const DecodeSeqs &rd, const AttnSeqs &rc, int row, int c,
-                                           float v0, float v1) {
-    const int pos = rd.pos[row];
-    const size_t at = (size_t)rc.layer * rc.ls[row] + (size_t)pos * a.kvd;
-    if (c >= a.qd + a.kvd) {
-        *(float2 *)(rc.v[row] + at + (c - a.qd - a.kvd)) = make_float2(v0, v1);
-        return;
-    }
-    const bool isq = c < a.qd;
-    const int j = isq ? c : c - a.qd;
-    const float2 cs = rd.rope[row][(size_t)pos * (a.hd >> 1) + ((j % a.hd) >> 1)];
-    const float r0 = __fsub_rn(__fmul_rn(v0, cs.x), __fmul_rn(v1, cs.y));
-    const float r1 = __fadd_rn(__fmul_rn(v0, cs.y), __fmul_rn(v1, cs.x));
-    if (isq)
-        *(float2 *)(a.q_out + (size_t)row * a.qd + j) = make_float2(__fmul_rn(r0, a.q_scale), __fmul_rn(r1, a.q_scale));
-    else
-        *(float2 *)(rc.k[row] + at + j) = make_float2(r0, r1);
-}
-
 __device__ __forceinline__ ArgAcc wave_argmax(ArgAcc a) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -569,12 +541,9 @@ __device__ __forceinline__ void arg_push(ArgAcc &p, float v, int i) {  // sequen
 // columns 2l, 2l + 1 of the tile, or (SwiGLU, lanes 0..31) the packed group
 // 4l .. 4l + 3 = gate and up of outputs 2l, 2l + 1.  Every split's partials
 // of a batch are requested before the first is used; the sums run in split
-// order.  ROPE (STORE of the qkv rows of a batched decode step, row = the
-// sequence): the lane's column pair is a RoPE pair; q and k are rotated in
-// f32 without contraction (as the single-sequence step's QKV epilogue) and q
-// scaled, and k and v go to the caches at the row's position.
-template <int EPI, bool ROPE>
-__device__ __forceinline__ void skinny_epi_body(const SkArgs &a, const DecodeSeqs *rd, const AttnSeqs *rc) {
+// order.
+template <int EPI>
+__global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
     const int tile = blockIdx.x;
     constexpr bool SW = EPI == SKE_SWIGLU;
     constexpr int NB = SW ? 16 : 32;  // splits per load batch
@@ -628,12 +597,8 @@ __device__ __forceinline__ void skinny_epi_body(const SkArgs &a, const DecodeSeq
                 if (ok0) v0 = yr[c] + v0;
                 if (ok1) v1 = yr[c1] + v1;
             }
-            if constexpr (ROPE) {  // c is even and the row length qd + 2 kvd is even: the pair is whole
-                if (ok1) rope_store(a, *rd, *rc, row, c, v0, v1);
-            } else {
-                if (ok0) yr[c] = v0;
-                if (ok1) yr[c1] = v1;
-            }
+            if (ok0) yr[c] = v0;
+            if (ok1) yr[c1] = v1;
             if constexpr (EPI == SKE_RESID) {
                 if (a.ss_out) {
                     double q = (ok0 ? (double)v0 * (double)v0 : 0.0) + (ok1 ? (double)v1 * (double)v1 : 0.0);
@@ -688,15 +653,6 @@ __device__ __forceinline__ void skinny_epi_body(const SkArgs &a, const DecodeSeq
             }
         }
     }
-}
-
-template <int EPI>
-__global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
-    skinny_epi_body<EPI, false>(a, nullptr, nullptr);
-}
-
-__global__ __launch_bounds__(SK_NT) void k_skinny_epi_rope(SkArgs a, DecodeSeqs d, AttnSeqs c) {
-    skinny_epi_body<SKE_STORE, true>(a, &d, &c);
 }
 
 // y[row][col] = scale * (sum of the splits' partials, in split order) (+ bias[col]);
@@ -856,14 +812,15 @@ int launch_skinny(const SkinnyMM &mm, float *ws, size_t ws_bytes, hipStream_t s)
 
 int skinny_tiles(const Packed &w) { return plan(w.k, w.rows).tiles; }
 
-int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStream_t s) {
+int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStream_t s, SkinnyParts *parts) {
     const Packed &w = *f.w;
     const bool sw = f.epi == SKE_SWIGLU;
-    if (f.epi < SKE_STORE || f.epi > SKE_LOGITS) return set_error(SCRY_ERR_INVALID, "skinny: epilogue %d", f.epi);
+    if (f.epi < SKE_NONE || f.epi > SKE_LOGITS || (f.epi == SKE_NONE) != (parts != nullptr))
+        return set_error(SCRY_ERR_INVALID, "skinny: epilogue %d", f.epi);
     if (w.bf16 || (w.fused ? (!sw || w.rows != 2 * w.n || w.rows % 4 != 0) : (sw || w.rows != w.n)))
         return set_error(SCRY_ERR_UNSUPPORTED,
                          "skinny matmul: int8 weight rows only (the fused gate/up pair with the swiglu output)");
-    if (f.m < 1 || f.m > SK_ROWS || f.ldx < w.k || f.ldy < w.n || !f.x || !f.y)
+    if (f.m < 1 || f.m > SK_ROWS || f.ldx < w.k || !f.x || (f.epi != SKE_NONE && (f.ldy < w.n || !f.y)))
         return set_error(SCRY_ERR_INVALID, "skinny matmul: %d rows (1..%d), ldx %d, ldy %d", f.m, SK_ROWS, f.ldx,
                          f.ldy);
     if (w.k % 8 != 0) return set_error(SCRY_ERR_UNSUPPORTED, "skinny matmul: k %% 8 != 0");
@@ -873,13 +830,6 @@ int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStr
         return set_error(SCRY_ERR_INVALID, "skinny matmul: RMSNorm input needs 1..64 partial sums per row");
     if (f.epi == SKE_LOGITS && (!f.pv || !f.pi || !f.pn))
         return set_error(SCRY_ERR_INVALID, "skinny matmul: logits epilogue needs argmax partials");
-    if (f.rope_d) {
-        const DecodeSeqs &d = *f.rope_d;
-        const AttnSeqs &c = *f.rope_c;
-        if (f.epi != SKE_STORE || !f.rope_c || !f.q_out || c.n != d.n || d.n != f.m || !d.pos || f.hd < 2 ||
-            f.hd % 2 || f.qd % f.hd || f.kvd % f.hd || w.n != f.qd + 2 * f.kvd || (uintptr_t)f.q_out % 8)
-            return set_error(SCRY_ERR_INVALID, "skinny matmul: rope epilogue needs the qkv rows of the batched step");
-    }
     // the workspace bound below holds: 256 gives no more splits than 512
     const SkPlan p = plan(w.k, w.rows, w.s32 ? 512 : 256);
     if (ws_bytes < skinny_ws_bytes(f.m, w.k, w.rows))
@@ -913,15 +863,11 @@ int launch_skinny_fused(const SkinnyFused &f, float *ws, size_t ws_bytes, hipStr
     a.pv = f.pv;
     a.pi = f.pi;
     a.pn = f.pn;
-    a.q_out = f.q_out;
-    a.qd = f.qd;
-    a.kvd = f.kvd;
-    a.hd = f.hd;
-    a.q_scale = f.q_scale;
     SCRY_TRY(f.norm_w ? launch_main<true>(a, p.ks, b32, s) : launch_main<false>(a, p.ks, b32, s));
-    if (f.rope_d) {
-        hipLaunchKernelGGL(k_skinny_epi_rope, dim3(a.tiles), dim3(SK_NT), 0, s, a, *f.rope_d, *f.rope_c);
-        SCRY_HIP(hipGetLastError());
+    if (parts) {
+        parts->n_split = p.n_split;
+        parts->n_pad = p.n_pad;
+        parts->scale = a.scale;
         return SCRY_OK;
     }
     switch (f.epi) {
