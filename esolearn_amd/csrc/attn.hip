@@ -161,7 +161,11 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk, PRO 
             // only is not skipped: with mx = -inf its sum becomes NaN (the
             // reference's softmax of a NaN score is NaN, cpu.rs:336-366)
             if (!any) continue;
-            const float f = expf(m[r] - mx);
+            // the running softmax's exponentials by v_exp_f32 (2^(x log2 e)):
+            // relative error about |x| 2^-24 plus an ulp against expf, 1e-6 where
+            // a weight e^x (x <= 0 against the running maximum) is above 2^-20
+            // and so can move the sums; expf took 3% of the attention time
+            const float f = __expf(m[r] - mx);
             l[r] *= f;
             o[r].x *= f;
             o[r].y *= f;
@@ -169,7 +173,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs &a, const int blk, PRO 
             o[r].w *= f;
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const float p = expf(sc[u] - mx);
+                const float p = __expf(sc[u] - mx);
                 l[r] += p;
                 o[r].x += p * vv[u].x;
                 o[r].y += p * vv[u].y;
