@@ -95,6 +95,11 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
     mb = E.LlamaModel.new_random(cfg, seed=0, quant_mode=EL.QUANT_BF16, init_on_device=True)
     pm_bf16, _, toks_bf16 = mb.bench_prefill(np.stack(prompts), 1)
     mb.free()
+    # the builder-defined block-32 int8 weights (one scale per 32 values of a
+    # row; the GEMMs take the split-bf16 matrix-core path)
+    m32 = E.LlamaModel.new_random(cfg, seed=0, quant_mode=EL.QUANT_BLOCK32, init_on_device=True)
+    pm_b32, _, toks_b32 = m32.bench_prefill(np.stack(prompts), 1)
+    m32.free()
     h, ffn, L = cfg.hidden_size, cfg.intermediate_size, cfg.n_layers
     hd = h // cfg.n_heads
     qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
@@ -106,7 +111,7 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
     print(f"[bench] prefill {n_seq}x{s}: {pm:.1f} ms ({rows / pm * 1e3:.0f} tok/s, projections "
           f"{tf:.1f} TFLOP/s); decode {n_seq}x{decode_steps}: {dm:.1f} ms, batched {dm_b:.1f} ms "
           f"(tokens equal: {bool((toks_b == toks).all())}); init {t_init:.1f} s; "
-          f"bf16 model prefill {pm_bf16:.1f} ms", file=sys.stderr, flush=True)
+          f"bf16 model prefill {pm_bf16:.1f} ms; block-32 model prefill {pm_b32:.1f} ms", file=sys.stderr, flush=True)
     return {
         "workload": "llama3-8b-shape int8: 4 x 2048-token prompts, batched prefill of the first "
                     "2047 tokens each (GEMMs on the int8 matrix cores: activations as per-row 24-bit "
@@ -136,6 +141,9 @@ def prefill_config5(E, n_seq: int = 4, n_prompt: int = 2048, decode_steps: int =
         "bf16_model_prefill_ms": round(pm_bf16, 2),
         "bf16_model_prefill_tok_s": round(rows / (pm_bf16 / 1e3), 1),
         "bf16_model_first_tokens": [int(t) for t in toks_bf16[:, 0]],
+        "block32_model_prefill_ms": round(pm_b32, 2),
+        "block32_model_prefill_tok_s": round(rows / (pm_b32 / 1e3), 1),
+        "block32_model_first_tokens": [int(t) for t in toks_b32[:, 0]],
     }
 
 

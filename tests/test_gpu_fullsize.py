@@ -227,6 +227,59 @@ def test_config5_dims_two_layers_vs_oracle(hip, orc):
         orc.set_threads(0)
 
 
+def test_config5_dims_block32_two_layers_vs_oracle(hip, orc):
+    """Block-32 int8 weights (builder-defined: one scale per 32 values of a
+    row) at the config-5 tensor shapes with 2 layers; both models from the same
+    seeded host init.  Two 64-token prompts: the batched prefill of the first 63
+    tokens, then 8 greedy steps per sequence token by token, and the batched
+    decode step of both sequences (decode_batch: the bf16-plane skinny kernel
+    with per-block scales), against the oracle's block-32 greedy run (forward
+    mode 2).  Identical tokens, logits within 1e-3 at every step."""
+    cfg = dict(LLAMA3_8B, n_layers=2)
+    NS, NP = 8, 64
+    print("[case] config-5 dims, 2 layers, block-32: host init (GPU and oracle)", flush=True)
+    orc.set_threads(16)
+    om = orc.Llama(orc.LlamaConfig(**cfg), 7, quantize=True, keep_f32=False, block32=True)
+    hm = hip.LlamaModel.new_random(hip.LlamaConfig(**cfg), 7, hip.QUANT_BLOCK32)
+    V = cfg["vocab_size"]
+    prompts = np.stack([orc.prompt_ids(s + 11, NP, V) for s in range(2)])
+    try:
+        print("[case] config-5 dims, block-32: prefill + token-by-token decode", flush=True)
+        caches = [hm.new_llama_kv_cache(NP + NS) for _ in range(2)]
+        hm.prefill(caches, prompts[:, :NP - 1], want_logits=False)
+        gpu = []
+        for s in range(2):
+            tok, pos, lgs, ts = int(prompts[s, NP - 1]), NP - 1, [], []
+            for _ in range(NS):
+                lg, am = hm.forward_with_llama_cache(tok, pos, caches[s])
+                lgs.append(lg)
+                ts.append(am)
+                tok, pos = am, pos + 1
+            gpu.append((np.array(ts), np.stack(lgs)))
+            caches[s].free()
+        print("[case] config-5 dims, block-32: decode_batch of 2 sequences", flush=True)
+        cs = [hm.new_llama_kv_cache(NP + NS) for _ in range(2)]
+        hm.prefill(cs, prompts[:, :NP - 1], want_logits=False)
+        bt, bl = hm.decode_batch(cs, prompts[:, NP - 1], NS, want_logits=True)
+        for c in cs:
+            c.free()
+    finally:
+        hm.free()
+    try:
+        for s in range(2):
+            print(f"[case] config-5 dims, block-32: oracle greedy run of sequence {s}", flush=True)
+            ref_t, ref_l = om.generate_greedy(prompts[s], NS, mode=2, want_logits=True)
+            e = max(rel_err(gpu[s][1][i], ref_l[i]) for i in range(NS))
+            eb = max(rel_err(bl[i, s], ref_l[i]) for i in range(NS))
+            print(f"[err] config-5 dims block-32 seq {s}: decode {e:.3e}, decode_batch {eb:.3e}", flush=True)
+            assert e < LOGIT_TOL and eb < LOGIT_TOL
+            assert (gpu[s][0] == ref_t).all()
+            assert (bt[s] == ref_t).all()
+    finally:
+        om.close()
+        orc.set_threads(0)
+
+
 @pytest.fixture(scope="module")
 def model8b(hip):
     print("[case] config 5 model: Llama-3-8B shape, seed 0, device init (as bench.py)", flush=True)
