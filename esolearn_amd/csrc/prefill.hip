@@ -1343,7 +1343,10 @@ __global__ __launch_bounds__(64 * MQW) void k_attn_mfma(PrefillAttn a, PrefillSe
 //   online softmax per query over the 32 keys (4 lanes l % 16 + 16 g);
 //   O^T += V^T P^T with the 32 keys as the MFMA's k: slot 8 g + e is key
 //     4 g + e (e < 4) of the first half and 16 + 4 g + (e - 4) of the
-//     second, which is exactly the P values lane (l % 16, g) holds.
+//     second, which is exactly the P values lane (l % 16, g) holds.  The V
+//     tile stores each 32-key chunk in that slot order, so a lane's 8 keys
+//     are one 16-byte read (two 8-byte reads 32 bytes apart made 2-way bank
+//     conflicts at the padded row stride).
 constexpr int BQW = 8, BQ = 16 * BQW, BKT = 64;  // waves; query rows; keys per tile
 
 // bf16 hi / lo words of two values with the hardware round-to-nearest-even
@@ -1418,7 +1421,8 @@ __global__ __launch_bounds__(64 * BQW) void k_attn_bf3(PrefillAttn a, PrefillSeq
             u32x4 v0 = u32x4{0u, 0u, 0u, 0u}, v1 = v0;
             if (k0 + j < kend) v0 = *(const u32x4 *)(src + (size_t)(k0 + j) * HD + 8 * c);
             if (k0 + j + 1 < kend) v1 = *(const u32x4 *)(src + (size_t)(k0 + j + 1) * HD + 8 * c);
-            u16 *dst = (pl ? sVl : sVh) + (8 * c) * VLD + j;
+            const int jj = j & 31;  // key 16 h + 4 g + e of its chunk -> slot 8 g + 4 h + e
+            u16 *dst = (pl ? sVl : sVh) + (8 * c) * VLD + (j - jj) + 8 * ((jj >> 2) & 3) + 4 * (jj >> 4) + (jj & 3);
             const unsigned a0[4] = {v0.x, v0.y, v0.z, v0.w}, a1[4] = {v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -1476,13 +1480,8 @@ __global__ __launch_bounds__(64 * BQW) void k_attn_bf3(PrefillAttn a, PrefillSeq
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
                 o[dt] *= alpha;
-                const int vr = (16 * dt + lr) * VLD + c32 + 4 * lg;
-                u32x4 vh, vl;
-                const uint2 h0 = *(const uint2 *)(sVh + vr), h1 = *(const uint2 *)(sVh + vr + 16);
-                const uint2 l0 = *(const uint2 *)(sVl + vr), l1 = *(const uint2 *)(sVl + vr + 16);
-                vh.x = h0.x, vh.y = h0.y, vh.z = h1.x, vh.w = h1.y;
-                vl.x = l0.x, vl.y = l0.y, vl.z = l1.x, vl.w = l1.y;
-                const bf16x8 bvh = __builtin_bit_cast(bf16x8, vh), bvl = __builtin_bit_cast(bf16x8, vl);
+                const int vr = (16 * dt + lr) * VLD + c32 + 8 * lg;
+                const bf16x8 bvh = *(const bf16x8 *)(sVh + vr), bvl = *(const bf16x8 *)(sVl + vr);
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bvh, ph, o[dt], 0, 0, 0);
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bvh, pl, o[dt], 0, 0, 0);
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bvl, ph, o[dt], 0, 0, 0);
