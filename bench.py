@@ -59,8 +59,8 @@ INT8_MFMA_PEAK_TOPS = 5000.0  # dense
 # profiles/prefill_llama3_8b_mfma_counters.md (SQ_VALU_MFMA_BUSY_CYCLES over
 # GRBM_GUI_ACTIVE / 8 x 1024 SIMDs); counters cannot be read inside this
 # process, so the line carries the profile's figures with their source.
-PREFILL_MFMA_BUSY_PROFILE = {"qkv": 0.551, "o": 0.502, "gate_up": 0.586, "down": 0.584, "attention": 0.238,
-                             "prefill": 0.480, "source": "profiles/prefill_llama3_8b_mfma_counters.md"}
+PREFILL_MFMA_BUSY_PROFILE = {"qkv": 0.553, "o": 0.503, "gate_up": 0.584, "down": 0.583, "attention": 0.343,
+                             "prefill": 0.502, "source": "profiles/prefill_llama3_8b_mfma_counters.md"}
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_projections_pmc_traffic.md")
 
 
