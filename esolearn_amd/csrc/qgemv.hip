@@ -14,6 +14,43 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
     if (a.ts) wg_stamp_end(a.ts);
 }
 
+// The split-k body for one activation row of int8 per-tensor weights with
+// k % 16 == 0 (every lane's 16 activation values wholly inside or past k) and
+// the Llama chunk counts: 4 (k <= 4096; two row groups of 8 waves), 11 and 14
+// (the down projections; one row group of 11 or 14 waves).  Wave 0 finishes
+// last, after the barrier.
+constexpr int sk_r(int nch) { return nch == 4 ? 8 : 8; }        // rows per wave
+constexpr int sk_groups(int nch) { return nch == 4 ? 2 : 1; }  // row groups per workgroup
+bool use_sk(int nch, int m, int wt, int k) {
+    return wt == WT_I8 && m == 1 && (nch == 4 || nch == 11 || nch == 14) && k % 16 == 0;
+}
+int sk_rows(int nch) { return sk_groups(nch) * sk_r(nch); }  // rows per workgroup
+
+template <int EPI, int PRO, int NCH>
+__global__ __launch_bounds__(64 * NCH * sk_groups(NCH)) void k_qgemv_sk(KArgs a) {
+    if (a.ts) wg_stamp_begin(a.ts);
+    qgemv_sk_block<EPI, PRO, NCH, sk_groups(NCH), sk_r(NCH)>(a, blockIdx.x);
+    if (a.ts && __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) == 0)
+        a.ts[2 * wg_linear_id() + 1] = __builtin_amdgcn_s_memrealtime();
+}
+
+template <int EPI, int PRO, int NCH>
+int launch_sk_t(const KArgs &ka, hipStream_t s) {
+    constexpr int RPW = sk_groups(NCH) * sk_r(NCH);
+    hipLaunchKernelGGL((k_qgemv_sk<EPI, PRO, NCH>), dim3((ka.rows + RPW - 1) / RPW),
+                       dim3(64 * NCH * sk_groups(NCH)), 0, s, ka);
+    SCRY_HIP(hipGetLastError());
+    return SCRY_OK;
+}
+
+template <int EPI, int PRO>
+int launch_sk(const KArgs &ka, hipStream_t s) {
+    if (ka.nch == 4) return launch_sk_t<EPI, PRO, 4>(ka, s);
+    if (ka.nch == 11) return launch_sk_t<EPI, PRO, 11>(ka, s);
+    if (ka.nch == 14) return launch_sk_t<EPI, PRO, 14>(ka, s);
+    return set_error(SCRY_ERR_INVALID, "qgemv: no split-k shape for %d chunks", ka.nch);
+}
+
 // Compile-time chunk count (straight-line stream) for the k on the Llama
 // paths; 0 = runtime loop.  Several activation rows share a weight pass only
 // in the store epilogue with k <= 4096.
@@ -99,6 +136,7 @@ int launch_mt(const KArgs &ka, Sel sel, hipStream_t s) {
 
 template <int EPI, int PRO>
 int launch_wt(const KArgs &ka, int wt, Sel sel, hipStream_t s) {
+    if (use_sk(ka.nch, ka.m, wt, ka.k)) return launch_sk<EPI, PRO>(ka, s);
     if (wt == WT_BF16) return launch_mt<EPI, PRO, WT_BF16>(ka, sel, s);
     if (wt == WT_I8B32) return launch_mt<EPI, PRO, WT_I8B32>(ka, sel, s);
     return launch_mt<EPI, PRO, WT_I8>(ka, sel, s);
@@ -126,6 +164,7 @@ int row_chunks(const Packed &w) { return (w.bf16 ? 2 * w.k + 1023 : w.k + 1023) 
 }  // namespace
 
 int qgemv_blocks(int epi, const Packed &w, int m) {
+    if (use_sk(row_chunks(w), m, weight_type(w), w.k)) return (w.rows + sk_rows(row_chunks(w)) - 1) / sk_rows(row_chunks(w));
     const Sel sel = select_cfg(epi, row_chunks(w), m, weight_type(w));
     const Shape S = shape_for(sel.nch_t, sel.mt);
     return (w.rows + S.rwt * S.nw - 1) / (S.rwt * S.nw);

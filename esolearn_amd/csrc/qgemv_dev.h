@@ -551,5 +551,277 @@ __device__ __forceinline__ void qgemv_block(const KArgs &a, const int bx, const 
     }
 }
 
+// ---- split-k single-row GEMV (int8 per-tensor weights, one activation row,
+// NCH chunks of 1 KiB, k % 16 == 0).
+//
+// A workgroup of NCH * RG waves holds RG row groups of R rows; wave (g, c)
+// streams chunk c of its group's rows.  Lane L keeps the 16 activation
+// values x[1024 c + 16 L .. + 15] in registers, read straight from memory
+// next to its weight requests (one 16-byte load per row), so the stream needs
+// no LDS stage and no barrier before it, and each activation value is read
+// once per workgroup.  A lane's per-row partials are reduced over the wave by
+// a transposed butterfly (R rows in log2(R) halving exchanges, then the rest
+// of the wave inside 64 / R lane groups), and the chunk partials of a row meet
+// in LDS at the single barrier; wave 0 sums them in chunk order and runs the
+// epilogue with one row per lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_addf(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// a + b over lane pairs l, l ^ O: lanes with bit O clear keep a's pair sums,
+// the others b's (O = 8 by DPP row_ror:8 within a 16-lane row, else ds_bpermute)
+template <int O>
+__device__ __forceinline__ float sk_pair(float a, float b, int lane) {
+    const bool hi = (lane & O) != 0;
+    const float keep = hi ? b : a, send = hi ? a : b;
+    if constexpr (O == 8)
+        return keep + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0x128, 0xF, 0xF, true));
+    else
+        return keep + __shfl_xor(send, O);
+}
+
+// Sum over the wave of each of R per-lane values: returns, in every lane, the
+// total of value index sk_row(lane).  log2(R) halving exchanges, then the
+// 64 / R lanes left holding parts of one value by DPP.
+template <int R>
+__device__ __forceinline__ float sk_reduce(const float (&v)[R], int lane) {
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "rows per wave: 1, 2, 4, 8 or 16");
+    float t;
+    if constexpr (R == 16) {
+        float u[8], w[4];
+#pragma unroll
+        for (int i = 0; i < 8; i++) u[i] = sk_pair<32>(v[i], v[i + 8], lane);
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = sk_pair<16>(u[i], u[i + 4], lane);
+        const float z0 = sk_pair<8>(w[0], w[2], lane), z1 = sk_pair<8>(w[1], w[3], lane);
+        t = sk_pair<4>(z0, z1, lane);
+    } else if constexpr (R == 8) {
+        const float u0 = sk_pair<32>(v[0], v[4], lane), u1 = sk_pair<32>(v[1], v[5], lane);
+        const float u2 = sk_pair<32>(v[2], v[6], lane), u3 = sk_pair<32>(v[3], v[7], lane);
+        t = sk_pair<8>(sk_pair<16>(u0, u2, lane), sk_pair<16>(u1, u3, lane), lane);
+    } else if constexpr (R == 4) {
+        t = sk_pair<16>(sk_pair<32>(v[0], v[2], lane), sk_pair<32>(v[1], v[3], lane), lane);
+    } else if constexpr (R == 2) {
+        t = sk_pair<32>(v[0], v[1], lane);
+    } else {
+        t = v[0];
+    }
+    constexpr int G = 64 / R;
+    if constexpr (G >= 2) t = dpp_addf<0xB1>(t);   // quad_perm [1,0,3,2]
+    if constexpr (G >= 4) t = dpp_addf<0x4E>(t);   // quad_perm [2,3,0,1]
+    if constexpr (G >= 8) t = dpp_addf<0x141>(t);  // row_half_mirror
+    if constexpr (G >= 16) t = dpp_addf<0x140>(t); // row_mirror
+    if constexpr (G >= 32) t += __shfl_xor(t, 16);
+    if constexpr (G >= 64) t += __shfl_xor(t, 32);
+    return t;
+}
+// the value index a lane holds after sk_reduce: lane bits 5, 4, 3 from the top
+template <int R>
+__device__ __forceinline__ int sk_row(int lane) {
+    return R == 16 ? (((lane >> 5) & 1) << 3) | (((lane >> 4) & 1) << 2) | (((lane >> 3) & 1) << 1) | ((lane >> 2) & 1)
+           : R == 8 ? (((lane >> 5) & 1) << 2) | (((lane >> 4) & 1) << 1) | ((lane >> 3) & 1)
+           : R == 4 ? (((lane >> 5) & 1) << 1) | ((lane >> 4) & 1)
+           : R == 2 ? (lane >> 5) & 1
+                    : 0;
+}
+
+template <int EPI, int PRO, int NCH, int RG, int R>
+__device__ __forceinline__ void qgemv_sk_block(const KArgs &a, const int bx) {
+    constexpr int NW = NCH * RG, RPW = RG * R, NT = 64 * NW;
+    static_assert(NW <= 16 && RPW <= 64, "split-k shape");
+    constexpr bool NORM = PRO != PRO_PLAIN;
+    __shared__ float s_part[RPW][NCH];
+    __shared__ double s_ss[NW];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = wave % NCH, g = wave / NCH;
+    const int rb = bx * RPW, row0 = rb + g * R;
+
+    // ---- 1. this lane's activation values, the RMSNorm inputs, the weights
+    const float *src = act_row<PRO, 1>(a, 0);
+    const unsigned xo = (unsigned)((c << 12) + (lane << 6));  // bytes of x[1024 c + 16 L]
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(src, (size_t)a.k * 4);
+    float4 x[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) x[j] = bload16f(xr, xo + 16 * j);  // past k: zeros
+    float4 gw[PRO == PRO_NORM ? 4 : 1];
+    if constexpr (PRO == PRO_NORM) {
+        const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.norm_w, (size_t)a.k * 4);
+#pragma unroll
+        for (int j = 0; j < 4; j++) gw[j] = bload16f(gr, xo + 16 * j);
+    }
+    float ssv[PRO == PRO_NORMP ? SSW : 1];
+    if constexpr (PRO == PRO_NORMP) {
+#pragma unroll
+        for (int j = 0; j < SSW; j++) ssv[j] = a.ss_in[min(tid + NT * j, a.n_ss - 1)];
+    }
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.W, (size_t)a.rows * a.kp);
+    u32x4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        w[r] = bload16(wr, (unsigned)(min(row0 + r, a.rows - 1) * a.kp) + (unsigned)(c << 10) + (unsigned)(lane << 4));
+    // EPI_RESID: the residual and the next norm's weight of the row lane t of
+    // wave 0 finishes (clamped: unconditional loads)
+    float pre_r = 0.f, pre_g = 0.f;
+    if constexpr (EPI == EPI_RESID) {
+        const int er = min(rb + min(lane, RPW - 1), a.rows - 1);
+        const float *Rs = a.resid ? a.resid : a.embed + (size_t)a.tokens[a.state->pos] * a.rows;
+        pre_r = Rs[er];
+        if (a.xg_out) pre_g = a.g_next[er];
+    }
+
+    // ---- 2. the RMSNorm's sum of squares (its loads were issued first)
+    if constexpr (NORM) {
+        double ssp = 0.0;
+        if constexpr (PRO == PRO_NORMP) {
+#pragma unroll
+            for (int j = 0; j < SSW; j++)
+                if (tid + NT * j < a.n_ss) ssp += ssv[j];
+        } else if (g == 0) {  // one row group covers the row once
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                ssp += (double)x[j].x * x[j].x + (double)x[j].y * x[j].y + (double)x[j].z * x[j].z +
+                       (double)x[j].w * x[j].w;
+        }
+        ssp = wave_sum_d_dpp(ssp);
+        if (lane == 0) s_ss[wave] = ssp;
+    }
+    if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[j].x *= gw[j].x;
+            x[j].y *= gw[j].y;
+            x[j].z *= gw[j].z;
+            x[j].w *= gw[j].w;
+        }
+    }
+
+    // ---- 3. the stream: sum_p (q + 128) x_p - 128 sum_p x_p per row
+    float xs = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) xs += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+    float p[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) p[r] = fmaf(-128.f, xs, dot16(w[r], x[0], x[1], x[2], x[3], 0.f));
+    const float tot = sk_reduce<R>(p, lane);
+    if ((lane & (64 / R - 1)) == 0) s_part[g * R + sk_row<R>(lane)][c] = tot;
+    __syncthreads();
+    if (wave != 0) return;
+
+    // ---- 4. wave 0: row rb + lane, its chunks summed in order, scaled
+    const int row = rb + lane;
+    const bool live = lane < RPW && row < a.rows;
+    float s = 0.f;
+    if (lane < RPW) {
+#pragma unroll
+        for (int cc = 0; cc < NCH; cc++) s += s_part[lane][cc];
+    }
+    const float sc = (EPI == EPI_SWIGLU && (row & 2)) ? a.scale2 : a.scale;
+    float val = sc * s;
+    float rs = 1.f;
+    if constexpr (NORM) {
+        double t = 0.0;
+#pragma unroll
+        for (int ww = 0; ww < NW; ww++) t += s_ss[ww];
+        rs = (float)(1.0 / sqrt(t / (double)a.k + (double)a.eps));
+    }
+    if constexpr (EPI == EPI_STORE || EPI == EPI_LOGITS) {
+        // a non-finite activation: the reference's sum of q x from the
+        // non-finite terms alone (see qgemv_block), one row at a time
+        unsigned long long bad = __ballot(live && isnan(val));
+        while (bad) {
+            const int t = __builtin_ctzll(bad);
+            bad &= bad - 1;
+            int cls = 0;
+            const size_t wrow_t = (size_t)(rb + t) * a.kp;
+#pragma unroll 1
+            for (int j = lane; j < a.k; j += 64) {
+                float xv = src[j];
+                if constexpr (PRO == PRO_NORM) xv *= a.norm_w[j];
+                if (!isfinite(xv)) {
+                    const int q = (int)(signed char)(a.W[wrow_t + j] ^ 0x80);
+                    const float tt = xv * ((float)q * a.scale);
+                    cls |= isnan(tt) ? 4 : tt > 0.f ? 1 : 2;
+                }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) cls |= __shfl_xor(cls, off);
+            if (lane == t && cls) val = (cls & 4) || cls == 3 ? __builtin_nanf("") : cls == 1 ? INFINITY : -INFINITY;
+        }
+    }
+
+    // ---- 5. epilogues (lane t: row rb + t)
+    if constexpr (EPI == EPI_STORE) {
+        if (live) a.y[row] = a.bias ? val + a.bias[row] : val;
+    } else if constexpr (EPI == EPI_RESID) {
+        const float v = pre_r + val;
+        if (live) {
+            if (a.xg_out) a.xg_out[row] = v * pre_g;
+            a.y[row] = v;
+        }
+        if (a.ss_out) {  // the next RMSNorm's sum of squares over this workgroup's rows
+            const double q = wave_sum_d_dpp(live ? (double)v * v : 0.0);
+            if (lane == 0) a.ss_out[bx] = (float)q;
+        }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        // rows 4i..4i+3 = gate[2i], gate[2i+1], up[2i], up[2i+1]
+        const int qg = (lane >> 1) * 4 + (lane & 1);
+        const float gv = __shfl(val, qg & 63), uv = __shfl(val, (qg + 2) & 63);
+        if (lane < RPW / 2 && rb + 2 * lane < a.rows) a.y[(rb >> 1) + lane] = silu_f(gv * rs) * (uv * rs);
+    } else if constexpr (EPI == EPI_QKV) {
+        const float x0 = __shfl(val, (2 * lane) & 63) * rs, x1 = __shfl(val, (2 * lane + 1) & 63) * rs;
+        const int j = rb + 2 * lane;
+        if (lane < RPW / 2 && j < a.rows) {
+            const int pos = a.state->pos, crow = a.state->cache_len;
+            const int hh = a.head_dim >> 1;
+            if (j < a.q_dim + a.kv_dim) {
+                const bool isq = j < a.q_dim;
+                const int jj = isq ? j : j - a.q_dim;
+                const float2 cs = a.rope_cs[(size_t)pos * hh + ((jj % a.head_dim) >> 1)];
+                // cpu.rs:655-658 in f32, no contraction
+                const float r0 = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
+                const float r1 = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+                if (isq) {
+                    a.q_out[jj] = __fmul_rn(r0, a.q_scale);
+                    a.q_out[jj + 1] = __fmul_rn(r1, a.q_scale);
+                } else {
+                    float *kr = a.k_cache + (size_t)crow * a.kv_dim;
+                    kr[jj] = r0;
+                    kr[jj + 1] = r1;
+                }
+            } else {
+                const int jj = j - a.q_dim - a.kv_dim;
+                float *vr = a.v_cache + (size_t)crow * a.kv_dim;
+                vr[jj] = x0;
+                vr[jj + 1] = x1;
+            }
+        }
+    } else if constexpr (EPI == EPI_LOGITS) {
+        const float v = val * rs;
+        if (live) a.y[row] = v;
+        // this workgroup's argmax partial: the order-free combine over its rows
+        ArgAcc acc{0.f, -1, -1};
+        if (live) {
+            if (isnan(v)) acc.nan = row;
+            else acc = ArgAcc{v, row, -1};
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            ArgAcc o;
+            o.v = __shfl_xor(acc.v, off);
+            o.i = __shfl_xor(acc.i, off);
+            o.nan = __shfl_xor(acc.nan, off);
+            acc = arg_combine(acc, o);
+        }
+        if (lane == 0) {
+            a.part_val[bx] = acc.v;
+            a.part_idx[bx] = acc.i;
+            a.part_nan[bx] = acc.nan;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace scry

@@ -69,6 +69,10 @@ SHAPES = [
     (3, 100, 65),       # ragged
     (2, 16, 5),
     (5, 2000, 33),      # runtime-chunk path
+    (1, 3088, 300),     # one row, 4 chunks, the last one 16 values wide
+    (1, 3080, 300),     # one row, k % 16 != 0
+    (1, 10256, 300),    # one row, 11 chunks, the last one 16 values wide
+    (1, 14336, 300),    # config-5 down at one row (14 chunks)
 ]
 
 
@@ -223,7 +227,7 @@ def test_skinny_matmul_nonfinite(hip, orc):
     assert rel_err(out[fin], ref[fin]) < 2e-5
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 4096, 512), (2, 4096, 512), (1, 11008, 256), (1, 300, 64)])
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 512), (2, 4096, 512), (1, 11008, 256), (1, 300, 64), (1, 3600, 130)])
 def test_gemv_matmul_nonfinite(hip, orc, m, k, n):
     """The GEMV rows (m <= 2) with Inf and NaN activations, as the skinny test
     above: Inf times a nonzero weight stays infinite, times 0 is NaN."""
