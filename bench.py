@@ -552,7 +552,7 @@ def main() -> int:
         "unit": "GB/s",
         "frac": round(proj[dom]["gbs"] / HBM_PEAK_GBS, 4),
         "traffic": measured_traffic(dom),
-        "kernel": f"k_qgemv ({dom} projection, decode epilogue)",
+        "kernel": f"k_qgemv_sk ({dom} projection, decode epilogue)",
         "bytes_per_launch": proj[dom]["bytes"],
         "avg_launch_us": proj[dom]["avg_us"],
     }
