@@ -14,43 +14,58 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
     if (a.ts) wg_stamp_end(a.ts);
 }
 
-// The split-k body for one activation row of int8 per-tensor weights with
-// k % 16 == 0 (every lane's 16 activation values wholly inside or past k) and
-// the Llama chunk counts: 4 (k <= 4096; two row groups of 4 waves), 11 and 14
-// (the down projections; one row group of 11 or 14 waves).  Rows per wave,
-// measured on the Llama-2-7B step (stamped graph replays): 8 at k <= 4096
-// (4: decode 553.5 against 576.5 tok/s; 16: 567.6-573.9 against 577.1), 4 for
-// the down projections (down 9.68 against 9.96-10.0 us at 8, 10.7 at 16).
-// Wave 0 finishes last, after the barrier.
-constexpr int sk_r(int epi, int nch) { return nch == 4 ? (epi == EPI_RESID ? 8 : 8) : 4; }  // rows per wave
-constexpr int sk_groups(int epi, int nch) { return nch == 4 ? (epi == EPI_RESID ? 2 : 2) : 1; }  // row groups per workgroup
+// The split-k body for one activation row with k % 16 == 0 (every lane's
+// activation values wholly inside or past k) at the Llama chunk counts:
+// int8 per-tensor and block-32 rows of 4 chunks (k <= 4096; two row groups of
+// 4 waves), 11 and 14 (the down projections; one row group of 11 or 14
+// waves); bf16 rows of 8 chunks (k = 4096; 8 waves), 22 and 28 (11 or 14
+// waves of two chunks).  Rows per wave, measured on the Llama-2-7B step
+// (stamped graph replays): 8 at k <= 4096 (4: decode 553.5 against 576.5
+// tok/s; 16: 567.6-573.9 against 577.1), 4 for the down projections (down
+// 9.68 against 9.96-10.0 us at 8, 10.7 at 16).  Wave 0 finishes last, after
+// the barrier.
+constexpr int sk_cpw(int wt, int nch) { return wt == WT_BF16 && nch > 8 ? 2 : 1; }  // chunks per wave
+constexpr int sk_r(int epi, int wt, int nch) { return nch == 4 || nch == 8 ? 8 : 4; }  // rows per wave
+constexpr int sk_groups(int epi, int wt, int nch) { return nch == 4 ? 2 : 1; }  // row groups per workgroup
+constexpr int sk_waves(int epi, int wt, int nch) { return nch / sk_cpw(wt, nch) * sk_groups(epi, wt, nch); }
 bool use_sk(int nch, int m, int wt, int k) {
-    return wt == WT_I8 && m == 1 && (nch == 4 || nch == 11 || nch == 14) && k % 16 == 0;
+    if (m != 1 || k % 16 != 0) return false;
+    return wt == WT_BF16 ? (nch == 8 || nch == 22 || nch == 28) : (nch == 4 || nch == 11 || nch == 14);
 }
-int sk_rows(int epi, int nch) { return sk_groups(epi, nch) * sk_r(epi, nch); }  // rows per workgroup
+int sk_rows(int epi, int wt, int nch) { return sk_groups(epi, wt, nch) * sk_r(epi, wt, nch); }  // rows per workgroup
 
-template <int EPI, int PRO, int NCH>
-__global__ __launch_bounds__(64 * NCH * sk_groups(EPI, NCH)) void k_qgemv_sk(KArgs a) {
+template <int EPI, int PRO, int WT, int NCH>
+__global__ __launch_bounds__(64 * sk_waves(EPI, WT, NCH)) void k_qgemv_sk(KArgs a) {
     if (a.ts) wg_stamp_begin(a.ts);
-    qgemv_sk_block<EPI, PRO, NCH, sk_groups(EPI, NCH), sk_r(EPI, NCH)>(a, blockIdx.x);
+    qgemv_sk_block<EPI, PRO, WT, NCH, sk_groups(EPI, WT, NCH), sk_r(EPI, WT, NCH), sk_cpw(WT, NCH)>(a, blockIdx.x);
     if (a.ts && __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) == 0)
         a.ts[2 * wg_linear_id() + 1] = __builtin_amdgcn_s_memrealtime();
 }
 
-template <int EPI, int PRO, int NCH>
+template <int EPI, int PRO, int WT, int NCH>
 int launch_sk_t(const KArgs &ka, hipStream_t s) {
-    constexpr int RPW = sk_groups(EPI, NCH) * sk_r(EPI, NCH);
-    hipLaunchKernelGGL((k_qgemv_sk<EPI, PRO, NCH>), dim3((ka.rows + RPW - 1) / RPW),
-                       dim3(64 * NCH * sk_groups(EPI, NCH)), 0, s, ka);
+    constexpr int RPW = sk_groups(EPI, WT, NCH) * sk_r(EPI, WT, NCH);
+    hipLaunchKernelGGL((k_qgemv_sk<EPI, PRO, WT, NCH>), dim3((ka.rows + RPW - 1) / RPW),
+                       dim3(64 * sk_waves(EPI, WT, NCH)), 0, s, ka);
     SCRY_HIP(hipGetLastError());
     return SCRY_OK;
 }
 
 template <int EPI, int PRO>
-int launch_sk(const KArgs &ka, hipStream_t s) {
-    if (ka.nch == 4) return launch_sk_t<EPI, PRO, 4>(ka, s);
-    if (ka.nch == 11) return launch_sk_t<EPI, PRO, 11>(ka, s);
-    if (ka.nch == 14) return launch_sk_t<EPI, PRO, 14>(ka, s);
+int launch_sk(const KArgs &ka, int wt, hipStream_t s) {
+    if (wt == WT_BF16) {
+        if (ka.nch == 8) return launch_sk_t<EPI, PRO, WT_BF16, 8>(ka, s);
+        if (ka.nch == 22) return launch_sk_t<EPI, PRO, WT_BF16, 22>(ka, s);
+        if (ka.nch == 28) return launch_sk_t<EPI, PRO, WT_BF16, 28>(ka, s);
+    } else if (wt == WT_I8B32) {
+        if (ka.nch == 4) return launch_sk_t<EPI, PRO, WT_I8B32, 4>(ka, s);
+        if (ka.nch == 11) return launch_sk_t<EPI, PRO, WT_I8B32, 11>(ka, s);
+        if (ka.nch == 14) return launch_sk_t<EPI, PRO, WT_I8B32, 14>(ka, s);
+    } else {
+        if (ka.nch == 4) return launch_sk_t<EPI, PRO, WT_I8, 4>(ka, s);
+        if (ka.nch == 11) return launch_sk_t<EPI, PRO, WT_I8, 11>(ka, s);
+        if (ka.nch == 14) return launch_sk_t<EPI, PRO, WT_I8, 14>(ka, s);
+    }
     return set_error(SCRY_ERR_INVALID, "qgemv: no split-k shape for %d chunks", ka.nch);
 }
 
@@ -139,7 +154,7 @@ int launch_mt(const KArgs &ka, Sel sel, hipStream_t s) {
 
 template <int EPI, int PRO>
 int launch_wt(const KArgs &ka, int wt, Sel sel, hipStream_t s) {
-    if (use_sk(ka.nch, ka.m, wt, ka.k)) return launch_sk<EPI, PRO>(ka, s);
+    if (use_sk(ka.nch, ka.m, wt, ka.k)) return launch_sk<EPI, PRO>(ka, wt, s);
     if (wt == WT_BF16) return launch_mt<EPI, PRO, WT_BF16>(ka, sel, s);
     if (wt == WT_I8B32) return launch_mt<EPI, PRO, WT_I8B32>(ka, sel, s);
     return launch_mt<EPI, PRO, WT_I8>(ka, sel, s);
@@ -167,7 +182,8 @@ int row_chunks(const Packed &w) { return (w.bf16 ? 2 * w.k + 1023 : w.k + 1023) 
 }  // namespace
 
 int qgemv_blocks(int epi, const Packed &w, int m) {
-    if (use_sk(row_chunks(w), m, weight_type(w), w.k)) return (w.rows + sk_rows(epi, row_chunks(w)) - 1) / sk_rows(epi, row_chunks(w));
+    const int wt = weight_type(w), nch = row_chunks(w);
+    if (use_sk(nch, m, wt, w.k)) return (w.rows + sk_rows(epi, wt, nch) - 1) / sk_rows(epi, wt, nch);
     const Sel sel = select_cfg(epi, row_chunks(w), m, weight_type(w));
     const Shape S = shape_for(sel.nch_t, sel.mt);
     return (w.rows + S.rwt * S.nw - 1) / (S.rwt * S.nw);
@@ -195,7 +211,7 @@ int qgemv_kargs(int epi, const GemvArgs &g, KArgs *out, int *wt_out, int *nch_ou
         return set_error(SCRY_ERR_INVALID, "qgemv: decode epilogues take one activation row");
     if (epi == EPI_QKV && (w.rows % 2 != 0 || g.head_dim % 2 != 0 || g.q_dim % 2 != 0 || g.kv_dim % 2 != 0))
         return set_error(SCRY_ERR_INVALID, "qgemv: qkv epilogue needs even head, q and kv sizes");
-    const int max_ss = SSW * 64 * (use_sk(nch, g.m, wt, w.k) ? nch * sk_groups(epi, nch) : shape_for(sel.nch_t, sel.mt).nw);
+    const int max_ss = SSW * 64 * (use_sk(nch, g.m, wt, w.k) ? sk_waves(epi, wt, nch) : shape_for(sel.nch_t, sel.mt).nw);
     if (g.ss_in && (g.n_ss < 1 || g.n_ss > max_ss || g.norm_w))
         return set_error(SCRY_ERR_INVALID,
                          "qgemv: pre-scaled RMSNorm input needs 1..%d partial sums and no norm weight", max_ss);

@@ -551,15 +551,17 @@ __device__ __forceinline__ void qgemv_block(const KArgs &a, const int bx, const 
     }
 }
 
-// ---- split-k single-row GEMV (int8 per-tensor weights, one activation row,
-// NCH chunks of 1 KiB, k % 16 == 0).
+// ---- split-k single-row GEMV (one activation row, NCH chunks of 1 KiB,
+// k % 16 == 0; int8 per-tensor or block-32 weights, or bf16 rows).
 //
-// A workgroup of NCH * RG waves holds RG row groups of R rows; wave (g, c)
-// streams chunk c of its group's rows.  Lane L keeps the 16 activation
-// values x[1024 c + 16 L .. + 15] in registers, read straight from memory
-// next to its weight requests (one 16-byte load per row), so the stream needs
-// no LDS stage and no barrier before it, and each activation value is read
-// once per workgroup.  A lane's per-row partials are reduced over the wave by
+// A workgroup of NCH / CPW * RG waves holds RG row groups of R rows; wave
+// (g, cw) streams chunks cw + j NCH / CPW (j < CPW) of its group's rows.  For
+// each of them lane L keeps the activation values under its 16 weight bytes
+// (int8: x[1024 c + 16 L .. + 15]; bf16: x[512 c + 8 L .. + 7]) in registers,
+// read straight from memory next to its weight requests (one 16-byte load per
+// row and chunk), so each activation value is read once per workgroup, and
+// the int8 stream needs no LDS stage and no barrier before it (the bf16
+// RMSNorm scale is formed first: one barrier while the weights are in flight).  A lane's per-row partials are reduced over the wave by
 // a transposed butterfly (R rows in log2(R) halving exchanges, then the rest
 // of the wave inside 64 / R lane groups), and the chunk partials of a row meet
 // in LDS at the single barrier; wave 0 sums them in chunk order and runs the
@@ -626,31 +628,40 @@ __device__ __forceinline__ int sk_row(int lane) {
                     : 0;
 }
 
-template <int EPI, int PRO, int NCH, int RG, int R>
+template <int EPI, int PRO, int WT, int NCH, int RG, int R, int CPW>
 __device__ __forceinline__ void qgemv_sk_block(const KArgs &a, const int bx) {
-    constexpr int NW = NCH * RG, RPW = RG * R, NT = 64 * NW;
-    static_assert(NW <= 16 && RPW <= 64, "split-k shape");
-    constexpr bool NORM = PRO != PRO_PLAIN;
-    __shared__ float s_part[RPW][NCH];
+    constexpr int NWC = NCH / CPW, NW = NWC * RG, RPW = RG * R, NT = 64 * NW;
+    static_assert(NCH % CPW == 0 && NW <= 16 && RPW <= 64, "split-k shape");
+    constexpr bool NORM = PRO != PRO_PLAIN, WB = WT == WT_BF16, B32 = WT == WT_I8B32;
+    constexpr int XF = WB ? 2 : 4;       // float4 of activations per lane and chunk
+    constexpr int CV = WB ? 512 : 1024;  // activation values per chunk
+    __shared__ float s_part[RPW][NWC];
     __shared__ double s_ss[NW];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int c = wave % NCH, g = wave / NCH;
+    const int cw = wave % NWC, g = wave / NWC;  // chunks cw + j NWC of row group g
     const int rb = bx * RPW, row0 = rb + g * R;
 
     // ---- 1. this lane's activation values, the RMSNorm inputs, the weights
     const float *src = act_row<PRO, 1>(a, 0);
-    const unsigned xo = (unsigned)((c << 12) + (lane << 6));  // bytes of x[1024 c + 16 L]
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(src, (size_t)a.k * 4);
-    float4 x[4];
+    float4 x[CPW][XF];
 #pragma unroll
-    for (int j = 0; j < 4; j++) x[j] = bload16f(xr, xo + 16 * j);  // past k: zeros
-    float4 gw[PRO == PRO_NORM ? 4 : 1];
+    for (int j = 0; j < CPW; j++) {
+        const unsigned xo = (unsigned)(((cw + j * NWC) * CV + lane * 4 * XF) * 4);
+#pragma unroll
+        for (int f = 0; f < XF; f++) x[j][f] = bload16f(xr, xo + 16 * f);  // past k: zeros
+    }
+    float4 gw[PRO == PRO_NORM ? CPW : 1][PRO == PRO_NORM ? XF : 1];
     if constexpr (PRO == PRO_NORM) {
         const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.norm_w, (size_t)a.k * 4);
 #pragma unroll
-        for (int j = 0; j < 4; j++) gw[j] = bload16f(gr, xo + 16 * j);
+        for (int j = 0; j < CPW; j++) {
+            const unsigned xo = (unsigned)(((cw + j * NWC) * CV + lane * 4 * XF) * 4);
+#pragma unroll
+            for (int f = 0; f < XF; f++) gw[j][f] = bload16f(gr, xo + 16 * f);
+        }
     }
     float ssv[PRO == PRO_NORMP ? SSW : 1];
     if constexpr (PRO == PRO_NORMP) {
@@ -658,10 +669,25 @@ __device__ __forceinline__ void qgemv_sk_block(const KArgs &a, const int bx) {
         for (int j = 0; j < SSW; j++) ssv[j] = a.ss_in[min(tid + NT * j, a.n_ss - 1)];
     }
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.W, (size_t)a.rows * a.kp);
-    u32x4 w[R];
+    u32x4 w[CPW][R];
 #pragma unroll
-    for (int r = 0; r < R; r++)
-        w[r] = bload16(wr, (unsigned)(min(row0 + r, a.rows - 1) * a.kp) + (unsigned)(c << 10) + (unsigned)(lane << 4));
+    for (int j = 0; j < CPW; j++)
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            w[j][r] = bload16(wr, (unsigned)(min(row0 + r, a.rows - 1) * a.kp) + (unsigned)((cw + j * NWC) << 10) +
+                                      (unsigned)(lane << 4));
+    // block-32: the scale of the 32-value block this lane's 16 bytes are half of
+    float bs[B32 ? CPW : 1][B32 ? R : 1];
+    if constexpr (B32) {
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s32, (size_t)a.rows * a.nb * sizeof(float));
+#pragma unroll
+        for (int j = 0; j < CPW; j++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                bs[j][r] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(
+                               sr, (min(row0 + r, a.rows - 1) * a.nb + (cw + j * NWC) * 32 + (lane >> 1)) * 4, 0, 0));
+    }
     // EPI_RESID: the residual and the next norm's weight of the row lane t of
     // wave 0 finishes (clamped: unconditional loads)
     float pre_r = 0.f, pre_g = 0.f;
@@ -681,32 +707,99 @@ __device__ __forceinline__ void qgemv_sk_block(const KArgs &a, const int bx) {
                 if (tid + NT * j < a.n_ss) ssp += ssv[j];
         } else if (g == 0) {  // one row group covers the row once
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                ssp += (double)x[j].x * x[j].x + (double)x[j].y * x[j].y + (double)x[j].z * x[j].z +
-                       (double)x[j].w * x[j].w;
+            for (int j = 0; j < CPW; j++)
+#pragma unroll
+                for (int f = 0; f < XF; f++)
+                    ssp += (double)x[j][f].x * x[j][f].x + (double)x[j][f].y * x[j][f].y +
+                           (double)x[j][f].z * x[j][f].z + (double)x[j][f].w * x[j][f].w;
         }
         ssp = wave_sum_d_dpp(ssp);
         if (lane == 0) s_ss[wave] = ssp;
     }
-    if constexpr (PRO == PRO_NORM) {
+    if constexpr (WB) {
+        // bf16 (cpu.rs:574-599, cuda.rs:1206-1290): each activation value is
+        // normalised, then rounded with the reference's cast, before the
+        // products, so rstd is formed first (one barrier; the weights are in
+        // flight): f32(f64(x) rstd f64(w)) for the embedding row, f32(f64(x g)
+        // rstd) from the residual GEMV's row
+        double rstd = 1.0;
+        if constexpr (NORM) {
+            __syncthreads();
+            double t = 0.0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            x[j].x *= gw[j].x;
-            x[j].y *= gw[j].y;
-            x[j].z *= gw[j].z;
-            x[j].w *= gw[j].w;
+            for (int ww = 0; ww < NW; ww++) t += s_ss[ww];
+            rstd = 1.0 / sqrt(t / (double)a.k + (double)a.eps);
         }
+#pragma unroll
+        for (int j = 0; j < CPW; j++)
+#pragma unroll
+            for (int f = 0; f < XF; f++) {
+                float4 v = x[j][f];
+                if constexpr (PRO == PRO_NORM) {
+                    v.x = (float)((double)v.x * rstd * (double)gw[j][f].x);
+                    v.y = (float)((double)v.y * rstd * (double)gw[j][f].y);
+                    v.z = (float)((double)v.z * rstd * (double)gw[j][f].z);
+                    v.w = (float)((double)v.w * rstd * (double)gw[j][f].w);
+                } else if constexpr (PRO == PRO_NORMP) {
+                    v.x = (float)((double)v.x * rstd);
+                    v.y = (float)((double)v.y * rstd);
+                    v.z = (float)((double)v.z * rstd);
+                    v.w = (float)((double)v.w * rstd);
+                }
+                x[j][f] = make_float4(bf16_cast(v.x), bf16_cast(v.y), bf16_cast(v.z), bf16_cast(v.w));
+            }
+    } else if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+        for (int j = 0; j < CPW; j++)
+#pragma unroll
+            for (int f = 0; f < XF; f++) {
+                x[j][f].x *= gw[j][f].x;
+                x[j][f].y *= gw[j][f].y;
+                x[j][f].z *= gw[j][f].z;
+                x[j][f].w *= gw[j][f].w;
+            }
     }
 
-    // ---- 3. the stream: sum_p (q + 128) x_p - 128 sum_p x_p per row
-    float xs = 0.f;
+    // ---- 3. the stream: int8, sum_p (q + 128) x_p - 128 sum_p x_p per row
+    // (block-32: per 16-value half block, scaled); bf16, the products of the
+    // rounded values (lanes past the row's kp bytes read the next row's bytes
+    // against zero activations: their weights are dropped, since bf16 bits
+    // can be infinite)
+    float xs[CPW];
 #pragma unroll
-    for (int j = 0; j < 4; j++) xs += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+    for (int j = 0; j < CPW; j++) {
+        xs[j] = 0.f;
+        if constexpr (!WB) {
+#pragma unroll
+            for (int f = 0; f < XF; f++) xs[j] += (x[j][f].x + x[j][f].y) + (x[j][f].z + x[j][f].w);
+        }
+    }
     float p[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) p[r] = fmaf(-128.f, xs, dot16(w[r], x[0], x[1], x[2], x[3], 0.f));
+    for (int r = 0; r < R; r++) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPW; j++) {
+            if constexpr (WB) {
+                const bool in = ((cw + j * NWC) << 10) + (lane << 4) < a.kp;
+                const u32x4 wv = in ? w[j][r] : u32x4{0u, 0u, 0u, 0u};
+                acc = dot8_bf16(wv, x[j][0], x[j][1], acc);
+            } else if constexpr (B32) {
+                acc = fmaf(bs[j][r], fmaf(-128.f, xs[j], dot16(w[j][r], x[j][0], x[j][1], x[j][2], x[j][3], 0.f)), acc);
+            } else {
+                acc = dot16(w[j][r], x[j][0], x[j][1], x[j][2], x[j][3], acc);
+            }
+        }
+        if constexpr (WT == WT_I8) {
+            float xt = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPW; j++) xt += xs[j];
+            acc = fmaf(-128.f, xt, acc);
+        }
+        p[r] = acc;
+    }
     const float tot = sk_reduce<R>(p, lane);
-    if ((lane & (64 / R - 1)) == 0) s_part[g * R + sk_row<R>(lane)][c] = tot;
+    if ((lane & (64 / R - 1)) == 0) s_part[g * R + sk_row<R>(lane)][cw] = tot;
     __syncthreads();
     if (wave != 0) return;
 
@@ -716,18 +809,20 @@ __device__ __forceinline__ void qgemv_sk_block(const KArgs &a, const int bx) {
     float s = 0.f;
     if (lane < RPW) {
 #pragma unroll
-        for (int cc = 0; cc < NCH; cc++) s += s_part[lane][cc];
+        for (int cc = 0; cc < NWC; cc++) s += s_part[lane][cc];
     }
-    const float sc = (EPI == EPI_SWIGLU && (row & 2)) ? a.scale2 : a.scale;
+    // int8 per tensor: the tensor scale (gate / up rows of the fused layout);
+    // block-32 and bf16 products are already scaled
+    const float sc = WT != WT_I8 ? 1.f : (EPI == EPI_SWIGLU && (row & 2)) ? a.scale2 : a.scale;
     float val = sc * s;
-    float rs = 1.f;
-    if constexpr (NORM) {
+    float rs = 1.f;  // int8: the RMSNorm scale applied to the dot products
+    if constexpr (NORM && !WB) {
         double t = 0.0;
 #pragma unroll
         for (int ww = 0; ww < NW; ww++) t += s_ss[ww];
         rs = (float)(1.0 / sqrt(t / (double)a.k + (double)a.eps));
     }
-    if constexpr (EPI == EPI_STORE || EPI == EPI_LOGITS) {
+    if constexpr (!WB && (EPI == EPI_STORE || EPI == EPI_LOGITS)) {
         // a non-finite activation: the reference's sum of q x from the
         // non-finite terms alone (see qgemv_block), one row at a time
         unsigned long long bad = __ballot(live && isnan(val));
@@ -742,7 +837,8 @@ __device__ __forceinline__ void qgemv_sk_block(const KArgs &a, const int bx) {
                 if constexpr (PRO == PRO_NORM) xv *= a.norm_w[j];
                 if (!isfinite(xv)) {
                     const int q = (int)(signed char)(a.W[wrow_t + j] ^ 0x80);
-                    const float tt = xv * ((float)q * a.scale);
+                    const float ws = B32 ? a.s32[(size_t)(rb + t) * a.nb + (j >> 5)] : a.scale;
+                    const float tt = xv * ((float)q * ws);
                     cls |= isnan(tt) ? 4 : tt > 0.f ? 1 : 2;
                 }
             }

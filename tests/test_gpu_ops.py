@@ -227,8 +227,10 @@ def test_skinny_matmul_nonfinite(hip, orc):
     assert rel_err(out[fin], ref[fin]) < 2e-5
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 4096, 512), (2, 4096, 512), (1, 11008, 256), (1, 300, 64), (1, 3600, 130)])
-def test_gemv_matmul_nonfinite(hip, orc, m, k, n):
+@pytest.mark.parametrize("m,k,n,b32", [(1, 4096, 512, False), (2, 4096, 512, False), (1, 11008, 256, False),
+                                        (1, 300, 64, False), (1, 3600, 130, False), (1, 4096, 300, True),
+                                        (1, 11008, 200, True)])
+def test_gemv_matmul_nonfinite(hip, orc, m, k, n, b32):
     """The GEMV rows (m <= 2) with Inf and NaN activations, as the skinny test
     above: Inf times a nonzero weight stays infinite, times 0 is NaN."""
     B = hip.HipBackend
@@ -240,9 +242,14 @@ def test_gemv_matmul_nonfinite(hip, orc, m, k, n):
         a[1, 100] = -np.inf
     q = rng.integers(-127, 128, (k, n)).astype(np.int8)
     q[3, :16] = 0
-    ref = orc.matmul_i8_f32(a, q, 0.01, m, k, n)
-    out = B.matmul_i8_f32(B.from_vec(a), B.i8_from_vec(q), 0.01, m, k, n).to_vec().reshape(m, n)
-    print(f"[nf] m={m} k={k}: inf gpu {int(np.isinf(out).sum())} ref {int(np.isinf(ref).sum())}, "
+    if b32:
+        s32 = rng.uniform(0.005, 0.02, (n, (k + 31) // 32)).astype(F)
+        ref = orc.matmul_i8_f32_b32(a, q, s32, m, k, n)
+        out = B.matmul_i8_f32_block32(B.from_vec(a), B.i8_from_vec(q), B.from_vec(s32), m, k, n).to_vec().reshape(m, n)
+    else:
+        ref = orc.matmul_i8_f32(a, q, 0.01, m, k, n)
+        out = B.matmul_i8_f32(B.from_vec(a), B.i8_from_vec(q), 0.01, m, k, n).to_vec().reshape(m, n)
+    print(f"[nf] m={m} k={k} b32={b32}: inf gpu {int(np.isinf(out).sum())} ref {int(np.isinf(ref).sum())}, "
           f"nan gpu {int(np.isnan(out).sum())} ref {int(np.isnan(ref).sum())}", flush=True)
     assert np.array_equal(np.isnan(out), np.isnan(ref))
     assert np.array_equal(np.isinf(out), np.isinf(ref))
