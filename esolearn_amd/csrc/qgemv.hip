@@ -18,19 +18,20 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
 // activation values wholly inside or past k) at the Llama chunk counts:
 // int8 per-tensor and block-32 rows of 4 chunks (k <= 4096; two row groups of
 // 4 waves), 11 and 14 (the down projections; one row group of 11 or 14
-// waves); bf16 rows of 8 chunks (k = 4096; 8 waves), 22 and 28 (11 or 14
-// waves of two chunks).  Rows per wave, measured on the Llama-2-7B step
-// (stamped graph replays): 8 at k <= 4096 (4: decode 553.5 against 576.5
-// tok/s; 16: 567.6-573.9 against 577.1), 4 for the down projections (down
-// 9.68 against 9.96-10.0 us at 8, 10.7 at 16).  Wave 0 finishes last, after
-// the barrier.
-constexpr int sk_cpw(int wt, int nch) { return wt == WT_BF16 && nch > 8 ? 2 : 1; }  // chunks per wave
+// waves); bf16 rows of 8 chunks (k = 4096; 8 waves).  Rows per wave, measured
+// on the Llama-2-7B step (stamped graph replays): 8 at k <= 4096 (4: decode
+// 553.5 against 576.5 tok/s; 16: 567.6-573.9 against 577.1), 4 for the down
+// projections (down 9.68 against 9.96-10.0 us at 8, 10.7 at 16).  The bf16
+// down rows (22 and 28 chunks) stay on the LDS-staged body: as 11 waves of
+// two chunks the bf16 model decoded 369-370 against 377-378 tok/s (4 rows
+// per wave; 364 with 8).  Wave 0 finishes last, after the barrier.
+constexpr int sk_cpw(int wt, int nch) { return wt == WT_BF16 && nch > 8 ? 2 : 1; }  // chunks per wave (2: measured only)
 constexpr int sk_r(int epi, int wt, int nch) { return nch == 4 || nch == 8 ? 8 : 4; }  // rows per wave
 constexpr int sk_groups(int epi, int wt, int nch) { return nch == 4 ? 2 : 1; }  // row groups per workgroup
 constexpr int sk_waves(int epi, int wt, int nch) { return nch / sk_cpw(wt, nch) * sk_groups(epi, wt, nch); }
 bool use_sk(int nch, int m, int wt, int k) {
     if (m != 1 || k % 16 != 0) return false;
-    return wt == WT_BF16 ? (nch == 8 || nch == 22 || nch == 28) : (nch == 4 || nch == 11 || nch == 14);
+    return wt == WT_BF16 ? nch == 8 : (nch == 4 || nch == 11 || nch == 14);
 }
 int sk_rows(int epi, int wt, int nch) { return sk_groups(epi, wt, nch) * sk_r(epi, wt, nch); }  // rows per workgroup
 
@@ -55,8 +56,6 @@ template <int EPI, int PRO>
 int launch_sk(const KArgs &ka, int wt, hipStream_t s) {
     if (wt == WT_BF16) {
         if (ka.nch == 8) return launch_sk_t<EPI, PRO, WT_BF16, 8>(ka, s);
-        if (ka.nch == 22) return launch_sk_t<EPI, PRO, WT_BF16, 22>(ka, s);
-        if (ka.nch == 28) return launch_sk_t<EPI, PRO, WT_BF16, 28>(ka, s);
     } else if (wt == WT_I8B32) {
         if (ka.nch == 4) return launch_sk_t<EPI, PRO, WT_I8B32, 4>(ka, s);
         if (ka.nch == 11) return launch_sk_t<EPI, PRO, WT_I8B32, 11>(ka, s);
