@@ -588,17 +588,9 @@ __device__ __forceinline__ float sk_pair(float a, float b, int lane) {
 // 64 / R lanes left holding parts of one value by DPP.
 template <int R>
 __device__ __forceinline__ float sk_reduce(const float (&v)[R], int lane) {
-    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "rows per wave: 1, 2, 4, 8 or 16");
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8, "rows per wave: 1, 2, 4 or 8");
     float t;
-    if constexpr (R == 16) {
-        float u[8], w[4];
-#pragma unroll
-        for (int i = 0; i < 8; i++) u[i] = sk_pair<32>(v[i], v[i + 8], lane);
-#pragma unroll
-        for (int i = 0; i < 4; i++) w[i] = sk_pair<16>(u[i], u[i + 4], lane);
-        const float z0 = sk_pair<8>(w[0], w[2], lane), z1 = sk_pair<8>(w[1], w[3], lane);
-        t = sk_pair<4>(z0, z1, lane);
-    } else if constexpr (R == 8) {
+    if constexpr (R == 8) {
         const float u0 = sk_pair<32>(v[0], v[4], lane), u1 = sk_pair<32>(v[1], v[5], lane);
         const float u2 = sk_pair<32>(v[2], v[6], lane), u3 = sk_pair<32>(v[3], v[7], lane);
         t = sk_pair<8>(sk_pair<16>(u0, u2, lane), sk_pair<16>(u1, u3, lane), lane);
@@ -621,8 +613,7 @@ __device__ __forceinline__ float sk_reduce(const float (&v)[R], int lane) {
 // the value index a lane holds after sk_reduce: lane bits 5, 4, 3 from the top
 template <int R>
 __device__ __forceinline__ int sk_row(int lane) {
-    return R == 16 ? (((lane >> 5) & 1) << 3) | (((lane >> 4) & 1) << 2) | (((lane >> 3) & 1) << 1) | ((lane >> 2) & 1)
-           : R == 8 ? (((lane >> 5) & 1) << 2) | (((lane >> 4) & 1) << 1) | ((lane >> 3) & 1)
+    return R == 8 ? (((lane >> 5) & 1) << 2) | (((lane >> 4) & 1) << 1) | ((lane >> 3) & 1)
            : R == 4 ? (((lane >> 5) & 1) << 1) | ((lane >> 4) & 1)
            : R == 2 ? (lane >> 5) & 1
                     : 0;
