@@ -21,7 +21,7 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
 // waves); bf16 rows of 8 chunks (k = 4096; 8 waves).  Rows per wave, measured
 // on the Llama-2-7B step (stamped graph replays): 8 at k <= 4096 (4: decode
 // 553.5 against 576.5 tok/s; 16: 567.6-573.9 against 577.1), 4 for the down
-// projections (down 9.68 against 9.96-10.0 us at 8, 10.7 at 16).  The bf16
+// projections (down 9.68 against 9.96-10.0 us at 8, 10.7 at 16, 12.4 at 2).  The bf16
 // down rows (22 and 28 chunks) stay on the LDS-staged body: as 11 waves of
 // two chunks the bf16 model decoded 369-370 against 377-378 tok/s (4 rows
 // per wave; 364 with 8).  Wave 0 finishes last, after the barrier.
