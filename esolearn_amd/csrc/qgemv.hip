@@ -22,10 +22,8 @@ __global__ __launch_bounds__(64 * shape_for(NCH, MT).nw) void k_qgemv(KArgs a) {
 // on the Llama-2-7B step (stamped graph replays): 8 at k <= 4096 (4: decode
 // 553.5 against 576.5 tok/s; 16: 567.6-573.9 against 577.1), 4 for the down
 // projections (down 9.68 against 9.96-10.0 us at 8, 10.7 at 16, 12.4 at 2).
-// gate/up takes one row group (4 waves, 2752 workgroups): its workgroups
-// stream in 12.7 instead of 15.6 us, the next launch then starts 4.0 instead
-// of 1.5 us after them, and the step gains 0.5% (572.3 against 569.6 tok/s;
-// event-timed gate/up 16.75 against 16.9 us).  The bf16
+// gate/up takes one row group (4 waves, 2752 workgroups): 572.3 against
+// 569.6 tok/s, event-timed gate/up 16.75 against 16.9 us.  The bf16
 // down rows (22 and 28 chunks) stay on the LDS-staged body: as 11 waves of
 // two chunks the bf16 model decoded 369-370 against 377-378 tok/s (4 rows
 // per wave; 364 with 8).  Wave 0 finishes last, after the barrier.
