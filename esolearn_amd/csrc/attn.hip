@@ -444,7 +444,8 @@ int launch_g(const AttnArgs &a, const AttnSeqs *b, const QkvPro *qp, int nrep, h
 int attn_pick_splits(int n_kv, int max_seq, int *n_splits, int *max_chunk) {
     // ~512 workgroups per launch (two per CU: measured at the 7B shape, 32 KV
     // groups, against 256: 9.83 against 10.08 us at 768 cached rows, 13.95
-    // against 14.3 us at 1536, decode +0.6%), at most 16 splits (the last
+    // against 14.3 us at 1536, decode +0.6%; against 384: 14.0 against 15.3 us
+    // at 1536, decode 568.4 against 564.5 tok/s), at most 16 splits (the last
     // split merges n_splits partials per query head), >= 16 rows per split
     int ns = (512 + n_kv - 1) / n_kv;
     if (ns > 16) ns = 16;
