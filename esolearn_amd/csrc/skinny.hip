@@ -555,6 +555,14 @@ __global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
         const float *p = a.part + (size_t)row * a.n_pad + c;
         double ssq = 0.0;
         if (a.ss_in && lane < a.n_ss_in) ssq = a.ss_in[(size_t)row * a.n_ss_in + lane];
+        // the residual values, requested with the partials (clamped in
+        // bounds, unconditional): otherwise their load waits for the sums
+        float r0 = 0.f, r1 = 0.f;
+        if constexpr (EPI == SKE_RESID) {
+            const float *yq = a.y + (size_t)row * a.ldy;
+            r0 = yq[min(c, a.n_out - 1)];
+            r1 = yq[min(c + 1, a.n_out - 1)];
+        }
         float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
         for (int i0 = 0; i0 < a.n_split; i0 += NB) {
             float2 q0[NB], q1[SW ? NB : 1];
@@ -594,8 +602,8 @@ __global__ __launch_bounds__(SK_NT) void k_skinny_epi(SkArgs a) {
             const bool ok0 = c < a.n_out, ok1 = c1 < a.n_out;
             float v0 = (float)((double)(s0 * a.scale) * rstd), v1 = (float)((double)(s1 * a.scale) * rstd);
             if constexpr (EPI == SKE_RESID) {  // llama.rs:556-569: x + o, x + down
-                if (ok0) v0 = yr[c] + v0;
-                if (ok1) v1 = yr[c1] + v1;
+                v0 = r0 + v0;
+                v1 = r1 + v1;
             }
             if (ok0) yr[c] = v0;
             if (ok1) yr[c1] = v1;
